@@ -1,0 +1,66 @@
+"""Build libgllm_hip.so (the C-ABI library of include/gllm_hip.h) for gfx950.
+
+One hipcc invocation over csrc/*.hip, output in-tree next to this file so the
+built library travels with the repository snapshot.  Flags:
+
+* ``-ffp-contract=off``: the kernels place every fused multiply-add
+  explicitly (fmaf) where the reference's AVX2 code uses VFMADD, and nowhere
+  else, so float results are bit-identical to the reference's amd64 order.
+* ``-fhip-fp32-correctly-rounded-divide-sqrt``: IEEE division (the Q8K scale
+  amax/127 and the softmax 1/denom must round exactly like the CPU).
+* ``-Xclang -target-feature -Xclang -packed-fp32-ops``: no packed fp32 math.
+"""
+from __future__ import annotations
+
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libgllm_hip.so")
+ARCH = os.environ.get("GLLM_OFFLOAD_ARCH", "gfx950")
+
+FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build libgllm_hip)")
+
+
+def sources():
+    return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source into libgllm_hip.so; returns its path."""
+    tmp = LIB + ".tmp"
+    cmd = [hipcc()] + FLAGS + sources() + ["-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

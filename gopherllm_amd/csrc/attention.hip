@@ -1,0 +1,484 @@
+// attention.hip -- HBM-resident F16 KV cache and GQA decode attention.
+//
+// Exact path (GLLM_ATTN_EXACT) evaluates the reference's two-pass attention
+// in its float order (onlineAttentionGroup4F16 model.go:3527-3588 and the
+// per-head onlineAttentionF16WithSink kv_f16.go:88-111, which perform the
+// same operations):
+//   s_t   = dotF32F16(q, k_t) * scale     8 fma lanes + tree (kernels_amd64.s:104-129)
+//   M     = max_t s_t
+//   w_t   = fastExpF32(s_t - M)           fastmath.go:47-77
+//   denom = sum_t w_t                     sequential in t
+//   out   = sum_t fma(w_t, v_t, out)      sequential in t (axpyF16, kernels_amd64.s:132-155)
+//   out  *= 1/denom                       ScaleF32
+// Split-K path (GLLM_ATTN_SPLITK) streams K/V tiles per (kv head, chunk)
+// with an online-softmax merge; it agrees with the exact path to float
+// rounding (not bitwise) and is the long-context fast path.
+#include <algorithm>
+
+#include "gllm_common.h"
+
+namespace gllm {
+
+// fastExpF32 (fastmath.go:47-77), operation for operation.
+__device__ __forceinline__ float fast_exp(float x) {
+    if (x > 88.02969f) return __int_as_float(0x7f800000);
+    if (x < -87.33654f) return 0.0f;
+    const float t = x * 1.44269502f;  // float32(1.4426950408889634)
+    int k;
+    if (t >= 0.0f) k = (int)(t + 0.5f);
+    else k = (int)(t - 0.5f);
+    const float r = (float)((double)x - (double)k * 0.6931471805599453);
+    const float p = 1.0f + r * (1.0f + r * (0.5f + r * ((float)(1.0 / 6) +
+                    r * ((float)(1.0 / 24) + r * ((float)(1.0 / 120) + r * (float)(1.0 / 720))))));
+    return p * __int_as_float((127 + k) << 23);
+}
+
+}  // namespace gllm
+
+struct gllm_hip_kv {
+    int layers, kv_dim_k, kv_dim_v, max_len;
+    uint16_t** k;  // host array of device pointers
+    uint16_t** v;
+    int device;
+};
+
+namespace gllm {
+
+__global__ void kv_store_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                uint16_t* __restrict__ kd, uint16_t* __restrict__ vd, int nk,
+                                int nv) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < nk) kd[i] = f32_to_f16_bits(k[i]);
+    if (i < nv) vd[i] = f32_to_f16_bits(v[i]);
+}
+
+// --- exact path ------------------------------------------------------------
+
+// Scores: one 8-lane group per (position, kv head); lane j owns elements
+// 8i + j (i = 0..hd/8-1), the AVX2 lane j of dotF32F16AVX2, and computes the
+// dots of all `kvmul` query heads sharing the row.  hd % 8 == 0, kvmul <= 8.
+// blockIdx.y indexes the query token: token t attends start .. end0 + t
+// (span0 + t positions), so one launch serves a whole causal prefill chunk.
+__global__ __launch_bounds__(256) void attn_scores_kernel(const float* __restrict__ q,
+                                                          const uint16_t* __restrict__ K,
+                                                          int kv_dim, int n_kv, int kvmul, int hd,
+                                                          int start, int span0, int span_max,
+                                                          float scale, float* __restrict__ scores) {
+    const int tok = blockIdx.y;
+    const int span = span0 + tok;
+    const int j = threadIdx.x & 7;
+    const int item = blockIdx.x * 32 + (threadIdx.x >> 3);  // (t, g)
+    if (item >= span * n_kv) return;
+    const int g = item % n_kv, ti = item / n_kv;
+    const int n_heads = n_kv * kvmul;
+    const float* qt = q + (size_t)tok * n_heads * hd;
+    float* st = scores + (size_t)tok * n_heads * span_max;
+    const uint16_t* krow = K + (size_t)(start + ti) * kv_dim + g * hd;
+    float acc[8];
+    for (int h = 0; h < kvmul; h++) acc[h] = 0.0f;
+    for (int i = 0; i < hd / 8; i++) {
+        const float kv = f16_bits_to_f32(krow[8 * i + j]);
+        for (int h = 0; h < kvmul; h++)
+            acc[h] = fmaf(kv, qt[(size_t)(g * kvmul + h) * hd + 8 * i + j], acc[h]);
+    }
+    for (int h = 0; h < kvmul; h++) {
+        const float sc = tree8(acc[h]);
+        if (j == 0) st[(size_t)(g * kvmul + h) * span_max + ti] = sc * scale;
+    }
+}
+
+// Softmax weights in place and the sequential denominator, one workgroup per
+// (head, token).  Max and exp are order-free; the sum runs in position order.
+__global__ __launch_bounds__(256) void attn_softmax_kernel(float* __restrict__ scores, int span0,
+                                                           int span_max, float* __restrict__ inv_denom) {
+    const int tok = blockIdx.y, h = blockIdx.x, n_heads = gridDim.x;
+    const int span = span0 + tok;
+    float* s = scores + ((size_t)tok * n_heads + h) * span_max;
+    float m = -__int_as_float(0x7f800000);
+    for (int i = threadIdx.x; i < span; i += 256) m = fmaxf(m, s[i]);
+    // reference: first score then strict >; for NaN-free scores, the maximum
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    __shared__ float wm[4];
+    if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    for (int i = threadIdx.x; i < span; i += 256) s[i] = fast_exp(s[i] - mx);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float denom = 0.0f;
+        for (int i = 0; i < span; i++) denom += s[i];
+        // ScaleF32(out, 1/denom); the per-head path's `denom > 0` guard never
+        // triggers since the largest weight is exactly 1.
+        inv_denom[(size_t)tok * n_heads + h] = denom > 0.0f ? 1.0f / denom : 1.0f;
+    }
+}
+
+// Values: one lane per (head, element) and token; out = fma(w_t, v_t, out)
+// in position order, then out *= 1/denom.
+__global__ __launch_bounds__(128) void attn_values_kernel(const float* __restrict__ weights,
+                                                          const float* __restrict__ inv_denom,
+                                                          const uint16_t* __restrict__ V,
+                                                          int kv_dim, int kvmul, int vd, int start,
+                                                          int span0, int span_max,
+                                                          float* __restrict__ out) {
+    const int h = blockIdx.x, tok = blockIdx.y, n_heads = gridDim.x;
+    const int d = threadIdx.x;
+    if (d >= vd) return;
+    const int span = span0 + tok;
+    const int g = h / kvmul;
+    const float* w = weights + ((size_t)tok * n_heads + h) * span_max;
+    const uint16_t* vcol = V + (size_t)start * kv_dim + g * vd + d;
+    float acc = 0.0f;
+    int t = 0;
+    for (; t + 4 <= span; t += 4) {
+        const float v0 = f16_bits_to_f32(vcol[(size_t)t * kv_dim]);
+        const float v1 = f16_bits_to_f32(vcol[(size_t)(t + 1) * kv_dim]);
+        const float v2 = f16_bits_to_f32(vcol[(size_t)(t + 2) * kv_dim]);
+        const float v3 = f16_bits_to_f32(vcol[(size_t)(t + 3) * kv_dim]);
+        acc = fmaf(w[t], v0, acc);
+        acc = fmaf(w[t + 1], v1, acc);
+        acc = fmaf(w[t + 2], v2, acc);
+        acc = fmaf(w[t + 3], v3, acc);
+    }
+    for (; t < span; t++) acc = fmaf(w[t], f16_bits_to_f32(vcol[(size_t)t * kv_dim]), acc);
+    out[((size_t)tok * n_heads + h) * vd + d] = acc * inv_denom[(size_t)tok * n_heads + h];
+}
+
+// --- split-K path ------------------------------------------------------------
+
+constexpr int kSplitTile = 64;  // positions per tile
+
+// One workgroup per (kv head, chunk of positions): all `kvmul` query heads of
+// the group share each K/V tile.  Writes per-head (max, sum, unnormalised out).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_splitk_kernel(const float* __restrict__ q,
+                                                          const uint16_t* __restrict__ K,
+                                                          const uint16_t* __restrict__ V,
+                                                          int kv_dim, int n_kv, int kvmul,
+                                                          int start, int span, int chunk,
+                                                          float scale, float* __restrict__ part_m,
+                                                          float* __restrict__ part_l,
+                                                          float* __restrict__ part_o) {
+    const int g = blockIdx.y;
+    const int c = blockIdx.x;
+    const int nchunks = gridDim.x;
+    const int t0 = c * chunk;
+    const int t1 = min(span, t0 + chunk);
+    __shared__ float qs[8][HD];
+    __shared__ float w[8][kSplitTile];
+    __shared__ float red[8][4];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < kvmul * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)g * kvmul * HD + i];
+    // running state per head (replicated in every thread that needs it)
+    float m_run[8], l_run[8];
+    for (int h = 0; h < 8; h++) {
+        m_run[h] = -__int_as_float(0x7f800000);
+        l_run[h] = 0.0f;
+    }
+    // output accumulators: thread owns (head, element) pairs tid, tid+256, ...
+    constexpr int kOutPer = (8 * HD + 255) / 256;
+    float o_acc[kOutPer];
+    for (int i = 0; i < kOutPer; i++) o_acc[i] = 0.0f;
+    __syncthreads();
+    for (int tt = t0; tt < t1; tt += kSplitTile) {
+        const int nt = min(kSplitTile, t1 - tt);
+        // scores: thread (p, h) for p < nt, h < kvmul; 256 threads = 64 x 4
+        for (int item = tid; item < nt * kvmul; item += 256) {
+            const int p = item / kvmul, h = item % kvmul;
+            const uint16_t* krow = K + (size_t)(start + tt + p) * kv_dim + g * HD;
+            float acc = 0.0f;
+#pragma unroll 8
+            for (int e = 0; e < HD; e += 2) {
+                const uint32_t two = *(const uint32_t*)(krow + e);
+                acc = fmaf(f16_bits_to_f32(two & 0xffffu), qs[h][e], acc);
+                acc = fmaf(f16_bits_to_f32(two >> 16), qs[h][e + 1], acc);
+            }
+            w[h][p] = acc * scale;
+        }
+        __syncthreads();
+        // per-head tile max and new running max (every thread computes the
+        // same values from LDS)
+        float alpha[8];
+        for (int h = 0; h < kvmul; h++) {
+            float mt = m_run[h];
+            for (int p = 0; p < nt; p++) mt = fmaxf(mt, w[h][p]);
+            alpha[h] = fast_exp(m_run[h] - mt);
+            if (m_run[h] == -__int_as_float(0x7f800000)) alpha[h] = 0.0f;
+            m_run[h] = mt;
+        }
+        __syncthreads();
+        for (int item = tid; item < nt * kvmul; item += 256) {
+            const int p = item / kvmul, h = item % kvmul;
+            w[h][p] = fast_exp(w[h][p] - m_run[h]);
+        }
+        __syncthreads();
+        for (int h = 0; h < kvmul; h++) {
+            float sum = 0.0f;
+            for (int p = 0; p < nt; p++) sum += w[h][p];
+            l_run[h] = l_run[h] * alpha[h] + sum;
+        }
+        for (int i = 0; i < kOutPer; i++) {
+            const int idx = tid + 256 * i;
+            if (idx < kvmul * HD) {
+                const int h = idx / HD, d = idx % HD;
+                float acc = o_acc[i] * alpha[h];
+                const uint16_t* vcol = V + (size_t)(start + tt) * kv_dim + g * HD + d;
+                for (int p = 0; p < nt; p++)
+                    acc = fmaf(w[h][p], f16_bits_to_f32(vcol[(size_t)p * kv_dim]), acc);
+                o_acc[i] = acc;
+            }
+        }
+        __syncthreads();
+    }
+    (void)red;
+    for (int i = 0; i < kOutPer; i++) {
+        const int idx = tid + 256 * i;
+        if (idx < kvmul * HD) {
+            const int h = idx / HD;
+            part_o[(((size_t)g * kvmul + h) * nchunks + c) * HD + idx % HD] = o_acc[i];
+        }
+    }
+    if (tid < kvmul) {
+        part_m[((size_t)g * kvmul + tid) * nchunks + c] = m_run[tid];
+        part_l[((size_t)g * kvmul + tid) * nchunks + c] = l_run[tid];
+    }
+}
+
+__global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict__ part_m,
+                                                         const float* __restrict__ part_l,
+                                                         const float* __restrict__ part_o,
+                                                         int nchunks, int hd,
+                                                         float* __restrict__ out) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    if (d >= hd) return;
+    const float* pm = part_m + (size_t)h * nchunks;
+    const float* pl = part_l + (size_t)h * nchunks;
+    float M = -__int_as_float(0x7f800000);
+    for (int c = 0; c < nchunks; c++) M = fmaxf(M, pm[c]);
+    float L = 0.0f, O = 0.0f;
+    for (int c = 0; c < nchunks; c++) {
+        if (pl[c] == 0.0f) continue;
+        const float a = fast_exp(pm[c] - M);
+        L = fmaf(pl[c], a, L);
+        O = fmaf(part_o[((size_t)h * nchunks + c) * hd + d], a, O);
+    }
+    out[(size_t)h * hd + d] = O * (1.0f / L);
+}
+
+// Exact attention for p consecutive query tokens: token t attends
+// start .. end0 + t.  d_q / d_out: [p][n_heads][hd].
+int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
+                 int start, int end0, int p, float scale, float* d_out, hipStream_t s) {
+    const int span0 = end0 - start + 1;
+    const int span_max = span0 + p - 1;
+    const int kvmul = n_heads / n_kv;
+    float* scr = (float*)thread_scratch(5, ((size_t)p * n_heads * (span_max + 1) + 64) * 4);
+    if (!scr) return GLLM_ENOMEM;
+    float* scores = scr;
+    float* inv = scr + (size_t)p * n_heads * span_max;
+    const int items = span_max * n_kv;
+    hipLaunchKernelGGL(attn_scores_kernel, dim3((items + 31) / 32, p), dim3(256), 0, s, d_q,
+                       kv->k[l], kv->kv_dim_k, n_kv, kvmul, hd, start, span0, span_max, scale,
+                       scores);
+    GLLM_HIP(hipGetLastError());
+    hipLaunchKernelGGL(attn_softmax_kernel, dim3(n_heads, p), dim3(256), 0, s, scores, span0,
+                       span_max, inv);
+    GLLM_HIP(hipGetLastError());
+    hipLaunchKernelGGL(attn_values_kernel, dim3(n_heads, p), dim3(128), 0, s, scores, inv,
+                       kv->v[l], kv->kv_dim_v, kvmul, hd, start, span0, span_max, d_out);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+int attend_splitk(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
+                  int start, int end, float scale, float* d_out, hipStream_t s) {
+    if (hd != 128) return fail(GLLM_EUNSUP, "split-K attention is built for head_dim 128");
+    const int span = end - start + 1;
+    const int kvmul = n_heads / n_kv;
+    // chunk so that n_kv * nchunks covers the device several times over
+    int nchunks = std::max(1, std::min(512 / std::max(1, n_kv), (span + kSplitTile - 1) / kSplitTile));
+    int chunk = (span + nchunks - 1) / nchunks;
+    chunk = (chunk + kSplitTile - 1) / kSplitTile * kSplitTile;
+    nchunks = (span + chunk - 1) / chunk;
+    const size_t nh = (size_t)n_heads;
+    float* scr = (float*)thread_scratch(6, (nh * nchunks * (2 + hd) + 64) * 4);
+    if (!scr) return GLLM_ENOMEM;
+    float* pm = scr;
+    float* pl = pm + nh * nchunks;
+    float* po = pl + nh * nchunks;
+    hipLaunchKernelGGL(attn_splitk_kernel<128>, dim3(nchunks, n_kv), dim3(256), 0, s, d_q, kv->k[l],
+                       kv->v[l], kv->kv_dim_k, n_kv, kvmul, start, span, chunk, scale, pm, pl, po);
+    GLLM_HIP(hipGetLastError());
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_heads), dim3(128), 0, s, pm, pl, po, nchunks, hd,
+                       d_out);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+int attend_dev_impl(gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
+                    int start, int end, float scale, int mode, float* d_out, hipStream_t s) {
+    if (!kv || !d_q || !d_out) return fail(GLLM_EINVAL, "attend: null pointer");
+    if (l < 0 || l >= kv->layers) return fail(GLLM_EINVAL, "attend: layer %d out of range", l);
+    if (n_kv <= 0 || n_heads % n_kv || n_heads / n_kv > 8 || hd % 8 || hd > 128 ||
+        n_kv * hd > kv->kv_dim_k || n_kv * hd > kv->kv_dim_v)
+        return fail(GLLM_EINVAL, "attend: heads %d/%d hd %d do not fit the cache", n_heads, n_kv, hd);
+    if (start < 0 || end < start || end >= kv->max_len)
+        return fail(GLLM_EINVAL, "attend: positions %d..%d outside 0..%d", start, end, kv->max_len - 1);
+    if (mode == GLLM_ATTN_SPLITK)
+        return attend_splitk(kv, l, d_q, n_heads, n_kv, hd, start, end, scale, d_out, s);
+    return attend_exact(kv, l, d_q, n_heads, n_kv, hd, start, end, 1, scale, d_out, s);
+}
+
+int kv_store_dev_impl(gllm_hip_kv* kv, int l, int pos, const float* d_k, const float* d_v,
+                      hipStream_t s) {
+    if (!kv || !d_k || !d_v) return fail(GLLM_EINVAL, "kv_store: null pointer");
+    if (l < 0 || l >= kv->layers || pos < 0 || pos >= kv->max_len)
+        return fail(GLLM_EINVAL, "kv_store: layer %d pos %d out of range", l, pos);
+    const int n = std::max(kv->kv_dim_k, kv->kv_dim_v);
+    hipLaunchKernelGGL(kv_store_kernel, dim3((n + 255) / 256), dim3(256), 0, s, d_k, d_v,
+                       kv->k[l] + (size_t)pos * kv->kv_dim_k, kv->v[l] + (size_t)pos * kv->kv_dim_v,
+                       kv->kv_dim_k, kv->kv_dim_v);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+}  // namespace gllm
+
+using namespace gllm;
+
+extern "C" {
+
+gllm_hip_kv* gllm_hip_kv_new(int layers, int kv_dim_k, int kv_dim_v, int max_len) {
+    if (layers <= 0 || kv_dim_k <= 0 || kv_dim_v <= 0 || max_len <= 0) {
+        fail(GLLM_EINVAL, "gllm_hip_kv_new: bad shape");
+        return nullptr;
+    }
+    gllm_hip_kv* kv = new gllm_hip_kv();
+    kv->layers = layers;
+    kv->kv_dim_k = kv_dim_k;
+    kv->kv_dim_v = kv_dim_v;
+    kv->max_len = max_len;
+    kv->k = new uint16_t*[layers]();
+    kv->v = new uint16_t*[layers]();
+    if (hipGetDevice(&kv->device) != hipSuccess) kv->device = 0;
+    for (int l = 0; l < layers; l++) {
+        if (hipMalloc(&kv->k[l], (size_t)max_len * kv_dim_k * 2) != hipSuccess ||
+            hipMalloc(&kv->v[l], (size_t)max_len * kv_dim_v * 2) != hipSuccess) {
+            (void)hipGetLastError();
+            fail(GLLM_ENOMEM, "gllm_hip_kv_new: out of device memory");
+            gllm_hip_kv_release(kv);
+            return nullptr;
+        }
+        // zeroed rows, like make([]uint16, ...) in NewKVCacheF16
+        if (hipMemset(kv->k[l], 0, (size_t)max_len * kv_dim_k * 2) != hipSuccess ||
+            hipMemset(kv->v[l], 0, (size_t)max_len * kv_dim_v * 2) != hipSuccess) {
+            (void)hipGetLastError();
+            fail(GLLM_EDEVICE, "gllm_hip_kv_new: hipMemset failed");
+            gllm_hip_kv_release(kv);
+            return nullptr;
+        }
+    }
+    return kv;
+}
+
+void gllm_hip_kv_release(gllm_hip_kv* kv) {
+    if (!kv) return;
+    for (int l = 0; l < kv->layers; l++) {
+        if (kv->k[l]) (void)hipFree(kv->k[l]);
+        if (kv->v[l]) (void)hipFree(kv->v[l]);
+    }
+    delete[] kv->k;
+    delete[] kv->v;
+    delete kv;
+}
+
+uint16_t* gllm_hip_kv_k_dev(gllm_hip_kv* kv, int l) {
+    if (!kv || l < 0 || l >= kv->layers) {
+        fail(GLLM_EINVAL, "gllm_hip_kv_k_dev: bad layer");
+        return nullptr;
+    }
+    return kv->k[l];
+}
+
+uint16_t* gllm_hip_kv_v_dev(gllm_hip_kv* kv, int l) {
+    if (!kv || l < 0 || l >= kv->layers) {
+        fail(GLLM_EINVAL, "gllm_hip_kv_v_dev: bad layer");
+        return nullptr;
+    }
+    return kv->v[l];
+}
+
+int gllm_hip_kv_read(gllm_hip_kv* kv, int l, int pos0, int n, uint16_t* k_out, uint16_t* v_out) {
+    if (!kv || l < 0 || l >= kv->layers || pos0 < 0 || n < 0 || pos0 + n > kv->max_len)
+        return fail(GLLM_EINVAL, "gllm_hip_kv_read: bad range");
+    // rows may have been written on another stream (the decoder's): drain the
+    // device first, then copy synchronously
+    GLLM_HIP(hipDeviceSynchronize());
+    if (k_out)
+        GLLM_HIP(hipMemcpy(k_out, kv->k[l] + (size_t)pos0 * kv->kv_dim_k,
+                           (size_t)n * kv->kv_dim_k * 2, hipMemcpyDeviceToHost));
+    if (v_out)
+        GLLM_HIP(hipMemcpy(v_out, kv->v[l] + (size_t)pos0 * kv->kv_dim_v,
+                           (size_t)n * kv->kv_dim_v * 2, hipMemcpyDeviceToHost));
+    return GLLM_OK;
+}
+
+int gllm_hip_kv_store_dev(gllm_hip_kv* kv, int l, int pos, const float* d_k, const float* d_v,
+                          void* stream) {
+    return kv_store_dev_impl(kv, l, pos, d_k, d_v, (hipStream_t)stream);
+}
+
+int gllm_hip_kv_store(gllm_hip_kv* kv, int l, int pos, const float* k, const float* v) {
+    if (!kv || !k || !v) return fail(GLLM_EINVAL, "gllm_hip_kv_store: null pointer");
+    hipStream_t s = thread_stream();
+    if (!s) return GLLM_EDEVICE;
+    float* d = (float*)thread_scratch(1, (size_t)(kv->kv_dim_k + kv->kv_dim_v) * 4);
+    if (!d) return GLLM_ENOMEM;
+    GLLM_HIP(hipMemcpyAsync(d, k, (size_t)kv->kv_dim_k * 4, hipMemcpyHostToDevice, s));
+    GLLM_HIP(hipMemcpyAsync(d + kv->kv_dim_k, v, (size_t)kv->kv_dim_v * 4, hipMemcpyHostToDevice, s));
+    GLLM_TRY(kv_store_dev_impl(kv, l, pos, d, d + kv->kv_dim_k, s));
+    GLLM_HIP(hipStreamSynchronize(s));
+    return GLLM_OK;
+}
+
+int gllm_hip_attend_dev(gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv_heads,
+                        int hd, int start, int end, float scale, int mode, float* d_out,
+                        void* stream) {
+    return attend_dev_impl(kv, l, d_q, n_heads, n_kv_heads, hd, start, end, scale, mode, d_out,
+                           (hipStream_t)stream);
+}
+
+// attendHeadGroup for one kv head: q_heads queries (host) -> out (host).
+int gllm_hip_attend_group(gllm_hip_kv* kv, int l, int kvh, const float* q, int q_heads, int hd,
+                          int vd, int start, int end, float scale, float softcap, float* out) {
+    if (!kv || !q || !out) return fail(GLLM_EINVAL, "gllm_hip_attend_group: null pointer");
+    if (softcap != 0.0f) return fail(GLLM_EUNSUP, "attention softcap is not on this path");
+    if (hd != vd) return fail(GLLM_EUNSUP, "key and value head dims must match");
+    if (l < 0 || l >= kv->layers || kvh < 0 || hd <= 0 || hd % 8 || hd > 128 ||
+        (size_t)(kvh + 1) * hd > (size_t)kv->kv_dim_k || (size_t)(kvh + 1) * vd > (size_t)kv->kv_dim_v ||
+        q_heads < 1 || q_heads > 8)
+        return fail(GLLM_EINVAL, "gllm_hip_attend_group: bad head arguments");
+    if (start < 0 || end < start || end >= kv->max_len)
+        return fail(GLLM_EINVAL, "gllm_hip_attend_group: positions %d..%d outside 0..%d", start,
+                    end, kv->max_len - 1);
+    hipStream_t s = thread_stream();
+    if (!s) return GLLM_EDEVICE;
+    float* d = (float*)thread_scratch(1, (size_t)q_heads * hd * 2 * 4);
+    if (!d) return GLLM_ENOMEM;
+    GLLM_HIP(hipMemcpyAsync(d, q, (size_t)q_heads * hd * 4, hipMemcpyHostToDevice, s));
+    // Present the group as a one-kv-head cache view starting at head kvh.
+    gllm_hip_kv view = *kv;
+    uint16_t* kp[1] = {kv->k[l] + (size_t)kvh * hd};
+    uint16_t* vp[1] = {kv->v[l] + (size_t)kvh * vd};
+    view.k = kp;
+    view.v = vp;
+    view.layers = 1;
+    GLLM_TRY(attend_exact(&view, 0, d, q_heads, 1, hd, start, end, 1, scale,
+                          d + (size_t)q_heads * hd, s));
+    GLLM_HIP(hipMemcpyAsync(out, d + (size_t)q_heads * hd, (size_t)q_heads * vd * 4,
+                            hipMemcpyDeviceToHost, s));
+    GLLM_HIP(hipStreamSynchronize(s));
+    return GLLM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,491 @@
+// decode.hip -- resident llama decoder on one device: the glue kernels of
+// ForwardBodyInto (model.go:2622-2820) / ForwardBatchInto
+// (forward_batch.go:336-613) in the reference's amd64 float order, and the
+// host driver that sequences them around the row kernels and attention.
+//
+//   embedding      DequantRowQ4KInto simd.go:1530-1557 (Weight.RowInto model.go:1034)
+//   rmsNormInto    model.go:2986-3011: ss = dotF32AVX2(x, x) (kernels_amd64.s:28-93),
+//                  scale = float32(1/sqrt(float64(ss/n + eps))), out = (x*w)*scale
+//   RoPE           prepareRopeScratch model.go:3020-3049 (host tables, the
+//                  same libm calls), applyPreparedRope interleaved :3051-3093
+//   storeKV        model.go:1466-1489 (f16 RNE)
+//   residual       addInPlace = AxpyF32(dst, 1, src) model.go:3857
+//   SwiGLU         siluMulF32AVX2 kernels_amd64.s:1630-1700
+//   greedy         ArgmaxMatvec model.go:754 / argmaxFiniteToken sampling.go:399
+#include <math.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "gllm_common.h"
+
+namespace gllm {
+int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* const* outs,
+             const int* strides, hipStream_t s);
+int launch_q8k_prep(const float* d_x, int cols, int p, const ActQ8& a, hipStream_t s);
+int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
+                 int start, int end0, int p, float scale, float* d_out, hipStream_t s);
+int attend_splitk(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
+                  int start, int end, float scale, float* d_out, hipStream_t s);
+int kv_store_dev_impl(gllm_hip_kv* kv, int l, int pos, const float* d_k, const float* d_v,
+                      hipStream_t s);
+int launch_argmax(const float* logits, int n, uint32_t* token, hipStream_t s);
+}  // namespace gllm
+
+struct gllm_hip_model {
+    gllm_hip_model_config cfg;
+    std::vector<gllm_hip_weight*> w;  // [layer * 7 + slot] for slots 0..6
+    gllm_hip_weight* tok_embd = nullptr;
+    gllm_hip_weight* output = nullptr;
+    float* d_norms = nullptr;  // [2 * n_layers + 1][dim]: attn, ffn per layer, then output
+    float* d_sin = nullptr;    // [max_len][head_dim/2]
+    float* d_cos = nullptr;
+    gllm_hip_kv* kv = nullptr;
+    hipStream_t stream = nullptr;
+    int max_p = 0;  // capacity of the activation buffers below (tokens)
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
+    float *proj = nullptr, *gate = nullptr, *up = nullptr, *hidden = nullptr, *logits = nullptr;
+    uint32_t* d_tokens = nullptr;
+    uint32_t* h_tokens = nullptr;  // pinned
+    void* act = nullptr;           // Q8K activation buffers
+    size_t act_n = 0;
+    int last_p = 0;
+};
+
+namespace gllm {
+
+// ---------------------------------------------------------------------------
+// kernels
+// ---------------------------------------------------------------------------
+
+// Token embedding rows from a Q4_K table: out[t][j] = d1*q - min1 per
+// DequantRowQ4KInto.  One workgroup per token, one thread per element.
+__global__ __launch_bounds__(256) void embed_q4k_kernel(const uint8_t* __restrict__ table,
+                                                        size_t rb, int dim,
+                                                        const uint32_t* __restrict__ tokens,
+                                                        float* __restrict__ out) {
+    const int t = blockIdx.x;
+    const uint8_t* row = table + (size_t)tokens[t] * rb;
+    for (int e = threadIdx.x; e < dim; e += blockDim.x) {
+        const int b = e >> 8, i = e & 255;
+        const uint8_t* blk = row + (size_t)b * 144;
+        const int j = i >> 5;  // sub-block
+        const uint8_t* sc = blk + 4;
+        int s, m;
+        if (j < 4) {
+            s = sc[j] & 63;
+            m = sc[j + 4] & 63;
+        } else {
+            s = (sc[j + 4] & 0x0f) | ((sc[j - 4] >> 6) << 4);
+            m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+        }
+        const float d = f16_bits_to_f32(blk[0] | (blk[1] << 8));
+        const float dmin = f16_bits_to_f32(blk[2] | (blk[3] << 8));
+        const int chunk = i >> 6, l = i & 31, hi = (i >> 5) & 1;
+        const uint8_t qb = blk[16 + chunk * 32 + l];
+        const int qv = hi ? (qb >> 4) : (qb & 0x0f);
+        const float d1 = d * (float)s;
+        const float min1 = dmin * (float)m;
+        out[(size_t)t * dim + e] = d1 * (float)qv - min1;
+    }
+}
+
+// rmsNormInto per token (one workgroup per token, 256 threads).  Lanes 0..31
+// run the 4 x 8 fma accumulators of dotF32AVX2 over 32-element strides.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
+                                                      const float* __restrict__ w, int n, float eps,
+                                                      float* __restrict__ out) {
+    const int t = blockIdx.x;
+    const float* xt = x + (size_t)t * n;
+    __shared__ float part[32];
+    __shared__ float s_scale;
+    const int tid = threadIdx.x;
+    const int n32 = n & ~31, n8 = n & ~7;
+    if (tid < 32) {
+        float y = 0.0f;
+        for (int i = 0; i < n32; i += 32) y = fmaf(xt[i + tid], xt[i + tid], y);
+        part[tid] = y;
+    }
+    __syncthreads();
+    if (tid < 8) {
+        float acc = (part[tid] + part[8 + tid]) + (part[16 + tid] + part[24 + tid]);
+        for (int i = n32; i < n8; i += 8) acc = fmaf(xt[i + tid], xt[i + tid], acc);
+        part[tid] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const float a0 = part[0] + part[4], a1 = part[1] + part[5];
+        const float a2 = part[2] + part[6], a3 = part[3] + part[7];
+        float ss = (a0 + a1) + (a2 + a3);
+        for (int i = n8; i < n; i++) ss = ss + xt[i] * xt[i];
+        s_scale = (float)(1.0 / sqrt((double)(ss / (float)n + eps)));
+    }
+    __syncthreads();
+    const float scale = s_scale;
+    for (int i = tid; i < n; i += 256) out[(size_t)t * n + i] = (xt[i] * w[i]) * scale;
+}
+
+// Interleaved RoPE on p tokens at positions pos0 + t, n_heads heads each.
+__global__ void rope_kernel(float* __restrict__ vec, int n_heads, int hd, int pos0,
+                            const float* __restrict__ sin_tab, const float* __restrict__ cos_tab) {
+    const int t = blockIdx.y;
+    const int pairs = hd / 2;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_heads * pairs) return;
+    const int h = i / pairs, pr = i % pairs;
+    const float s = sin_tab[(size_t)(pos0 + t) * pairs + pr];
+    const float c = cos_tab[(size_t)(pos0 + t) * pairs + pr];
+    float* sub = vec + ((size_t)t * n_heads + h) * hd;
+    const float v0 = sub[2 * pr], v1 = sub[2 * pr + 1];
+    sub[2 * pr] = v0 * c - v1 * s;
+    sub[2 * pr + 1] = v0 * s + v1 * c;
+}
+
+__global__ void kv_store_batch_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                      uint16_t* __restrict__ kd, uint16_t* __restrict__ vd,
+                                      int kv_dim, int pos0) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= kv_dim) return;
+    kd[(size_t)(pos0 + t) * kv_dim + i] = f32_to_f16_bits(k[(size_t)t * kv_dim + i]);
+    vd[(size_t)(pos0 + t) * kv_dim + i] = f32_to_f16_bits(v[(size_t)t * kv_dim + i]);
+}
+
+// dst = fma(src, 1, dst): one rounding of dst + src (axpyF32AVX2 with alpha 1).
+__global__ void residual_kernel(float* __restrict__ dst, const float* __restrict__ src, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = fmaf(src[i], 1.0f, dst[i]);
+}
+
+// siluMulF32AVX2, lane for lane.
+__global__ void silu_mul_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                float* __restrict__ out, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float g = gate[i];
+    const float lo_clamp = __uint_as_float(0xc2b0c0a5u);  // -88.376
+    const float log2e = __uint_as_float(0x3fb8aa3bu);
+    const float c1 = __uint_as_float(0x3f318000u);        // 0.693359375
+    const float c2 = __uint_as_float(0xb95e8083u);        // -2.12194440e-4
+    const float fx_lo = __uint_as_float(0xc2fc0000u);     // -126
+    const float a = __uint_as_float(__float_as_uint(g) | 0x80000000u);  // -|g|
+    // VMAXPS returns its second source when either operand is NaN
+    const float ac = (a != a) ? lo_clamp : (a > lo_clamp ? a : lo_clamp);
+    float fx = rintf(ac * log2e);                                       // VROUNDPS $0
+    fx = (fx != fx) ? fx_lo : (fx > fx_lo ? fx : fx_lo);
+    float r = fmaf(-fx, c1, ac);
+    r = fmaf(-fx, c2, r);
+    float y = fmaf(__uint_as_float(0x39506967u), r, __uint_as_float(0x3ab743ceu));
+    y = fmaf(y, r, __uint_as_float(0x3c088908u));
+    y = fmaf(y, r, __uint_as_float(0x3d2aa9c1u));
+    y = fmaf(y, r, __uint_as_float(0x3e2aaaaau));
+    y = fmaf(y, r, __uint_as_float(0x3f000000u));
+    const float r2 = r * r;
+    y = fmaf(y, r2, r);
+    y = y + 1.0f;
+    float e = y * __uint_as_float((uint32_t)((int)fx + 127) << 23);
+    if (a < lo_clamp) e = 0.0f;
+    const float num = (__float_as_uint(g) & 0x80000000u) ? e : 1.0f;
+    const float s = num / (1.0f + e);
+    out[i] = (g * s) * up[i];
+}
+
+// ---------------------------------------------------------------------------
+// host driver
+// ---------------------------------------------------------------------------
+
+static inline int grid1(size_t n, int block) { return (int)((n + block - 1) / block); }
+
+static int ensure_buffers(gllm_hip_model* m, int p) {
+    if (p <= m->max_p) return GLLM_OK;
+    const auto& c = m->cfg;
+    float** bufs[] = {&m->x, &m->xn, &m->q, &m->k, &m->v, &m->attn, &m->proj, &m->gate, &m->up,
+                      &m->hidden};
+    const size_t qd = (size_t)c.n_heads * c.head_dim, kvd = (size_t)c.n_kv_heads * c.head_dim;
+    const size_t sizes[] = {(size_t)c.dim, (size_t)c.dim, qd, kvd, kvd, qd, (size_t)c.dim,
+                            (size_t)c.hidden, (size_t)c.hidden, (size_t)c.hidden};
+    for (int i = 0; i < 10; i++) {
+        if (*bufs[i]) (void)hipFree(*bufs[i]);
+        *bufs[i] = nullptr;
+        GLLM_HIP(hipMalloc(bufs[i], sizes[i] * p * 4));
+    }
+    if (m->d_tokens) (void)hipFree(m->d_tokens);
+    if (m->h_tokens) (void)hipHostFree(m->h_tokens);
+    GLLM_HIP(hipMalloc(&m->d_tokens, (size_t)(p + 4) * 4));
+    GLLM_HIP(hipHostMalloc(&m->h_tokens, (size_t)(p + 4) * 4, hipHostMallocDefault));
+    const size_t an = act_bytes(std::max(c.dim, c.hidden), p);
+    if (m->act) (void)hipFree(m->act);
+    GLLM_HIP(hipMalloc(&m->act, an));
+    m->act_n = an;
+    m->max_p = p;
+    return GLLM_OK;
+}
+
+static int matvec(gllm_hip_model* m, int n, gllm_hip_weight* const* ws, const float* x, int p,
+                  float* const* outs) {
+    ActQ8 a;
+    act_carve(m->act, ws[0]->cols, p, &a);
+    GLLM_TRY(launch_q8k_prep(x, ws[0]->cols, p, a, m->stream));
+    return run_gemv(n, ws, a, p, outs, nullptr, m->stream);
+}
+
+// ForwardBatchInto / ForwardBodyInto for p consecutive tokens already in
+// m->d_tokens, at positions pos0 .. pos0+p-1.  Leaves the output-normed
+// hidden state of every token in m->xn.
+static int forward(gllm_hip_model* m, int pos0, int p) {
+    const auto& c = m->cfg;
+    hipStream_t s = m->stream;
+    const int hd = c.head_dim, kvd = c.n_kv_heads * hd, qd = c.n_heads * hd;
+    const float scale = (float)(1.0 / sqrt((double)hd));
+    hipLaunchKernelGGL(embed_q4k_kernel, dim3(p), dim3(256), 0, s, m->tok_embd->d_data,
+                       m->tok_embd->row_bytes, c.dim, m->d_tokens, m->x);
+    GLLM_HIP(hipGetLastError());
+    for (int l = 0; l < c.n_layers; l++) {
+        gllm_hip_weight** W = &m->w[(size_t)l * 7];
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3(p), dim3(256), 0, s, m->x,
+                           m->d_norms + (size_t)(2 * l) * c.dim, c.dim, c.rms_eps, m->xn);
+        GLLM_HIP(hipGetLastError());
+        {
+            gllm_hip_weight* ws[3] = {W[GLLM_T_WQ], W[GLLM_T_WK], W[GLLM_T_WV]};
+            float* outs[3] = {m->q, m->k, m->v};
+            GLLM_TRY(matvec(m, 3, ws, m->xn, p, outs));
+        }
+        hipLaunchKernelGGL(rope_kernel, dim3(grid1((size_t)c.n_heads * hd / 2, 256), p), dim3(256), 0,
+                           s, m->q, c.n_heads, hd, pos0, m->d_sin, m->d_cos);
+        GLLM_HIP(hipGetLastError());
+        hipLaunchKernelGGL(rope_kernel, dim3(grid1((size_t)c.n_kv_heads * hd / 2, 256), p), dim3(256),
+                           0, s, m->k, c.n_kv_heads, hd, pos0, m->d_sin, m->d_cos);
+        GLLM_HIP(hipGetLastError());
+        hipLaunchKernelGGL(kv_store_batch_kernel, dim3(grid1(kvd, 256), p), dim3(256), 0, s, m->k,
+                           m->v, gllm_hip_kv_k_dev(m->kv, l), gllm_hip_kv_v_dev(m->kv, l), kvd, pos0);
+        GLLM_HIP(hipGetLastError());
+        GLLM_TRY(attend_exact(m->kv, l, m->q, c.n_heads, c.n_kv_heads, hd, 0, pos0, p, scale,
+                              m->attn, s));
+        {
+            gllm_hip_weight* ws[1] = {W[GLLM_T_WO]};
+            float* outs[1] = {m->proj};
+            GLLM_TRY(matvec(m, 1, ws, m->attn, p, outs));
+        }
+        hipLaunchKernelGGL(residual_kernel, dim3(grid1((size_t)c.dim * p, 256)), dim3(256), 0, s, m->x,
+                           m->proj, (size_t)c.dim * p);
+        GLLM_HIP(hipGetLastError());
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3(p), dim3(256), 0, s, m->x,
+                           m->d_norms + (size_t)(2 * l + 1) * c.dim, c.dim, c.rms_eps, m->xn);
+        GLLM_HIP(hipGetLastError());
+        {
+            gllm_hip_weight* ws[2] = {W[GLLM_T_W1], W[GLLM_T_W3]};
+            float* outs[2] = {m->gate, m->up};
+            GLLM_TRY(matvec(m, 2, ws, m->xn, p, outs));
+        }
+        hipLaunchKernelGGL(silu_mul_kernel, dim3(grid1((size_t)c.hidden * p, 256)), dim3(256), 0, s,
+                           m->gate, m->up, m->hidden, (size_t)c.hidden * p);
+        GLLM_HIP(hipGetLastError());
+        {
+            gllm_hip_weight* ws[1] = {W[GLLM_T_W2]};
+            float* outs[1] = {m->proj};
+            GLLM_TRY(matvec(m, 1, ws, m->hidden, p, outs));
+        }
+        hipLaunchKernelGGL(residual_kernel, dim3(grid1((size_t)c.dim * p, 256)), dim3(256), 0, s, m->x,
+                           m->proj, (size_t)c.dim * p);
+        GLLM_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(p), dim3(256), 0, s, m->x,
+                       m->d_norms + (size_t)(2 * c.n_layers) * c.dim, c.dim, c.rms_eps, m->xn);
+    GLLM_HIP(hipGetLastError());
+    (void)qd;
+    m->last_p = p;
+    return GLLM_OK;
+}
+
+static int check_ready(const gllm_hip_model* m) {
+    if (!m) return fail(GLLM_EINVAL, "null model");
+    if (!m->tok_embd || !m->output) return fail(GLLM_EINVAL, "model: embedding/output not set");
+    if (m->tok_embd->type != GLLM_TYPE_Q4_K) return fail(GLLM_EUNSUP, "model: embedding must be Q4_K");
+    for (size_t i = 0; i < m->w.size(); i++)
+        if (!m->w[i]) return fail(GLLM_EINVAL, "model: layer %zu slot %zu not set", i / 7, i % 7);
+    return GLLM_OK;
+}
+
+}  // namespace gllm
+
+using namespace gllm;
+
+extern "C" {
+
+gllm_hip_model* gllm_hip_model_new(const gllm_hip_model_config* cfg) {
+    if (!cfg || cfg->n_layers <= 0 || cfg->dim <= 0 || cfg->dim % 256 || cfg->hidden % 256 ||
+        cfg->n_heads <= 0 || cfg->n_kv_heads <= 0 || cfg->n_heads % cfg->n_kv_heads ||
+        cfg->head_dim % 8 || cfg->head_dim > 128 || cfg->n_heads / cfg->n_kv_heads > 8 ||
+        cfg->n_heads * cfg->head_dim % 256 || cfg->vocab <= 0 || cfg->max_len <= 0) {
+        fail(GLLM_EINVAL, "gllm_hip_model_new: unsupported config");
+        return nullptr;
+    }
+    gllm_hip_model* m = new gllm_hip_model();
+    m->cfg = *cfg;
+    m->w.assign((size_t)cfg->n_layers * 7, nullptr);
+    auto bail = [&](const char* what) -> gllm_hip_model* {
+        (void)hipGetLastError();
+        fail(GLLM_ENOMEM, "gllm_hip_model_new: %s", what);
+        gllm_hip_model_release(m);
+        return nullptr;
+    };
+    if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) return bail("stream");
+    const size_t nn = (size_t)(2 * cfg->n_layers + 1) * cfg->dim;
+    if (hipMalloc(&m->d_norms, nn * 4) != hipSuccess) return bail("norms");
+    // RoPE tables (buildRopeInvFreq model.go:1728-1756, prepareRopeScratch
+    // model.go:3020-3049), computed on the host with the reference's
+    // float64 pow / sin / cos and uploaded once for every position.
+    const int pairs = cfg->head_dim / 2;
+    std::vector<float> inv(pairs), sn((size_t)cfg->max_len * pairs), cs((size_t)cfg->max_len * pairs);
+    for (int i = 0; i < pairs; i++) {
+        const float fi = (float)(i * 2);
+        const float base = (float)pow((double)cfg->rope_theta, (double)(fi / (float)cfg->head_dim));
+        inv[i] = 1.0f / (1.0f * base);
+    }
+    for (int pos = 0; pos < cfg->max_len; pos++)
+        for (int i = 0; i < pairs; i++) {
+            const double angle = (double)((float)pos * inv[i]);
+            sn[(size_t)pos * pairs + i] = (float)sin(angle) * 1.0f;
+            cs[(size_t)pos * pairs + i] = (float)cos(angle) * 1.0f;
+        }
+    if (hipMalloc(&m->d_sin, sn.size() * 4) != hipSuccess) return bail("rope tables");
+    if (hipMalloc(&m->d_cos, cs.size() * 4) != hipSuccess) return bail("rope tables");
+    if (hipMemcpy(m->d_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m->d_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return bail("rope upload");
+    const int kvd = cfg->n_kv_heads * cfg->head_dim;
+    m->kv = gllm_hip_kv_new(cfg->n_layers, kvd, kvd, cfg->max_len);
+    if (!m->kv) return bail("kv cache");
+    if (ensure_buffers(m, 1) != GLLM_OK) return bail("activation buffers");
+    if (hipMalloc(&m->logits, (size_t)cfg->vocab * 4) != hipSuccess) return bail("logits");
+    return m;
+}
+
+void gllm_hip_model_release(gllm_hip_model* m) {
+    if (!m) return;
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    float* bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->proj, m->gate, m->up, m->hidden,
+                     m->logits, m->d_norms, m->d_sin, m->d_cos};
+    for (float* b : bufs)
+        if (b) (void)hipFree(b);
+    if (m->d_tokens) (void)hipFree(m->d_tokens);
+    if (m->h_tokens) (void)hipHostFree(m->h_tokens);
+    if (m->act) (void)hipFree(m->act);
+    if (m->kv) gllm_hip_kv_release(m->kv);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+int gllm_hip_model_set_weight(gllm_hip_model* m, int layer, int slot, gllm_hip_weight* w) {
+    if (!m || !w) return fail(GLLM_EINVAL, "gllm_hip_model_set_weight: null argument");
+    const auto& c = m->cfg;
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    int rows = 0, cols = 0;
+    switch (slot) {
+    case GLLM_T_WQ: rows = qd; cols = c.dim; break;
+    case GLLM_T_WK: case GLLM_T_WV: rows = kvd; cols = c.dim; break;
+    case GLLM_T_WO: rows = c.dim; cols = qd; break;
+    case GLLM_T_W1: case GLLM_T_W3: rows = c.hidden; cols = c.dim; break;
+    case GLLM_T_W2: rows = c.dim; cols = c.hidden; break;
+    case GLLM_T_TOK_EMBD: case GLLM_T_OUTPUT: rows = c.vocab; cols = c.dim; break;
+    default: return fail(GLLM_EINVAL, "gllm_hip_model_set_weight: slot %d", slot);
+    }
+    if (w->rows != rows || w->cols != cols)
+        return fail(GLLM_EINVAL, "slot %d expects %dx%d, got %dx%d", slot, rows, cols, w->rows, w->cols);
+    if (slot == GLLM_T_TOK_EMBD) {
+        m->tok_embd = w;
+        return GLLM_OK;
+    }
+    if (slot == GLLM_T_OUTPUT) {
+        m->output = w;
+        return GLLM_OK;
+    }
+    if (layer < 0 || layer >= c.n_layers) return fail(GLLM_EINVAL, "layer %d out of range", layer);
+    m->w[(size_t)layer * 7 + slot] = w;
+    return GLLM_OK;
+}
+
+int gllm_hip_model_set_norm(gllm_hip_model* m, int layer, int slot, const float* w) {
+    if (!m || !w) return fail(GLLM_EINVAL, "gllm_hip_model_set_norm: null argument");
+    const auto& c = m->cfg;
+    size_t idx;
+    if (slot == GLLM_T_OUT_NORM) idx = 2 * (size_t)c.n_layers;
+    else if ((slot == GLLM_T_ATTN_NORM || slot == GLLM_T_FFN_NORM) && layer >= 0 && layer < c.n_layers)
+        idx = 2 * (size_t)layer + (slot == GLLM_T_FFN_NORM);
+    else return fail(GLLM_EINVAL, "gllm_hip_model_set_norm: slot %d layer %d", slot, layer);
+    GLLM_HIP(hipMemcpy(m->d_norms + idx * c.dim, w, (size_t)c.dim * 4, hipMemcpyHostToDevice));
+    return GLLM_OK;
+}
+
+int gllm_hip_model_decode(gllm_hip_model* m, uint32_t token, int pos, uint32_t* next) {
+    GLLM_TRY(check_ready(m));
+    if (!next) return fail(GLLM_EINVAL, "gllm_hip_model_decode: null next");
+    if (pos < 0 || pos >= m->cfg.max_len) return fail(GLLM_EINVAL, "position %d out of range", pos);
+    if (token >= (uint32_t)m->cfg.vocab) return fail(GLLM_EINVAL, "token %u out of range", token);
+    hipStream_t s = m->stream;
+    m->h_tokens[0] = token;
+    GLLM_HIP(hipMemcpyAsync(m->d_tokens, m->h_tokens, 4, hipMemcpyHostToDevice, s));
+    GLLM_TRY(forward(m, pos, 1));
+    {
+        gllm_hip_weight* ws[1] = {m->output};
+        float* outs[1] = {m->logits};
+        GLLM_TRY(matvec(m, 1, ws, m->xn, 1, outs));
+    }
+    GLLM_TRY(launch_argmax(m->logits, m->cfg.vocab, m->d_tokens + 1, s));
+    GLLM_HIP(hipMemcpyAsync(m->h_tokens + 1, m->d_tokens + 1, 4, hipMemcpyDeviceToHost, s));
+    GLLM_HIP(hipStreamSynchronize(s));
+    *next = m->h_tokens[1];
+    return GLLM_OK;
+}
+
+int gllm_hip_model_prefill(gllm_hip_model* m, const uint32_t* tokens, int n, int start_pos,
+                           uint32_t* first, float* logits) {
+    GLLM_TRY(check_ready(m));
+    if (!tokens || n <= 0 || !first) return fail(GLLM_EINVAL, "gllm_hip_model_prefill: bad arguments");
+    if (start_pos < 0 || start_pos + n > m->cfg.max_len)
+        return fail(GLLM_EINVAL, "prefill positions %d..%d exceed max_len", start_pos, start_pos + n - 1);
+    for (int i = 0; i < n; i++)
+        if (tokens[i] >= (uint32_t)m->cfg.vocab) return fail(GLLM_EINVAL, "token %u out of range", tokens[i]);
+    const int chunk = 64;
+    GLLM_TRY(ensure_buffers(m, std::min(n, chunk)));
+    hipStream_t s = m->stream;
+    for (int c0 = 0; c0 < n; c0 += chunk) {
+        const int p = std::min(chunk, n - c0);
+        memcpy(m->h_tokens, tokens + c0, (size_t)p * 4);
+        GLLM_HIP(hipMemcpyAsync(m->d_tokens, m->h_tokens, (size_t)p * 4, hipMemcpyHostToDevice, s));
+        GLLM_TRY(forward(m, start_pos + c0, p));
+        // h_tokens is reused by the next chunk's copy
+        GLLM_HIP(hipStreamSynchronize(s));
+    }
+    // computeLast: full logits of the last position (MatvecQ6KInto), then
+    // argmaxFiniteToken.
+    const float* last = m->xn + (size_t)(m->last_p - 1) * m->cfg.dim;
+    {
+        gllm_hip_weight* ws[1] = {m->output};
+        float* outs[1] = {m->logits};
+        GLLM_TRY(matvec(m, 1, ws, last, 1, outs));
+    }
+    GLLM_TRY(launch_argmax(m->logits, m->cfg.vocab, m->d_tokens + m->max_p, s));
+    GLLM_HIP(hipMemcpyAsync(m->h_tokens + m->max_p, m->d_tokens + m->max_p, 4, hipMemcpyDeviceToHost, s));
+    if (logits)
+        GLLM_HIP(hipMemcpyAsync(logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost, s));
+    GLLM_HIP(hipStreamSynchronize(s));
+    *first = m->h_tokens[m->max_p];
+    // keep the last token's hidden state where gllm_hip_model_hidden reads it
+    GLLM_HIP(hipMemcpyAsync(m->xn, last, (size_t)m->cfg.dim * 4, hipMemcpyDeviceToDevice, s));
+    GLLM_HIP(hipStreamSynchronize(s));
+    m->last_p = 1;
+    return GLLM_OK;
+}
+
+int gllm_hip_model_hidden(gllm_hip_model* m, float* out) {
+    if (!m || !out) return fail(GLLM_EINVAL, "gllm_hip_model_hidden: null argument");
+    const float* last = m->xn + (size_t)(std::max(1, m->last_p) - 1) * m->cfg.dim;
+    GLLM_HIP(hipMemcpyAsync(out, last, (size_t)m->cfg.dim * 4, hipMemcpyDeviceToHost, m->stream));
+    GLLM_HIP(hipStreamSynchronize(m->stream));
+    return GLLM_OK;
+}
+
+gllm_hip_kv* gllm_hip_model_kv(gllm_hip_model* m) { return m ? m->kv : nullptr; }
+
+}  // extern "C"

@@ -1,0 +1,712 @@
+// gemv.hip -- Q4_K / Q6_K / Q8_0 x Q8K row kernels for gfx950, weight
+// handles, and the matvec / argmax entry points of the C ABI.
+//
+// Lane mapping: eight consecutive lanes own one weight row; lane k plays the
+// role of int32 lane k of the reference's 256-bit AVX2 accumulators
+// (kernels_amd64.s:437-543, 1123-1220, 1321-1391).  For every 256-element
+// block it loads the four (Q4_K), six (Q6_K) or eight (Q8_0) weight dwords
+// whose bytes land in that AVX2 lane, forms the same exact int32 partial with
+// v_dot4_i32_i8, and advances the same per-lane fp32 chains with fmaf in
+// block order; the row ends with the reference's 8->4->2->1 tree.  The
+// result is therefore bit-identical to the amd64 kernels.
+#include <algorithm>
+#include <vector>
+
+#include "gllm_common.h"
+
+namespace gllm {
+
+constexpr int kRowsPerWG = 32;  // 256 threads / 8 lanes per row
+constexpr int kMaxTok = 8;      // activation rows per launch
+
+struct GemvJob {
+    const uint8_t* w[3];
+    float* out[3];
+    int rows[3];
+    int out_stride[3];
+    int wg_begin[4];
+    int n;
+    int blocks;
+    int cols;
+    size_t rb;
+    ActQ8 act;
+    int tok0;  // first activation row of this launch
+    int ntok;  // activation rows in this launch (<= NT)
+};
+
+__device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
+__device__ __forceinline__ int ubyte(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xffu); }
+
+template <int NT>
+__device__ __forceinline__ void store_rows(const GemvJob& j, int wi, int r, int k, const float* v) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        float s = tree8(v[t]);
+        if (k == 0 && t < j.ntok) j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = s;
+    }
+}
+
+__device__ __forceinline__ int locate(const GemvJob& j, int wg, int* wi) {
+    int i = 0;
+    while (i + 1 < j.n && wg >= j.wg_begin[i + 1]) i++;
+    *wi = i;
+    return (wg - j.wg_begin[i]) * kRowsPerWG;
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K: 144-byte blocks [d f16][dmin f16][12 B 6-bit scales/mins][128 B nibbles]
+// (simd.go:1530-1557).  AVX2 lane k covers bytes 4k..4k+3 of each of the four
+// 32-byte nibble chunks (Q4KQ8CHUNK, kernels_amd64.s:443-455).
+// ---------------------------------------------------------------------------
+template <int NT>
+__global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJob j) {
+    int wi;
+    const int r = locate(j, blockIdx.x, &wi) + (threadIdx.x >> 3);
+    const int k = threadIdx.x & 7;
+    if (r >= j.rows[wi]) return;
+    const uint8_t* row = j.w[wi] + (size_t)r * j.rb;
+    const int B = j.blocks;
+    float accF[NT], accM[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) accF[t] = accM[t] = 0.0f;
+    const int8_t* q8 = j.act.q8perm + (size_t)j.tok0 * j.cols + k * 32;
+    const float* xsc = j.act.xscale + (size_t)j.tok0 * B;
+    const float* xs32 = j.act.xs32 + (size_t)j.tok0 * (j.cols / 32) + k;
+#pragma unroll 2
+    for (int b = 0; b < B; b++) {
+        const uint8_t* blk = row + (size_t)b * 144;
+        const uint4 h = *(const uint4*)blk;
+        const uint32_t w0 = *(const uint32_t*)(blk + 16 + 4 * k);
+        const uint32_t w1 = *(const uint32_t*)(blk + 48 + 4 * k);
+        const uint32_t w2 = *(const uint32_t*)(blk + 80 + 4 * k);
+        const uint32_t w3 = *(const uint32_t*)(blk + 112 + 4 * k);
+        const float d = f16_bits_to_f32(h.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(h.x >> 16);
+        // getScaleMinK4 for all eight sub-blocks (simd.go:1672-1677)
+        const uint32_t sc03 = h.y & 0x3f3f3f3fu;
+        const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+        const uint32_t m03 = h.z & 0x3f3f3f3fu;
+        const uint32_t m47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+        const int mk = ubyte(k < 4 ? m03 : m47, k & 3);
+        const int l0 = (int)(w0 & 0x0f0f0f0fu), h0 = (int)((w0 >> 4) & 0x0f0f0f0fu);
+        const int l1 = (int)(w1 & 0x0f0f0f0fu), h1 = (int)((w1 >> 4) & 0x0f0f0f0fu);
+        const int l2 = (int)(w2 & 0x0f0f0f0fu), h2 = (int)((w2 >> 4) & 0x0f0f0f0fu);
+        const int l3 = (int)(w3 & 0x0f0f0f0fu), h3 = (int)((w3 >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (t < j.ntok) {
+                const int4 qa = *(const int4*)(q8 + (size_t)t * j.cols + b * 256);
+                const int4 qb = *(const int4*)(q8 + (size_t)t * j.cols + b * 256 + 16);
+                int acc = ubyte(sc03, 0) * sdot4(l0, qa.x, 0);
+                acc += ubyte(sc03, 1) * sdot4(h0, qa.y, 0);
+                acc += ubyte(sc03, 2) * sdot4(l1, qa.z, 0);
+                acc += ubyte(sc03, 3) * sdot4(h1, qa.w, 0);
+                acc += ubyte(sc47, 0) * sdot4(l2, qb.x, 0);
+                acc += ubyte(sc47, 1) * sdot4(h2, qb.y, 0);
+                acc += ubyte(sc47, 2) * sdot4(l3, qb.z, 0);
+                acc += ubyte(sc47, 3) * sdot4(h3, qb.w, 0);
+                const float dxs = d * xsc[(size_t)t * B + b];                 // VMULSS
+                accF[t] = fmaf((float)acc, dxs, accF[t]);                       // VFMADD231PS
+                const float mx = (float)mk * xs32[(size_t)t * (j.cols / 32) + b * 8];  // VMULPS
+                accM[t] = fmaf(dmin, mx, accM[t]);                              // VFMADD231PS
+            }
+        }
+    }
+    float v[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) v[t] = accF[t] - accM[t];  // VSUBPS
+    store_rows<NT>(j, wi, r, k, v);
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K, repacked at upload: per row, B blocks of 208 bytes
+// [ql 128][qh 64][int8 scales 16] followed by B f16 d values.  AVX2 lane k
+// covers bytes 4k..4k+3 of each 32-byte quad (Q6KQ8QUAD,
+// kernels_amd64.s:1130-1142); lanes 0-3 use scale 8h+2c, lanes 4-7 8h+2c+1.
+// ---------------------------------------------------------------------------
+template <int NT>
+__global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
+    int wi;
+    const int r = locate(j, blockIdx.x, &wi) + (threadIdx.x >> 3);
+    const int k = threadIdx.x & 7;
+    if (r >= j.rows[wi]) return;
+    const int B = j.blocks;
+    const uint8_t* row = j.w[wi] + (size_t)r * j.rb;
+    const uint16_t* dv = (const uint16_t*)(row + (size_t)B * 208);
+    const int hk = k >> 2;
+    float accF[NT], accM[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) accF[t] = accM[t] = 0.0f;
+    const int8_t* q8 = j.act.q8perm + (size_t)j.tok0 * j.cols + k * 32;
+    const float* xsc = j.act.xscale + (size_t)j.tok0 * B;
+    const float* xs16 = j.act.xs16 + (size_t)j.tok0 * (j.cols / 16) + k;
+#pragma unroll 2
+    for (int b = 0; b < B; b++) {
+        const uint8_t* blk = row + (size_t)b * 208;
+        const uint32_t ql0 = *(const uint32_t*)(blk + 4 * k);
+        const uint32_t ql1 = *(const uint32_t*)(blk + 32 + 4 * k);
+        const uint32_t ql2 = *(const uint32_t*)(blk + 64 + 4 * k);
+        const uint32_t ql3 = *(const uint32_t*)(blk + 96 + 4 * k);
+        const uint32_t qh0 = *(const uint32_t*)(blk + 128 + 4 * k);
+        const uint32_t qh1 = *(const uint32_t*)(blk + 160 + 4 * k);
+        const uint4 sv = *(const uint4*)(blk + 192);
+        const float d = f16_bits_to_f32(dv[b]);
+        // codes of quad (h, c), c = 0..3 (m = 4h + c)
+        int code[8];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t y0 = h ? ql2 : ql0, y1 = h ? ql3 : ql1, qh = h ? qh1 : qh0;
+            code[4 * h + 0] = (int)((y0 & 0x0f0f0f0fu) | ((qh & 0x03030303u) << 4));
+            code[4 * h + 1] = (int)((y1 & 0x0f0f0f0fu) | (((qh >> 2) & 0x03030303u) << 4));
+            code[4 * h + 2] = (int)(((y0 >> 4) & 0x0f0f0f0fu) | (((qh >> 4) & 0x03030303u) << 4));
+            code[4 * h + 3] = (int)(((y1 >> 4) & 0x0f0f0f0fu) | (((qh >> 6) & 0x03030303u) << 4));
+        }
+        // scale of quad m: byte 8h + 2c + hk of the 16 scale bytes
+        const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+        int scl[8];
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const int idx = 2 * m + hk;  // = 8h + 2c + hk
+            scl[m] = sbyte(sw[idx >> 2], idx & 3);
+        }
+        const float sk = (float)sbyte(sw[k >> 2], k & 3);
+        const float sk8 = (float)sbyte(sw[2 + (k >> 2)], k & 3);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (t < j.ntok) {
+                const int4 qa = *(const int4*)(q8 + (size_t)t * j.cols + b * 256);
+                const int4 qb = *(const int4*)(q8 + (size_t)t * j.cols + b * 256 + 16);
+                int acc = scl[0] * sdot4(code[0], qa.x, 0);
+                acc += scl[1] * sdot4(code[1], qa.y, 0);
+                acc += scl[2] * sdot4(code[2], qa.z, 0);
+                acc += scl[3] * sdot4(code[3], qa.w, 0);
+                acc += scl[4] * sdot4(code[4], qb.x, 0);
+                acc += scl[5] * sdot4(code[5], qb.y, 0);
+                acc += scl[6] * sdot4(code[6], qb.z, 0);
+                acc += scl[7] * sdot4(code[7], qb.w, 0);
+                const float* xs = xs16 + (size_t)t * (j.cols / 16) + b * 16;
+                float o = sk * xs[0];                                  // VMULPS
+                o = fmaf(sk8, xs[8], o);                                // VFMADD231PS
+                accM[t] = fmaf(d, o, accM[t]);                          // VFMADD231PS
+                const float dxs = d * xsc[(size_t)t * B + b];           // VMULSS
+                accF[t] = fmaf((float)acc, dxs, accF[t]);               // VFMADD231PS
+            }
+        }
+    }
+    float v[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) v[t] = accF[t] - accM[t];
+    store_rows<NT>(j, wi, r, k, v);
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0, repacked at upload: per 256-element group, [8 x f16 d][8 x 32 int8]
+// (272 bytes, 16-byte aligned).  AVX2 lane k covers bytes 4k..4k+3 of each
+// 32-value block (Q80CHUNK, kernels_amd64.s:1321-1345).
+// ---------------------------------------------------------------------------
+template <int NT>
+__global__ __launch_bounds__(256) void gemv_q8_0_kernel(GemvJob j) {
+    int wi;
+    const int r = locate(j, blockIdx.x, &wi) + (threadIdx.x >> 3);
+    const int k = threadIdx.x & 7;
+    if (r >= j.rows[wi]) return;
+    const int B = j.blocks;
+    const uint8_t* row = j.w[wi] + (size_t)r * j.rb;
+    float acc11[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc11[t] = 0.0f;
+    const int8_t* q8 = j.act.q8perm + (size_t)j.tok0 * j.cols + k * 32;
+    const float* xsc = j.act.xscale + (size_t)j.tok0 * B;
+#pragma unroll 2
+    for (int b = 0; b < B; b++) {
+        const uint8_t* blk = row + (size_t)b * 272;
+        const uint4 dh = *(const uint4*)blk;
+        float dj[8];
+        const uint32_t dw[4] = {dh.x, dh.y, dh.z, dh.w};
+#pragma unroll
+        for (int q = 0; q < 8; q++) dj[q] = f16_bits_to_f32((dw[q >> 1] >> (16 * (q & 1))) & 0xffffu);
+        int wv[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) wv[q] = *(const int*)(blk + 16 + 32 * q + 4 * k);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (t < j.ntok) {
+                const int4 qa = *(const int4*)(q8 + (size_t)t * j.cols + b * 256);
+                const int4 qb = *(const int4*)(q8 + (size_t)t * j.cols + b * 256 + 16);
+                const int xq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+                float acc12 = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; q++) acc12 = fmaf((float)sdot4(wv[q], xq[q], 0), dj[q], acc12);
+                acc11[t] = fmaf(acc12, xsc[(size_t)t * B + b], acc11[t]);
+            }
+        }
+    }
+    store_rows<NT>(j, wi, r, k, acc11);
+}
+
+// Debug: the exact int32 lane sums of every (row, block).
+__global__ __launch_bounds__(256) void lane_ints_kernel(const uint8_t* __restrict__ w, int type,
+                                                        int rows, int B, size_t rb, ActQ8 act,
+                                                        int32_t* __restrict__ out) {
+    const int r = blockIdx.x * kRowsPerWG + (threadIdx.x >> 3);
+    const int k = threadIdx.x & 7;
+    if (r >= rows) return;
+    const uint8_t* row = w + (size_t)r * rb;
+    const int8_t* q8 = act.q8perm + k * 32;
+    for (int b = 0; b < B; b++) {
+        const int4 qa = *(const int4*)(q8 + b * 256);
+        const int4 qb = *(const int4*)(q8 + b * 256 + 16);
+        const int xq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        int acc = 0;
+        if (type == GLLM_TYPE_Q4_K) {
+            const uint8_t* blk = row + (size_t)b * 144;
+            const uint4 h = *(const uint4*)blk;
+            const uint32_t sc03 = h.y & 0x3f3f3f3fu;
+            const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+            for (int s = 0; s < 4; s++) {
+                const uint32_t wd = *(const uint32_t*)(blk + 16 + 32 * s + 4 * k);
+                const uint32_t sc = s < 2 ? sc03 : sc47;
+                acc += ubyte(sc, (2 * s) & 3) * sdot4((int)(wd & 0x0f0f0f0fu), xq[2 * s], 0);
+                acc += ubyte(sc, (2 * s + 1) & 3) * sdot4((int)((wd >> 4) & 0x0f0f0f0fu), xq[2 * s + 1], 0);
+            }
+        } else if (type == GLLM_TYPE_Q6_K) {
+            const uint8_t* blk = row + (size_t)b * 208;
+            const int8_t* sc = (const int8_t*)(blk + 192);
+            for (int m = 0; m < 8; m++) {
+                const int h = m >> 2, c = m & 3;
+                const uint32_t y = *(const uint32_t*)(blk + 64 * h + ((c & 1) ? 32 : 0) + 4 * k);
+                const uint32_t qh = *(const uint32_t*)(blk + 128 + 32 * h + 4 * k);
+                const uint32_t code = ((y >> (4 * (c >> 1))) & 0x0f0f0f0fu) |
+                                      (((qh >> (2 * c)) & 0x03030303u) << 4);
+                acc += (int)sc[8 * h + 2 * c + (k >> 2)] * sdot4((int)code, xq[m], 0);
+            }
+        } else {
+            const uint8_t* blk = row + (size_t)b * 272;
+            for (int q = 0; q < 8; q++) acc += sdot4(*(const int*)(blk + 16 + 32 * q + 4 * k), xq[q], 0);
+        }
+        out[((size_t)r * B + b) * 8 + k] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Greedy argmax over a logits vector: finite values only, strict >, lowest
+// index on ties, 0 when nothing is finite (argmaxQ6KRowsQ8,
+// kernels_amd64.go:294-331; finiteLogit sampling.go:385).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool finite_logit(float v) {
+    return (__float_as_uint(v) & 0x7f800000u) != 0x7f800000u;
+}
+
+// Packs (value, row) so that a larger key is a larger value, or the same
+// value at a lower row; 0 means "nothing finite seen".
+__device__ __forceinline__ unsigned long long argmax_key(float v, int r) {
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)r);
+}
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
+                                                      uint32_t* __restrict__ token) {
+    unsigned long long best = 0;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const float v = logits[i];
+        if (finite_logit(v)) {
+            const unsigned long long key = argmax_key(v, i);
+            best = key > best ? key : best;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const unsigned long long o = __shfl_xor(best, off);
+        best = o > best ? o : best;
+    }
+    __shared__ unsigned long long wbest[16];
+    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = 0;
+        for (int i = 0; i < 16; i++) b = wbest[i] > b ? wbest[i] : b;
+        *token = b ? 0xffffffffu - (uint32_t)(b & 0xffffffffu) : 0u;
+    }
+}
+
+int launch_argmax(const float* logits, int n, uint32_t* token, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, n, token);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Upload-time repacks (same bytes, 16-byte aligned blocks) and their inverse.
+// ---------------------------------------------------------------------------
+__global__ void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int type,
+                              int rows, int B, size_t rb, int inverse) {
+    const size_t total = (size_t)rows * rb;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / rb, o = i % rb;  // o: offset in the reference row
+        size_t n;                             // offset in the repacked row
+        if (type == GLLM_TYPE_Q6_K) {
+            const size_t b = o / 210, e = o % 210;
+            n = e < 208 ? b * 208 + e : (size_t)B * 208 + b * 2 + (e - 208);
+        } else {  // Q8_0
+            const size_t g = o / 272, e = o % 272, q = e / 34, f = e % 34;
+            n = g * 272 + (f < 2 ? q * 2 + f : 16 + q * 32 + (f - 2));
+        }
+        if (inverse) dst[r * rb + o] = src[r * rb + n];
+        else dst[r * rb + n] = src[r * rb + o];
+    }
+}
+
+int launch_repack(const uint8_t* src, uint8_t* dst, int type, int rows, int B, size_t rb,
+                  int inverse, hipStream_t s) {
+    const size_t total = (size_t)rows * rb;
+    int grid = (int)std::min<size_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, s, src, dst, type, rows, B, rb,
+                       inverse);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+size_t ref_row_bytes(int type, int cols) {
+    switch (type) {
+    case GLLM_TYPE_Q4_K: return (size_t)(cols / 256) * 144;
+    case GLLM_TYPE_Q6_K: return (size_t)(cols / 256) * 210;
+    case GLLM_TYPE_Q8_0: return (size_t)(cols / 32) * 34;
+    default: return 0;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launch helpers
+// ---------------------------------------------------------------------------
+
+template <int NT>
+int launch_gemv_nt(const GemvJob& j, int type, int grid, hipStream_t s) {
+    switch (type) {
+    case GLLM_TYPE_Q4_K: hipLaunchKernelGGL(gemv_q4k_kernel<NT>, dim3(grid), dim3(256), 0, s, j); break;
+    case GLLM_TYPE_Q6_K: hipLaunchKernelGGL(gemv_q6k_kernel<NT>, dim3(grid), dim3(256), 0, s, j); break;
+    case GLLM_TYPE_Q8_0: hipLaunchKernelGGL(gemv_q8_0_kernel<NT>, dim3(grid), dim3(256), 0, s, j); break;
+    default: return fail(GLLM_EUNSUP, "gemv: unsupported type %d", type);
+    }
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+int validate_weight(const gllm_hip_weight* w) {
+    if (!w || !w->d_data) return fail(GLLM_EINVAL, "null weight handle");
+    if (w->type != GLLM_TYPE_Q4_K && w->type != GLLM_TYPE_Q6_K && w->type != GLLM_TYPE_Q8_0)
+        return fail(GLLM_EUNSUP, "weight type %d has no row kernel", w->type);
+    return GLLM_OK;
+}
+
+// Row kernels for n weights against p activation rows already quantised
+// into `act` (activation rows tok0 .. tok0+p-1 of act).
+int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* const* outs,
+             const int* strides, hipStream_t s) {
+    if (n < 1 || n > 3) return fail(GLLM_EINVAL, "gemv: %d weights (1..3 supported)", n);
+    GemvJob j{};
+    j.n = n;
+    const gllm_hip_weight* w0 = ws[0];
+    j.blocks = w0->blocks;
+    j.cols = w0->cols;
+    j.rb = w0->row_bytes;
+    j.act = act;
+    int wg = 0;
+    for (int i = 0; i < n; i++) {
+        j.w[i] = ws[i]->d_data;
+        j.out[i] = outs[i];
+        j.rows[i] = ws[i]->rows;
+        j.out_stride[i] = strides ? strides[i] : ws[i]->rows;
+        j.wg_begin[i] = wg;
+        wg += (ws[i]->rows + kRowsPerWG - 1) / kRowsPerWG;
+    }
+    j.wg_begin[n] = wg;
+    if (wg == 0) return GLLM_OK;
+    for (int t0 = 0; t0 < p; t0 += kMaxTok) {
+        j.tok0 = t0;
+        j.ntok = std::min(kMaxTok, p - t0);
+        int rc = j.ntok == 1 ? launch_gemv_nt<1>(j, w0->type, wg, s)
+               : j.ntok <= 4 ? launch_gemv_nt<4>(j, w0->type, wg, s)
+                             : launch_gemv_nt<8>(j, w0->type, wg, s);
+        GLLM_TRY(rc);
+    }
+    return GLLM_OK;
+}
+
+int matvec_multi(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float* const* outs,
+                 const int* strides, hipStream_t s, int scratch_slot) {
+    for (int i = 0; i < n; i++) GLLM_TRY(validate_weight(ws[i]));
+    for (int i = 1; i < n; i++)
+        if (ws[i]->cols != ws[0]->cols || ws[i]->type != ws[0]->type)
+            return fail(GLLM_EINVAL, "fused matvec needs one type and one cols (%d/%d vs %d/%d)",
+                        ws[i]->type, ws[i]->cols, ws[0]->type, ws[0]->cols);
+    if (n > 1 && ws[0]->type == GLLM_TYPE_Q8_0)
+        return fail(GLLM_EUNSUP, "fused Q8_0 matvec: the reference uses its float kernel here");
+    if (p <= 0) return fail(GLLM_EINVAL, "p = %d", p);
+    for (int i = 0; i < n; i++)
+        if (strides && strides[i] < ws[i]->rows) return fail(GLLM_EINVAL, "out stride < rows");
+    const int cols = ws[0]->cols;
+    void* sc = thread_scratch(scratch_slot, act_bytes(cols, p));
+    if (!sc) return GLLM_ENOMEM;
+    ActQ8 act;
+    act_carve(sc, cols, p, &act);
+    GLLM_TRY(launch_q8k_prep(d_xs, cols, p, act, s));
+    return run_gemv(n, ws, act, p, outs, strides, s);
+}
+
+}  // namespace gllm
+
+using namespace gllm;
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+static gllm_hip_weight* weight_alloc(int ggml_type, int rows, int cols, size_t len) {
+    if (ggml_type != GLLM_TYPE_Q4_K && ggml_type != GLLM_TYPE_Q6_K && ggml_type != GLLM_TYPE_Q8_0) {
+        fail(GLLM_EUNSUP, "weight type %d not supported", ggml_type);
+        return nullptr;
+    }
+    if (rows <= 0 || cols <= 0 || cols % 256) {
+        fail(GLLM_EINVAL, "weight shape %dx%d (cols must be a positive multiple of 256)", rows, cols);
+        return nullptr;
+    }
+    const size_t rb = ref_row_bytes(ggml_type, cols);
+    if (len < rb * (size_t)rows) {
+        fail(GLLM_EINVAL, "weight bytes %zu < rows*row_bytes %zu", len, rb * (size_t)rows);
+        return nullptr;
+    }
+    gllm_hip_weight* w = new gllm_hip_weight();
+    w->type = ggml_type;
+    w->rows = rows;
+    w->cols = cols;
+    w->blocks = cols / 256;
+    w->row_bytes = rb;
+    if (hipGetDevice(&w->device) != hipSuccess) w->device = 0;
+    if (hipMalloc(&w->d_data, rb * (size_t)rows) != hipSuccess) {
+        (void)hipGetLastError();
+        fail(GLLM_ENOMEM, "hipMalloc(%zu) for weight failed", rb * (size_t)rows);
+        delete w;
+        return nullptr;
+    }
+    return w;
+}
+
+static gllm_hip_weight* weight_finish(gllm_hip_weight* w, const uint8_t* d_src, hipStream_t s) {
+    int rc = GLLM_OK;
+    const size_t bytes = w->row_bytes * (size_t)w->rows;
+    if (w->type == GLLM_TYPE_Q4_K) {
+        rc = check(hipMemcpyAsync(w->d_data, d_src, bytes, hipMemcpyDeviceToDevice, s), "copy weight");
+    } else {
+        rc = launch_repack(d_src, w->d_data, w->type, w->rows, w->blocks, w->row_bytes, 0, s);
+    }
+    if (rc == GLLM_OK) rc = check(hipStreamSynchronize(s), "weight upload");
+    if (rc != GLLM_OK) {
+        (void)hipFree(w->d_data);
+        delete w;
+        return nullptr;
+    }
+    return w;
+}
+
+gllm_hip_weight* gllm_hip_weight_new(const void* data, size_t len, int ggml_type, int rows,
+                                     int cols) {
+    if (!data) {
+        fail(GLLM_EINVAL, "gllm_hip_weight_new: null data");
+        return nullptr;
+    }
+    gllm_hip_weight* w = weight_alloc(ggml_type, rows, cols, len);
+    if (!w) return nullptr;
+    hipStream_t s = thread_stream();
+    const size_t bytes = w->row_bytes * (size_t)rows;
+    if (ggml_type == GLLM_TYPE_Q4_K) {
+        if (check(hipMemcpy(w->d_data, data, bytes, hipMemcpyHostToDevice), "upload weight") != GLLM_OK) {
+            (void)hipFree(w->d_data);
+            delete w;
+            return nullptr;
+        }
+        return w;
+    }
+    void* tmp = nullptr;
+    if (hipMalloc(&tmp, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        fail(GLLM_ENOMEM, "hipMalloc(%zu) for weight staging failed", bytes);
+        (void)hipFree(w->d_data);
+        delete w;
+        return nullptr;
+    }
+    if (check(hipMemcpy(tmp, data, bytes, hipMemcpyHostToDevice), "upload weight") != GLLM_OK) {
+        (void)hipFree(tmp);
+        (void)hipFree(w->d_data);
+        delete w;
+        return nullptr;
+    }
+    gllm_hip_weight* out = weight_finish(w, (const uint8_t*)tmp, s);
+    (void)hipFree(tmp);
+    return out;
+}
+
+gllm_hip_weight* gllm_hip_weight_from_device(const void* d_data, size_t len, int ggml_type,
+                                             int rows, int cols, void* stream) {
+    if (!d_data) {
+        fail(GLLM_EINVAL, "gllm_hip_weight_from_device: null data");
+        return nullptr;
+    }
+    gllm_hip_weight* w = weight_alloc(ggml_type, rows, cols, len);
+    if (!w) return nullptr;
+    return weight_finish(w, (const uint8_t*)d_data, stream ? (hipStream_t)stream : thread_stream());
+}
+
+void gllm_hip_weight_release(gllm_hip_weight* w) {
+    if (!w) return;
+    if (w->d_data) (void)hipFree(w->d_data);
+    delete w;
+}
+
+int gllm_hip_weight_shape(const gllm_hip_weight* w, int* ggml_type, int* rows, int* cols) {
+    if (!w) return fail(GLLM_EINVAL, "null weight handle");
+    if (ggml_type) *ggml_type = w->type;
+    if (rows) *rows = w->rows;
+    if (cols) *cols = w->cols;
+    return GLLM_OK;
+}
+
+int gllm_hip_weight_download_dev(const gllm_hip_weight* w, void* d_dst, void* stream) {
+    if (!w || !d_dst) return fail(GLLM_EINVAL, "gllm_hip_weight_download_dev: bad arguments");
+    hipStream_t s = (hipStream_t)stream;
+    if (w->type == GLLM_TYPE_Q4_K) {
+        GLLM_HIP(hipMemcpyAsync(d_dst, w->d_data, w->row_bytes * (size_t)w->rows,
+                                hipMemcpyDeviceToDevice, s));
+        return GLLM_OK;
+    }
+    return launch_repack(w->d_data, (uint8_t*)d_dst, w->type, w->rows, w->blocks, w->row_bytes, 1, s);
+}
+
+int gllm_hip_matvec_dev(gllm_hip_weight* w, const float* d_xs, int p, float* d_outs,
+                        int out_stride, void* stream) {
+    if (!d_xs || !d_outs) return fail(GLLM_EINVAL, "gllm_hip_matvec_dev: null pointer");
+    gllm_hip_weight* ws[1] = {w};
+    float* outs[1] = {d_outs};
+    int strides[1] = {out_stride > 0 ? out_stride : (w ? w->rows : 0)};
+    return matvec_multi(1, ws, d_xs, p, outs, strides, (hipStream_t)stream, 0);
+}
+
+int gllm_hip_matvec_multi_dev(int n, gllm_hip_weight* const* ws, const float* d_xs, int p,
+                              float* const* d_outs, const int* out_strides, void* stream) {
+    if (!ws || !d_xs || !d_outs || n < 1 || n > 3)
+        return fail(GLLM_EINVAL, "gllm_hip_matvec_multi_dev: bad arguments");
+    for (int i = 0; i < n; i++)
+        if (!d_outs[i]) return fail(GLLM_EINVAL, "gllm_hip_matvec_multi_dev: null output");
+    return matvec_multi(n, ws, d_xs, p, d_outs, out_strides, (hipStream_t)stream, 0);
+}
+
+// Host-pointer forms: stage through pinned memory on the thread's stream.
+static int matvec_host(int n, gllm_hip_weight* const* ws, const float* x, int p, float* const* outs) {
+    for (int i = 0; i < n; i++) GLLM_TRY(validate_weight(ws[i]));
+    if (!x || p <= 0) return fail(GLLM_EINVAL, "matvec: bad input");
+    hipStream_t s = thread_stream();
+    if (!s) return GLLM_EDEVICE;
+    const int cols = ws[0]->cols;
+    size_t out_total = 0;
+    for (int i = 0; i < n; i++) out_total += (size_t)ws[i]->rows * p;
+    float* d_x = (float*)thread_scratch(1, (size_t)cols * p * 4);
+    float* d_out = (float*)thread_scratch(2, out_total * 4);
+    if (!d_x || !d_out) return GLLM_ENOMEM;
+    GLLM_HIP(hipMemcpyAsync(d_x, x, (size_t)cols * p * 4, hipMemcpyHostToDevice, s));
+    float* douts[3];
+    int strides[3];
+    size_t off = 0;
+    for (int i = 0; i < n; i++) {
+        douts[i] = d_out + off;
+        strides[i] = ws[i]->rows;
+        off += (size_t)ws[i]->rows * p;
+    }
+    GLLM_TRY(matvec_multi(n, ws, d_x, p, douts, strides, s, 0));
+    for (int i = 0; i < n; i++)
+        GLLM_HIP(hipMemcpyAsync(outs[i], douts[i], (size_t)ws[i]->rows * p * 4,
+                                hipMemcpyDeviceToHost, s));
+    GLLM_HIP(hipStreamSynchronize(s));
+    return GLLM_OK;
+}
+
+int gllm_hip_matvec(gllm_hip_weight* w, const float* x, float* out) {
+    if (!out) return fail(GLLM_EINVAL, "gllm_hip_matvec: null out");
+    gllm_hip_weight* ws[1] = {w};
+    float* outs[1] = {out};
+    return matvec_host(1, ws, x, 1, outs);
+}
+
+int gllm_hip_matvec2(gllm_hip_weight* a, gllm_hip_weight* b, const float* x, float* out_a,
+                     float* out_b) {
+    if (!out_a || !out_b) return fail(GLLM_EINVAL, "gllm_hip_matvec2: null out");
+    gllm_hip_weight* ws[2] = {a, b};
+    float* outs[2] = {out_a, out_b};
+    return matvec_host(2, ws, x, 1, outs);
+}
+
+int gllm_hip_matvec3(gllm_hip_weight* a, gllm_hip_weight* b, gllm_hip_weight* c, const float* x,
+                     float* out_a, float* out_b, float* out_c) {
+    if (!out_a || !out_b || !out_c) return fail(GLLM_EINVAL, "gllm_hip_matvec3: null out");
+    gllm_hip_weight* ws[3] = {a, b, c};
+    float* outs[3] = {out_a, out_b, out_c};
+    return matvec_host(3, ws, x, 1, outs);
+}
+
+int gllm_hip_matvec_batch(gllm_hip_weight* w, const float* xs, int p, float* outs) {
+    if (!outs) return fail(GLLM_EINVAL, "gllm_hip_matvec_batch: null out");
+    gllm_hip_weight* ws[1] = {w};
+    float* o[1] = {outs};
+    return matvec_host(1, ws, xs, p, o);
+}
+
+int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token, void* stream) {
+    GLLM_TRY(validate_weight(w));
+    if (!d_x || !d_token) return fail(GLLM_EINVAL, "gllm_hip_argmax_dev: null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    float* logits = (float*)thread_scratch(3, (size_t)w->rows * 4);
+    if (!logits) return GLLM_ENOMEM;
+    gllm_hip_weight* ws[1] = {w};
+    float* outs[1] = {logits};
+    int strides[1] = {w->rows};
+    GLLM_TRY(matvec_multi(1, ws, d_x, 1, outs, strides, s, 0));
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, w->rows, d_token);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+int gllm_hip_argmax(gllm_hip_weight* w, const float* x, uint32_t* token) {
+    GLLM_TRY(validate_weight(w));
+    if (!x || !token) return fail(GLLM_EINVAL, "gllm_hip_argmax: null pointer");
+    hipStream_t s = thread_stream();
+    if (!s) return GLLM_EDEVICE;
+    float* d_x = (float*)thread_scratch(1, (size_t)w->cols * 4);
+    uint32_t* d_tok = (uint32_t*)thread_scratch(4, 64);
+    uint32_t* h_tok = (uint32_t*)thread_pinned(0, 64);
+    if (!d_x || !d_tok || !h_tok) return GLLM_ENOMEM;
+    GLLM_HIP(hipMemcpyAsync(d_x, x, (size_t)w->cols * 4, hipMemcpyHostToDevice, s));
+    GLLM_TRY(gllm_hip_argmax_dev(w, d_x, d_tok, s));
+    GLLM_HIP(hipMemcpyAsync(h_tok, d_tok, 4, hipMemcpyDeviceToHost, s));
+    GLLM_HIP(hipStreamSynchronize(s));
+    *token = *h_tok;
+    return GLLM_OK;
+}
+
+int gllm_hip_lane_ints_dev(gllm_hip_weight* w, const float* d_x, int32_t* d_ints, void* stream) {
+    GLLM_TRY(validate_weight(w));
+    if (!d_x || !d_ints) return fail(GLLM_EINVAL, "gllm_hip_lane_ints_dev: null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    void* sc = thread_scratch(0, act_bytes(w->cols, 1));
+    if (!sc) return GLLM_ENOMEM;
+    ActQ8 act;
+    act_carve(sc, w->cols, 1, &act);
+    GLLM_TRY(launch_q8k_prep(d_x, w->cols, 1, act, s));
+    const int grid = (w->rows + kRowsPerWG - 1) / kRowsPerWG;
+    hipLaunchKernelGGL(lane_ints_kernel, dim3(grid), dim3(256), 0, s, w->d_data, w->type, w->rows,
+                       w->blocks, w->row_bytes, act, d_ints);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+}  // extern "C"

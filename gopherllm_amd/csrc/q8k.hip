@@ -1,0 +1,112 @@
+// q8k.hip -- Q8K activation quantiser and the exact-float xsums.
+//
+// One workgroup per (256-element block, activation row).  Reproduces
+//   q8kQuantizePortable  quant_q8k_portable.go:36-62 (== kernels_amd64.s:348-436)
+//   sumF32Groups32       kernels_amd64.s:208-230  (Q4_K dmin term)
+//   sumF32Groups16 x 32  kernels_amd64.s:234-254 + ScaleF32(xs, 32) (Q6_K offset)
+// bit for bit, and writes q8 in the lane-permuted layout the row kernels read
+// (q8perm_offset in gllm_common.h).
+#include "gllm_common.h"
+
+namespace gllm {
+
+size_t act_bytes(int cols, int p) {
+    size_t n = (size_t)cols * p;                   // q8perm
+    n += (size_t)(cols / 256) * p * 4;             // xscale
+    n = (n + 255) & ~(size_t)255;
+    n += (size_t)(cols / 32) * p * 4;              // xs32
+    n += (size_t)(cols / 16) * p * 4;              // xs16
+    return n + 256;
+}
+
+void act_carve(void* base, int cols, int p, ActQ8* a) {
+    uint8_t* c = (uint8_t*)base;
+    a->q8perm = (int8_t*)c;
+    c += (size_t)cols * p;
+    a->xscale = (float*)c;
+    c += (size_t)(cols / 256) * p * 4;
+    c = (uint8_t*)(((uintptr_t)c + 255) & ~(uintptr_t)255);
+    a->xs32 = (float*)c;
+    c += (size_t)(cols / 32) * p * 4;
+    a->xs16 = (float*)c;
+    a->cols = cols;
+    a->p = p;
+}
+
+// plain == true writes q8 in element order (the debug entry point) instead of
+// the lane-permuted order.
+__global__ __launch_bounds__(256) void q8k_prep_kernel(const float* __restrict__ x, int cols,
+                                                       ActQ8 a, int8_t* __restrict__ plain_q8,
+                                                       float* __restrict__ plain_scale) {
+    const int b = blockIdx.x, t = blockIdx.y, e = threadIdx.x;
+    const int nb = cols / 256;
+    __shared__ float sx[256];
+    __shared__ float wmax[4];
+    const float v = x[(size_t)t * cols + (size_t)b * 256 + e];
+    sx[e] = v;
+    // amax over the block; v_max_f32 is IEEE maxNum, so a NaN element is
+    // skipped exactly like the reference's `a > amax` scan.
+    float m = fabsf(v);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((e & 63) == 0) wmax[e >> 6] = m;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    float scale = 0.0f;
+    int q = 0;
+    if (amax != 0.0f && amax == amax) {
+        scale = amax / 127.0f;
+        const float inv = 127.0f / amax;
+        q = (int)rintf(v * inv);
+    }
+    if (plain_q8) {
+        plain_q8[(size_t)t * cols + (size_t)b * 256 + e] = (int8_t)q;
+        if (e == 0) plain_scale[(size_t)t * nb + b] = scale;
+        return;
+    }
+    a.q8perm[(size_t)t * cols + (size_t)b * 256 + q8perm_offset(e)] = (int8_t)q;
+    if (e == 0) a.xscale[(size_t)t * nb + b] = scale;
+    if (e < 8) {
+        // sumF32Groups32: v_k = ((x[k] + x[8+k]) + x[16+k]) + x[24+k]
+        const float* g = sx + 32 * e;
+        float s[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) s[k] = ((g[k] + g[8 + k]) + g[16 + k]) + g[24 + k];
+        const float a0 = s[0] + s[4], a1 = s[1] + s[5], a2 = s[2] + s[6], a3 = s[3] + s[7];
+        a.xs32[(size_t)t * (cols / 32) + b * 8 + e] = (a0 + a1) + (a2 + a3);
+    } else if (e >= 64 && e < 80) {
+        // sumF32Groups16: v_k = x[k] + x[8+k], then the same tree, then x32
+        const int gi = e - 64;
+        const float* g = sx + 16 * gi;
+        float s[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) s[k] = g[k] + g[8 + k];
+        const float a0 = s[0] + s[4], a1 = s[1] + s[5], a2 = s[2] + s[6], a3 = s[3] + s[7];
+        a.xs16[(size_t)t * (cols / 16) + b * 16 + gi] = ((a0 + a1) + (a2 + a3)) * 32.0f;
+    }
+}
+
+int launch_q8k_prep(const float* d_x, int cols, int p, const ActQ8& a, hipStream_t s) {
+    if (cols <= 0 || cols % 256 || p <= 0) return fail(GLLM_EINVAL, "q8k: cols %d p %d", cols, p);
+    dim3 grid(cols / 256, p);
+    hipLaunchKernelGGL(q8k_prep_kernel, grid, dim3(256), 0, s, d_x, cols, a, (int8_t*)nullptr,
+                       (float*)nullptr);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+}  // namespace gllm
+
+using namespace gllm;
+
+extern "C" int gllm_hip_q8k_quantize_dev(const float* d_x, int cols, int p, int8_t* d_q8,
+                                         float* d_scales, void* stream) {
+    if (!d_x || !d_q8 || !d_scales || cols <= 0 || cols % 256 || p <= 0)
+        return fail(GLLM_EINVAL, "gllm_hip_q8k_quantize_dev: bad arguments");
+    ActQ8 a{};
+    dim3 grid(cols / 256, p);
+    hipLaunchKernelGGL(q8k_prep_kernel, grid, dim3(256), 0, (hipStream_t)stream, d_x, cols, a,
+                       d_q8, d_scales);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}

@@ -1,0 +1,225 @@
+/*
+ * gllm_hip.h -- C ABI of the MI355X (gfx950) quantized-matvec and
+ * F16-KV decode-attention path of GopherLLM.
+ *
+ * The Go engine reaches these through cgo exactly as it reaches its Metal
+ * backend today (internal/metal/metal_darwin.go:557-1001): weights are
+ * uploaded once at load time and kept as opaque handles on the Weight struct
+ * (model.go:2454), every dispatch site tries the device first and falls back
+ * to the CPU kernel when the call reports failure (model.go:700-725).
+ *
+ * Conventions
+ *  - Plain C types only; no torch or HIP types.  `stream` arguments are a
+ *    hipStream_t passed as void* (NULL = the legacy default stream).
+ *  - Every int-returning call returns GLLM_OK (0) on success and a negative
+ *    GLLM_E* code on failure, having written nothing to the outputs;
+ *    gllm_hip_last_error() then describes the failure (per calling thread).
+ *  - "host" entry points take host pointers and block until the result is in
+ *    the caller's buffer (the Metal seam's waitUntilCompleted contract);
+ *    "_dev" entry points take device pointers and only enqueue on `stream`.
+ *  - Shapes follow the reference: cols % 256 == 0 for the Q8K row kernels
+ *    (simd.go:264), weights are row-major GGUF tensors with rows = dims[1],
+ *    cols = dims[0] (model.go:2393-2396).
+ *  - Thread safety: handles may be used from several host threads at once;
+ *    host entry points use per-thread streams and per-thread scratch.
+ *    A KV cache or model handle must not be mutated by two threads at once
+ *    (the reference serialises requests per Runner, runtime.go:816-817).
+ */
+#ifndef GLLM_HIP_H
+#define GLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML tensor types accepted by the row kernels (gguf.go:27-60). */
+#define GLLM_TYPE_F32 0
+#define GLLM_TYPE_Q8_0 8
+#define GLLM_TYPE_Q4_K 12
+#define GLLM_TYPE_Q6_K 14
+
+#define GLLM_OK 0
+#define GLLM_EINVAL (-1)   /* bad argument or shape */
+#define GLLM_EDEVICE (-2)  /* HIP runtime error */
+#define GLLM_ENOMEM (-3)   /* device allocation failed */
+#define GLLM_EUNSUP (-4)   /* type or shape not supported by this path */
+
+/* ---------------------------------------------------------------------- */
+/* Runtime                                                                 */
+/* ---------------------------------------------------------------------- */
+
+/* 1 when a gfx950 device is usable (replaces gllm_metal_available,
+ * internal/metal/metal_darwin.go:396). */
+int gllm_hip_available(void);
+/* Message of the last failure on the calling thread (replaces
+ * gllm_metal_last_error, internal/metal/metal_darwin.go:400). */
+const char* gllm_hip_last_error(void);
+/* Select the device used by handles created afterwards on this thread. */
+int gllm_hip_set_device(int device);
+/* Library version string, for logs. */
+const char* gllm_hip_version(void);
+
+/* ---------------------------------------------------------------------- */
+/* Weights (prepareMetalWeight, model.go:2454; gllm_metal_new_q4k,         */
+/* internal/metal/metal_darwin.go:557)                                     */
+/* ---------------------------------------------------------------------- */
+
+typedef struct gllm_hip_weight gllm_hip_weight;
+
+/* Upload `len` bytes of a GGUF tensor (rows x cols of ggml_type) from host
+ * memory; the host bytes may be released after the call.  Q6_K and Q8_0 rows
+ * are repacked once into 16-byte aligned blocks (same size, same values). */
+gllm_hip_weight* gllm_hip_weight_new(const void* data, size_t len, int ggml_type, int rows,
+                                     int cols);
+/* Same, from bytes already in device memory (copied, then repacked). */
+gllm_hip_weight* gllm_hip_weight_from_device(const void* d_data, size_t len, int ggml_type,
+                                             int rows, int cols, void* stream);
+/* replaces gllm_metal_release_weight (internal/metal/metal_darwin.go:1001) */
+void gllm_hip_weight_release(gllm_hip_weight* w);
+int gllm_hip_weight_shape(const gllm_hip_weight* w, int* ggml_type, int* rows, int* cols);
+/* Device bytes of the weight in the reference's GGUF layout (undoing the
+ * repack); dst is a device buffer of rows*row_bytes. */
+int gllm_hip_weight_download_dev(const gllm_hip_weight* w, void* d_dst, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Matvec (Weight.MatvecInto model.go:670; MatvecQ4KInto simd.go:261,      */
+/* MatvecQ6KInto simd.go:413, MatvecQ8_0Into simd.go:204)                  */
+/* ---------------------------------------------------------------------- */
+
+/* out[r] = W[r,:] . x.  x: cols floats, out: rows floats.  Quantises x to
+ * Q8K (q8kQuantize) and folds the exact-float xsums term, reproducing the
+ * reference's amd64 row kernels bit for bit.  (gllm_metal_q4k_matvec,
+ * internal/metal/metal_darwin.go:740) */
+int gllm_hip_matvec(gllm_hip_weight* w, const float* x, float* out);
+/* Two / three weights sharing one activation vector (MatvecQ4K2IntoWithXSums
+ * simd.go:295, Q4KMatvec3IntoWithXSums metal.go:14, MatvecQ4K2Q6KIntoWithXSums
+ * simd.go:331, MatvecQ6K2Into / MatvecQ6K3Into simd.go:443/483).  Q4_K and
+ * Q6_K only: the reference routes Q8_0 pairs to its float kernel
+ * (model.go:3213-3230), which this path does not reproduce. */
+int gllm_hip_matvec2(gllm_hip_weight* a, gllm_hip_weight* b, const float* x, float* out_a,
+                     float* out_b);
+int gllm_hip_matvec3(gllm_hip_weight* a, gllm_hip_weight* b, gllm_hip_weight* c,
+                     const float* x, float* out_a, float* out_b, float* out_c);
+/* p activation rows xs[p][cols] -> outs[p][rows] (matvecBatchQ8,
+ * kernels_amd64.go:470); per-row results equal p separate matvecs. */
+int gllm_hip_matvec_batch(gllm_hip_weight* w, const float* xs, int p, float* outs);
+/* Greedy token: argmax over finite W.x, lowest row on ties
+ * (Weight.ArgmaxMatvec model.go:754 -> argmaxQ6KRowsQ8 kernels_amd64.go:294). */
+int gllm_hip_argmax(gllm_hip_weight* w, const float* x, uint32_t* token);
+
+/* Device-pointer forms.  d_xs: p rows of cols floats (row stride cols);
+ * d_outs: p rows of out_stride floats (out_stride >= rows). */
+int gllm_hip_matvec_dev(gllm_hip_weight* w, const float* d_xs, int p, float* d_outs,
+                        int out_stride, void* stream);
+/* n weights (same cols, same type) against the same activations; one
+ * quantisation of x is shared by all of them. */
+int gllm_hip_matvec_multi_dev(int n, gllm_hip_weight* const* ws, const float* d_xs, int p,
+                              float* const* d_outs, const int* out_strides, void* stream);
+int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token, void* stream);
+
+/* Q8K activation quantisation alone (q8kQuantize, kernels_amd64.s:348-436):
+ * p rows of cols floats -> q8 [p][cols] in element order and scales
+ * [p][cols/256]. */
+int gllm_hip_q8k_quantize_dev(const float* d_x, int cols, int p, int8_t* d_q8,
+                              float* d_scales, void* stream);
+/* Debug: the exact integer lane sums of every (row, block): d_ints holds
+ * rows*(cols/256)*8 int32 (ref: the int32 lanes of q4kDotQ8KRow /
+ * q6kDotQ8KRow / q8_0DotQ8KRow). */
+int gllm_hip_lane_ints_dev(gllm_hip_weight* w, const float* d_x, int32_t* d_ints,
+                           void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* RTN encoders (QuantizeRowQ4K quantize_rtn.go:128, QuantizeRowQ6K :331,  */
+/* QuantizeRowQ8_0 :35) run on the device: d_src rows x cols floats ->     */
+/* d_dst in the reference's GGUF layout.                                   */
+/* ---------------------------------------------------------------------- */
+int gllm_hip_quantize_rows_dev(int ggml_type, const float* d_src, int rows, int cols,
+                               void* d_dst, void* stream);
+/* Deterministic synthetic data: n floats ~ N(0, std^2) from (seed, stream
+ * id), counter based; used to build the benchmark models on the device. */
+int gllm_hip_fill_normal_dev(float* d_out, size_t n, uint64_t seed, float std, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* F16 KV cache and GQA decode attention (KVCache model.go:1321,           */
+/* NewKVCacheF16 :1396, storeKV :1466, attendHeadGroup :1516)              */
+/* ---------------------------------------------------------------------- */
+
+typedef struct gllm_hip_kv gllm_hip_kv;
+
+#define GLLM_ATTN_EXACT 0   /* two-pass, the reference's float order */
+#define GLLM_ATTN_SPLITK 1  /* split-K online softmax, tolerance-level */
+
+gllm_hip_kv* gllm_hip_kv_new(int layers, int kv_dim_k, int kv_dim_v, int max_len);
+void gllm_hip_kv_release(gllm_hip_kv* kv);
+/* Device pointer of layer l's K (or V) rows: [max_len][kv_dim] uint16. */
+uint16_t* gllm_hip_kv_k_dev(gllm_hip_kv* kv, int l);
+uint16_t* gllm_hip_kv_v_dev(gllm_hip_kv* kv, int l);
+/* Copy n positions starting at pos0 of layer l to host (f16 bits); either
+ * output may be NULL.  (The rows a prefix cache would copy, runtime.go:1334.) */
+int gllm_hip_kv_read(gllm_hip_kv* kv, int l, int pos0, int n, uint16_t* k_out, uint16_t* v_out);
+/* storeKV: round k, v (host floats) to f16 RNE at position pos. */
+int gllm_hip_kv_store(gllm_hip_kv* kv, int l, int pos, const float* k, const float* v);
+int gllm_hip_kv_store_dev(gllm_hip_kv* kv, int l, int pos, const float* d_k,
+                          const float* d_v, void* stream);
+/* attendHeadGroup: q_heads query heads sharing kv head kvh, positions
+ * start..end inclusive; out (q_heads*vd floats) is overwritten.  softcap
+ * must be 0 (the llama graph). */
+int gllm_hip_attend_group(gllm_hip_kv* kv, int l, int kvh, const float* q, int q_heads,
+                          int hd, int vd, int start, int end, float scale, float softcap,
+                          float* out);
+/* All heads of one decode position: d_q [n_heads][hd] -> d_out [n_heads][hd];
+ * head h reads kv head h / (n_heads / n_kv_heads). */
+int gllm_hip_attend_dev(gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv_heads,
+                        int hd, int start, int end, float scale, int mode, float* d_out,
+                        void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Resident llama decoder (ForwardBodyInto model.go:2622,                  */
+/* ForwardBatchInto forward_batch.go:316, forwardGreedyToken               */
+/* runtime.go:1607)                                                        */
+/* ---------------------------------------------------------------------- */
+
+typedef struct gllm_hip_model gllm_hip_model;
+
+typedef struct gllm_hip_model_config {
+    int n_layers, dim, hidden, n_heads, n_kv_heads, head_dim, vocab, max_len;
+    float rms_eps, rope_theta;
+} gllm_hip_model_config;
+
+/* Tensor slots for gllm_hip_model_set_weight / _set_norm. */
+#define GLLM_T_WQ 0
+#define GLLM_T_WK 1
+#define GLLM_T_WV 2
+#define GLLM_T_WO 3
+#define GLLM_T_W1 4   /* ffn gate */
+#define GLLM_T_W2 5   /* ffn down */
+#define GLLM_T_W3 6   /* ffn up */
+#define GLLM_T_TOK_EMBD 7
+#define GLLM_T_OUTPUT 8
+#define GLLM_T_ATTN_NORM 9
+#define GLLM_T_FFN_NORM 10
+#define GLLM_T_OUT_NORM 11
+
+gllm_hip_model* gllm_hip_model_new(const gllm_hip_model_config* cfg);
+void gllm_hip_model_release(gllm_hip_model* m);
+/* The model borrows the weight handle; it must outlive the model. */
+int gllm_hip_model_set_weight(gllm_hip_model* m, int layer, int slot, gllm_hip_weight* w);
+/* RMSNorm weights, dim host floats (copied). */
+int gllm_hip_model_set_norm(gllm_hip_model* m, int layer, int slot, const float* w);
+/* One decode step at position pos; *next = greedy token. */
+int gllm_hip_model_decode(gllm_hip_model* m, uint32_t token, int pos, uint32_t* next);
+/* Prefill n tokens from start_pos; *first = greedy token from the last
+ * position's logits; logits (vocab host floats) may be NULL. */
+int gllm_hip_model_prefill(gllm_hip_model* m, const uint32_t* tokens, int n, int start_pos,
+                           uint32_t* first, float* logits);
+/* Normed final hidden state of the last step (dim host floats). */
+int gllm_hip_model_hidden(gllm_hip_model* m, float* out);
+gllm_hip_kv* gllm_hip_model_kv(gllm_hip_model* m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

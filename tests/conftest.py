@@ -1,0 +1,77 @@
+"""Shared fixtures.  GPU tests are marked `gpu`; everything else runs on CPU.
+
+Synthetic data: numpy PCG64 streams from fixed seeds (the reference's own
+tests use Go math/rand, which cannot be regenerated here).  Weights are
+N(0, 0.02) quantised with the oracle's restatement of the reference RTN
+encoders; activations N(0, 1).
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+from oracle import oracle as ref  # noqa: E402  (checker only)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) device")
+
+
+def normal(seed, shape, std=1.0):
+    return (np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(std)
+            ).astype(np.float32)
+
+
+def quant_matrix(qtype, rows, cols, seed, std=0.02):
+    w = normal(seed, (rows, cols), std)
+    return ref.quantize_rows(qtype, w), w
+
+
+def tiny_llama(seed=1, n_layers=2, dim=512, hidden=1024, n_heads=8, n_kv_heads=2, head_dim=64,
+               vocab=1000, layer_type=ref.Q4_K, out_type=ref.Q6_K):
+    """A small llama-shaped model with the reference's tensor roles
+    (model.go:2027 loadLayer) and RMSNorm weights of 1.0."""
+    cfg = dict(n_layers=n_layers, dim=dim, hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv_heads,
+               head_dim=head_dim, vocab=vocab, rms_eps=1e-5, rope_theta=500000.0,
+               emb_type=ref.Q4_K, out_type=out_type, layer_type=layer_type)
+    qd, kvd = n_heads * head_dim, n_kv_heads * head_dim
+    s = seed * 1000
+    m = {"config": cfg}
+    m["tok_embd"], _ = quant_matrix(ref.Q4_K, vocab, dim, s + 1)
+    m["output"], _ = quant_matrix(out_type, vocab, dim, s + 2)
+    m["out_norm"] = np.ones(dim, np.float32)
+    shapes = {"wq": (qd, dim), "wk": (kvd, dim), "wv": (kvd, dim), "wo": (dim, qd),
+              "w1": (hidden, dim), "w2": (dim, hidden), "w3": (hidden, dim)}
+    for k, (r, c) in shapes.items():
+        m[k] = [quant_matrix(layer_type, r, c, s + 10 + 10 * l + list(shapes).index(k))[0]
+                for l in range(n_layers)]
+    m["attn_norm"] = [np.ones(dim, np.float32) for _ in range(n_layers)]
+    m["ffn_norm"] = [np.ones(dim, np.float32) for _ in range(n_layers)]
+    return m
+
+
+@pytest.fixture(scope="session")
+def oracle_lib():
+    ref.build()
+    return ref.lib()
+
+
+@pytest.fixture(scope="session")
+def hip():
+    """The product library on a gfx950 device; skips when no GPU is present
+    (CPU runs), fails loudly if the library is missing on a GPU box."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import gopherllm_amd as g
+    g.load()
+    if not g.available():
+        pytest.fail("libgllm_hip loaded but no gfx950 device: " + g._lib.last_error())
+    return g

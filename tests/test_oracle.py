@@ -1,0 +1,501 @@
+"""Pins the CPU oracle (oracle/gllm_oracle.c) before anything is compared
+against it.  Every check is an independent fact -- a table from the
+reference's own tests (tests/golden/reference_fixtures.json), a closed form, a
+brute-force integer evaluation with a different decomposition, a float64
+textbook form, or an invariant -- chosen so that a dropped term, a wrong sign
+or index, or a transposed operand fails at least one of them.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from conftest import normal, quant_matrix, tiny_llama
+from oracle import oracle as ref
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_fixtures.json")))
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+# ---------------------------------------------------------------- f16 ------
+
+def test_f16_roundtrip_exhaustive(oracle_lib):
+    # kv_f16_test.go:13-29: every f16 survives f16 -> f32 -> f16
+    h = np.arange(65536, dtype=np.uint16)
+    f = ref.f16_to_f32(h)
+    nan = np.isnan(f)
+    assert np.array_equal(ref.f32_to_f16(f)[~nan], h[~nan])
+    back = ref.f32_to_f16(f[nan])
+    assert np.all((back & 0x7C00) == 0x7C00) and np.all((back & 0x03FF) != 0)
+    # widening is exact: equals IEEE binary16 -> binary32 (numpy's float16)
+    assert np.array_equal(bits(f[~nan]), bits(h.view(np.float16).astype(np.float32)[~nan]))
+
+
+def test_f16_rne_table(oracle_lib):
+    for x, want in GOLD["f32_to_f16_rne"]:
+        x = -np.inf if x == "-inf" else x
+        assert int(ref.f32_to_f16(np.array([x], np.float32))[0]) == want, x
+
+
+def test_f32_to_f16_matches_ieee_on_random_values(oracle_lib):
+    x = np.concatenate([normal(5, 200000, 3.0), normal(6, 20000, 1e-5), normal(7, 20000, 3e4)])
+    assert np.array_equal(ref.f32_to_f16(x), x.astype(np.float16).view(np.uint16))
+
+
+# ---------------------------------------------------------------- q8k ------
+
+def test_round_to_even_ties(oracle_lib):
+    for v, want in GOLD["round_to_even"]:
+        got = ref.lib().ref_round_to_even_f32(v)
+        assert bits(got) == bits(np.float32(want)), (v, got, want)
+    eighths = np.arange(-127 * 8, 127 * 8 + 1) / 8.0
+    got = np.array([ref.lib().ref_round_to_even_f32(float(v)) for v in eighths], np.float32)
+    assert np.array_equal(got, np.rint(eighths).astype(np.float32))
+
+
+def test_q8k_closed_forms_and_degenerate_blocks(oracle_lib):
+    x = np.ones(512, np.float32)
+    x[256:] = -1
+    q8, sc = ref.q8k_quantize(x)
+    assert np.all(q8[:256] == 127) and np.all(q8[256:] == -127)
+    assert np.all(sc == np.float32(1) / np.float32(127))
+    # zeros and all-NaN blocks -> scale 0, quants 0
+    # (quant_q8k_portable_amd64_test.go:161-185)
+    for blk in (np.zeros(256, np.float32), np.full(256, np.nan, np.float32)):
+        q8, sc = ref.q8k_quantize(blk)
+        assert sc[0] == 0 and np.all(q8 == 0)
+
+
+def test_q8k_invariants_on_edge_pattern(oracle_lib):
+    spec = GOLD["q8k_quantize_edges"]
+    i = np.arange(spec["cols"])
+    x = (((i % 53) - 26) / 26).astype(np.float32)
+    for lo, hi in spec["zero_ranges"]:
+        x[lo:hi] = 0
+    x[767] = spec["x767"]
+    q8, sc = ref.q8k_quantize(x)
+    for b in range(4):
+        xb, qb = x[b * 256:(b + 1) * 256], q8[b * 256:(b + 1) * 256].astype(np.int32)
+        amax = np.abs(xb).max()
+        if amax == 0:
+            assert sc[b] == 0 and np.all(qb == 0)
+            continue
+        assert sc[b] == np.float32(amax) / np.float32(127)
+        assert np.abs(qb).max() == 127 and qb[np.argmax(np.abs(xb))] == np.sign(xb[np.argmax(np.abs(xb))]) * 127
+        # each code is the nearest integer to x/scale (ties aside)
+        err = np.abs(qb - xb.astype(np.float64) / float(sc[b]))
+        assert err.max() <= 0.5 + 1e-5
+        assert np.all(np.sign(qb) * np.sign(xb) >= 0)
+    assert q8[767] == -127
+
+
+def test_xsums_exact_on_integer_inputs(oracle_lib):
+    # integer-valued inputs sum exactly in any order, so both restated orders
+    # must equal the exact group sums (pins the element-to-group mapping)
+    x = (np.random.default_rng(3).integers(-1000, 1000, 4096)).astype(np.float32)
+    want32 = x.reshape(-1, 32).sum(1)
+    want16 = x.reshape(-1, 16).sum(1) * 32
+    for order in (ref.GENERIC, ref.AMD64):
+        assert np.array_equal(ref.xsums32(x, order), want32)
+        assert np.array_equal(ref.xsums16(x, order), want16)
+
+
+def test_xsums_orders_close_to_float64(oracle_lib):
+    x = normal(4, 14336)
+    w32 = x.astype(np.float64).reshape(-1, 32).sum(1)
+    for order in (ref.GENERIC, ref.AMD64):
+        assert np.allclose(ref.xsums32(x, order), w32, rtol=1e-5, atol=1e-5)
+    # the two orders differ in rounding on random data (they are not aliases)
+    assert not np.array_equal(ref.xsums32(x, ref.GENERIC), ref.xsums32(x, ref.AMD64))
+
+
+# ------------------------------------------------------- block decoding ----
+
+def q4k_codes(row, blocks):
+    """(d, dmin, sc[8], m[8], codes[256]) per block from the byte layout."""
+    out = []
+    for b in range(blocks):
+        blk = row[b * 144:(b + 1) * 144]
+        d, dmin = np.frombuffer(blk[:4].tobytes(), np.float16).astype(np.float64)
+        s = blk[4:16].astype(np.int64)
+        sc = np.concatenate([s[0:4] & 63, (s[8:12] & 15) | ((s[0:4] >> 6) << 4)])
+        m = np.concatenate([s[4:8] & 63, (s[8:12] >> 4) | ((s[4:8] >> 6) << 4)])
+        q = blk[16:].astype(np.int64).reshape(4, 32)
+        codes = np.stack([q & 15, q >> 4], 1).reshape(256)  # chunk s: low 32 then high 32
+        out.append((d, dmin, sc, m, codes))
+    return out
+
+
+def q6k_codes(row, blocks):
+    out = []
+    for b in range(blocks):
+        blk = row[b * 210:(b + 1) * 210].astype(np.int64)
+        d = float(np.frombuffer(row[b * 210 + 208:b * 210 + 210].tobytes(), np.float16)[0])
+        sc = blk[192:208].astype(np.int8).astype(np.int64)
+        codes = np.zeros(256, np.int64)
+        for h in range(2):
+            ql, qh = blk[64 * h:64 * h + 64], blk[128 + 32 * h:160 + 32 * h]
+            for c in range(4):
+                lo = ql[32 * (c & 1):32 * (c & 1) + 32]
+                lo = (lo & 15) if c < 2 else (lo >> 4)
+                codes[128 * h + 32 * c:128 * h + 32 * c + 32] = lo | (((qh >> (2 * c)) & 3) << 4)
+        out.append((d, sc, codes))
+    return out
+
+
+def brute_lane_ints(qtype, row, q8, blocks):
+    """Integer lane sums by element: lane(e) = (e % 32) // 4, each element
+    weighted by its own sub-block scale."""
+    q8 = q8.astype(np.int64)
+    e = np.arange(256)
+    lane = (e % 32) // 4
+    res = np.zeros((blocks, 8), np.int64)
+    if qtype == ref.Q4_K:
+        for b, (_, _, sc, _, codes) in enumerate(q4k_codes(row, blocks)):
+            prod = sc[e // 32] * codes * q8[b * 256:(b + 1) * 256]
+            res[b] = np.bincount(lane, prod, 8)
+    elif qtype == ref.Q6_K:
+        for b, (_, sc, codes) in enumerate(q6k_codes(row, blocks)):
+            prod = sc[e // 16] * codes * q8[b * 256:(b + 1) * 256]
+            res[b] = np.bincount(lane, prod, 8)
+    else:
+        w = row.reshape(-1, 34)[:, 2:].view(np.int8).astype(np.int64).reshape(blocks, 256)
+        for b in range(blocks):
+            res[b] = np.bincount(lane, w[b] * q8[b * 256:(b + 1) * 256], 8)
+    return res
+
+
+def brute_dot(qtype, row, q8, xsc, xsums, blocks):
+    """float64 evaluation of the row dot, element by element."""
+    q8 = q8.astype(np.float64)
+    e = np.arange(256)
+    total = 0.0
+    if qtype == ref.Q4_K:
+        for b, (d, dmin, sc, m, codes) in enumerate(q4k_codes(row, blocks)):
+            total += d * float(xsc[b]) * float(np.sum(sc[e // 32] * codes * q8[b * 256:(b + 1) * 256]))
+            total -= dmin * float(np.sum(m * xsums[b * 8:(b + 1) * 8].astype(np.float64)))
+    elif qtype == ref.Q6_K:
+        for b, (d, sc, codes) in enumerate(q6k_codes(row, blocks)):
+            total += d * float(xsc[b]) * float(np.sum(sc[e // 16] * codes * q8[b * 256:(b + 1) * 256]))
+            total -= d * float(np.sum(sc * xsums[b * 16:(b + 1) * 16].astype(np.float64)))
+    else:
+        g = row.reshape(-1, 34)
+        d = np.frombuffer(g[:, :2].copy().tobytes(), np.float16).astype(np.float64)
+        w = g[:, 2:].view(np.int8).astype(np.float64)
+        for b in range(blocks):
+            for j in range(8):
+                total += float(xsc[b]) * d[b * 8 + j] * float(np.dot(w[b * 8 + j], q8[b * 256 + j * 32:b * 256 + j * 32 + 32]))
+    return total
+
+
+def lane_pattern_row(qtype, blocks):
+    if qtype == ref.Q4_K:
+        row = np.zeros(blocks * 144, np.uint8)
+        for b in range(blocks):
+            blk = row[b * 144:(b + 1) * 144]
+            blk[0:4] = [0x00, 0x3C, 0x00, 0x30]
+            i = np.arange(4, 16)
+            blk[4:16] = (i * 37 + b * 11) & 0xFF
+            i = np.arange(16, 144)
+            blk[16:144] = (i * 89 + b * 7) & 0xFF
+        return row
+    row = np.zeros(blocks * 210, np.uint8)
+    for b in range(blocks):
+        i = np.arange(208)
+        row[b * 210:b * 210 + 208] = (i * 131 + b * 17) & 0xFF
+        row[b * 210 + 208:b * 210 + 210] = [0x00, 0x3C]
+    return row
+
+
+def acts(qtype, x, order=ref.AMD64):
+    q8, xsc = ref.q8k_quantize(x)
+    xs = ref.xsums32(x, order) if qtype == ref.Q4_K else ref.xsums16(x, order)
+    return q8, xsc, xs
+
+
+# ------------------------------------------------------------ row dots ----
+
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_q4k_extremes_closed_form(oracle_lib, sign):
+    spec = GOLD["q4k_extremes"]
+    cols = spec["cols"]
+    row = np.full(cols // 256 * 144, 0xFF, np.uint8)
+    for b in range(cols // 256):
+        row[b * 144:b * 144 + 4] = [0x00, 0x3C, 0x00, 0x3C]
+    x = np.full(cols, sign, np.float32)
+    q8, xsc, xs = acts(ref.Q4_K, x)
+    for order in (ref.GENERIC, ref.AMD64):
+        got = ref.row_dot(ref.Q4_K, row, q8, xsc, xs, order)
+        assert abs(got - sign * spec["expect"]) <= 1e-6 * spec["expect"]
+    assert np.all(ref.lane_ints(ref.Q4_K, row, q8) == sign * spec["lane_int"])
+
+
+@pytest.mark.parametrize("scbyte", [0x7F, 0x80])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_q6k_extremes_closed_form(oracle_lib, scbyte, sign):
+    spec = GOLD["q6k_extremes"]
+    cols = spec["cols"]
+    row = np.zeros(cols // 256 * 210, np.uint8)
+    for b in range(cols // 256):
+        row[b * 210:b * 210 + 192] = 0xFF
+        row[b * 210 + 192:b * 210 + 208] = scbyte
+        row[b * 210 + 208:b * 210 + 210] = [0x00, 0x3C]
+    want = sign * spec["expect_per_scale"]["127" if scbyte == 0x7F else "-128"]
+    x = np.full(cols, sign, np.float32)
+    q8, xsc, xs = acts(ref.Q6_K, x)
+    for order in (ref.GENERIC, ref.AMD64):
+        got = ref.row_dot(ref.Q6_K, row, q8, xsc, xs, order)
+        assert abs(got - want) <= 1e-6 * abs(want), (order, got, want)
+
+
+@pytest.mark.parametrize("wv", [127, -127])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_q8_0_extremes_closed_form(oracle_lib, wv, sign):
+    spec = GOLD["q8_0_extremes"]
+    cols = spec["cols"]
+    row = np.zeros(cols // 32 * 34, np.uint8).reshape(-1, 34)
+    row[:, 0:2] = [0x00, 0x3C]
+    row[:, 2:] = np.uint8(wv & 0xFF)
+    row = row.reshape(-1)
+    x = np.full(cols, sign, np.float32)
+    q8, xsc = ref.q8k_quantize(x)
+    want = np.sign(wv) * sign * spec["expect"]
+    for order in (ref.GENERIC, ref.AMD64):
+        got = ref.row_dot(ref.Q8_0, row, q8, xsc, None, order)
+        assert abs(got - want) <= 1e-6 * abs(want)
+
+
+@pytest.mark.parametrize("qtype", [ref.Q4_K, ref.Q6_K])
+def test_lane_order_patterns(oracle_lib, qtype):
+    # q4k_q8_amd64_audit_test.go:93-152: unique per-element bytes / activations
+    cols = 512
+    row = lane_pattern_row(qtype, cols // 256)
+    i = np.arange(cols)
+    x = ((((i % 97) - 48) / 48) if qtype == ref.Q4_K else (((i % 89) - 44) / 44)).astype(np.float32)
+    q8, xsc, xs = acts(qtype, x)
+    ints = ref.lane_ints(qtype, row, q8)
+    assert np.array_equal(ints, brute_lane_ints(qtype, row, q8, cols // 256))
+    want = brute_dot(qtype, row, q8, xsc, xs, cols // 256)
+    for order in (ref.GENERIC, ref.AMD64):
+        q8o, xsco, xso = acts(qtype, x, order)
+        got = ref.row_dot(qtype, row, q8o, xsco, xso, order)
+        assert abs(got - want) <= 1e-5 * (1 + abs(want)), (order, got, want)
+
+
+@pytest.mark.parametrize("qtype", [ref.Q4_K, ref.Q6_K, ref.Q8_0])
+@pytest.mark.parametrize("cols", [256, 1024, 4096])
+def test_row_dots_on_random_rows(oracle_lib, qtype, cols):
+    data, _ = quant_matrix(qtype, 8, cols, 100 + cols + qtype)
+    rb = ref.row_bytes(qtype, cols)
+    x = normal(200 + cols, cols)
+    x[256:512] = 0  # zero block (the reference suites do the same)
+    for r in range(8):
+        row = data[r * rb:(r + 1) * rb]
+        q8, xsc, xs = acts(qtype, x)
+        assert np.array_equal(ref.lane_ints(qtype, row, q8), brute_lane_ints(qtype, row, q8, cols // 256))
+        want = brute_dot(qtype, row, q8, xsc, xs, cols // 256)
+        ga = ref.row_dot(qtype, row, q8, xsc, xs, ref.AMD64)
+        q8g, xscg, xsg = acts(qtype, x, ref.GENERIC)
+        gg = ref.row_dot(qtype, row, q8g, xscg, xsg, ref.GENERIC)
+        assert abs(ga - want) <= 1e-5 * (1 + abs(want))
+        assert abs(gg - want) <= 1e-5 * (1 + abs(want))
+        # the reference's house rule between its two implementations
+        assert abs(ga - gg) <= 1e-3 * (1 + abs(gg))
+        if ref.lib().ref_has_avx2():
+            assert bits(ref.row_dot_avx2(qtype, row, q8, xsc, xs)) == bits(ga)
+
+
+@pytest.mark.parametrize("qtype", [ref.Q4_K, ref.Q6_K, ref.Q8_0])
+def test_int8_path_close_to_float_path(oracle_lib, qtype):
+    # q4k_q8_amd64_test.go:217-246 requireCosine >= 0.999
+    rows, cols = 96, 1024
+    data, _ = quant_matrix(qtype, rows, cols, 7 + qtype)
+    x = normal(8, cols)
+    got = ref.matvec(qtype, data, x, rows, cols)
+    want = ref.dequant(qtype, data, rows, cols).astype(np.float64) @ x.astype(np.float64)
+    cos = np.dot(got, want) / (np.linalg.norm(got) * np.linalg.norm(want))
+    assert cos >= 0.999
+
+
+def test_matvec_batch_equals_per_token_and_fast_port(oracle_lib):
+    rows, cols = 64, 1024
+    for qtype in (ref.Q4_K, ref.Q6_K, ref.Q8_0):
+        data, _ = quant_matrix(qtype, rows, cols, 30 + qtype)
+        xs = normal(31, (5, cols))
+        batch = ref.matvec_batch(qtype, data, xs, rows, cols)
+        for t in range(5):
+            assert np.array_equal(bits(batch[t]), bits(ref.matvec(qtype, data, xs[t], rows, cols)))
+        fast = ref.matvec_batch_fast(qtype, data, xs, rows, cols)
+        if fast is not None:
+            assert np.array_equal(bits(fast), bits(batch))
+
+
+def test_argmax_rules(oracle_lib):
+    rows, cols = 200, 512
+    data, _ = quant_matrix(ref.Q6_K, rows, cols, 40)
+    x = normal(41, cols)
+    logits = ref.matvec(ref.Q6_K, data, x, rows, cols)
+    assert ref.argmax_matvec(ref.Q6_K, data, x, rows, cols) == int(np.argmax(logits))
+    # zero-scale rows: every logit 0 -> lowest index (simd_test.go:520-535)
+    zero = np.zeros_like(data)
+    assert ref.argmax_matvec(ref.Q6_K, zero, x, rows, cols) == 0
+    # non-finite logits are skipped; ties keep the lowest index
+    lg = np.array([np.nan, 1.0, np.inf, 3.0, 3.0, -np.inf], np.float32)
+    assert ref.argmax_finite(lg) == 3
+    assert ref.argmax_finite(np.array([np.nan, np.inf], np.float32)) == 0
+
+
+# ------------------------------------------------------------ encoders ----
+
+def test_q4k_dequant_known(oracle_lib):
+    spec = GOLD["q4k_dequant_known"]
+    row = np.zeros(144, np.uint8)
+    row[0:4] = spec["header"]
+    row[4:16] = spec["scales"]
+    row[16:] = spec["qbyte"]
+    got = ref.dequant_row(ref.Q4_K, row, 256)
+    for i in range(0, 256, 64):
+        assert np.all(got[i:i + 32] == spec["expect_low"])
+        assert np.all(got[i + 32:i + 64] == spec["expect_high"])
+
+
+def test_rtn_known_values(oracle_lib):
+    # quantize_rtn_test.go:99-113
+    x = (np.arange(32) - 16).astype(np.float32)
+    deq = ref.dequant_row(ref.Q8_0, ref.quantize_rows(ref.Q8_0, x[None]), 32)
+    assert np.abs(deq - x).max() <= 0.08
+    # quantize_rtn_test.go:153-181, 250-262
+    half = np.full((1, 256), 0.5, np.float32)
+    deq = ref.dequant_row(ref.Q4_K, ref.quantize_rows(ref.Q4_K, half), 256)
+    assert not np.isnan(deq).any() and np.abs(deq - 0.5).max() <= 0.05
+    zero = np.zeros((1, 256), np.float32)
+    for qt in (ref.Q4_K, ref.Q6_K):
+        assert np.all(ref.dequant_row(qt, ref.quantize_rows(qt, zero), 256) == 0)
+
+
+@pytest.mark.parametrize("qtype,bound", [(ref.Q4_K, 0.35), (ref.Q6_K, 0.07), (ref.Q8_0, 0.02)])
+def test_rtn_roundtrip_error_bounds(oracle_lib, qtype, bound):
+    # quantize_rtn_test.go round-trip tests: error within a fraction of the
+    # value scale, dequant finite
+    for trial in range(10):
+        s = 1.0 + trial * 0.3
+        x = normal(500 + trial, (4, 256), s)
+        deq = ref.dequant(qtype, ref.quantize_rows(qtype, x), 4, 256)
+        assert np.isfinite(deq).all()
+        assert np.abs(deq - x).max() <= bound * s * 1.2
+
+
+def test_q4k_scale_packing_roundtrip(oracle_lib):
+    # packScaleMinK4All inverse of getScaleMinK4 (quantize_rtn_test.go): a
+    # block whose sub-blocks span distinct ranges decodes its own ranges back
+    rng = np.random.default_rng(9)
+    for _ in range(20):
+        x = np.concatenate([rng.uniform(-lo, hi, 32) for lo, hi in rng.uniform(0.1, 4, (8, 2))])
+        x = x.astype(np.float32)[None]
+        deq = ref.dequant_row(ref.Q4_K, ref.quantize_rows(ref.Q4_K, x), 256)
+        for j in range(8):
+            sub, dj = x[0, 32 * j:32 * j + 32], deq[32 * j:32 * j + 32]
+            assert abs(dj.min() - sub.min()) < 0.15 * (sub.max() - sub.min()) + 0.1
+            assert abs(dj.max() - sub.max()) < 0.15 * (sub.max() - sub.min()) + 0.1
+
+
+# -------------------------------------------------------------- helpers ----
+
+def test_fast_exp_against_libm(oracle_lib):
+    for name, scores in GOLD["attention_scores"].items():
+        s = np.array(scores, np.float32)
+        m = s.max()
+        got = np.array([ref.fast_exp(float(np.float32(v - m))) for v in s], np.float64)
+        want = np.exp((s - m).astype(np.float64))
+        assert np.abs(got - want).max() <= 2e-6, name
+        assert abs(got.sum() - want.sum()) <= 2e-5 * max(1.0, want.sum())
+    xs = np.linspace(-87, 88, 20001, dtype=np.float32)
+    got = np.array([ref.fast_exp(float(v)) for v in xs])
+    assert np.max(np.abs(got / np.exp(xs.astype(np.float64)) - 1)) < 4e-7
+    assert ref.fast_exp(89.0) == math.inf and ref.fast_exp(-88.0) == 0.0
+
+
+def test_silu_mul_against_float64_and_boundaries(oracle_lib):
+    # q4k_q8_amd64_audit_test.go:156-186 sweep + specials
+    g = np.concatenate([np.arange(-90, 90, 0.003), [87.68, -87.68, 88.376, -88.376, 88.3763,
+                        -88.3763, 127.5, -127.5, 1e-40, -1e-40, 0]]).astype(np.float32)
+    up = np.ones_like(g)
+    got = ref.silu_mul(g, up).astype(np.float64)
+    gd = g.astype(np.float64)
+    want = gd / (1 + np.exp(-gd))
+    assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want)))
+    big = ref.silu_mul(np.array([-3.4028235e38, 3.4028235e38], np.float32), np.ones(2, np.float32))
+    assert big[0] == 0 and big[1] == np.float32(3.4028235e38)
+    # the up factor multiplies last
+    u = normal(3, g.size)
+    assert np.array_equal(ref.silu_mul(g, u), (ref.silu_mul(g, up) * u).astype(np.float32))
+
+
+def test_rmsnorm_and_dot_against_float64(oracle_lib):
+    for n in (4096, 14336, 100, 37):
+        x = normal(n, n)
+        w = normal(n + 1, n)
+        d = ref.dot_f32(x, w)
+        assert abs(d - float(np.dot(x.astype(np.float64), w.astype(np.float64)))) <= 1e-5 * np.sqrt(n)
+        got = ref.rmsnorm(x, w, 1e-5).astype(np.float64)
+        xd = x.astype(np.float64)
+        want = xd * w / np.sqrt(np.mean(xd * xd) + 1e-5)
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+def test_rope_against_complex_rotation(oracle_lib):
+    hd = 128
+    inv = ref.rope_inv_freq(500000.0, hd)
+    assert inv[0] == 1.0  # model_rope_test.go:51-58
+    assert np.allclose(inv, 500000.0 ** (-np.arange(0, hd, 2) / hd), rtol=1e-6)
+    for pos in (0, 1, 513, 4095):
+        s, c = ref.rope_sincos(pos, inv)
+        v = normal(pos, 4 * hd)
+        got = ref.rope_apply(v, hd, 4, s, c).astype(np.float64)
+        z = (v[0::2] + 1j * v[1::2]).astype(np.complex128)
+        # the reference rounds the angle to float32 before sin/cos
+        # (model.go:3044: float64(float32(pos) * invFreq[i]))
+        ang = np.tile((np.float32(pos) * inv).astype(np.float64), 4)
+        zr = z * np.exp(1j * ang)
+        want = np.empty(4 * hd)
+        want[0::2], want[1::2] = zr.real, zr.imag
+        assert np.allclose(got, want, rtol=1e-5, atol=2e-5)
+
+
+def test_attention_two_pass_matches_textbook(oracle_lib):
+    # kv_f16_test.go:143-213 naiveAttentionRef, tolerance 1e-5
+    hd, ctx, qh = 128, 300, 4
+    q = normal(1, qh * hd)
+    kv = normal(2, (2, ctx, hd))
+    k16, v16 = ref.f32_to_f16(kv[0]), ref.f32_to_f16(kv[1])
+    scale = np.float32(1 / np.sqrt(hd))
+    for start, end in ((0, ctx - 1), (17, 200), (5, 5)):
+        got = ref.attend_group_f16(q, k16, v16, qh, hd, hd, hd, hd, start, end, scale)
+        K = ref.f16_to_f32(k16).astype(np.float64)[start:end + 1]
+        V = ref.f16_to_f32(v16).astype(np.float64)[start:end + 1]
+        for h in range(qh):
+            s = K @ q[h * hd:(h + 1) * hd].astype(np.float64) * float(scale)
+            w = np.exp(s - s.max())
+            want = (w / w.sum()) @ V
+            assert np.allclose(got[h * hd:(h + 1) * hd], want, rtol=1e-5, atol=1e-6)
+
+
+def test_tiny_llama_greedy_is_deterministic(oracle_lib):
+    m = tiny_llama(seed=2)
+    prompt = np.random.default_rng(3).integers(0, m["config"]["vocab"], 9)
+    a = ref.Llama(m, max_len=32)
+    b = ref.Llama(m, max_len=32)
+    ta, tb = a.generate(prompt, 6), b.generate(prompt, 6)
+    assert np.array_equal(ta, tb)
+    # the first token is argmax of the prefill logits
+    c = ref.Llama(m, max_len=32)
+    tok, logits = c.prefill(prompt)
+    assert tok == ta[0] == int(np.argmax(logits))
+    # decode after prefill continues from the same cache
+    nxt, hid = c.decode(tok, len(prompt))
+    assert nxt == ta[1] and np.isfinite(hid).all()
