@@ -1,0 +1,275 @@
+#!/usr/bin/env python3
+"""Headline benchmark: Q4_K x Q8_K GEMV on one MI355X.
+
+Workload (gate/up shape): W is 14336 x 4096 drawn
+N(0, 0.02) on the device and encoded to Q4_K by the device RTN encoder
+(QuantizeRowQ4K); x is N(0, 1).  One step is one MatvecQ4KInto (simd.go:261):
+Q8K quantisation of x plus the row kernels over all 14336 rows.  Weight
+copies rotate so the working set (>= 300 MB) exceeds the 256 MB Infinity
+Cache, i.e. every step streams its weights from HBM.  Steps are replayed from
+a HIP graph (captured through torch.cuda.CUDAGraph on the launch stream) so
+host launch overhead is not measured.
+
+value      = algorithmic bytes per step / time per step, bytes =
+             rows*(cols/256)*144 + 4*cols + 4*rows (whole MatvecQ4KInto)
+roofline   = the same bytes / the row kernel's own average duration (HIP
+             events around graph replays of the row kernel alone), against
+             the 8 TB/s HBM3E peak; traffic from profiles/ (rocprofv3 PMC)
+cpu_baseline = the oracle's AVX2 port of kernels_amd64.s (bit-identical
+             results) on this host's cores, same bytes formula, rotating the
+             same weight copies.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q4_K×Q8_K GEMV GB/s (% HBM peak); decode tok/s on 8B-shape Q4_K synth"
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+ROWS, COLS = 14336, 4096
+PMC_FILE = os.path.join(ROOT, "profiles", "gemv_q4k_14336x4096_pmc.json")
+
+
+def alg_bytes(rows, cols, p=1):
+    return rows * (cols // 256) * 144 + p * (4 * cols + 4 * rows)
+
+
+def make_weights(g, torch, rows, cols, copies, seed):
+    """copies of a Q4_K matrix, generated and encoded on the device."""
+    tmp = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    raw = torch.empty(rows * (cols // 256) * 144, dtype=torch.uint8, device="cuda")
+    ws = []
+    for c in range(copies):
+        g.fill_normal_dev(tmp, seed + c, 0.02)
+        g.quantize_rows_dev(g.TYPE_Q4_K, tmp, raw)
+        ws.append(g.Weight.from_device(raw, g.TYPE_Q4_K, rows, cols))
+    torch.cuda.synchronize()
+    del tmp, raw
+    return ws
+
+
+def timed_graph(torch, body, reps):
+    """Capture body() once, replay it `reps` times between events; returns
+    (ms per replay)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()  # eager warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body()
+    graph.replay()
+    torch.cuda.synchronize()
+    return graph
+
+
+def run(args):
+    import numpy as np
+    import torch
+
+    import gopherllm_amd as g
+
+    g.load()
+    if not torch.cuda.is_available() or not g.available():
+        raise SystemExit("bench.py needs an MI355X (gfx950) device: " + g._lib.last_error())
+    rows, cols = ROWS, COLS
+    wbytes = rows * (cols // 256) * 144
+    copies = args.copies or max(2, math.ceil(300e6 / wbytes))
+    weights = make_weights(g, torch, rows, cols, copies, seed=1000)
+    x = torch.empty(cols, dtype=torch.float32, device="cuda")
+    g.fill_normal_dev(x, 7, 1.0)
+    act = torch.empty(g.act_bytes(cols, 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+
+    # correctness guard: the benchmarked launch sequence equals the blocking
+    # host entry point on the same inputs
+    xh = x.cpu().numpy()
+    want = weights[0].matvec_into(xh)
+    g.q8k_prepare_dev(x, act)
+    weights[0].matvec_q8_dev(act, 1, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+    def full_steps():  # `copies` whole MatvecQ4KInto steps
+        for w in weights:
+            g.q8k_prepare_dev(x, act)
+            w.matvec_q8_dev(act, 1, out)
+
+    def kernel_only():  # the row kernel alone, activations already quantised
+        for w in weights:
+            w.matvec_q8_dev(act, 1, out)
+
+    g.q8k_prepare_dev(x, act)
+    full = timed_graph(torch, full_steps, 1)
+    kern = timed_graph(torch, kernel_only, 1)
+
+    reps = max(1, math.ceil(args.steps / copies))
+    wreps = max(1, math.ceil(args.warmup / copies)) if args.warmup > 0 else 0
+    steps = reps * copies
+    for _ in range(wreps):
+        full.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        full.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / steps
+
+    for _ in range(wreps):
+        kern.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        kern.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    kernel_us = e0.elapsed_time(e1) / steps * 1e3
+
+    # replayed graphs still produce the eager result
+    full.replay()
+    torch.cuda.synchronize()
+    last = weights[-1].matvec_into(xh)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), last.view(np.uint32))
+
+    nbytes = alg_bytes(rows, cols)
+    value = nbytes / (ms_per_step * 1e-3) / 1e9
+    achieved = nbytes / (kernel_us * 1e-6) / 1e9
+    traffic = None
+    if os.path.exists(PMC_FILE):
+        pmc = json.load(open(PMC_FILE))
+        traffic = pmc.get("traffic_bytes_per_launch")
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": wreps * copies,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: W ~ N(0,0.02) encoded Q4_K on device (QuantizeRowQ4K), x ~ N(0,1)",
+        "config": {
+            "workload": "Q4_K x Q8_K GEMV 14336x4096 batch 1 (configs[1] gate/up; one step = "
+                        "MatvecQ4KInto: Q8K quantise + row kernels)",
+            "rows": rows, "cols": cols, "weight_copies": copies,
+            "rotating_bytes": copies * wbytes, "hip_graph": True,
+            "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "gemv_q4k_kernel<1>",
+            "kernel_avg_us": round(kernel_us, 3),
+            "bytes_per_launch": nbytes,
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(weights, xh, rows, cols, args.cpu_seconds, torch)
+    return line
+
+
+def cpu_baseline(weights, xh, rows, cols, seconds, torch):
+    """The oracle's AVX2 port of kernels_amd64.s on this host, all cores, over
+    the same rotating weight copies (downloaded from the device)."""
+    import numpy as np
+
+    from oracle import oracle as ref
+
+    host = []
+    for w in weights:
+        buf = torch.empty(rows * (cols // 256) * 144, dtype=torch.uint8, device="cuda")
+        w.download_dev(buf)
+        torch.cuda.synchronize()
+        host.append(buf.cpu().numpy())
+    cores = len(os.sched_getaffinity(0))
+    kind = "port"
+    fast = ref.matvec_batch_fast(ref.Q4_K, host[0], xh, rows, cols, threads=cores)
+    if fast is None:
+        raise SystemExit("host lacks AVX2/FMA/F16C for the CPU baseline")
+    n, t0 = 0, time.perf_counter()
+    while True:
+        ref.matvec_batch_fast(ref.Q4_K, host[n % len(host)], xh, rows, cols, threads=cores)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 2000:
+            break
+    gbs = alg_bytes(rows, cols) * n / el / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": cores, "kind": kind,
+            "sample": f"{n} MatvecQ4KInto calls (14336x4096 Q4_K, AVX2 port of kernels_amd64.s, "
+                      f"{len(host)} rotating weight copies) in {el:.1f} s"}
+
+
+def profile_run():
+    """Eager launches for rocprofv3 counter passes (no graphs, no timing):
+    20 row-kernel launches over the rotating copies, then 5 plain device
+    copies of 512 MiB that calibrate FETCH_SIZE / WRITE_SIZE against a known
+    byte count."""
+    import torch
+
+    import gopherllm_amd as g
+
+    g.load()
+    rows, cols = ROWS, COLS
+    wbytes = rows * (cols // 256) * 144
+    copies = max(2, math.ceil(300e6 / wbytes))
+    weights = make_weights(g, torch, rows, cols, copies, seed=1000)
+    x = torch.empty(cols, dtype=torch.float32, device="cuda")
+    g.fill_normal_dev(x, 7, 1.0)
+    act = torch.empty(g.act_bytes(cols, 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    g.q8k_prepare_dev(x, act)
+    for i in range(20):
+        weights[i % copies].matvec_q8_dev(act, 1, out)
+    torch.cuda.synchronize()
+    src = torch.ones(512 << 18, dtype=torch.float32, device="cuda")  # 512 MiB
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_run": "done", "gemv_launches": 20, "copy_bytes": src.numel() * 4}),
+          flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--profile-run", action="store_true",
+                    help="eager launches for rocprofv3 counter collection")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: >= 300 MB)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.profile_run:
+        profile_run()
+        return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the path would shard by output rows, see DESIGN.md)", file=sys.stderr)
+        raise SystemExit(2)
+    line = run(args)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

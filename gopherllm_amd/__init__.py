@@ -7,7 +7,7 @@ libgllm_hip.so.
 """
 from ._lib import (TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, ATTN_EXACT, ATTN_SPLITK, GllmError,  # noqa: F401
                    lib_path, load)
-from .api import (KVCacheF16, Weight, available, fill_normal_dev, matvec2_into,  # noqa: F401
+from .api import (KVCacheF16, Weight, act_bytes, available, q8k_prepare_dev, fill_normal_dev, matvec2_into,  # noqa: F401
                   matvec3_into, matvec_multi_dev, matvec_q4k_into, matvec_q6k_into,
                   matvec_q8_0_into, q8k_quantize_dev, quantize_rows_dev, row_bytes)
 

@@ -52,6 +52,9 @@ SIGNATURES = {
     "gllm_hip_matvec_dev": (i32, [vp, vp, i32, vp, i32, vp]),
     "gllm_hip_matvec_multi_dev": (i32, [i32, vp, vp, i32, vp, vp, vp]),
     "gllm_hip_argmax_dev": (i32, [vp, vp, vp, vp]),
+    "gllm_hip_act_bytes": (sz, [i32, i32]),
+    "gllm_hip_q8k_prepare_dev": (i32, [vp, i32, i32, vp, vp]),
+    "gllm_hip_matvec_q8_dev": (i32, [vp, vp, i32, vp, i32, vp]),
     "gllm_hip_q8k_quantize_dev": (i32, [vp, i32, i32, vp, vp, vp]),
     "gllm_hip_lane_ints_dev": (i32, [vp, vp, vp, vp]),
     "gllm_hip_quantize_rows_dev": (i32, [i32, vp, i32, i32, vp, vp]),

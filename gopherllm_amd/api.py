@@ -116,6 +116,12 @@ class Weight:
              _stream(stream))
         return out
 
+    def matvec_q8_dev(self, act, p, out, stream=None):
+        """Row kernels only, against activations quantised by q8k_prepare_dev."""
+        call("gllm_hip_matvec_q8_dev", self.handle, _dev_ptr(act), p, _dev_ptr(out),
+             out.shape[-1], _stream(stream))
+        return out
+
     def argmax_dev(self, x, token_out, stream=None):
         call("gllm_hip_argmax_dev", self.handle, _dev_ptr(x), _dev_ptr(token_out), _stream(stream))
         return token_out
@@ -171,6 +177,18 @@ def matvec3_into(a: Weight, b: Weight, c: Weight, x):
     call("gllm_hip_matvec3", a.handle, b.handle, c.handle, _np_ptr(x), _np_ptr(oa),
          _np_ptr(ob), _np_ptr(oc))
     return oa, ob, oc
+
+
+def act_bytes(cols: int, p: int = 1) -> int:
+    """Bytes of the quantised-activation buffer for p rows of cols."""
+    return int(load().gllm_hip_act_bytes(cols, p))
+
+
+def q8k_prepare_dev(xs, act, stream=None):
+    """acquireQ8 + xsums for p rows of xs into the device buffer `act`."""
+    p = xs.shape[0] if xs.dim() == 2 else 1
+    call("gllm_hip_q8k_prepare_dev", _dev_ptr(xs), xs.shape[-1], p, _dev_ptr(act), _stream(stream))
+    return act
 
 
 def q8k_quantize_dev(x, q8_out, scales_out, stream=None):

@@ -82,7 +82,8 @@ __global__ __launch_bounds__(256) void embed_q4k_kernel(const uint8_t* __restric
         const float d = f16_bits_to_f32(blk[0] | (blk[1] << 8));
         const float dmin = f16_bits_to_f32(blk[2] | (blk[3] << 8));
         const int chunk = i >> 6, l = i & 31, hi = (i >> 5) & 1;
-        const uint8_t qb = blk[16 + chunk * 32 + l];
+        // the upload repack moved nibble byte 32*chunk + l to 16*(l/4) + 4*chunk + l%4
+        const uint8_t qb = blk[16 + (l >> 2) * 16 + chunk * 4 + (l & 3)];
         const int qv = hi ? (qb >> 4) : (qb & 0x0f);
         const float d1 = d * (float)s;
         const float min1 = dmin * (float)m;

@@ -54,68 +54,316 @@ __device__ __forceinline__ int locate(const GemvJob& j, int wg, int* wi) {
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K: 144-byte blocks [d f16][dmin f16][12 B 6-bit scales/mins][128 B nibbles]
-// (simd.go:1530-1557).  AVX2 lane k covers bytes 4k..4k+3 of each of the four
-// 32-byte nibble chunks (Q4KQ8CHUNK, kernels_amd64.s:443-455).
+// Q4_K: 144-byte blocks [d f16][dmin f16][12 B 6-bit scales/mins][128 B
+// nibbles] (simd.go:1530-1557).  AVX2 lane k covers bytes 4k..4k+3 of each of
+// the four 32-byte nibble chunks (Q4KQ8CHUNK, kernels_amd64.s:443-455).  The
+// upload repack stores those 16 bytes contiguously (nibble byte 32s + 4k + j
+// moves to 16k + 4s + j; header and block size unchanged), so a lane reads
+// its share of a block with one 16-byte load.
+//
+// G lanes share one AVX2 lane k of one row: lane g takes blocks g, g+G, ...
+// and every round of G blocks advances the sequential fp32 chains through
+// the G lanes with a quad-permute rotation (lane g adds its block to the
+// value lane g-1 produced a step earlier), so the chains see the blocks in
+// exactly the reference's order.
 // ---------------------------------------------------------------------------
+
+// rotate a value one lane up inside groups of G lanes (lane g receives g-1)
+template <int G>
+__device__ __forceinline__ float rot_prev(float v) {
+    if constexpr (G == 1) {
+        return v;
+    } else if constexpr (G == 2) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    } else {
+        static_assert(G == 4, "G must be 1, 2 or 4");
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x93, 0xF, 0xF, false));
+    }
+}
+
+// 8-lane tree across k when the k lanes of a row sit G lanes apart.
+template <int G>
+__device__ __forceinline__ float tree8_strided(float v) {
+    v = v + __shfl_xor(v, 4 * G, 8 * G);
+    v = v + __shfl_xor(v, 1 * G, 8 * G);
+    v = v + __shfl_xor(v, 2 * G, 8 * G);
+    return v;
+}
+
+__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Activation staging through registers: stage_load issues plain loads of
+// this launch's tokens (q8, xs32, xscale) before the weight prefetch, and
+// stage_store writes them to LDS afterwards.  Plain loads retire in issue
+// order, so the compiler's own vmcnt waits for the staging registers leave
+// the weight loads in flight.  Layout: [NT*cols q8][NT*cols/32 xs32][NT*B
+// xscale].  SQ = 16-byte q8 chunks per thread (the launcher checks capacity).
 template <int NT>
-__global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJob j) {
-    int wi;
-    const int r = locate(j, blockIdx.x, &wi) + (threadIdx.x >> 3);
-    const int k = threadIdx.x & 7;
-    if (r >= j.rows[wi]) return;
-    const uint8_t* row = j.w[wi] + (size_t)r * j.rb;
-    const int B = j.blocks;
-    float accF[NT], accM[NT];
+struct Stage {
+    static constexpr int SQ = NT == 1 ? 4 : 8;
+    uint4 q[SQ];
+    uint4 x;
+    float s;
+};
+
+template <int NT>
+__device__ __forceinline__ void stage_load(const GemvJob& j, Stage<NT>& st) {
+    const int tid = threadIdx.x;
+    const int cols = j.cols, B = j.blocks, nt = j.ntok;
+    const uint4* gq = (const uint4*)(j.act.q8perm + (size_t)j.tok0 * cols);
+    // unconditional loads with clamped indices (straight-line code, so they
+    // stay ahead of the weight prefetch); stage_store writes only the valid ones
+    const int qn = nt * cols / 16;
 #pragma unroll
-    for (int t = 0; t < NT; t++) accF[t] = accM[t] = 0.0f;
-    const int8_t* q8 = j.act.q8perm + (size_t)j.tok0 * j.cols + k * 32;
-    const float* xsc = j.act.xscale + (size_t)j.tok0 * B;
-    const float* xs32 = j.act.xs32 + (size_t)j.tok0 * (j.cols / 32) + k;
-#pragma unroll 2
-    for (int b = 0; b < B; b++) {
-        const uint8_t* blk = row + (size_t)b * 144;
-        const uint4 h = *(const uint4*)blk;
-        const uint32_t w0 = *(const uint32_t*)(blk + 16 + 4 * k);
-        const uint32_t w1 = *(const uint32_t*)(blk + 48 + 4 * k);
-        const uint32_t w2 = *(const uint32_t*)(blk + 80 + 4 * k);
-        const uint32_t w3 = *(const uint32_t*)(blk + 112 + 4 * k);
-        const float d = f16_bits_to_f32(h.x & 0xffffu);
-        const float dmin = f16_bits_to_f32(h.x >> 16);
-        // getScaleMinK4 for all eight sub-blocks (simd.go:1672-1677)
-        const uint32_t sc03 = h.y & 0x3f3f3f3fu;
-        const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
-        const uint32_t m03 = h.z & 0x3f3f3f3fu;
-        const uint32_t m47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
-        const int mk = ubyte(k < 4 ? m03 : m47, k & 3);
-        const int l0 = (int)(w0 & 0x0f0f0f0fu), h0 = (int)((w0 >> 4) & 0x0f0f0f0fu);
-        const int l1 = (int)(w1 & 0x0f0f0f0fu), h1 = (int)((w1 >> 4) & 0x0f0f0f0fu);
-        const int l2 = (int)(w2 & 0x0f0f0f0fu), h2 = (int)((w2 >> 4) & 0x0f0f0f0fu);
-        const int l3 = (int)(w3 & 0x0f0f0f0fu), h3 = (int)((w3 >> 4) & 0x0f0f0f0fu);
+    for (int i = 0; i < Stage<NT>::SQ; i++) st.q[i] = gq[min(tid + 256 * i, qn - 1)];
+    const uint4* gx = (const uint4*)(j.act.xs32 + (size_t)j.tok0 * (cols / 32));
+    st.x = gx[min(tid, nt * cols / 128 - 1)];
+    st.s = j.act.xscale[(size_t)j.tok0 * B + min(tid, nt * B - 1)];
+}
+
+template <int NT>
+__device__ __forceinline__ void stage_store(const GemvJob& j, const Stage<NT>& st, uint8_t* smem) {
+    const int tid = threadIdx.x;
+    const int cols = j.cols, nt = j.ntok;
+    const int qn = nt * cols / 16;
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            if (t < j.ntok) {
-                const int4 qa = *(const int4*)(q8 + (size_t)t * j.cols + b * 256);
-                const int4 qb = *(const int4*)(q8 + (size_t)t * j.cols + b * 256 + 16);
-                int acc = ubyte(sc03, 0) * sdot4(l0, qa.x, 0);
-                acc += ubyte(sc03, 1) * sdot4(h0, qa.y, 0);
-                acc += ubyte(sc03, 2) * sdot4(l1, qa.z, 0);
-                acc += ubyte(sc03, 3) * sdot4(h1, qa.w, 0);
-                acc += ubyte(sc47, 0) * sdot4(l2, qb.x, 0);
-                acc += ubyte(sc47, 1) * sdot4(h2, qb.y, 0);
-                acc += ubyte(sc47, 2) * sdot4(l3, qb.z, 0);
-                acc += ubyte(sc47, 3) * sdot4(h3, qb.w, 0);
-                const float dxs = d * xsc[(size_t)t * B + b];                 // VMULSS
-                accF[t] = fmaf((float)acc, dxs, accF[t]);                       // VFMADD231PS
-                const float mx = (float)mk * xs32[(size_t)t * (j.cols / 32) + b * 8];  // VMULPS
-                accM[t] = fmaf(dmin, mx, accM[t]);                              // VFMADD231PS
+    for (int i = 0; i < Stage<NT>::SQ; i++)
+        if (tid + 256 * i < qn) ((uint4*)smem)[tid + 256 * i] = st.q[i];
+    uint8_t* sx = smem + (size_t)NT * cols;
+    if (tid < nt * cols / 128) ((uint4*)sx)[tid] = st.x;
+    float* ss = (float*)(sx + (size_t)NT * (cols / 8));
+    if (tid < nt * j.blocks) ss[tid] = st.s;
+}
+
+template <int NT>
+__device__ __forceinline__ bool stage_fits(int cols, int blocks) {
+    return NT * cols / 16 <= 256 * Stage<NT>::SQ && NT * cols / 128 <= 256 && NT * blocks <= 256;
+}
+
+// Direct global->LDS copies issued from inline assembly.  The compiler does
+// not see them as outstanding vector-memory operations, which is the point:
+// they are issued before the weight prefetch and retire first (in order), so
+// its vmcnt waits for the weight registers stay exact, and the kernel waits
+// for the copies itself (vmcnt <= number of weight loads) before s_barrier.
+// M0 holds the wave's LDS destination; lane i writes M0 + 16*i (4*i).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+__device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds_dst) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gsrc), "s"(lds_dst)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void lds_copy4(const void* gsrc, uint32_t lds_dst) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+                 :
+                 : "v"(gsrc), "s"(lds_dst)
+                 : "memory", "m0");
+}
+
+// Stage this launch's activations (q8, xs32, xscale of ntok tokens) into LDS
+// with lds_copy16 / lds_copy4.  Layout: [NT*cols q8][NT*cols/32 xs32][NT*B
+// xscale].  Every byte range is a multiple of the copy width.
+template <int NT>
+__device__ __forceinline__ void stage_act_asm(const GemvJob& j, uint8_t* smem) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int cols = j.cols, B = j.blocks, nt = j.ntok;
+    const uint8_t* gq = (const uint8_t*)(j.act.q8perm + (size_t)j.tok0 * cols);
+    const int qbytes = nt * cols;
+    for (int base = wave * 1024; base < qbytes; base += 4096)
+        if (base + lane * 16 < qbytes) lds_copy16(gq + base + lane * 16, lds_addr(smem + base));
+    const uint8_t* gx = (const uint8_t*)(j.act.xs32 + (size_t)j.tok0 * (cols / 32));
+    uint8_t* sx = smem + (size_t)NT * cols;
+    const int xbytes = nt * (cols / 8);
+    for (int base = wave * 1024; base < xbytes; base += 4096)
+        if (base + lane * 16 < xbytes) lds_copy16(gx + base + lane * 16, lds_addr(sx + base));
+    const uint8_t* gs = (const uint8_t*)(j.act.xscale + (size_t)j.tok0 * B);
+    uint8_t* ss = sx + (size_t)NT * (cols / 8);
+    const int sbytes = nt * B * 4;
+    for (int base = wave * 256; base < sbytes; base += 1024)
+        if (base + lane * 4 < sbytes) lds_copy4(gs + base + lane * 4, lds_addr(ss + base));
+}
+
+// Copy the activations of this launch's tokens (q8, xs32, xscale) into LDS
+// with direct global->LDS loads; the caller waits (vmcnt 0) and barriers.
+// Layout: [NT*cols q8][NT*cols/32 xs32][NT*B xscale].
+template <int NT>
+__device__ __forceinline__ void stage_act(const GemvJob& j, uint8_t* smem) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int cols = j.cols, B = j.blocks, nt = j.ntok;
+    const uint8_t* gq = (const uint8_t*)(j.act.q8perm + (size_t)j.tok0 * cols);
+    const int qbytes = nt * cols;
+    for (int base = wave * 1024; base < qbytes; base += 4096)
+        if (base + lane * 16 < qbytes)
+            __builtin_amdgcn_global_load_lds(gq + base + lane * 16, (lds_void*)(smem + base), 16, 0, 0);
+    const uint8_t* gx = (const uint8_t*)(j.act.xs32 + (size_t)j.tok0 * (cols / 32));
+    uint8_t* sx = smem + (size_t)NT * cols;
+    const int xbytes = nt * (cols / 8);
+    for (int base = wave * 1024; base < xbytes; base += 4096)
+        if (base + lane * 16 < xbytes)
+            __builtin_amdgcn_global_load_lds(gx + base + lane * 16, (lds_void*)(sx + base), 16, 0, 0);
+    const uint8_t* gs = (const uint8_t*)(j.act.xscale + (size_t)j.tok0 * B);
+    uint8_t* ss = sx + (size_t)NT * (cols / 8);
+    const int sbytes = nt * B * 4;
+    for (int base = wave * 256; base < sbytes; base += 1024)
+        if (base + lane * 4 < sbytes)
+            __builtin_amdgcn_global_load_lds(gs + base + lane * 4, (lds_void*)(ss + base), 4, 0, 0);
+}
+
+__device__ __forceinline__ void wait_all_vmem() {
+    // s_waitcnt vmcnt(0), expcnt/lgkmcnt unconstrained
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+// s_waitcnt vmcnt(N) for a compile-time N (gfx9 encoding: vmcnt bits [3:0]
+// and [15:14], expcnt [6:4] and lgkmcnt [11:8] left unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmem_le() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// One Q4_K block of one AVX2 lane for NT tokens: exact int32 lane sum,
+// then the G-lane rotated fp32 chain steps (see the comment above).
+template <int NT, int G>
+__device__ __forceinline__ void q4k_block(const uint4 h, const uint4 q, int b, int k, int ntok,
+                                          const int8_t* q8b, const float* xs32b, const float* xscb,
+                                          int cols, int B, float* accF, float* accM) {
+    const float d = f16_bits_to_f32(h.x & 0xffffu);
+    const float dmin = f16_bits_to_f32(h.x >> 16);
+    // getScaleMinK4 for all eight sub-blocks (simd.go:1672-1677)
+    const uint32_t sc03 = h.y & 0x3f3f3f3fu;
+    const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t m03 = h.z & 0x3f3f3f3fu;
+    const uint32_t m47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+    const float mkf = (float)ubyte(k < 4 ? m03 : m47, k & 3);
+    const int l0 = (int)(q.x & 0x0f0f0f0fu), h0 = (int)((q.x >> 4) & 0x0f0f0f0fu);
+    const int l1 = (int)(q.y & 0x0f0f0f0fu), h1 = (int)((q.y >> 4) & 0x0f0f0f0fu);
+    const int l2 = (int)(q.z & 0x0f0f0f0fu), h2 = (int)((q.z >> 4) & 0x0f0f0f0fu);
+    const int l3 = (int)(q.w & 0x0f0f0f0fu), h3 = (int)((q.w >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        if (NT == 1 || t < ntok) {
+            const int8_t* qp = q8b + (size_t)t * cols + b * 256 + k * 32;
+            const int4 qa = *(const int4*)qp;
+            const int4 qb = *(const int4*)(qp + 16);
+            int acc = mad24(ubyte(sc03, 0), sdot4(l0, qa.x, 0), 0);
+            acc = mad24(ubyte(sc03, 1), sdot4(h0, qa.y, 0), acc);
+            acc = mad24(ubyte(sc03, 2), sdot4(l1, qa.z, 0), acc);
+            acc = mad24(ubyte(sc03, 3), sdot4(h1, qa.w, 0), acc);
+            acc = mad24(ubyte(sc47, 0), sdot4(l2, qb.x, 0), acc);
+            acc = mad24(ubyte(sc47, 1), sdot4(h2, qb.y, 0), acc);
+            acc = mad24(ubyte(sc47, 2), sdot4(l3, qb.z, 0), acc);
+            acc = mad24(ubyte(sc47, 3), sdot4(h3, qb.w, 0), acc);
+            const float iv = (float)acc;
+            const float dxs = d * xscb[(size_t)t * B + b];                       // VMULSS
+            const float mx = mkf * xs32b[(size_t)t * (cols / 32) + b * 8 + k];   // VMULPS
+#pragma unroll
+            for (int step = 0; step < G; step++) {
+                accF[t] = fmaf(iv, dxs, rot_prev<G>(accF[t]));   // VFMADD231PS
+                accM[t] = fmaf(dmin, mx, rot_prev<G>(accM[t]));  // VFMADD231PS
             }
         }
     }
-    float v[NT];
+}
+
+// NL = blocks per lane (B / G) and D = prefetch depth are compile-time, with
+// NL % D == 0, so every load is unconditional straight-line code and the
+// compiler can keep D blocks per lane in flight.  The weight prefetch is
+// issued before the activation staging so both latencies overlap.
+template <int NT, int G, int NL, int D>
+__global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJob j) {
+    static_assert(NL % D == 0, "prefetch depth must divide the blocks per lane");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x;
+    const int B = j.blocks, cols = j.cols;
+    const int gi = tid % G, k = (tid / G) & 7, rl = tid / (8 * G);
+    int wi = 0;
+    while (wi + 1 < j.n && (int)blockIdx.x >= j.wg_begin[wi + 1]) wi++;
+    const int r = ((int)blockIdx.x - j.wg_begin[wi]) * (32 / G) + rl;
+    const bool live = r < j.rows[wi];
+    const int rr = live ? r : j.rows[wi] - 1;  // dead lanes read a valid row, write nothing
+    const uint8_t* lane_row = j.w[wi] + (size_t)rr * j.rb + (size_t)gi * 144 + 16 * k;
+    // Activations first (direct-to-LDS copies), then the weight prefetch; the
+    // copies retire before the 2*D weight loads, so vmcnt <= 2*D means the
+    // staged bytes are in LDS while the weights are still streaming.  A bare
+    // s_barrier follows: a memory fence would drain the weight loads too.
+    stage_act_asm<NT>(j, smem);
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 H[D], Q[D];
 #pragma unroll
-    for (int t = 0; t < NT; t++) v[t] = accF[t] - accM[t];  // VSUBPS
-    store_rows<NT>(j, wi, r, k, v);
+    for (int i = 0; i < D; i++) {
+        const uint8_t* blk = lane_row + (size_t)i * G * 144;
+        Q[i] = *(const uint4*)(blk + 16);
+        H[i] = *(const uint4*)(blk - 16 * k);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmem_le<2 * D>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const int8_t* q8b = (const int8_t*)smem;
+    const float* xs32b = (const float*)(smem + (size_t)NT * cols);
+    const float* xscb = xs32b + (size_t)NT * (cols / 32);
+    float accF[NT], accM[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) accF[t] = accM[t] = 0.0f;
+#pragma unroll
+    for (int i0 = 0; i0 < NL; i0 += D) {
+#pragma unroll
+        for (int ii = 0; ii < D; ii++) {
+            const uint4 h = H[ii], q = Q[ii];
+            if (i0 + D < NL) {
+                const uint8_t* blk = lane_row + (size_t)(i0 + D + ii) * G * 144;
+                Q[ii] = *(const uint4*)(blk + 16);
+                H[ii] = *(const uint4*)(blk - 16 * k);
+            }
+            q4k_block<NT, G>(h, q, (i0 + ii) * G + gi, k, j.ntok, q8b, xs32b, xscb, cols, B, accF,
+                             accM);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const float v = tree8_strided<G>(accF[t] - accM[t]);  // VSUBPS + tree
+        if (live && k == 0 && gi == G - 1 && t < j.ntok)
+            j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
+    }
+}
+
+// Any block count (B % G == 0): runtime trip count, activations read from
+// global memory.  Used for shapes without a compiled NL.
+template <int NT, int G>
+__global__ __launch_bounds__(256) void gemv_q4k_any_kernel(GemvJob j) {
+    const int tid = threadIdx.x;
+    const int B = j.blocks, cols = j.cols;
+    const int gi = tid % G, k = (tid / G) & 7, rl = tid / (8 * G);
+    int wi = 0;
+    while (wi + 1 < j.n && (int)blockIdx.x >= j.wg_begin[wi + 1]) wi++;
+    const int r = ((int)blockIdx.x - j.wg_begin[wi]) * (32 / G) + rl;
+    if (r >= j.rows[wi]) return;
+    const uint8_t* lane_row = j.w[wi] + (size_t)r * j.rb + (size_t)gi * 144;
+    const int8_t* q8b = j.act.q8perm + (size_t)j.tok0 * cols;
+    const float* xs32b = j.act.xs32 + (size_t)j.tok0 * (cols / 32);
+    const float* xscb = j.act.xscale + (size_t)j.tok0 * B;
+    float accF[NT], accM[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) accF[t] = accM[t] = 0.0f;
+    for (int i = 0; i < B / G; i++) {
+        const uint8_t* blk = lane_row + (size_t)i * G * 144;
+        q4k_block<NT, G>(*(const uint4*)blk, *(const uint4*)(blk + 16 + 16 * k), i * G + gi, k,
+                         j.ntok, q8b, xs32b, xscb, cols, B, accF, accM);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const float v = tree8_strided<G>(accF[t] - accM[t]);
+        if (k == 0 && gi == G - 1 && t < j.ntok)
+            j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -264,7 +512,7 @@ __global__ __launch_bounds__(256) void lane_ints_kernel(const uint8_t* __restric
             const uint32_t sc03 = h.y & 0x3f3f3f3fu;
             const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
             for (int s = 0; s < 4; s++) {
-                const uint32_t wd = *(const uint32_t*)(blk + 16 + 32 * s + 4 * k);
+                const uint32_t wd = *(const uint32_t*)(blk + 16 + 16 * k + 4 * s);  // repacked
                 const uint32_t sc = s < 2 ? sc03 : sc47;
                 acc += ubyte(sc, (2 * s) & 3) * sdot4((int)(wd & 0x0f0f0f0fu), xq[2 * s], 0);
                 acc += ubyte(sc, (2 * s + 1) & 3) * sdot4((int)((wd >> 4) & 0x0f0f0f0fu), xq[2 * s + 1], 0);
@@ -346,7 +594,16 @@ __global__ void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restri
          i += (size_t)gridDim.x * blockDim.x) {
         const size_t r = i / rb, o = i % rb;  // o: offset in the reference row
         size_t n;                             // offset in the repacked row
-        if (type == GLLM_TYPE_Q6_K) {
+        if (type == GLLM_TYPE_Q4_K) {
+            // nibble byte 32s + 4k + j -> 16k + 4s + j (header unchanged)
+            const size_t b = o / 144, e = o % 144;
+            if (e < 16) {
+                n = o;
+            } else {
+                const size_t qi = e - 16, s4 = qi / 32, l = qi % 32;
+                n = b * 144 + 16 + (l / 4) * 16 + s4 * 4 + (l % 4);
+            }
+        } else if (type == GLLM_TYPE_Q6_K) {
             const size_t b = o / 210, e = o % 210;
             n = e < 208 ? b * 208 + e : (size_t)B * 208 + b * 2 + (e - 208);
         } else {  // Q8_0
@@ -381,10 +638,64 @@ size_t ref_row_bytes(int type, int cols) {
 // launch helpers
 // ---------------------------------------------------------------------------
 
+// Activation bytes one Q4_K workgroup stages in LDS for NT tokens.
+static size_t q4k_stage_bytes(int nt, int cols) {
+    return (size_t)nt * ((size_t)cols + (size_t)(cols / 32) * 4 + (size_t)(cols / 256) * 4);
+}
+constexpr size_t kMaxStage = 48 << 10;
+
+template <int NT, int G>
+int launch_q4k(GemvJob& j, const int* rows, int n, hipStream_t s) {
+    int wg = 0;
+    for (int i = 0; i < n; i++) {
+        j.wg_begin[i] = wg;
+        wg += (rows[i] + 32 / G - 1) / (32 / G);
+    }
+    j.wg_begin[n] = wg;
+    const size_t stage = q4k_stage_bytes(NT, j.cols);
+    const int nl = j.blocks / G;
+    const int sq = NT == 1 ? 4 : 8;  // Stage<NT>::SQ
+    const bool fits = NT * j.cols / 16 <= 256 * sq && NT * j.cols / 128 <= 256 &&
+                      NT * j.blocks <= 256 && stage <= kMaxStage;
+    dim3 grid(wg), block(256);
+    if (!fits) {
+        hipLaunchKernelGGL((gemv_q4k_any_kernel<NT, G>), grid, block, 0, s, j);
+    } else if (nl == 1) {
+        hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, 1, 1>), grid, block, stage, s, j);
+    } else if (nl == 4) {
+        hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, 4, 4>), grid, block, stage, s, j);
+    } else if (nl == 8) {
+        hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, 8, 8>), grid, block, stage, s, j);
+    } else if (nl == 14) {
+        hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, 14, 7>), grid, block, stage, s, j);
+    } else if (nl == 16) {
+        hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, 16, 8>), grid, block, stage, s, j);
+    } else {
+        hipLaunchKernelGGL((gemv_q4k_any_kernel<NT, G>), grid, block, 0, s, j);
+    }
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+// Lanes per AVX2 lane: the smallest G dividing the block count that puts at
+// least ~2048 waves (8 per CU) on the device.
+static int pick_g(int total_rows, int blocks) {
+    for (int g = 1; g <= 4; g *= 2)
+        if (blocks % g == 0 && (long)total_rows * 8 * g / 64 >= 2048) return g;
+    return blocks % 4 == 0 ? 4 : (blocks % 2 == 0 ? 2 : 1);
+}
+
 template <int NT>
-int launch_gemv_nt(const GemvJob& j, int type, int grid, hipStream_t s) {
+int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t s) {
+    if (type == GLLM_TYPE_Q4_K) {
+        int total = 0;
+        for (int i = 0; i < j.n; i++) total += rows[i];
+        const int g = pick_g(total, j.blocks);
+        return g == 1 ? launch_q4k<NT, 1>(j, rows, j.n, s)
+             : g == 2 ? launch_q4k<NT, 2>(j, rows, j.n, s)
+                      : launch_q4k<NT, 4>(j, rows, j.n, s);
+    }
     switch (type) {
-    case GLLM_TYPE_Q4_K: hipLaunchKernelGGL(gemv_q4k_kernel<NT>, dim3(grid), dim3(256), 0, s, j); break;
     case GLLM_TYPE_Q6_K: hipLaunchKernelGGL(gemv_q6k_kernel<NT>, dim3(grid), dim3(256), 0, s, j); break;
     case GLLM_TYPE_Q8_0: hipLaunchKernelGGL(gemv_q8_0_kernel<NT>, dim3(grid), dim3(256), 0, s, j); break;
     default: return fail(GLLM_EUNSUP, "gemv: unsupported type %d", type);
@@ -426,9 +737,9 @@ int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* 
     for (int t0 = 0; t0 < p; t0 += kMaxTok) {
         j.tok0 = t0;
         j.ntok = std::min(kMaxTok, p - t0);
-        int rc = j.ntok == 1 ? launch_gemv_nt<1>(j, w0->type, wg, s)
-               : j.ntok <= 4 ? launch_gemv_nt<4>(j, w0->type, wg, s)
-                             : launch_gemv_nt<8>(j, w0->type, wg, s);
+        int rc = j.ntok == 1 ? launch_gemv_nt<1>(j, w0->type, wg, j.rows, s)
+               : j.ntok <= 4 ? launch_gemv_nt<4>(j, w0->type, wg, j.rows, s)
+                             : launch_gemv_nt<8>(j, w0->type, wg, j.rows, s);
         GLLM_TRY(rc);
     }
     return GLLM_OK;
@@ -495,13 +806,7 @@ static gllm_hip_weight* weight_alloc(int ggml_type, int rows, int cols, size_t l
 }
 
 static gllm_hip_weight* weight_finish(gllm_hip_weight* w, const uint8_t* d_src, hipStream_t s) {
-    int rc = GLLM_OK;
-    const size_t bytes = w->row_bytes * (size_t)w->rows;
-    if (w->type == GLLM_TYPE_Q4_K) {
-        rc = check(hipMemcpyAsync(w->d_data, d_src, bytes, hipMemcpyDeviceToDevice, s), "copy weight");
-    } else {
-        rc = launch_repack(d_src, w->d_data, w->type, w->rows, w->blocks, w->row_bytes, 0, s);
-    }
+    int rc = launch_repack(d_src, w->d_data, w->type, w->rows, w->blocks, w->row_bytes, 0, s);
     if (rc == GLLM_OK) rc = check(hipStreamSynchronize(s), "weight upload");
     if (rc != GLLM_OK) {
         (void)hipFree(w->d_data);
@@ -521,14 +826,6 @@ gllm_hip_weight* gllm_hip_weight_new(const void* data, size_t len, int ggml_type
     if (!w) return nullptr;
     hipStream_t s = thread_stream();
     const size_t bytes = w->row_bytes * (size_t)rows;
-    if (ggml_type == GLLM_TYPE_Q4_K) {
-        if (check(hipMemcpy(w->d_data, data, bytes, hipMemcpyHostToDevice), "upload weight") != GLLM_OK) {
-            (void)hipFree(w->d_data);
-            delete w;
-            return nullptr;
-        }
-        return w;
-    }
     void* tmp = nullptr;
     if (hipMalloc(&tmp, bytes) != hipSuccess) {
         (void)hipGetLastError();
@@ -576,11 +873,6 @@ int gllm_hip_weight_shape(const gllm_hip_weight* w, int* ggml_type, int* rows, i
 int gllm_hip_weight_download_dev(const gllm_hip_weight* w, void* d_dst, void* stream) {
     if (!w || !d_dst) return fail(GLLM_EINVAL, "gllm_hip_weight_download_dev: bad arguments");
     hipStream_t s = (hipStream_t)stream;
-    if (w->type == GLLM_TYPE_Q4_K) {
-        GLLM_HIP(hipMemcpyAsync(d_dst, w->d_data, w->row_bytes * (size_t)w->rows,
-                                hipMemcpyDeviceToDevice, s));
-        return GLLM_OK;
-    }
     return launch_repack(w->d_data, (uint8_t*)d_dst, w->type, w->rows, w->blocks, w->row_bytes, 1, s);
 }
 
@@ -600,6 +892,33 @@ int gllm_hip_matvec_multi_dev(int n, gllm_hip_weight* const* ws, const float* d_
     for (int i = 0; i < n; i++)
         if (!d_outs[i]) return fail(GLLM_EINVAL, "gllm_hip_matvec_multi_dev: null output");
     return matvec_multi(n, ws, d_xs, p, d_outs, out_strides, (hipStream_t)stream, 0);
+}
+
+size_t gllm_hip_act_bytes(int cols, int p) {
+    if (cols <= 0 || cols % 256 || p <= 0) return 0;
+    return act_bytes(cols, p);
+}
+
+int gllm_hip_q8k_prepare_dev(const float* d_xs, int cols, int p, void* d_act, void* stream) {
+    if (!d_xs || !d_act || cols <= 0 || cols % 256 || p <= 0)
+        return fail(GLLM_EINVAL, "gllm_hip_q8k_prepare_dev: bad arguments");
+    ActQ8 act;
+    act_carve(d_act, cols, p, &act);
+    return launch_q8k_prep(d_xs, cols, p, act, (hipStream_t)stream);
+}
+
+int gllm_hip_matvec_q8_dev(gllm_hip_weight* w, const void* d_act, int p, float* d_outs,
+                           int out_stride, void* stream) {
+    GLLM_TRY(validate_weight(w));
+    if (!d_act || !d_outs || p <= 0) return fail(GLLM_EINVAL, "gllm_hip_matvec_q8_dev: bad arguments");
+    if (out_stride <= 0) out_stride = w->rows;
+    if (out_stride < w->rows) return fail(GLLM_EINVAL, "out stride < rows");
+    ActQ8 act;
+    act_carve((void*)d_act, w->cols, p, &act);
+    gllm_hip_weight* ws[1] = {w};
+    float* outs[1] = {d_outs};
+    int strides[1] = {out_stride};
+    return run_gemv(1, ws, act, p, outs, strides, (hipStream_t)stream);
 }
 
 // Host-pointer forms: stage through pinned memory on the thread's stream.

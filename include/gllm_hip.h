@@ -120,6 +120,16 @@ int gllm_hip_matvec_multi_dev(int n, gllm_hip_weight* const* ws, const float* d_
                               float* const* d_outs, const int* out_strides, void* stream);
 int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token, void* stream);
 
+/* Split form of the same call, for callers that quantise once and dot many
+ * matrices (acquireQ8 + fillQ4KXSums/fillQ6KXSums16, kernels_amd64.go:246,
+ * then dotQ4KRowsQ8 / dotQ6KRowsQ8 / dotQ8_0RowsQ8, kernels_amd64.go:268-285,
+ * 611-619).  d_act is a caller-owned device buffer of
+ * gllm_hip_act_bytes(cols, p) bytes holding the quantised activations. */
+size_t gllm_hip_act_bytes(int cols, int p);
+int gllm_hip_q8k_prepare_dev(const float* d_xs, int cols, int p, void* d_act, void* stream);
+int gllm_hip_matvec_q8_dev(gllm_hip_weight* w, const void* d_act, int p, float* d_outs,
+                           int out_stride, void* stream);
+
 /* Q8K activation quantisation alone (q8kQuantize, kernels_amd64.s:348-436):
  * p rows of cols floats -> q8 [p][cols] in element order and scales
  * [p][cols/256]. */
