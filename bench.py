@@ -210,7 +210,7 @@ def cpu_baseline(weights, xh, rows, cols, seconds, torch):
         ref.matvec_batch_fast(ref.Q4_K, host[n % len(host)], xh, rows, cols, threads=cores)
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 2000:
+        if el >= seconds:
             break
     gbs = alg_bytes(rows, cols) * n / el / 1e9
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": cores, "kind": kind,
