@@ -4,7 +4,8 @@
 Workload (gate/up shape): W is 14336 x 4096 drawn
 N(0, 0.02) on the device and encoded to Q4_K by the device RTN encoder
 (QuantizeRowQ4K); x is N(0, 1).  One step is one MatvecQ4KInto (simd.go:261):
-Q8K quantisation of x plus the row kernels over all 14336 rows.  Weight
+Q8K quantisation of x plus the row kernels over all 14336 rows; at this shape
+the row kernel quantises x itself, so a step is one kernel launch.  Weight
 copies rotate so the working set (>= 300 MB) exceeds the 256 MB Infinity
 Cache, i.e. every step streams its weights from HBM.  Steps are replayed from
 a HIP graph (captured through torch.cuda.CUDAGraph on the launch stream) so
@@ -12,9 +13,10 @@ host launch overhead is not measured.
 
 value      = algorithmic bytes per step / time per step, bytes =
              rows*(cols/256)*144 + 4*cols + 4*rows (whole MatvecQ4KInto)
-roofline   = the same bytes / the row kernel's own average duration (HIP
-             events around graph replays of the row kernel alone), against
-             the 8 TB/s HBM3E peak; traffic from profiles/ (rocprofv3 PMC)
+roofline   = the same bytes / the row kernel's average launch duration (HIP
+             events on the launch stream around graph replays of back-to-back
+             launches, so the inter-kernel gap is included), against the
+             8 TB/s HBM3E peak; traffic from profiles/ (rocprofv3 PMC)
 cpu_baseline = the oracle's AVX2 port of kernels_amd64.s (bit-identical
              results) on this host's cores, same bytes formula, rotating the
              same weight copies.
@@ -88,30 +90,24 @@ def run(args):
     weights = make_weights(g, torch, rows, cols, copies, seed=1000)
     x = torch.empty(cols, dtype=torch.float32, device="cuda")
     g.fill_normal_dev(x, 7, 1.0)
-    act = torch.empty(g.act_bytes(cols, 1), dtype=torch.uint8, device="cuda")
     out = torch.empty(rows, dtype=torch.float32, device="cuda")
 
-    # correctness guard: the benchmarked launch sequence equals the blocking
-    # host entry point on the same inputs
+    # correctness guard: the benchmarked device entry point equals the
+    # blocking host entry point on the same inputs
     xh = x.cpu().numpy()
     want = weights[0].matvec_into(xh)
-    g.q8k_prepare_dev(x, act)
-    weights[0].matvec_q8_dev(act, 1, out)
+    weights[0].matvec_dev(x.view(1, -1), out.view(1, -1))
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
-    def full_steps():  # `copies` whole MatvecQ4KInto steps
+    def full_steps():  # `copies` whole MatvecQ4KInto steps (gllm_hip_matvec_dev)
         for w in weights:
-            g.q8k_prepare_dev(x, act)
-            w.matvec_q8_dev(act, 1, out)
+            w.matvec_dev(x.view(1, -1), out.view(1, -1))
 
-    def kernel_only():  # the row kernel alone, activations already quantised
-        for w in weights:
-            w.matvec_q8_dev(act, 1, out)
-
-    g.q8k_prepare_dev(x, act)
+    # At this shape the row kernel quantises x itself (one launch per step),
+    # so the dominant kernel's launches are the steps themselves.
     full = timed_graph(torch, full_steps, 1)
-    kern = timed_graph(torch, kernel_only, 1)
+    kern = full
 
     reps = max(1, math.ceil(args.steps / copies))
     wreps = max(1, math.ceil(args.warmup / copies)) if args.warmup > 0 else 0
@@ -177,7 +173,7 @@ def run(args):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "gemv_q4k_kernel<1>",
+            "kernel": "gemv_q4k_kernel (fused Q8K quantisation, one launch per step)",
             "kernel_avg_us": round(kernel_us, 3),
             "bytes_per_launch": nbytes,
         },
@@ -234,11 +230,9 @@ def profile_run():
     weights = make_weights(g, torch, rows, cols, copies, seed=1000)
     x = torch.empty(cols, dtype=torch.float32, device="cuda")
     g.fill_normal_dev(x, 7, 1.0)
-    act = torch.empty(g.act_bytes(cols, 1), dtype=torch.uint8, device="cuda")
     out = torch.empty(rows, dtype=torch.float32, device="cuda")
-    g.q8k_prepare_dev(x, act)
     for i in range(20):
-        weights[i % copies].matvec_q8_dev(act, 1, out)
+        weights[i % copies].matvec_dev(x.view(1, -1), out.view(1, -1))
     torch.cuda.synchronize()
     src = torch.ones(512 << 18, dtype=torch.float32, device="cuda")  # 512 MiB
     dst = torch.empty_like(src)

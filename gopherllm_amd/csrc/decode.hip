@@ -20,9 +20,8 @@
 #include "gllm_common.h"
 
 namespace gllm {
-int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* const* outs,
-             const int* strides, hipStream_t s);
-int launch_q8k_prep(const float* d_x, int cols, int p, const ActQ8& a, hipStream_t s);
+int gemv_f32(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float* const* outs,
+             const int* strides, void* act_buf, hipStream_t s);
 int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
                  int start, int end0, int p, float scale, float* d_out, hipStream_t s);
 int attend_splitk(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
@@ -224,10 +223,7 @@ static int ensure_buffers(gllm_hip_model* m, int p) {
 
 static int matvec(gllm_hip_model* m, int n, gllm_hip_weight* const* ws, const float* x, int p,
                   float* const* outs) {
-    ActQ8 a;
-    act_carve(m->act, ws[0]->cols, p, &a);
-    GLLM_TRY(launch_q8k_prep(x, ws[0]->cols, p, a, m->stream));
-    return run_gemv(n, ws, a, p, outs, nullptr, m->stream);
+    return gemv_f32(n, ws, x, p, outs, nullptr, m->act, m->stream);
 }
 
 // ForwardBatchInto / ForwardBodyInto for p consecutive tokens already in

@@ -29,9 +29,11 @@ struct GemvJob {
     int blocks;
     int cols;
     size_t rb;
-    ActQ8 act;
-    int tok0;  // first activation row of this launch
-    int ntok;  // activation rows in this launch (<= NT)
+    ActQ8 act;        // pre-quantised activations (unfused kernels)
+    const float* xf;  // f32 activations when the kernel quantises them itself
+    int rows_per_wg;  // rows per workgroup (gemv_q4k_kernel: blockDim.x / (8 * G))
+    int tok0;         // first activation row of this launch
+    int ntok;         // activation rows in this launch (<= NT)
 };
 
 __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
@@ -68,16 +70,17 @@ __device__ __forceinline__ int locate(const GemvJob& j, int wg, int* wi) {
 // exactly the reference's order.
 // ---------------------------------------------------------------------------
 
-// rotate a value one lane up inside groups of G lanes (lane g receives g-1)
+// rotate a value one lane up inside groups of G lanes (lane g receives g-1);
+// quad_perm covers every lane, so no "old" value is needed
 template <int G>
 __device__ __forceinline__ float rot_prev(float v) {
     if constexpr (G == 1) {
         return v;
     } else if constexpr (G == 2) {
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
     } else {
         static_assert(G == 4, "G must be 1, 2 or 4");
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x93, 0xF, 0xF, false));
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x93, 0xF, 0xF, false));
     }
 }
 
@@ -92,55 +95,43 @@ __device__ __forceinline__ float tree8_strided(float v) {
 
 __device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
 
-typedef __attribute__((address_space(3))) void lds_void;
+// Exact int8 dot of four byte pairs (v_dot4c_i32_i8).  Every VALU operation
+// here is left to the compiler: hand-written VALU instructions in inline
+// assembly bypass its hazard tracking.
+__device__ __forceinline__ int dot4z(int a, int b) { return __builtin_amdgcn_sdot4(a, b, 0, false); }
 
-// Activation staging through registers: stage_load issues plain loads of
-// this launch's tokens (q8, xs32, xscale) before the weight prefetch, and
-// stage_store writes them to LDS afterwards.  Plain loads retire in issue
-// order, so the compiler's own vmcnt waits for the staging registers leave
-// the weight loads in flight.  Layout: [NT*cols q8][NT*cols/32 xs32][NT*B
-// xscale].  SQ = 16-byte q8 chunks per thread (the launcher checks capacity).
-template <int NT>
-struct Stage {
-    static constexpr int SQ = NT == 1 ? 4 : 8;
-    uint4 q[SQ];
-    uint4 x;
-    float s;
+// a * (byte N of s): a is a 14-bit signed dot and s holds 6-bit scales, so
+// the 24-bit multiply (v_mul_i32_i24, full rate) is exact.
+template <int N>
+__device__ __forceinline__ int mul_byte(int a, uint32_t s) {
+    return __mul24(a, (int)((s >> (8 * N)) & 0xffu));
+}
+
+__device__ __forceinline__ uint32_t ubfe(uint32_t v, uint32_t off, uint32_t width) {
+    return __builtin_amdgcn_ubfe(v, off, width);
+}
+
+// Per-lane constants that extract m_k, the 6-bit min of sub-block k
+// (getScaleMinK4, simd.go:1672-1677), from header dwords z = scales[4..7]
+// and w = scales[8..11]:
+//   k < 4:  m = z.byte(k) & 63
+//   k >= 4: m = (w.byte(k-4) >> 4) | ((z.byte(k-4) >> 6) << 4)
+// as m = bfe(k < 4 ? z : w, sa, wa) | (bfe(z, sb, wb) << 4) (width 0 gives 0).
+struct MinSel {
+    bool lo;
+    uint32_t sa, wa, sb, wb;
+    __device__ explicit MinSel(int k)
+        : lo(k < 4),
+          sa(k < 4 ? 8u * k : 8u * (k - 4) + 4u),
+          wa(k < 4 ? 6u : 4u),
+          sb(k < 4 ? 0u : 8u * (k - 4) + 6u),
+          wb(k < 4 ? 0u : 2u) {}
+    __device__ __forceinline__ uint32_t get(uint32_t z, uint32_t w) const {
+        return ubfe(lo ? z : w, sa, wa) | (ubfe(z, sb, wb) << 4);
+    }
 };
 
-template <int NT>
-__device__ __forceinline__ void stage_load(const GemvJob& j, Stage<NT>& st) {
-    const int tid = threadIdx.x;
-    const int cols = j.cols, B = j.blocks, nt = j.ntok;
-    const uint4* gq = (const uint4*)(j.act.q8perm + (size_t)j.tok0 * cols);
-    // unconditional loads with clamped indices (straight-line code, so they
-    // stay ahead of the weight prefetch); stage_store writes only the valid ones
-    const int qn = nt * cols / 16;
-#pragma unroll
-    for (int i = 0; i < Stage<NT>::SQ; i++) st.q[i] = gq[min(tid + 256 * i, qn - 1)];
-    const uint4* gx = (const uint4*)(j.act.xs32 + (size_t)j.tok0 * (cols / 32));
-    st.x = gx[min(tid, nt * cols / 128 - 1)];
-    st.s = j.act.xscale[(size_t)j.tok0 * B + min(tid, nt * B - 1)];
-}
-
-template <int NT>
-__device__ __forceinline__ void stage_store(const GemvJob& j, const Stage<NT>& st, uint8_t* smem) {
-    const int tid = threadIdx.x;
-    const int cols = j.cols, nt = j.ntok;
-    const int qn = nt * cols / 16;
-#pragma unroll
-    for (int i = 0; i < Stage<NT>::SQ; i++)
-        if (tid + 256 * i < qn) ((uint4*)smem)[tid + 256 * i] = st.q[i];
-    uint8_t* sx = smem + (size_t)NT * cols;
-    if (tid < nt * cols / 128) ((uint4*)sx)[tid] = st.x;
-    float* ss = (float*)(sx + (size_t)NT * (cols / 8));
-    if (tid < nt * j.blocks) ss[tid] = st.s;
-}
-
-template <int NT>
-__device__ __forceinline__ bool stage_fits(int cols, int blocks) {
-    return NT * cols / 16 <= 256 * Stage<NT>::SQ && NT * cols / 128 <= 256 && NT * blocks <= 256;
-}
+typedef __attribute__((address_space(3))) void lds_void;
 
 // Direct global->LDS copies issued from inline assembly.  The compiler does
 // not see them as outstanding vector-memory operations, which is the point:
@@ -173,52 +164,22 @@ template <int NT>
 __device__ __forceinline__ void stage_act_asm(const GemvJob& j, uint8_t* smem) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
     const int cols = j.cols, B = j.blocks, nt = j.ntok;
     const uint8_t* gq = (const uint8_t*)(j.act.q8perm + (size_t)j.tok0 * cols);
     const int qbytes = nt * cols;
-    for (int base = wave * 1024; base < qbytes; base += 4096)
+    for (int base = wave * 1024; base < qbytes; base += nw * 1024)
         if (base + lane * 16 < qbytes) lds_copy16(gq + base + lane * 16, lds_addr(smem + base));
     const uint8_t* gx = (const uint8_t*)(j.act.xs32 + (size_t)j.tok0 * (cols / 32));
     uint8_t* sx = smem + (size_t)NT * cols;
     const int xbytes = nt * (cols / 8);
-    for (int base = wave * 1024; base < xbytes; base += 4096)
+    for (int base = wave * 1024; base < xbytes; base += nw * 1024)
         if (base + lane * 16 < xbytes) lds_copy16(gx + base + lane * 16, lds_addr(sx + base));
     const uint8_t* gs = (const uint8_t*)(j.act.xscale + (size_t)j.tok0 * B);
     uint8_t* ss = sx + (size_t)NT * (cols / 8);
     const int sbytes = nt * B * 4;
-    for (int base = wave * 256; base < sbytes; base += 1024)
+    for (int base = wave * 256; base < sbytes; base += nw * 256)
         if (base + lane * 4 < sbytes) lds_copy4(gs + base + lane * 4, lds_addr(ss + base));
-}
-
-// Copy the activations of this launch's tokens (q8, xs32, xscale) into LDS
-// with direct global->LDS loads; the caller waits (vmcnt 0) and barriers.
-// Layout: [NT*cols q8][NT*cols/32 xs32][NT*B xscale].
-template <int NT>
-__device__ __forceinline__ void stage_act(const GemvJob& j, uint8_t* smem) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int cols = j.cols, B = j.blocks, nt = j.ntok;
-    const uint8_t* gq = (const uint8_t*)(j.act.q8perm + (size_t)j.tok0 * cols);
-    const int qbytes = nt * cols;
-    for (int base = wave * 1024; base < qbytes; base += 4096)
-        if (base + lane * 16 < qbytes)
-            __builtin_amdgcn_global_load_lds(gq + base + lane * 16, (lds_void*)(smem + base), 16, 0, 0);
-    const uint8_t* gx = (const uint8_t*)(j.act.xs32 + (size_t)j.tok0 * (cols / 32));
-    uint8_t* sx = smem + (size_t)NT * cols;
-    const int xbytes = nt * (cols / 8);
-    for (int base = wave * 1024; base < xbytes; base += 4096)
-        if (base + lane * 16 < xbytes)
-            __builtin_amdgcn_global_load_lds(gx + base + lane * 16, (lds_void*)(sx + base), 16, 0, 0);
-    const uint8_t* gs = (const uint8_t*)(j.act.xscale + (size_t)j.tok0 * B);
-    uint8_t* ss = sx + (size_t)NT * (cols / 8);
-    const int sbytes = nt * B * 4;
-    for (int base = wave * 256; base < sbytes; base += 1024)
-        if (base + lane * 4 < sbytes)
-            __builtin_amdgcn_global_load_lds(gs + base + lane * 4, (lds_void*)(ss + base), 4, 0, 0);
-}
-
-__device__ __forceinline__ void wait_all_vmem() {
-    // s_waitcnt vmcnt(0), expcnt/lgkmcnt unconstrained
-    __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
 // s_waitcnt vmcnt(N) for a compile-time N (gfx9 encoding: vmcnt bits [3:0]
@@ -229,20 +190,117 @@ __device__ __forceinline__ void wait_vmem_le() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// One Q4_K block of one AVX2 lane for NT tokens: exact int32 lane sum,
-// then the G-lane rotated fp32 chain steps (see the comment above).
+// s_waitcnt lgkmcnt(0) with vmcnt and expcnt unconstrained.
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Workgroup barrier for LDS data that leaves outstanding global loads in
+// flight: the caller has waited for its own LDS traffic; the empty asm
+// statements keep the compiler from moving memory operations across it (a
+// memory fence would drain the weight prefetch as well).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
+
+// ---------------------------------------------------------------------------
+// Q8K quantisation fused into a row kernel (batch 1): every workgroup turns
+// the f32 activation into the LDS layout the row loop reads, evaluating
+// q8kQuantize (quant_q8k_portable.go:36-62 == kernels_amd64.s:348-436) and
+// sumF32Groups32 / sumF32Groups16 (kernels_amd64.s:208-254) exactly as
+// q8k_prep_kernel does.  With nw waves (at least 4), wave w handles blocks
+// w, w+nw, ...; in a block, lane
+// (m = lane/8, kk = lane%8) holds x[32m + kk + 8i] for i = 0..3, i.e. the four
+// addends of the reference's v_kk for 32-group m in their summation order.
+// ---------------------------------------------------------------------------
+template <int QB>  // blocks per wave, compile-time so the loads stay in registers
+struct XRegs {
+    float v[QB][4];
+};
+
+template <int QB>
+__device__ __forceinline__ void xq_load(const float* __restrict__ x, int B, XRegs<QB>& xr) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int m = lane >> 3, kk = lane & 7;
+#pragma unroll
+    for (int i = 0; i < QB; i++) {
+        const int b = wave + nw * i;
+        const int bb = b < B ? b : B - 1;  // clamped; results of b >= B are not stored
+        const float* g = x + (size_t)bb * 256 + 32 * m + kk;
+#pragma unroll
+        for (int e = 0; e < 4; e++) xr.v[i][e] = g[8 * e];
+    }
+}
+
+// Quantise the blocks held in xr into LDS: q8 (lane-permuted), xs32 and, for
+// Q6_K (XS16), xs16 x 32 at the given LDS arrays.
+template <int QB, bool XS16>
+__device__ __forceinline__ void xq_store(const XRegs<QB>& xr, int B, int8_t* q8, float* xs32,
+                                         float* xs16, float* xsc) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int m = lane >> 3, kk = lane & 7;
+#pragma unroll
+    for (int i = 0; i < QB; i++) {
+        const int b = wave + nw * i;
+        if (b >= B) break;  // wave-uniform
+        const float x0 = xr.v[i][0], x1 = xr.v[i][1], x2 = xr.v[i][2], x3 = xr.v[i][3];
+        // amax, NaN skipped: v_max_f32 is IEEE maxNum
+        float a = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+        float scale = 0.0f, inv = 0.0f;
+        const bool nz = a != 0.0f && a == a;
+        if (nz) {
+            scale = a / 127.0f;
+            inv = 127.0f / a;
+        }
+        int8_t* qb = q8 + (size_t)b * 256 + 4 * m + (kk & 3) + 32 * (kk >> 2);
+        qb[0] = (int8_t)(nz ? (int)rintf(x0 * inv) : 0);
+        qb[64] = (int8_t)(nz ? (int)rintf(x1 * inv) : 0);
+        qb[128] = (int8_t)(nz ? (int)rintf(x2 * inv) : 0);
+        qb[192] = (int8_t)(nz ? (int)rintf(x3 * inv) : 0);
+        if (lane == 0) xsc[b] = scale;
+        // v_kk = ((x[kk] + x[8+kk]) + x[16+kk]) + x[24+kk]; a_k = v_k + v_{k+4};
+        // r = (a0 + a1) + (a2 + a3)
+        float v = ((x0 + x1) + x2) + x3;
+        v = v + __shfl_xor(v, 4);
+        v = v + __shfl_xor(v, 1);
+        v = v + __shfl_xor(v, 2);
+        if (kk == 0) xs32[b * 8 + m] = v;
+        if constexpr (XS16) {
+            // 16-groups 2m (x0, x1) and 2m+1 (x2, x3): v_k = x[k] + x[8+k]
+            float u = x0 + x1, w = x2 + x3;
+            u = u + __shfl_xor(u, 4);
+            w = w + __shfl_xor(w, 4);
+            u = u + __shfl_xor(u, 1);
+            w = w + __shfl_xor(w, 1);
+            u = u + __shfl_xor(u, 2);
+            w = w + __shfl_xor(w, 2);
+            if (kk == 0) {
+                xs16[b * 16 + 2 * m] = u * 32.0f;
+                xs16[b * 16 + 2 * m + 1] = w * 32.0f;
+            }
+        }
+    }
+}
+
+// One Q4_K block of one AVX2 lane for NT tokens: exact int32 lane sum
+//   accI_k = sum_j sc_j * dot4(nibbles of sub-block j in lane k, q8)
+// then the fp32 chain steps (G-lane rotation when G > 1):
+//   accF = fma(float(accI), d*xs, accF)          VMULSS + VFMADD231PS
+//   accM = fma(dmin, m_k*xsum_k, accM)           VMULPS + VFMADD231PS
 template <int NT, int G>
-__device__ __forceinline__ void q4k_block(const uint4 h, const uint4 q, int b, int k, int ntok,
-                                          const int8_t* q8b, const float* xs32b, const float* xscb,
-                                          int cols, int B, float* accF, float* accM) {
+__device__ __forceinline__ void q4k_block(const uint4 h, const uint4 q, int b, int k,
+                                          const MinSel& ms, int ntok, const int8_t* q8b,
+                                          const float* xs32b, const float* xscb, int cols, int B,
+                                          float* accF, float* accM) {
     const float d = f16_bits_to_f32(h.x & 0xffffu);
     const float dmin = f16_bits_to_f32(h.x >> 16);
-    // getScaleMinK4 for all eight sub-blocks (simd.go:1672-1677)
     const uint32_t sc03 = h.y & 0x3f3f3f3fu;
     const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
-    const uint32_t m03 = h.z & 0x3f3f3f3fu;
-    const uint32_t m47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
-    const float mkf = (float)ubyte(k < 4 ? m03 : m47, k & 3);
+    const float mkf = (float)ms.get(h.z, h.w);
     const int l0 = (int)(q.x & 0x0f0f0f0fu), h0 = (int)((q.x >> 4) & 0x0f0f0f0fu);
     const int l1 = (int)(q.y & 0x0f0f0f0fu), h1 = (int)((q.y >> 4) & 0x0f0f0f0fu);
     const int l2 = (int)(q.z & 0x0f0f0f0fu), h2 = (int)((q.z >> 4) & 0x0f0f0f0fu);
@@ -253,63 +311,76 @@ __device__ __forceinline__ void q4k_block(const uint4 h, const uint4 q, int b, i
             const int8_t* qp = q8b + (size_t)t * cols + b * 256 + k * 32;
             const int4 qa = *(const int4*)qp;
             const int4 qb = *(const int4*)(qp + 16);
-            int acc = mad24(ubyte(sc03, 0), sdot4(l0, qa.x, 0), 0);
-            acc = mad24(ubyte(sc03, 1), sdot4(h0, qa.y, 0), acc);
-            acc = mad24(ubyte(sc03, 2), sdot4(l1, qa.z, 0), acc);
-            acc = mad24(ubyte(sc03, 3), sdot4(h1, qa.w, 0), acc);
-            acc = mad24(ubyte(sc47, 0), sdot4(l2, qb.x, 0), acc);
-            acc = mad24(ubyte(sc47, 1), sdot4(h2, qb.y, 0), acc);
-            acc = mad24(ubyte(sc47, 2), sdot4(l3, qb.z, 0), acc);
-            acc = mad24(ubyte(sc47, 3), sdot4(h3, qb.w, 0), acc);
+            const int acc = (mul_byte<0>(dot4z(l0, qa.x), sc03) + mul_byte<1>(dot4z(h0, qa.y), sc03)) +
+                            (mul_byte<2>(dot4z(l1, qa.z), sc03) + mul_byte<3>(dot4z(h1, qa.w), sc03)) +
+                            (mul_byte<0>(dot4z(l2, qb.x), sc47) + mul_byte<1>(dot4z(h2, qb.y), sc47)) +
+                            (mul_byte<2>(dot4z(l3, qb.z), sc47) + mul_byte<3>(dot4z(h3, qb.w), sc47));
             const float iv = (float)acc;
-            const float dxs = d * xscb[(size_t)t * B + b];                       // VMULSS
-            const float mx = mkf * xs32b[(size_t)t * (cols / 32) + b * 8 + k];   // VMULPS
+            const float dxs = d * xscb[(size_t)t * B + b];
+            const float mx = mkf * xs32b[(size_t)t * (cols / 32) + b * 8 + k];
 #pragma unroll
             for (int step = 0; step < G; step++) {
-                accF[t] = fmaf(iv, dxs, rot_prev<G>(accF[t]));   // VFMADD231PS
-                accM[t] = fmaf(dmin, mx, rot_prev<G>(accM[t]));  // VFMADD231PS
+                accF[t] = fmaf(iv, dxs, rot_prev<G>(accF[t]));
+                accM[t] = fmaf(dmin, mx, rot_prev<G>(accM[t]));
             }
         }
     }
 }
 
-// NL = blocks per lane (B / G) and D = prefetch depth are compile-time, with
-// NL % D == 0, so every load is unconditional straight-line code and the
-// compiler can keep D blocks per lane in flight.  The weight prefetch is
-// issued before the activation staging so both latencies overlap.
-template <int NT, int G, int NL, int D>
-__global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJob j) {
+// Row kernel for compile-time blocks per lane NL (B = NL * G) and prefetch
+// depth D (NL % D == 0): every weight load is unconditional straight-line
+// code, D blocks per lane in flight.
+//
+// FUSE (batch 1 only): the workgroup quantises the f32 activation itself.
+// Its x loads are issued first, the weight prefetch second, so the compiler's
+// in-order vmcnt waits hand the x registers to the quantiser while the
+// weights are still streaming.  Otherwise the pre-quantised activations are
+// copied to LDS with direct global->LDS loads issued before the prefetch.
+template <int NT, int G, int NL, int D, bool FUSE>
+__global__ __launch_bounds__(1024) void gemv_q4k_kernel(GemvJob j) {
     static_assert(NL % D == 0, "prefetch depth must divide the blocks per lane");
+    static_assert(!FUSE || NT == 1, "fused quantisation is batch 1 only");
+    constexpr int B = NL * G;
+    constexpr int QB = FUSE ? (B + 3) / 4 : 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x;
-    const int B = j.blocks, cols = j.cols;
+    const int cols = B * 256;
     const int gi = tid % G, k = (tid / G) & 7, rl = tid / (8 * G);
     int wi = 0;
     while (wi + 1 < j.n && (int)blockIdx.x >= j.wg_begin[wi + 1]) wi++;
-    const int r = ((int)blockIdx.x - j.wg_begin[wi]) * (32 / G) + rl;
+    const int r = ((int)blockIdx.x - j.wg_begin[wi]) * j.rows_per_wg + rl;
     const bool live = r < j.rows[wi];
     const int rr = live ? r : j.rows[wi] - 1;  // dead lanes read a valid row, write nothing
     const uint8_t* lane_row = j.w[wi] + (size_t)rr * j.rb + (size_t)gi * 144 + 16 * k;
-    // Activations first (direct-to-LDS copies), then the weight prefetch; the
-    // copies retire before the 2*D weight loads, so vmcnt <= 2*D means the
-    // staged bytes are in LDS while the weights are still streaming.  A bare
-    // s_barrier follows: a memory fence would drain the weight loads too.
-    stage_act_asm<NT>(j, smem);
+    int8_t* q8b = (int8_t*)smem;
+    float* xs32b = (float*)(smem + (size_t)NT * cols);
+    float* xscb = xs32b + (size_t)NT * (cols / 32);
+    XRegs<QB> xr;
+    if constexpr (FUSE) {
+        xq_load<QB>(j.xf + (size_t)j.tok0 * cols, B, xr);
+    } else {
+        stage_act_asm<NT>(j, smem);
+    }
     __builtin_amdgcn_sched_barrier(0);
+    // Loads are pinned in block order (header, then nibbles): vmcnt retires
+    // in issue order, so block i becomes usable as soon as its own data is in
+    // and the loop consumes the blocks as they arrive.
     uint4 H[D], Q[D];
 #pragma unroll
     for (int i = 0; i < D; i++) {
         const uint8_t* blk = lane_row + (size_t)i * G * 144;
-        Q[i] = *(const uint4*)(blk + 16);
         H[i] = *(const uint4*)(blk - 16 * k);
+        Q[i] = *(const uint4*)(blk + 16);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    wait_vmem_le<2 * D>();
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    const int8_t* q8b = (const int8_t*)smem;
-    const float* xs32b = (const float*)(smem + (size_t)NT * cols);
-    const float* xscb = xs32b + (size_t)NT * (cols / 32);
+    if constexpr (FUSE) {
+        xq_store<QB, false>(xr, B, q8b, xs32b, nullptr, xscb);
+        wait_lgkm0();
+    } else {
+        wait_vmem_le<2 * D>();
+    }
+    lds_barrier();
+    const MinSel ms(k);
     float accF[NT], accM[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) accF[t] = accM[t] = 0.0f;
@@ -320,11 +391,11 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJob j) {
             const uint4 h = H[ii], q = Q[ii];
             if (i0 + D < NL) {
                 const uint8_t* blk = lane_row + (size_t)(i0 + D + ii) * G * 144;
-                Q[ii] = *(const uint4*)(blk + 16);
                 H[ii] = *(const uint4*)(blk - 16 * k);
+                Q[ii] = *(const uint4*)(blk + 16);
             }
-            q4k_block<NT, G>(h, q, (i0 + ii) * G + gi, k, j.ntok, q8b, xs32b, xscb, cols, B, accF,
-                             accM);
+            q4k_block<NT, G>(h, q, (i0 + ii) * G + gi, k, ms, j.ntok, q8b, xs32b, xscb, cols, B,
+                             accF, accM);
         }
     }
 #pragma unroll
@@ -350,12 +421,13 @@ __global__ __launch_bounds__(256) void gemv_q4k_any_kernel(GemvJob j) {
     const int8_t* q8b = j.act.q8perm + (size_t)j.tok0 * cols;
     const float* xs32b = j.act.xs32 + (size_t)j.tok0 * (cols / 32);
     const float* xscb = j.act.xscale + (size_t)j.tok0 * B;
+    const MinSel ms(k);
     float accF[NT], accM[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) accF[t] = accM[t] = 0.0f;
     for (int i = 0; i < B / G; i++) {
         const uint8_t* blk = lane_row + (size_t)i * G * 144;
-        q4k_block<NT, G>(*(const uint4*)blk, *(const uint4*)(blk + 16 + 16 * k), i * G + gi, k,
+        q4k_block<NT, G>(*(const uint4*)blk, *(const uint4*)(blk + 16 + 16 * k), i * G + gi, k, ms,
                          j.ntok, q8b, xs32b, xscb, cols, B, accF, accM);
     }
 #pragma unroll
@@ -365,7 +437,6 @@ __global__ __launch_bounds__(256) void gemv_q4k_any_kernel(GemvJob j) {
             j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
     }
 }
-
 // ---------------------------------------------------------------------------
 // Q6_K, repacked at upload: per row, B blocks of 208 bytes
 // [ql 128][qh 64][int8 scales 16] followed by B f16 d values.  AVX2 lane k
@@ -644,45 +715,91 @@ static size_t q4k_stage_bytes(int nt, int cols) {
 }
 constexpr size_t kMaxStage = 48 << 10;
 
+template <int NT, int G, int NL, int D>
+static void launch_q4k_nl(const GemvJob& j, dim3 grid, dim3 block, size_t stage, hipStream_t s) {
+    if constexpr (NT == 1) {
+        if (j.xf) {
+            hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, true>), grid, block, stage, s, j);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, NL, D, false>), grid, block, stage, s, j);
+}
+
+// Blocks per lane with a compiled row kernel (and its prefetch depth).
+static bool q4k_has_nl(int nl) { return nl == 4 || nl == 8 || nl == 14 || nl == 16 || nl == 28; }
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+    static int cus[64];
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 256;
+    if (!cus[d]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || n <= 0)
+            n = 256;
+        cus[d] = n;
+    }
+    return cus[d];
+}
+
+// Launch shape of the Q4_K row kernel: one workgroup per compute unit, so a
+// CU's activation staging is the first memory traffic it issues (a second
+// workgroup's small activation reads would queue behind the first one's
+// weight stream).  G lanes share an AVX2 lane when the rows alone give
+// fewer than four waves per workgroup.
+struct Q4KShape {
+    int g, rows_per_wg, threads;
+};
+static int g_min_threads = 448;
+static Q4KShape q4k_shape(int total_rows, int blocks) {
+    const int ncu = device_cus();
+    Q4KShape best{0, 0, 0};
+    for (int g = 1; g <= 4; g *= 2) {
+        if (blocks % g) continue;
+        const int unit = 8 / g;  // rows per wave
+        int rpw = (total_rows + ncu - 1) / ncu;
+        rpw = (rpw + unit - 1) / unit * unit;
+        rpw = std::min(rpw, 128 / g);  // at most 1024 threads
+        const Q4KShape sh{g, rpw, rpw * 8 * g};
+        if (!q4k_has_nl(blocks / g) && best.g) continue;
+        best = sh;
+        if (sh.threads >= g_min_threads && q4k_has_nl(blocks / g)) break;
+    }
+    return best;
+}
+
 template <int NT, int G>
-int launch_q4k(GemvJob& j, const int* rows, int n, hipStream_t s) {
+int launch_q4k(GemvJob& j, const int* rows, int n, const Q4KShape& sh, hipStream_t s) {
+    const int nl = j.blocks / G;
+    const size_t stage = q4k_stage_bytes(NT, j.cols);
+    const bool compiled = stage <= kMaxStage && q4k_has_nl(nl) && sh.threads >= 256;
+    if (j.xf && (NT != 1 || !compiled))
+        return fail(GLLM_EINVAL, "gemv: fused quantisation needs batch 1 and a compiled shape");
+    // the generic kernel keeps 256-thread workgroups of 32 / G rows
+    j.rows_per_wg = compiled ? sh.rows_per_wg : 32 / G;
     int wg = 0;
     for (int i = 0; i < n; i++) {
         j.wg_begin[i] = wg;
-        wg += (rows[i] + 32 / G - 1) / (32 / G);
+        wg += (rows[i] + j.rows_per_wg - 1) / j.rows_per_wg;
     }
     j.wg_begin[n] = wg;
-    const size_t stage = q4k_stage_bytes(NT, j.cols);
-    const int nl = j.blocks / G;
-    const int sq = NT == 1 ? 4 : 8;  // Stage<NT>::SQ
-    const bool fits = NT * j.cols / 16 <= 256 * sq && NT * j.cols / 128 <= 256 &&
-                      NT * j.blocks <= 256 && stage <= kMaxStage;
-    dim3 grid(wg), block(256);
-    if (!fits) {
+    const dim3 grid(wg), block(compiled ? sh.threads : 256);
+    if (!compiled) {
         hipLaunchKernelGGL((gemv_q4k_any_kernel<NT, G>), grid, block, 0, s, j);
-    } else if (nl == 1) {
-        hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, 1, 1>), grid, block, stage, s, j);
     } else if (nl == 4) {
-        hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, 4, 4>), grid, block, stage, s, j);
+        launch_q4k_nl<NT, G, 4, 4>(j, grid, block, stage, s);
     } else if (nl == 8) {
-        hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, 8, 8>), grid, block, stage, s, j);
+        launch_q4k_nl<NT, G, 8, 8>(j, grid, block, stage, s);
     } else if (nl == 14) {
-        hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, 14, 7>), grid, block, stage, s, j);
+        launch_q4k_nl<NT, G, 14, 7>(j, grid, block, stage, s);
     } else if (nl == 16) {
-        hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, 16, 8>), grid, block, stage, s, j);
+        launch_q4k_nl<NT, G, 16, 4>(j, grid, block, stage, s);
     } else {
-        hipLaunchKernelGGL((gemv_q4k_any_kernel<NT, G>), grid, block, 0, s, j);
+        launch_q4k_nl<NT, G, 28, 7>(j, grid, block, stage, s);
     }
     GLLM_HIP(hipGetLastError());
     return GLLM_OK;
-}
-
-// Lanes per AVX2 lane: the smallest G dividing the block count that puts at
-// least ~2048 waves (8 per CU) on the device.
-static int pick_g(int total_rows, int blocks) {
-    for (int g = 1; g <= 4; g *= 2)
-        if (blocks % g == 0 && (long)total_rows * 8 * g / 64 >= 2048) return g;
-    return blocks % 4 == 0 ? 4 : (blocks % 2 == 0 ? 2 : 1);
 }
 
 template <int NT>
@@ -690,10 +807,10 @@ int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t 
     if (type == GLLM_TYPE_Q4_K) {
         int total = 0;
         for (int i = 0; i < j.n; i++) total += rows[i];
-        const int g = pick_g(total, j.blocks);
-        return g == 1 ? launch_q4k<NT, 1>(j, rows, j.n, s)
-             : g == 2 ? launch_q4k<NT, 2>(j, rows, j.n, s)
-                      : launch_q4k<NT, 4>(j, rows, j.n, s);
+        const Q4KShape sh = q4k_shape(total, j.blocks);
+        return sh.g == 1 ? launch_q4k<NT, 1>(j, rows, j.n, sh, s)
+             : sh.g == 2 ? launch_q4k<NT, 2>(j, rows, j.n, sh, s)
+                         : launch_q4k<NT, 4>(j, rows, j.n, sh, s);
     }
     switch (type) {
     case GLLM_TYPE_Q6_K: hipLaunchKernelGGL(gemv_q6k_kernel<NT>, dim3(grid), dim3(256), 0, s, j); break;
@@ -714,10 +831,12 @@ int validate_weight(const gllm_hip_weight* w) {
 // Row kernels for n weights against p activation rows already quantised
 // into `act` (activation rows tok0 .. tok0+p-1 of act).
 int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* const* outs,
-             const int* strides, hipStream_t s) {
+             const int* strides, hipStream_t s, const float* xf) {
     if (n < 1 || n > 3) return fail(GLLM_EINVAL, "gemv: %d weights (1..3 supported)", n);
+    if (xf && p != 1) return fail(GLLM_EINVAL, "gemv: fused quantisation is batch 1 only");
     GemvJob j{};
     j.n = n;
+    j.xf = xf;
     const gllm_hip_weight* w0 = ws[0];
     j.blocks = w0->blocks;
     j.cols = w0->cols;
@@ -745,6 +864,36 @@ int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* 
     return GLLM_OK;
 }
 
+// True when the batch-1 row kernels for these weights quantise x themselves.
+static bool fused_quant(int n, gllm_hip_weight* const* ws) {
+    if (ws[0]->type != GLLM_TYPE_Q4_K) return false;
+    int total = 0;
+    for (int i = 0; i < n; i++) total += ws[i]->rows;
+    // every workgroup quantises the whole of x: worth it for rows up to 4096
+    // wide (one launch instead of two); wider rows pay more in-kernel work
+    // than the separate launch costs
+    if (ws[0]->cols > 4096) return false;
+    const Q4KShape sh = q4k_shape(total, ws[0]->blocks);
+    return sh.threads >= 256 && q4k_has_nl(ws[0]->blocks / sh.g) &&
+           q4k_stage_bytes(1, ws[0]->cols) <= kMaxStage;
+}
+
+// W.x for p rows of f32 activations: one fused launch at batch 1 when the
+// shape has one, else q8kQuantize + xsums into `act` (act_bytes(cols, p)
+// bytes of device scratch) followed by the row kernels.
+int gemv_f32(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float* const* outs,
+             const int* strides, void* act_buf, hipStream_t s) {
+    const int cols = ws[0]->cols;
+    if (p == 1 && fused_quant(n, ws)) {
+        ActQ8 none{};
+        return run_gemv(n, ws, none, 1, outs, strides, s, d_xs);
+    }
+    ActQ8 act;
+    act_carve(act_buf, cols, p, &act);
+    GLLM_TRY(launch_q8k_prep(d_xs, cols, p, act, s));
+    return run_gemv(n, ws, act, p, outs, strides, s, nullptr);
+}
+
 int matvec_multi(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float* const* outs,
                  const int* strides, hipStream_t s, int scratch_slot) {
     for (int i = 0; i < n; i++) GLLM_TRY(validate_weight(ws[i]));
@@ -757,13 +906,9 @@ int matvec_multi(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, fl
     if (p <= 0) return fail(GLLM_EINVAL, "p = %d", p);
     for (int i = 0; i < n; i++)
         if (strides && strides[i] < ws[i]->rows) return fail(GLLM_EINVAL, "out stride < rows");
-    const int cols = ws[0]->cols;
-    void* sc = thread_scratch(scratch_slot, act_bytes(cols, p));
+    void* sc = thread_scratch(scratch_slot, act_bytes(ws[0]->cols, p));
     if (!sc) return GLLM_ENOMEM;
-    ActQ8 act;
-    act_carve(sc, cols, p, &act);
-    GLLM_TRY(launch_q8k_prep(d_xs, cols, p, act, s));
-    return run_gemv(n, ws, act, p, outs, strides, s);
+    return gemv_f32(n, ws, d_xs, p, outs, strides, sc, s);
 }
 
 }  // namespace gllm
@@ -918,7 +1063,7 @@ int gllm_hip_matvec_q8_dev(gllm_hip_weight* w, const void* d_act, int p, float* 
     gllm_hip_weight* ws[1] = {w};
     float* outs[1] = {d_outs};
     int strides[1] = {out_stride};
-    return run_gemv(1, ws, act, p, outs, strides, (hipStream_t)stream);
+    return run_gemv(1, ws, act, p, outs, strides, (hipStream_t)stream, nullptr);
 }
 
 // Host-pointer forms: stage through pinned memory on the thread's stream.
