@@ -214,6 +214,71 @@ def cpu_baseline(weights, xh, rows, cols, seconds, torch):
                       f"{len(host)} rotating weight copies) in {el:.1f} s"}
 
 
+def decode_bench(args):
+    """synthetic Llama-3-8B-shape decoder (Q4_K layers, Q6_K
+    head), 512-token prompt, 128 greedy tokens.  Prefill and decode are
+    timed separately on a second run (the first warms buffers up); every
+    decode step returns its token to the host, as the reference's runner
+    loop consumes it (runtime.go:1129-1170)."""
+    import numpy as np
+    import torch
+
+    from gopherllm_amd import synth
+
+    cfg = dict(synth.LLAMA3_8B)
+    P, N = 512, 128
+    t0 = time.perf_counter()
+    d = synth.build_decoder(cfg, max_len=P + N, seed=1)
+    build_s = time.perf_counter() - t0
+    prompt = np.random.default_rng(2024).integers(0, cfg["vocab"], P)
+    warm = d.generate(prompt, N)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tok = d.prefill(prompt)
+    t1 = time.perf_counter()
+    toks = [tok]
+    for i in range(1, N):
+        tok = d.decode(tok, P + i - 1)
+        toks.append(tok)
+    t2 = time.perf_counter()
+    assert np.array_equal(np.array(toks, np.uint32), warm), "decode is not deterministic"
+    layer_bytes = sum(r * (c // 256) * 144 for r, c in synth.layer_shapes(cfg).values())
+    head_bytes = cfg["vocab"] * (cfg["dim"] // 256) * 210
+    kv_per_pos = cfg["n_layers"] * cfg["n_kv_heads"] * cfg["head_dim"] * 2 * 2
+    mean_ctx = P + (N - 1) / 2.0
+    tok_bytes = cfg["n_layers"] * layer_bytes + head_bytes + kv_per_pos * mean_ctx
+    dec_s = (t2 - t1) / (N - 1)
+    out = {
+        "workload": "configs[4]: Llama-3-8B-shape synthetic decoder, Q4_K layers + Q6_K head, "
+                    "prompt 512 uniform-random ids, 127 timed greedy decode steps",
+        "tok_s": round(1.0 / dec_s, 2),
+        "ms_per_token": round(dec_s * 1e3, 4),
+        "prefill_tok_s": round(P / (t1 - t0), 2),
+        "bytes_per_token": int(tok_bytes),
+        "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tok_bytes, 1),
+        "frac": round((tok_bytes / dec_s) / (HBM_PEAK_GBS * 1e9), 4),
+        "model_build_s": round(build_s, 2),
+    }
+    if not args.no_cpu_baseline:
+        from oracle import oracle as ref
+
+        m = synth.host_model(d)
+        d.release()
+        cpu = ref.Llama(m, P + N, fast=True)
+        cores = len(os.sched_getaffinity(0))
+        tok = cpu.prefill(prompt[:1])[0]
+        steps, c0 = 0, time.perf_counter()
+        while steps < 64 and (steps < 4 or time.perf_counter() - c0 < args.cpu_seconds):
+            tok = cpu.decode(tok, 1 + steps)[0]
+            steps += 1
+        el = time.perf_counter() - c0
+        out["cpu_baseline"] = {"value": round(steps / el, 3), "unit": "tok/s", "cores": cores,
+                               "kind": "port",
+                               "sample": f"{steps} greedy decode steps at positions 1..{steps} "
+                                         f"(AVX2 port of kernels_amd64.s, same weights) in {el:.1f} s"}
+    return out
+
+
 def profile_run():
     """Eager launches for rocprofv3 counter passes (no graphs, no timing):
     20 row-kernel launches over the rotating copies, then 5 plain device
@@ -253,6 +318,8 @@ def main():
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: >= 300 MB)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the configs[4] full-model decode measurement")
     args = ap.parse_args()
     if args.profile_run:
         profile_run()
@@ -262,6 +329,8 @@ def main():
               "(the path would shard by output rows, see DESIGN.md)", file=sys.stderr)
         raise SystemExit(2)
     line = run(args)
+    if not args.no_decode:
+        line["decode"] = decode_bench(args)
     print(json.dumps(line), flush=True)
 
 

@@ -998,7 +998,9 @@ gllm_hip_weight* gllm_hip_weight_from_device(const void* d_data, size_t len, int
     }
     gllm_hip_weight* w = weight_alloc(ggml_type, rows, cols, len);
     if (!w) return nullptr;
-    return weight_finish(w, (const uint8_t*)d_data, stream ? (hipStream_t)stream : thread_stream());
+    // NULL is the legacy default stream, as for every _dev entry point: the
+    // repack must be ordered after whatever produced d_data on that stream.
+    return weight_finish(w, (const uint8_t*)d_data, (hipStream_t)stream);
 }
 
 void gllm_hip_weight_release(gllm_hip_weight* w) {

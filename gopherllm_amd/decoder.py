@@ -32,6 +32,8 @@ class LlamaDecoder:
         self._cfg = c
         self.handle = call_ptr("gllm_hip_model_new", C.byref(c))
         self._weights = []
+        self._by_slot = {}  # (layer, slot) -> Weight
+        self._norms = {}    # (layer, slot) -> host copy
 
     def release(self):
         if self.handle:
@@ -50,10 +52,19 @@ class LlamaDecoder:
     def set_weight(self, layer: int, slot: int, w: Weight):
         call("gllm_hip_model_set_weight", self.handle, layer, slot, w.handle)
         self._weights.append(w)
+        self._by_slot[(layer, slot)] = w
 
     def set_norm(self, layer: int, slot: int, values):
         v = np.ascontiguousarray(values, np.float32)
         call("gllm_hip_model_set_norm", self.handle, layer, slot, v.ctypes.data_as(C.c_void_p))
+        self._norms[(layer, slot)] = v.copy()
+
+    def weights_by_slot(self):
+        """{(layer, slot): Weight}; the embedding and output sit at layer 0."""
+        return dict(self._by_slot)
+
+    def norm(self, layer: int, slot: int):
+        return self._norms[(layer, slot)]
 
     @classmethod
     def from_host_model(cls, model: dict, max_len: int) -> "LlamaDecoder":

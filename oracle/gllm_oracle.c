@@ -981,6 +981,7 @@ void ref_attend_group_f16(const float* q, const uint16_t* keys, const uint16_t* 
 struct ref_llama_state {
     ref_llama m;
     int threads;
+    int fast; /* row dots through the AVX2 port (bit-identical to the amd64 order) */
     uint16_t** kc;
     uint16_t** vc;
     float* inv_freq;
@@ -1030,6 +1031,16 @@ void ref_llama_state_free(ref_llama_state* s) {
 const uint16_t* ref_llama_kcache(ref_llama_state* s, int l) { return s->kc[l]; }
 const uint16_t* ref_llama_vcache(ref_llama_state* s, int l) { return s->vc[l]; }
 
+void ref_llama_set_fast(ref_llama_state* s, int on) { s->fast = on && ref_has_avx2(); }
+
+/* W.x in the amd64 order: the lane-level restatement, or its AVX2 port when
+ * s->fast is set (the two are bit-identical; the port is only faster). */
+static void llama_matvec(ref_llama_state* s, int type, const uint8_t* w, const float* x, int rows,
+                         int cols, float* out) {
+    if (s->fast && ref_matvec_batch_fast(type, w, x, 1, rows, cols, out, s->threads) == 0) return;
+    ref_matvec(type, w, x, rows, cols, out, REF_ORDER_AMD64, s->threads);
+}
+
 /* ForwardBodyInto (model.go:2622-2820) for the plain llama graph; leaves the
  * output-normed hidden state in s->xn. */
 static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
@@ -1042,9 +1053,9 @@ static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
     float scale = (float)(1.0 / sqrt((double)hd));
     for (int l = 0; l < m->n_layers; l++) {
         ref_rmsnorm(s->x, m->attn_norm[l], m->rms_eps, dim, s->xn);
-        ref_matvec(m->layer_type, m->wq[l], s->xn, m->n_heads * hd, dim, s->q, REF_ORDER_AMD64, s->threads);
-        ref_matvec(m->layer_type, m->wk[l], s->xn, kvd, dim, s->k, REF_ORDER_AMD64, s->threads);
-        ref_matvec(m->layer_type, m->wv[l], s->xn, kvd, dim, s->v, REF_ORDER_AMD64, s->threads);
+        llama_matvec(s, m->layer_type, m->wq[l], s->xn, m->n_heads * hd, dim, s->q);
+        llama_matvec(s, m->layer_type, m->wk[l], s->xn, kvd, dim, s->k);
+        llama_matvec(s, m->layer_type, m->wv[l], s->xn, kvd, dim, s->v);
         ref_rope_apply(s->q, hd, m->n_heads, hd / 2, s->sinv, s->cosv);
         ref_rope_apply(s->k, hd, m->n_kv_heads, hd / 2, s->sinv, s->cosv);
         ref_f32_to_f16_row(s->k, s->kc[l] + (long)pos * kvd, kvd);
@@ -1053,13 +1064,13 @@ static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
             ref_attend_group_f16(s->q + (long)g * kvmul * hd, s->kc[l] + (long)g * hd,
                                  s->vc[l] + (long)g * hd, kvmul, kvd, kvd, hd, hd, 0, pos, scale,
                                  s->attn + (long)g * kvmul * hd);
-        ref_matvec(m->layer_type, m->wo[l], s->attn, dim, m->n_heads * hd, s->proj, REF_ORDER_AMD64, s->threads);
+        llama_matvec(s, m->layer_type, m->wo[l], s->attn, dim, m->n_heads * hd, s->proj);
         for (int i = 0; i < dim; i++) s->x[i] = fmaf(s->proj[i], 1.0f, s->x[i]);
         ref_rmsnorm(s->x, m->ffn_norm[l], m->rms_eps, dim, s->xn);
-        ref_matvec(m->layer_type, m->w1[l], s->xn, m->hidden, dim, s->gate, REF_ORDER_AMD64, s->threads);
-        ref_matvec(m->layer_type, m->w3[l], s->xn, m->hidden, dim, s->up, REF_ORDER_AMD64, s->threads);
+        llama_matvec(s, m->layer_type, m->w1[l], s->xn, m->hidden, dim, s->gate);
+        llama_matvec(s, m->layer_type, m->w3[l], s->xn, m->hidden, dim, s->up);
         ref_silu_mul(s->gate, s->up, s->hidden, m->hidden);
-        ref_matvec(m->layer_type, m->w2[l], s->hidden, dim, m->hidden, s->proj, REF_ORDER_AMD64, s->threads);
+        llama_matvec(s, m->layer_type, m->w2[l], s->hidden, dim, m->hidden, s->proj);
         for (int i = 0; i < dim; i++) s->x[i] = fmaf(s->proj[i], 1.0f, s->x[i]);
     }
     ref_rmsnorm(s->x, m->out_norm, m->rms_eps, dim, s->xn);
@@ -1069,6 +1080,12 @@ static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
 uint32_t ref_llama_decode(ref_llama_state* s, uint32_t token, int pos, float* hidden_out) {
     llama_body(s, token, pos);
     if (hidden_out) memcpy(hidden_out, s->xn, sizeof(float) * s->m.dim);
+    if (s->fast) {
+        /* argmax(W.x) over finite logits, lowest index on ties, equals
+         * argmaxQ6KRowsQ8's result (kernels_amd64.go:294-331) */
+        llama_matvec(s, s->m.out_type, s->m.output, s->xn, s->m.vocab, s->m.dim, s->logits);
+        return ref_argmax_finite(s->logits, s->m.vocab);
+    }
     return ref_argmax_matvec(s->m.out_type, s->m.output, s->xn, s->m.vocab, s->m.dim,
                              REF_ORDER_AMD64, s->threads);
 }
@@ -1082,8 +1099,7 @@ uint32_t ref_llama_prefill(ref_llama_state* s, const uint32_t* tokens, int n, in
                            int chunk, float* logits_out) {
     (void)chunk;
     for (int t = 0; t < n; t++) llama_body(s, tokens[t], start_pos + t);
-    ref_matvec(s->m.out_type, s->m.output, s->xn, s->m.vocab, s->m.dim, s->logits,
-               REF_ORDER_AMD64, s->threads);
+    llama_matvec(s, s->m.out_type, s->m.output, s->xn, s->m.vocab, s->m.dim, s->logits);
     if (logits_out) memcpy(logits_out, s->logits, sizeof(float) * s->m.vocab);
     return ref_argmax_finite(s->logits, s->m.vocab);
 }

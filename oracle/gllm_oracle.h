@@ -114,6 +114,8 @@ typedef struct ref_llama {
 typedef struct ref_llama_state ref_llama_state;
 ref_llama_state* ref_llama_state_new(const ref_llama* m, int threads);
 void ref_llama_state_free(ref_llama_state* s);
+/* route the row dots through the AVX2 port (no-op without AVX2/FMA/F16C) */
+void ref_llama_set_fast(ref_llama_state* s, int on);
 /* one decode step at position pos; writes the normed final hidden state into
  * hidden_out (dim floats, may be NULL) and returns the greedy token */
 uint32_t ref_llama_decode(ref_llama_state* s, uint32_t token, int pos, float* hidden_out);

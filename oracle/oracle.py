@@ -75,6 +75,7 @@ def lib():
             "ref_attend_group_f16": (None, [vp, vp, vp, i, l, l, i, i, i, i, f, vp]),
             "ref_llama_state_new": (vp, [vp, i]),
             "ref_llama_state_free": (None, [vp]),
+            "ref_llama_set_fast": (None, [vp, i]),
             "ref_llama_decode": (C.c_uint32, [vp, C.c_uint32, i, vp]),
             "ref_llama_prefill": (C.c_uint32, [vp, vp, i, i, i, vp]),
             "ref_llama_generate": (None, [vp, vp, i, i, i, vp]),
@@ -246,6 +247,10 @@ def dot_f32_f16(a, b):
     return lib().ref_dot_f32_f16(_p(a), _p(b), min(a.size, b.size))
 
 
+def has_avx2() -> bool:
+    return bool(lib().ref_has_avx2())
+
+
 def fast_exp(x):
     return lib().ref_fast_exp(float(x))
 
@@ -312,7 +317,7 @@ class Llama:
     """Owns a ref_llama_state over a model dict produced by the tests' model
     builder (numpy arrays kept alive here)."""
 
-    def __init__(self, model, max_len, threads=0):
+    def __init__(self, model, max_len, threads=0, fast=False):
         cfg = model["config"]
         self._keep = []
         L = lib()
@@ -341,6 +346,8 @@ class Llama:
         self._s = s
         self.cfg = cfg
         self.state = L.ref_llama_state_new(C.byref(s), threads)
+        # fast: row dots through the AVX2 port (bit-identical, for full-size models)
+        L.ref_llama_set_fast(self.state, 1 if fast else 0)
 
     def close(self):
         if self.state:

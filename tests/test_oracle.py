@@ -499,3 +499,26 @@ def test_tiny_llama_greedy_is_deterministic(oracle_lib):
     # decode after prefill continues from the same cache
     nxt, hid = c.decode(tok, len(prompt))
     assert nxt == ta[1] and np.isfinite(hid).all()
+
+
+def test_tiny_llama_fast_port_identical_to_lane_restatement(oracle_lib):
+    """The AVX2-port decoder (used for full-size greedy checks) produces the
+    same tokens, hidden states and KV rows as the lane-level restatement."""
+    if not ref.has_avx2():
+        pytest.skip("host lacks AVX2/FMA/F16C")
+    for lt, ot in ((ref.Q4_K, ref.Q6_K), (ref.Q6_K, ref.Q6_K), (ref.Q8_0, ref.Q6_K)):
+        m = tiny_llama(seed=5, layer_type=lt, out_type=ot)
+        prompt = np.random.default_rng(6).integers(0, m["config"]["vocab"], 11)
+        slow = ref.Llama(m, max_len=32)
+        fast = ref.Llama(m, max_len=32, fast=True)
+        assert np.array_equal(slow.generate(prompt, 8), fast.generate(prompt, 8))
+        for l in range(m["config"]["n_layers"]):
+            assert np.array_equal(slow.kcache(l, 32), fast.kcache(l, 32))
+            assert np.array_equal(slow.vcache(l, 32), fast.vcache(l, 32))
+        s2, f2 = ref.Llama(m, max_len=32), ref.Llama(m, max_len=32, fast=True)
+        ts, ls = s2.prefill(prompt)
+        tf, lf = f2.prefill(prompt)
+        assert ts == tf and np.array_equal(ls.view(np.uint32), lf.view(np.uint32))
+        a, ha = s2.decode(ts, len(prompt))
+        b, hb = f2.decode(tf, len(prompt))
+        assert a == b and np.array_equal(ha.view(np.uint32), hb.view(np.uint32))
