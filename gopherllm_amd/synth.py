@@ -8,7 +8,7 @@ Tensors are generated on the device (gllm_hip_fill_normal_dev, a counter-based
 generator keyed by (seed, tensor)) and encoded there
 (gllm_hip_quantize_rows_dev), so a 4.4 GB model is resident in about a
 second.  `host_model` downloads the GGUF-layout bytes (undoing the upload
-repack) for the CPU oracle.
+repack) for host-side checking.
 """
 from __future__ import annotations
 
@@ -86,7 +86,7 @@ def build_decoder(cfg: dict, max_len: int, seed: int = 1) -> LlamaDecoder:
 
 def host_model(d: LlamaDecoder) -> dict:
     """GGUF-layout host copies of a decoder's weights, in the model-dict form
-    the tests' builders produce (for the CPU oracle)."""
+    the tests' builders produce (for host-side checking)."""
     import torch
 
     cfg = dict(d.config)
