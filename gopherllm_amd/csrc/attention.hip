@@ -144,6 +144,162 @@ __global__ __launch_bounds__(128) void attn_values_kernel(const float* __restric
     out[((size_t)tok * n_heads + h) * vd + d] = acc * inv_denom[(size_t)tok * n_heads + h];
 }
 
+// Exact path for head_dim 128 in two launches that keep the three-kernel
+// arithmetic (and so its results) while spreading the work over many CUs:
+//   attn_scores128_kernel  one workgroup per (kv head, 64-position chunk,
+//       query token); thread (head, position) runs the eight lanes of
+//       dotF32F16AVX2 (sequential fma chains over elements 8i + j) and the
+//       8->4->2->1 tree, then * scale.  Scores go to a global scratch row
+//       per (token, head).
+//   attn_softmax_values_kernel  one workgroup per (query head, token): the
+//       row is read into LDS, max, fastExpF32(s - max), the denominator
+//       summed in position order by one thread, then one thread per element
+//       runs out = fma(w_t, v_t, out) in position order over V tiles staged
+//       through LDS (prefetched from kernel entry), and * 1/denom.
+constexpr int kFusedHD = 128;
+constexpr int kScoreChunk = 64;   // positions per scores workgroup
+constexpr int kVTile = 64;        // positions per staged V tile (16 KB)
+constexpr int kVPrefetch = 4;     // tiles in flight per thread (registers)
+constexpr int kSmaxSpan = 6144;   // longest span the softmax/values kernel keeps in LDS (< 64 KB)
+
+__global__ __launch_bounds__(256) void attn_scores128_kernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ K, int kv_dim, int n_kv, int kvmul,
+    int start, int span0, int span_max, float scale, float* __restrict__ scores,
+    const int* __restrict__ d_end) {
+    __shared__ float qs[4 * kFusedHD];
+    const int g = blockIdx.x, chunk = blockIdx.y, tok = blockIdx.z;
+    const int tid = threadIdx.x;
+    if (d_end) span0 = *d_end - start + 1;  // position read on the device (graph replay)
+    const int span = span0 + tok;
+    if (chunk * kScoreChunk >= span) return;  // uniform
+    const int n_heads = n_kv * kvmul;
+    const float* qg = q + ((size_t)tok * n_heads + (size_t)g * kvmul) * kFusedHD;
+    for (int i = tid; i < kvmul * kFusedHD; i += 256) qs[i] = qg[i];
+    __syncthreads();
+    const int h = tid / kScoreChunk, t = chunk * kScoreChunk + tid % kScoreChunk;
+    if (h >= kvmul || t >= span) return;
+    const uint4* krow = (const uint4*)(K + (size_t)(start + t) * kv_dim + (size_t)g * kFusedHD);
+    uint4 kr[kFusedHD / 8];
+#pragma unroll
+    for (int c = 0; c < kFusedHD / 8; c++) kr[c] = krow[c];
+    const float* qh = qs + h * kFusedHD;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kFusedHD / 8; c++) {
+        const uint32_t kw[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
+        const float4 qa = *(const float4*)(qh + 8 * c);
+        const float4 qb = *(const float4*)(qh + 8 * c + 4);
+        const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            acc[j] = fmaf(f16_bits_to_f32((kw[j >> 1] >> (16 * (j & 1))) & 0xffffu), qv[j], acc[j]);
+    }
+    const float a0 = acc[0] + acc[4], a1 = acc[1] + acc[5];
+    const float a2 = acc[2] + acc[6], a3 = acc[3] + acc[7];
+    scores[((size_t)tok * n_heads + (size_t)g * kvmul + h) * span_max + t] =
+        ((a0 + a1) + (a2 + a3)) * scale;
+}
+
+__global__ __launch_bounds__(256) void attn_softmax_values_kernel(
+    const float* __restrict__ scores, const uint16_t* __restrict__ V, int kv_dim, int kvmul,
+    int start, int span0, int span_max, float* __restrict__ out, const int* __restrict__ d_end) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int h = blockIdx.x, tok = blockIdx.y, n_heads = gridDim.x;
+    const int tid = threadIdx.x;
+    if (d_end) span0 = *d_end - start + 1;
+    const int span = span0 + tok;
+    const int g = h / kvmul;
+    const int wlen = (span_max + 3) & ~3;             // keeps the V tiles 16-byte aligned
+    float* w = lds;                                   // [wlen]
+    float* red = w + wlen;                            // [8]
+    uint16_t* vt = (uint16_t*)(red + 8);              // [2][kVTile][128] f16
+    // V prefetch first: thread (position lp, quarter lc) owns 64 bytes of a
+    // tile row, kVPrefetch tiles ahead
+    const uint16_t* Vg = V + (size_t)start * kv_dim + (size_t)g * kFusedHD;
+    const int lp = tid >> 2, lc = tid & 3;
+    const int ntiles = (span + kVTile - 1) / kVTile;
+    uint4 pre[kVPrefetch][4];
+#pragma unroll
+    for (int i = 0; i < kVPrefetch; i++) {
+        const uint4* src = (const uint4*)(Vg + (size_t)min(i * kVTile + lp, span - 1) * kv_dim + 32 * lc);
+#pragma unroll
+        for (int u = 0; u < 4; u++) pre[i][u] = src[u];
+    }
+    const float* srow = scores + ((size_t)tok * n_heads + h) * span_max;
+    float m = -__int_as_float(0x7f800000);
+    for (int t = tid; t < span; t += 256) {
+        const float v = srow[t];
+        w[t] = v;
+        m = fmaxf(m, v);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int t = tid; t < span; t += 256) w[t] = fast_exp(w[t] - mx);
+    // (the first tile barrier orders the exp writes before their readers)
+    // values: threads 0..127 own one element each; thread 128 (a wave that
+    // only stages V) sums the denominator tile by tile, in position order
+    const int d = tid;
+    const bool chain = tid < kFusedHD;
+    const bool summer = tid == kFusedHD;
+    float acc = 0.0f, denom = 0.0f;
+    for (int it0 = 0; it0 < ntiles; it0 += kVPrefetch) {
+#pragma unroll
+        for (int ii = 0; ii < kVPrefetch; ii++) {
+            const int it = it0 + ii;
+            if (it >= ntiles) break;  // uniform
+            uint16_t* buf = vt + (size_t)(it & 1) * kVTile * kFusedHD;
+            uint4* dst = (uint4*)(buf + lp * kFusedHD + 32 * lc);
+#pragma unroll
+            for (int u = 0; u < 4; u++) dst[u] = pre[ii][u];
+            if (it + kVPrefetch < ntiles) {
+                const uint4* src = (const uint4*)(Vg + (size_t)min((it + kVPrefetch) * kVTile + lp, span - 1) * kv_dim + 32 * lc);
+#pragma unroll
+                for (int u = 0; u < 4; u++) pre[ii][u] = src[u];
+            }
+            wait_lgkm0();
+            lds_barrier();
+            const int base = it * kVTile;
+            const int n = min(kVTile, span - base);
+            if (chain) {
+                int p = 0;
+                for (; p + 16 <= n; p += 16) {
+                    float wv[16], vv[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) {
+                        wv[u] = w[base + p + u];
+                        vv[u] = f16_bits_to_f32(buf[(p + u) * kFusedHD + d]);
+                    }
+#pragma unroll
+                    for (int u = 0; u < 16; u++) acc = fmaf(wv[u], vv[u], acc);
+                }
+                for (; p < n; p++) acc = fmaf(w[base + p], f16_bits_to_f32(buf[p * kFusedHD + d]), acc);
+            } else if (summer) {
+                int p = 0;
+                for (; p + 16 <= n; p += 16) {
+                    float wb[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) wb[u] = w[base + p + u];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) denom = denom + wb[u];
+                }
+                for (; p < n; p++) denom = denom + w[base + p];
+            }
+        }
+    }
+    if (summer) red[4] = denom > 0.0f ? 1.0f / denom : 1.0f;
+    __syncthreads();
+    if (chain) out[((size_t)tok * n_heads + h) * kFusedHD + d] = acc * red[4];
+}
+
+static size_t smax_lds_bytes(int span_max) {
+    return ((size_t)((span_max + 3) & ~3) + 8) * 4 + 2 * (size_t)kVTile * kFusedHD * 2;
+}
+
 // --- split-K path ------------------------------------------------------------
 
 constexpr int kSplitTile = 64;  // positions per tile
@@ -267,11 +423,38 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict
 
 // Exact attention for p consecutive query tokens: token t attends
 // start .. end0 + t.  d_q / d_out: [p][n_heads][hd].
+bool attend_exact_graphable(const gllm_hip_kv* kv, int n_heads, int n_kv, int hd, int span_cap) {
+    return hd == kFusedHD && n_heads / n_kv <= 4 && kv->kv_dim_k == kv->kv_dim_v &&
+           span_cap <= kSmaxSpan;
+}
+
+// scratch: p * n_heads * span_max floats of device memory, or null for the
+// calling thread's scratch.  d_end (with p == 1): the end position is read
+// on the device and span_cap bounds the span, so the launches do not depend
+// on the position (a captured decode step replays for every position).
 int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
-                 int start, int end0, int p, float scale, float* d_out, hipStream_t s) {
+                 int start, int end0, int p, float scale, float* d_out, hipStream_t s,
+                 float* scratch, const int* d_end, int span_cap) {
     const int span0 = end0 - start + 1;
-    const int span_max = span0 + p - 1;
+    const int span_max = d_end ? span_cap : span0 + p - 1;
     const int kvmul = n_heads / n_kv;
+    if (d_end && (p != 1 || !attend_exact_graphable(kv, n_heads, n_kv, hd, span_cap)))
+        return fail(GLLM_EUNSUP, "attend: device-side positions need the head_dim 128 path");
+    if (hd == kFusedHD && kvmul <= 4 && kv->kv_dim_k == kv->kv_dim_v && span_max <= kSmaxSpan) {
+        float* sc = scratch ? scratch
+                            : (float*)thread_scratch(5, (size_t)p * n_heads * span_max * 4 + 256);
+        if (!sc) return GLLM_ENOMEM;
+        const int nchunk = (span_max + kScoreChunk - 1) / kScoreChunk;
+        hipLaunchKernelGGL(attn_scores128_kernel, dim3(n_kv, nchunk, p), dim3(256), 0, s, d_q,
+                           kv->k[l], kv->kv_dim_k, n_kv, kvmul, start, span0, span_max, scale, sc,
+                           d_end);
+        GLLM_HIP(hipGetLastError());
+        hipLaunchKernelGGL(attn_softmax_values_kernel, dim3(n_heads, p), dim3(256),
+                           smax_lds_bytes(span_max), s, sc, kv->v[l], kv->kv_dim_v, kvmul, start,
+                           span0, span_max, d_out, d_end);
+        GLLM_HIP(hipGetLastError());
+        return GLLM_OK;
+    }
     float* scr = (float*)thread_scratch(5, ((size_t)p * n_heads * (span_max + 1) + 64) * 4);
     if (!scr) return GLLM_ENOMEM;
     float* scores = scr;
@@ -326,7 +509,8 @@ int attend_dev_impl(gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n
         return fail(GLLM_EINVAL, "attend: positions %d..%d outside 0..%d", start, end, kv->max_len - 1);
     if (mode == GLLM_ATTN_SPLITK)
         return attend_splitk(kv, l, d_q, n_heads, n_kv, hd, start, end, scale, d_out, s);
-    return attend_exact(kv, l, d_q, n_heads, n_kv, hd, start, end, 1, scale, d_out, s);
+    return attend_exact(kv, l, d_q, n_heads, n_kv, hd, start, end, 1, scale, d_out, s, nullptr,
+                        nullptr, 0);
 }
 
 int kv_store_dev_impl(gllm_hip_kv* kv, int l, int pos, const float* d_k, const float* d_v,
@@ -474,7 +658,7 @@ int gllm_hip_attend_group(gllm_hip_kv* kv, int l, int kvh, const float* q, int q
     view.v = vp;
     view.layers = 1;
     GLLM_TRY(attend_exact(&view, 0, d, q_heads, 1, hd, start, end, 1, scale,
-                          d + (size_t)q_heads * hd, s));
+                          d + (size_t)q_heads * hd, s, nullptr, nullptr, 0));
     GLLM_HIP(hipMemcpyAsync(out, d + (size_t)q_heads * hd, (size_t)q_heads * vd * 4,
                             hipMemcpyDeviceToHost, s));
     GLLM_HIP(hipStreamSynchronize(s));

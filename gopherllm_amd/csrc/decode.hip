@@ -22,13 +22,19 @@
 namespace gllm {
 int gemv_f32(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float* const* outs,
              const int* strides, void* act_buf, hipStream_t s);
+int gemv_silu_f32(gllm_hip_weight* w, const float* gate, const float* up, int p, float* out,
+                  void* act_buf, float* hidden, hipStream_t s);
 int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
-                 int start, int end0, int p, float scale, float* d_out, hipStream_t s);
+                 int start, int end0, int p, float scale, float* d_out, hipStream_t s,
+                 float* scratch, const int* d_end, int span_cap);
+bool attend_exact_graphable(const gllm_hip_kv* kv, int n_heads, int n_kv, int hd, int span_cap);
 int attend_splitk(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
                   int start, int end, float scale, float* d_out, hipStream_t s);
 int kv_store_dev_impl(gllm_hip_kv* kv, int l, int pos, const float* d_k, const float* d_v,
                       hipStream_t s);
-int launch_argmax(const float* logits, int n, uint32_t* token, hipStream_t s);
+int launch_argmax(const float* logits, int n, uint32_t* token, unsigned long long* keys,
+                  hipStream_t s);
+size_t argmax_keys(int n);
 }  // namespace gllm
 
 struct gllm_hip_model {
@@ -46,8 +52,13 @@ struct gllm_hip_model {
     float *proj = nullptr, *gate = nullptr, *up = nullptr, *hidden = nullptr, *logits = nullptr;
     uint32_t* d_tokens = nullptr;
     uint32_t* h_tokens = nullptr;  // pinned
+    unsigned long long* argmax_keys = nullptr;  // argmax_keys(vocab) entries
     void* act = nullptr;           // Q8K activation buffers
     size_t act_n = 0;
+    float* scores = nullptr;       // attention scores, max_p * n_heads * max_len
+    int* d_pos = nullptr;          // decode position read by the captured decode step
+    int* h_pos = nullptr;          // pinned staging for it
+    hipGraphExec_t decode_graph = nullptr;  // one decode step, captured after a first eager step
     int last_p = 0;
 };
 
@@ -90,26 +101,72 @@ __global__ __launch_bounds__(256) void embed_q4k_kernel(const uint8_t* __restric
     }
 }
 
-// rmsNormInto per token (one workgroup per token, 256 threads).  Lanes 0..31
-// run the 4 x 8 fma accumulators of dotF32AVX2 over 32-element strides.
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
-                                                      const float* __restrict__ w, int n, float eps,
-                                                      float* __restrict__ out) {
-    const int t = blockIdx.x;
-    const float* xt = x + (size_t)t * n;
+// addInPlace (x = fma(proj, 1, x): one rounding of x + proj, model.go:3857)
+// followed by rmsNormInto (model.go:2986-3011); with proj null, the norm
+// alone.  One workgroup per token, 256 threads; every global load (x, proj
+// and the norm weights, as float4) is issued up front, and x is staged in
+// LDS so lanes 0..31, the 4 x 8 fma accumulators of dotF32AVX2 over
+// 32-element strides, run their sequential chains from LDS.  n % 4 == 0 and
+// n <= 4 * 256 * kNormVec.
+constexpr int kNormVec = 8;  // float4 per thread: n up to 8192
+
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(float* __restrict__ x,
+                                                          const float* __restrict__ proj,
+                                                          const float* __restrict__ w, int n,
+                                                          float eps, float* __restrict__ out) {
+    extern __shared__ float xs[];  // n floats
     __shared__ float part[32];
     __shared__ float s_scale;
-    const int tid = threadIdx.x;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int n4 = n >> 2;
+    float4* xt = (float4*)(x + (size_t)t * n);
+    const float4* pt = proj ? (const float4*)(proj + (size_t)t * n) : nullptr;
+    const float4* w4 = (const float4*)w;
+    float4 xv[kNormVec], pv[kNormVec], wv[kNormVec];
+#pragma unroll
+    for (int u = 0; u < kNormVec; u++) {
+        const int i = tid + 256 * u;
+        if (i < n4) {
+            xv[u] = xt[i];
+            wv[u] = w4[i];
+            if (pt) pv[u] = pt[i];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kNormVec; u++) {
+        const int i = tid + 256 * u;
+        if (i < n4) {
+            float4 v = xv[u];
+            if (pt) {
+                v.x = fmaf(pv[u].x, 1.0f, v.x);
+                v.y = fmaf(pv[u].y, 1.0f, v.y);
+                v.z = fmaf(pv[u].z, 1.0f, v.z);
+                v.w = fmaf(pv[u].w, 1.0f, v.w);
+                xt[i] = v;
+            }
+            xv[u] = v;
+            ((float4*)xs)[i] = v;
+        }
+    }
+    __syncthreads();
     const int n32 = n & ~31, n8 = n & ~7;
     if (tid < 32) {
         float y = 0.0f;
-        for (int i = 0; i < n32; i += 32) y = fmaf(xt[i + tid], xt[i + tid], y);
+        int i = 0;
+        for (; i + 16 * 32 <= n32; i += 16 * 32) {
+            float xb[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) xb[u] = xs[i + 32 * u + tid];
+#pragma unroll
+            for (int u = 0; u < 16; u++) y = fmaf(xb[u], xb[u], y);
+        }
+        for (; i < n32; i += 32) y = fmaf(xs[i + tid], xs[i + tid], y);
         part[tid] = y;
     }
     __syncthreads();
     if (tid < 8) {
         float acc = (part[tid] + part[8 + tid]) + (part[16 + tid] + part[24 + tid]);
-        for (int i = n32; i < n8; i += 8) acc = fmaf(xt[i + tid], xt[i + tid], acc);
+        for (int i = n32; i < n8; i += 8) acc = fmaf(xs[i + tid], xs[i + tid], acc);
         part[tid] = acc;
     }
     __syncthreads();
@@ -117,77 +174,60 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
         const float a0 = part[0] + part[4], a1 = part[1] + part[5];
         const float a2 = part[2] + part[6], a3 = part[3] + part[7];
         float ss = (a0 + a1) + (a2 + a3);
-        for (int i = n8; i < n; i++) ss = ss + xt[i] * xt[i];
+        for (int i = n8; i < n; i++) ss = ss + xs[i] * xs[i];
         s_scale = (float)(1.0 / sqrt((double)(ss / (float)n + eps)));
     }
     __syncthreads();
     const float scale = s_scale;
-    for (int i = tid; i < n; i += 256) out[(size_t)t * n + i] = (xt[i] * w[i]) * scale;
+    float4* o4 = (float4*)(out + (size_t)t * n);
+#pragma unroll
+    for (int u = 0; u < kNormVec; u++) {
+        const int i = tid + 256 * u;
+        if (i < n4) {
+            const float4 v = xv[u], ww = wv[u];
+            o4[i] = make_float4((v.x * ww.x) * scale, (v.y * ww.y) * scale, (v.z * ww.z) * scale,
+                                (v.w * ww.w) * scale);
+        }
+    }
 }
 
-// Interleaved RoPE on p tokens at positions pos0 + t, n_heads heads each.
-__global__ void rope_kernel(float* __restrict__ vec, int n_heads, int hd, int pos0,
-                            const float* __restrict__ sin_tab, const float* __restrict__ cos_tab) {
+// Interleaved RoPE (applyPreparedRope, model.go:3051-3093) on the q and k
+// rows of p tokens at positions pos0 + t, then storeKV (model.go:1466-1489):
+// the rotated k and the v row rounded to f16 into the cache.  Thread i owns
+// rotation pair i of q and of k and elements 2i, 2i+1 of v.
+__global__ void rope_kv_kernel(float* __restrict__ q, float* __restrict__ k,
+                               const float* __restrict__ v, int n_heads, int n_kv, int hd, int pos0,
+                               const float* __restrict__ sin_tab, const float* __restrict__ cos_tab,
+                               uint16_t* __restrict__ kd, uint16_t* __restrict__ vd,
+                               const int* __restrict__ d_pos) {
     const int t = blockIdx.y;
-    const int pairs = hd / 2;
+    if (d_pos) pos0 = *d_pos;  // position read on the device (graph replay)
+    const int pairs = hd / 2, kv_dim = n_kv * hd;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n_heads * pairs) return;
-    const int h = i / pairs, pr = i % pairs;
-    const float s = sin_tab[(size_t)(pos0 + t) * pairs + pr];
-    const float c = cos_tab[(size_t)(pos0 + t) * pairs + pr];
-    float* sub = vec + ((size_t)t * n_heads + h) * hd;
-    const float v0 = sub[2 * pr], v1 = sub[2 * pr + 1];
-    sub[2 * pr] = v0 * c - v1 * s;
-    sub[2 * pr + 1] = v0 * s + v1 * c;
-}
-
-__global__ void kv_store_batch_kernel(const float* __restrict__ k, const float* __restrict__ v,
-                                      uint16_t* __restrict__ kd, uint16_t* __restrict__ vd,
-                                      int kv_dim, int pos0) {
-    const int t = blockIdx.y;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= kv_dim) return;
-    kd[(size_t)(pos0 + t) * kv_dim + i] = f32_to_f16_bits(k[(size_t)t * kv_dim + i]);
-    vd[(size_t)(pos0 + t) * kv_dim + i] = f32_to_f16_bits(v[(size_t)t * kv_dim + i]);
-}
-
-// dst = fma(src, 1, dst): one rounding of dst + src (axpyF32AVX2 with alpha 1).
-__global__ void residual_kernel(float* __restrict__ dst, const float* __restrict__ src, size_t n) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) dst[i] = fmaf(src[i], 1.0f, dst[i]);
-}
-
-// siluMulF32AVX2, lane for lane.
-__global__ void silu_mul_kernel(const float* __restrict__ gate, const float* __restrict__ up,
-                                float* __restrict__ out, size_t n) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const float g = gate[i];
-    const float lo_clamp = __uint_as_float(0xc2b0c0a5u);  // -88.376
-    const float log2e = __uint_as_float(0x3fb8aa3bu);
-    const float c1 = __uint_as_float(0x3f318000u);        // 0.693359375
-    const float c2 = __uint_as_float(0xb95e8083u);        // -2.12194440e-4
-    const float fx_lo = __uint_as_float(0xc2fc0000u);     // -126
-    const float a = __uint_as_float(__float_as_uint(g) | 0x80000000u);  // -|g|
-    // VMAXPS returns its second source when either operand is NaN
-    const float ac = (a != a) ? lo_clamp : (a > lo_clamp ? a : lo_clamp);
-    float fx = rintf(ac * log2e);                                       // VROUNDPS $0
-    fx = (fx != fx) ? fx_lo : (fx > fx_lo ? fx : fx_lo);
-    float r = fmaf(-fx, c1, ac);
-    r = fmaf(-fx, c2, r);
-    float y = fmaf(__uint_as_float(0x39506967u), r, __uint_as_float(0x3ab743ceu));
-    y = fmaf(y, r, __uint_as_float(0x3c088908u));
-    y = fmaf(y, r, __uint_as_float(0x3d2aa9c1u));
-    y = fmaf(y, r, __uint_as_float(0x3e2aaaaau));
-    y = fmaf(y, r, __uint_as_float(0x3f000000u));
-    const float r2 = r * r;
-    y = fmaf(y, r2, r);
-    y = y + 1.0f;
-    float e = y * __uint_as_float((uint32_t)((int)fx + 127) << 23);
-    if (a < lo_clamp) e = 0.0f;
-    const float num = (__float_as_uint(g) & 0x80000000u) ? e : 1.0f;
-    const float s = num / (1.0f + e);
-    out[i] = (g * s) * up[i];
+    const int pos = pos0 + t;
+    const int pr = i % pairs;
+    const float sn = sin_tab[(size_t)pos * pairs + pr];
+    const float cs = cos_tab[(size_t)pos * pairs + pr];
+    if (i < n_heads * pairs) {
+        float* e = q + (size_t)t * n_heads * hd + 2 * i;
+        const float v0 = e[0], v1 = e[1];
+        e[0] = v0 * cs - v1 * sn;
+        e[1] = v0 * sn + v1 * cs;
+    }
+    if (i < n_kv * pairs) {
+        float* e = k + (size_t)t * kv_dim + 2 * i;
+        const float v0 = e[0], v1 = e[1];
+        const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
+        e[0] = r0;
+        e[1] = r1;
+        uint16_t* kc = kd + (size_t)pos * kv_dim + 2 * i;
+        kc[0] = f32_to_f16_bits(r0);
+        kc[1] = f32_to_f16_bits(r1);
+        const float* vr = v + (size_t)t * kv_dim + 2 * i;
+        uint16_t* vc = vd + (size_t)pos * kv_dim + 2 * i;
+        vc[0] = f32_to_f16_bits(vr[0]);
+        vc[1] = f32_to_f16_bits(vr[1]);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -195,6 +235,11 @@ __global__ void silu_mul_kernel(const float* __restrict__ gate, const float* __r
 // ---------------------------------------------------------------------------
 
 static inline int grid1(size_t n, int block) { return (int)((n + block - 1) / block); }
+
+static void drop_decode_graph(gllm_hip_model* m) {
+    if (m->decode_graph) (void)hipGraphExecDestroy(m->decode_graph);
+    m->decode_graph = nullptr;
+}
 
 static int ensure_buffers(gllm_hip_model* m, int p) {
     if (p <= m->max_p) return GLLM_OK;
@@ -217,7 +262,10 @@ static int ensure_buffers(gllm_hip_model* m, int p) {
     if (m->act) (void)hipFree(m->act);
     GLLM_HIP(hipMalloc(&m->act, an));
     m->act_n = an;
+    if (m->scores) (void)hipFree(m->scores);
+    GLLM_HIP(hipMalloc(&m->scores, (size_t)p * c.n_heads * c.max_len * 4 + 256));
     m->max_p = p;
+    drop_decode_graph(m);  // it captured the old buffers
     return GLLM_OK;
 }
 
@@ -228,18 +276,21 @@ static int matvec(gllm_hip_model* m, int n, gllm_hip_weight* const* ws, const fl
 
 // ForwardBatchInto / ForwardBodyInto for p consecutive tokens already in
 // m->d_tokens, at positions pos0 .. pos0+p-1.  Leaves the output-normed
-// hidden state of every token in m->xn.
-static int forward(gllm_hip_model* m, int pos0, int p) {
+// hidden state of every token in m->xn.  With d_pos (p == 1), the position
+// is read on the device instead, so the launches do not depend on it.
+static int forward(gllm_hip_model* m, int pos0, int p, const int* d_pos = nullptr) {
     const auto& c = m->cfg;
     hipStream_t s = m->stream;
-    const int hd = c.head_dim, kvd = c.n_kv_heads * hd, qd = c.n_heads * hd;
+    const int hd = c.head_dim, kvd = c.n_kv_heads * hd;
     const float scale = (float)(1.0 / sqrt((double)hd));
+    const size_t norm_lds = (size_t)c.dim * 4;
     hipLaunchKernelGGL(embed_q4k_kernel, dim3(p), dim3(256), 0, s, m->tok_embd->d_data,
                        m->tok_embd->row_bytes, c.dim, m->d_tokens, m->x);
     GLLM_HIP(hipGetLastError());
+    const float* pending = nullptr;  // FFN output still to be added to the residual
     for (int l = 0; l < c.n_layers; l++) {
         gllm_hip_weight** W = &m->w[(size_t)l * 7];
-        hipLaunchKernelGGL(rmsnorm_kernel, dim3(p), dim3(256), 0, s, m->x,
+        hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(p), dim3(256), norm_lds, s, m->x, pending,
                            m->d_norms + (size_t)(2 * l) * c.dim, c.dim, c.rms_eps, m->xn);
         GLLM_HIP(hipGetLastError());
         {
@@ -247,26 +298,19 @@ static int forward(gllm_hip_model* m, int pos0, int p) {
             float* outs[3] = {m->q, m->k, m->v};
             GLLM_TRY(matvec(m, 3, ws, m->xn, p, outs));
         }
-        hipLaunchKernelGGL(rope_kernel, dim3(grid1((size_t)c.n_heads * hd / 2, 256), p), dim3(256), 0,
-                           s, m->q, c.n_heads, hd, pos0, m->d_sin, m->d_cos);
-        GLLM_HIP(hipGetLastError());
-        hipLaunchKernelGGL(rope_kernel, dim3(grid1((size_t)c.n_kv_heads * hd / 2, 256), p), dim3(256),
-                           0, s, m->k, c.n_kv_heads, hd, pos0, m->d_sin, m->d_cos);
-        GLLM_HIP(hipGetLastError());
-        hipLaunchKernelGGL(kv_store_batch_kernel, dim3(grid1(kvd, 256), p), dim3(256), 0, s, m->k,
-                           m->v, gllm_hip_kv_k_dev(m->kv, l), gllm_hip_kv_v_dev(m->kv, l), kvd, pos0);
+        const int pairs = std::max(c.n_heads, c.n_kv_heads) * (hd / 2);
+        hipLaunchKernelGGL(rope_kv_kernel, dim3(grid1((size_t)pairs, 256), p), dim3(256), 0, s, m->q,
+                           m->k, m->v, c.n_heads, c.n_kv_heads, hd, pos0, m->d_sin, m->d_cos,
+                           gllm_hip_kv_k_dev(m->kv, l), gllm_hip_kv_v_dev(m->kv, l), d_pos);
         GLLM_HIP(hipGetLastError());
         GLLM_TRY(attend_exact(m->kv, l, m->q, c.n_heads, c.n_kv_heads, hd, 0, pos0, p, scale,
-                              m->attn, s));
+                              m->attn, s, m->scores, d_pos, c.max_len));
         {
             gllm_hip_weight* ws[1] = {W[GLLM_T_WO]};
             float* outs[1] = {m->proj};
             GLLM_TRY(matvec(m, 1, ws, m->attn, p, outs));
         }
-        hipLaunchKernelGGL(residual_kernel, dim3(grid1((size_t)c.dim * p, 256)), dim3(256), 0, s, m->x,
-                           m->proj, (size_t)c.dim * p);
-        GLLM_HIP(hipGetLastError());
-        hipLaunchKernelGGL(rmsnorm_kernel, dim3(p), dim3(256), 0, s, m->x,
+        hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(p), dim3(256), norm_lds, s, m->x, m->proj,
                            m->d_norms + (size_t)(2 * l + 1) * c.dim, c.dim, c.rms_eps, m->xn);
         GLLM_HIP(hipGetLastError());
         {
@@ -274,24 +318,25 @@ static int forward(gllm_hip_model* m, int pos0, int p) {
             float* outs[2] = {m->gate, m->up};
             GLLM_TRY(matvec(m, 2, ws, m->xn, p, outs));
         }
-        hipLaunchKernelGGL(silu_mul_kernel, dim3(grid1((size_t)c.hidden * p, 256)), dim3(256), 0, s,
-                           m->gate, m->up, m->hidden, (size_t)c.hidden * p);
-        GLLM_HIP(hipGetLastError());
-        {
-            gllm_hip_weight* ws[1] = {W[GLLM_T_W2]};
-            float* outs[1] = {m->proj};
-            GLLM_TRY(matvec(m, 1, ws, m->hidden, p, outs));
-        }
-        hipLaunchKernelGGL(residual_kernel, dim3(grid1((size_t)c.dim * p, 256)), dim3(256), 0, s, m->x,
-                           m->proj, (size_t)c.dim * p);
-        GLLM_HIP(hipGetLastError());
+        GLLM_TRY(gemv_silu_f32(W[GLLM_T_W2], m->gate, m->up, p, m->proj, m->act, m->hidden, s));
+        pending = m->proj;
     }
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(p), dim3(256), 0, s, m->x,
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(p), dim3(256), norm_lds, s, m->x, pending,
                        m->d_norms + (size_t)(2 * c.n_layers) * c.dim, c.dim, c.rms_eps, m->xn);
     GLLM_HIP(hipGetLastError());
-    (void)qd;
+    (void)kvd;
     m->last_p = p;
     return GLLM_OK;
+}
+
+// One greedy decode step on the token in d_tokens[0]: forward, the output
+// projection (full logits), then argmax into d_tokens[1].
+static int decode_step(gllm_hip_model* m, int pos, const int* d_pos) {
+    GLLM_TRY(forward(m, pos, 1, d_pos));
+    gllm_hip_weight* ws[1] = {m->output};
+    float* outs[1] = {m->logits};
+    GLLM_TRY(matvec(m, 1, ws, m->xn, 1, outs));
+    return launch_argmax(m->logits, m->cfg.vocab, m->d_tokens + 1, m->argmax_keys, m->stream);
 }
 
 static int check_ready(const gllm_hip_model* m) {
@@ -311,6 +356,7 @@ extern "C" {
 
 gllm_hip_model* gllm_hip_model_new(const gllm_hip_model_config* cfg) {
     if (!cfg || cfg->n_layers <= 0 || cfg->dim <= 0 || cfg->dim % 256 || cfg->hidden % 256 ||
+        cfg->dim > 4 * 256 * kNormVec ||
         cfg->n_heads <= 0 || cfg->n_kv_heads <= 0 || cfg->n_heads % cfg->n_kv_heads ||
         cfg->head_dim % 8 || cfg->head_dim > 128 || cfg->n_heads / cfg->n_kv_heads > 8 ||
         cfg->n_heads * cfg->head_dim % 256 || cfg->vocab <= 0 || cfg->max_len <= 0) {
@@ -355,6 +401,10 @@ gllm_hip_model* gllm_hip_model_new(const gllm_hip_model_config* cfg) {
     if (!m->kv) return bail("kv cache");
     if (ensure_buffers(m, 1) != GLLM_OK) return bail("activation buffers");
     if (hipMalloc(&m->logits, (size_t)cfg->vocab * 4) != hipSuccess) return bail("logits");
+    if (hipMalloc(&m->argmax_keys, argmax_keys(cfg->vocab) * 8) != hipSuccess)
+        return bail("argmax keys");
+    if (hipMalloc(&m->d_pos, 64) != hipSuccess) return bail("position");
+    if (hipHostMalloc(&m->h_pos, 64, hipHostMallocDefault) != hipSuccess) return bail("position");
     return m;
 }
 
@@ -368,6 +418,11 @@ void gllm_hip_model_release(gllm_hip_model* m) {
     if (m->d_tokens) (void)hipFree(m->d_tokens);
     if (m->h_tokens) (void)hipHostFree(m->h_tokens);
     if (m->act) (void)hipFree(m->act);
+    if (m->argmax_keys) (void)hipFree(m->argmax_keys);
+    drop_decode_graph(m);
+    if (m->scores) (void)hipFree(m->scores);
+    if (m->d_pos) (void)hipFree(m->d_pos);
+    if (m->h_pos) (void)hipHostFree(m->h_pos);
     if (m->kv) gllm_hip_kv_release(m->kv);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
@@ -375,6 +430,7 @@ void gllm_hip_model_release(gllm_hip_model* m) {
 
 int gllm_hip_model_set_weight(gllm_hip_model* m, int layer, int slot, gllm_hip_weight* w) {
     if (!m || !w) return fail(GLLM_EINVAL, "gllm_hip_model_set_weight: null argument");
+    drop_decode_graph(m);
     const auto& c = m->cfg;
     const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
     int rows = 0, cols = 0;
@@ -421,14 +477,33 @@ int gllm_hip_model_decode(gllm_hip_model* m, uint32_t token, int pos, uint32_t* 
     if (token >= (uint32_t)m->cfg.vocab) return fail(GLLM_EINVAL, "token %u out of range", token);
     hipStream_t s = m->stream;
     m->h_tokens[0] = token;
+    m->h_pos[0] = pos;
     GLLM_HIP(hipMemcpyAsync(m->d_tokens, m->h_tokens, 4, hipMemcpyHostToDevice, s));
-    GLLM_TRY(forward(m, pos, 1));
-    {
-        gllm_hip_weight* ws[1] = {m->output};
-        float* outs[1] = {m->logits};
-        GLLM_TRY(matvec(m, 1, ws, m->xn, 1, outs));
+    GLLM_HIP(hipMemcpyAsync(m->d_pos, m->h_pos, 4, hipMemcpyHostToDevice, s));
+    if (m->decode_graph) {
+        GLLM_HIP(hipGraphLaunch(m->decode_graph, s));
+    } else {
+        // The first step runs eagerly (and leaves every buffer it needs
+        // allocated); the same launches, reading the position on the device,
+        // are then captured and replayed for every later step.
+        GLLM_TRY(decode_step(m, pos, nullptr));
+        const auto& c = m->cfg;
+        if (attend_exact_graphable(m->kv, c.n_heads, c.n_kv_heads, c.head_dim, c.max_len)) {
+            hipGraph_t g = nullptr;
+            GLLM_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            const int rc = decode_step(m, 0, m->d_pos);
+            const hipError_t ec = hipStreamEndCapture(s, &g);
+            if (rc != GLLM_OK) {
+                if (g) (void)hipGraphDestroy(g);
+                return rc;
+            }
+            GLLM_HIP(ec);
+            const hipError_t ei = hipGraphInstantiate(&m->decode_graph, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (ei != hipSuccess) m->decode_graph = nullptr;
+            GLLM_HIP(ei);
+        }
     }
-    GLLM_TRY(launch_argmax(m->logits, m->cfg.vocab, m->d_tokens + 1, s));
     GLLM_HIP(hipMemcpyAsync(m->h_tokens + 1, m->d_tokens + 1, 4, hipMemcpyDeviceToHost, s));
     GLLM_HIP(hipStreamSynchronize(s));
     *next = m->h_tokens[1];
@@ -462,7 +537,7 @@ int gllm_hip_model_prefill(gllm_hip_model* m, const uint32_t* tokens, int n, int
         float* outs[1] = {m->logits};
         GLLM_TRY(matvec(m, 1, ws, last, 1, outs));
     }
-    GLLM_TRY(launch_argmax(m->logits, m->cfg.vocab, m->d_tokens + m->max_p, s));
+    GLLM_TRY(launch_argmax(m->logits, m->cfg.vocab, m->d_tokens + m->max_p, m->argmax_keys, s));
     GLLM_HIP(hipMemcpyAsync(m->h_tokens + m->max_p, m->d_tokens + m->max_p, 4, hipMemcpyDeviceToHost, s));
     if (logits)
         GLLM_HIP(hipMemcpyAsync(logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost, s));

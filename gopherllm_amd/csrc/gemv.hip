@@ -133,30 +133,6 @@ struct MinSel {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Direct global->LDS copies issued from inline assembly.  The compiler does
-// not see them as outstanding vector-memory operations, which is the point:
-// they are issued before the weight prefetch and retire first (in order), so
-// its vmcnt waits for the weight registers stay exact, and the kernel waits
-// for the copies itself (vmcnt <= number of weight loads) before s_barrier.
-// M0 holds the wave's LDS destination; lane i writes M0 + 16*i (4*i).
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-__device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds_dst) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-                 :
-                 : "v"(gsrc), "s"(lds_dst)
-                 : "memory", "m0");
-}
-
-__device__ __forceinline__ void lds_copy4(const void* gsrc, uint32_t lds_dst) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
-                 :
-                 : "v"(gsrc), "s"(lds_dst)
-                 : "memory", "m0");
-}
-
 // Stage this launch's activations (q8, xs32, xscale of ntok tokens) into LDS
 // with lds_copy16 / lds_copy4.  Layout: [NT*cols q8][NT*cols/32 xs32][NT*B
 // xscale].  Every byte range is a multiple of the copy width.
@@ -180,29 +156,6 @@ __device__ __forceinline__ void stage_act_asm(const GemvJob& j, uint8_t* smem) {
     const int sbytes = nt * B * 4;
     for (int base = wave * 256; base < sbytes; base += nw * 256)
         if (base + lane * 4 < sbytes) lds_copy4(gs + base + lane * 4, lds_addr(ss + base));
-}
-
-// s_waitcnt vmcnt(N) for a compile-time N (gfx9 encoding: vmcnt bits [3:0]
-// and [15:14], expcnt [6:4] and lgkmcnt [11:8] left unconstrained).
-template <int N>
-__device__ __forceinline__ void wait_vmem_le() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// s_waitcnt lgkmcnt(0) with vmcnt and expcnt unconstrained.
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
-
-// Workgroup barrier for LDS data that leaves outstanding global loads in
-// flight: the caller has waited for its own LDS traffic; the empty asm
-// statements keep the compiler from moving memory operations across it (a
-// memory fence would drain the weight prefetch as well).
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::: "memory");
 }
 
 // ---------------------------------------------------------------------------
@@ -624,33 +577,67 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int r) {
     return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)r);
 }
 
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
-                                                      uint32_t* __restrict__ token) {
-    unsigned long long best = 0;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float v = logits[i];
-        if (finite_logit(v)) {
-            const unsigned long long key = argmax_key(v, i);
-            best = key > best ? key : best;
-        }
-    }
+// Two stages: 256-thread workgroups each reduce kArgmaxChunk logits to one
+// key, then one workgroup reduces the keys.  Keys compare larger for a
+// larger finite value, or the same value at a lower row, so the result is
+// the lowest-index maximum regardless of the reduction order.
+constexpr int kArgmaxChunk = 4096;
+
+__device__ __forceinline__ unsigned long long wg_max_key(unsigned long long best) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         const unsigned long long o = __shfl_xor(best, off);
         best = o > best ? o : best;
     }
     __shared__ unsigned long long wbest[16];
+    const int nw = blockDim.x >> 6;
     if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned long long b = 0;
-        for (int i = 0; i < 16; i++) b = wbest[i] > b ? wbest[i] : b;
-        *token = b ? 0xffffffffu - (uint32_t)(b & 0xffffffffu) : 0u;
-    }
+    unsigned long long b = 0;
+    for (int i = 0; i < nw; i++) b = wbest[i] > b ? wbest[i] : b;
+    return b;
 }
 
-int launch_argmax(const float* logits, int n, uint32_t* token, hipStream_t s) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, n, token);
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ logits,
+                                                             int n,
+                                                             unsigned long long* __restrict__ keys) {
+    const int lo = blockIdx.x * kArgmaxChunk;
+    const int hi = min(n, lo + kArgmaxChunk);
+    unsigned long long best = 0;
+    for (int i = lo + threadIdx.x; i < hi; i += 256) {
+        const float v = logits[i];
+        if (finite_logit(v)) {
+            const unsigned long long key = argmax_key(v, i);
+            best = key > best ? key : best;
+        }
+    }
+    best = wg_max_key(best);
+    if (threadIdx.x == 0) keys[blockIdx.x] = best;
+}
+
+__global__ __launch_bounds__(1024) void argmax_final_kernel(const unsigned long long* __restrict__ keys,
+                                                            int nk, uint32_t* __restrict__ token) {
+    unsigned long long best = 0;
+    for (int i = threadIdx.x; i < nk; i += 1024) best = keys[i] > best ? keys[i] : best;
+    best = wg_max_key(best);
+    if (threadIdx.x == 0) *token = best ? 0xffffffffu - (uint32_t)(best & 0xffffffffu) : 0u;
+}
+
+__global__ void silu_mul_rows_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                     float* __restrict__ out, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = silu_mul(gate[i], up[i]);
+}
+
+size_t argmax_keys(int n) { return (size_t)(n + kArgmaxChunk - 1) / kArgmaxChunk; }
+
+// keys: device scratch of argmax_keys(n) entries.
+int launch_argmax(const float* logits, int n, uint32_t* token, unsigned long long* keys,
+                  hipStream_t s) {
+    const int nk = (int)argmax_keys(n);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(nk), dim3(256), 0, s, logits, n, keys);
+    GLLM_HIP(hipGetLastError());
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1024), 0, s, keys, nk, token);
     GLLM_HIP(hipGetLastError());
     return GLLM_OK;
 }
@@ -865,7 +852,7 @@ int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* 
 }
 
 // True when the batch-1 row kernels for these weights quantise x themselves.
-static bool fused_quant(int n, gllm_hip_weight* const* ws) {
+bool fused_quant(int n, gllm_hip_weight* const* ws) {
     if (ws[0]->type != GLLM_TYPE_Q4_K) return false;
     int total = 0;
     for (int i = 0; i < n; i++) total += ws[i]->rows;
@@ -892,6 +879,27 @@ int gemv_f32(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float*
     act_carve(act_buf, cols, p, &act);
     GLLM_TRY(launch_q8k_prep(d_xs, cols, p, act, s));
     return run_gemv(n, ws, act, p, outs, strides, s, nullptr);
+}
+
+// W.siluMulF32(gate, up) for p rows (the FFN down projection): the SwiGLU is
+// evaluated inside the Q8K quantiser when the row kernel takes pre-quantised
+// activations; a fused-quantisation shape gets it materialised in `hidden`
+// first.
+int gemv_silu_f32(gllm_hip_weight* w, const float* gate, const float* up, int p, float* out,
+                  void* act_buf, float* hidden, hipStream_t s) {
+    gllm_hip_weight* ws[1] = {w};
+    float* outs[1] = {out};
+    if (p == 1 && fused_quant(1, ws)) {
+        const size_t n = (size_t)w->cols;
+        hipLaunchKernelGGL(silu_mul_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                           gate, up, hidden, n);
+        GLLM_HIP(hipGetLastError());
+        return gemv_f32(1, ws, hidden, 1, outs, nullptr, act_buf, s);
+    }
+    ActQ8 act;
+    act_carve(act_buf, w->cols, p, &act);
+    GLLM_TRY(launch_q8k_prep_silu(gate, up, w->cols, p, act, s));
+    return run_gemv(1, ws, act, p, outs, nullptr, s, nullptr);
 }
 
 int matvec_multi(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float* const* outs,
@@ -1137,9 +1145,9 @@ int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token,
     float* outs[1] = {logits};
     int strides[1] = {w->rows};
     GLLM_TRY(matvec_multi(1, ws, d_x, 1, outs, strides, s, 0));
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, w->rows, d_token);
-    GLLM_HIP(hipGetLastError());
-    return GLLM_OK;
+    auto* keys = (unsigned long long*)thread_scratch(7, argmax_keys(w->rows) * 8);
+    if (!keys) return GLLM_ENOMEM;
+    return launch_argmax(logits, w->rows, d_token, keys, s);
 }
 
 int gllm_hip_argmax(gllm_hip_weight* w, const float* x, uint32_t* token) {

@@ -49,6 +49,9 @@ struct ActQ8 {
 size_t act_bytes(int cols, int p);
 void act_carve(void* base, int cols, int p, ActQ8* a);
 int launch_q8k_prep(const float* d_x, int cols, int p, const ActQ8& a, hipStream_t s);
+// Same, for the activation siluMulF32(gate, up) computed on the fly.
+int launch_q8k_prep_silu(const float* d_gate, const float* d_up, int cols, int p, const ActQ8& a,
+                         hipStream_t s);
 
 struct WeightDesc;  // defined in gemv.hip
 
@@ -107,6 +110,84 @@ __device__ __forceinline__ float tree8(float v) {
     v = v + __shfl_xor(v, 1, 8);
     v = v + __shfl_xor(v, 2, 8);
     return v;
+}
+
+// siluMulF32AVX2 (kernels_amd64.s:1630-1700) for one element, lane for lane:
+// the Cephes exp of -|g| with the reference's constants, then
+// (g * (g < 0 ? e : 1) / (1 + e)) * up.
+__device__ __forceinline__ float silu_mul(float g, float up) {
+    const float lo_clamp = __uint_as_float(0xc2b0c0a5u);  // -88.376
+    const float log2e = __uint_as_float(0x3fb8aa3bu);
+    const float c1 = __uint_as_float(0x3f318000u);        // 0.693359375
+    const float c2 = __uint_as_float(0xb95e8083u);        // -2.12194440e-4
+    const float fx_lo = __uint_as_float(0xc2fc0000u);     // -126
+    const float a = __uint_as_float(__float_as_uint(g) | 0x80000000u);  // -|g|
+    // VMAXPS returns its second source when either operand is NaN
+    const float ac = (a != a) ? lo_clamp : (a > lo_clamp ? a : lo_clamp);
+    float fx = rintf(ac * log2e);                                       // VROUNDPS $0
+    fx = (fx != fx) ? fx_lo : (fx > fx_lo ? fx : fx_lo);
+    float r = fmaf(-fx, c1, ac);
+    r = fmaf(-fx, c2, r);
+    float y = fmaf(__uint_as_float(0x39506967u), r, __uint_as_float(0x3ab743ceu));
+    y = fmaf(y, r, __uint_as_float(0x3c088908u));
+    y = fmaf(y, r, __uint_as_float(0x3d2aa9c1u));
+    y = fmaf(y, r, __uint_as_float(0x3e2aaaaau));
+    y = fmaf(y, r, __uint_as_float(0x3f000000u));
+    const float r2 = r * r;
+    y = fmaf(y, r2, r);
+    y = y + 1.0f;
+    float e = y * __uint_as_float((uint32_t)((int)fx + 127) << 23);
+    if (a < lo_clamp) e = 0.0f;
+    const float num = (__float_as_uint(g) & 0x80000000u) ? e : 1.0f;
+    const float s = num / (1.0f + e);
+    return (g * s) * up;
+}
+
+// Direct global->LDS copies issued from inline assembly.  The compiler does
+// not see them as outstanding vector-memory operations, which is the point:
+// they are issued before the weight prefetch and retire first (in order), so
+// its vmcnt waits for the weight registers stay exact, and the kernel waits
+// for the copies itself (vmcnt <= number of weight loads) before s_barrier.
+// M0 holds the wave's LDS destination; lane i writes M0 + 16*i (4*i).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+__device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds_dst) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gsrc), "s"(lds_dst)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void lds_copy4(const void* gsrc, uint32_t lds_dst) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+                 :
+                 : "v"(gsrc), "s"(lds_dst)
+                 : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) for a compile-time N (gfx9 encoding: vmcnt bits [3:0]
+// and [15:14], expcnt [6:4] and lgkmcnt [11:8] left unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmem_le() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// s_waitcnt lgkmcnt(0) with vmcnt and expcnt unconstrained.
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Workgroup barrier for LDS data that leaves outstanding global loads in
+// flight: the caller has waited for its own LDS traffic; the empty asm
+// statements keep the compiler from moving memory operations across it (a
+// memory fence would drain the weight prefetch as well).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
 }
 
 }  // namespace gllm

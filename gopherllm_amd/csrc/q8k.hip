@@ -34,15 +34,19 @@ void act_carve(void* base, int cols, int p, ActQ8* a) {
 }
 
 // plain == true writes q8 in element order (the debug entry point) instead of
-// the lane-permuted order.
+// the lane-permuted order.  With `up` set, the activation is
+// siluMulF32(x, up) (the FFN's SwiGLU), evaluated here instead of in a launch
+// of its own.
 __global__ __launch_bounds__(256) void q8k_prep_kernel(const float* __restrict__ x, int cols,
                                                        ActQ8 a, int8_t* __restrict__ plain_q8,
-                                                       float* __restrict__ plain_scale) {
+                                                       float* __restrict__ plain_scale,
+                                                       const float* __restrict__ up) {
     const int b = blockIdx.x, t = blockIdx.y, e = threadIdx.x;
     const int nb = cols / 256;
     __shared__ float sx[256];
     __shared__ float wmax[4];
-    const float v = x[(size_t)t * cols + (size_t)b * 256 + e];
+    const size_t idx = (size_t)t * cols + (size_t)b * 256 + e;
+    const float v = up ? silu_mul(x[idx], up[idx]) : x[idx];
     sx[e] = v;
     // amax over the block; v_max_f32 is IEEE maxNum, so a NaN element is
     // skipped exactly like the reference's `a > amax` scan.
@@ -90,7 +94,17 @@ int launch_q8k_prep(const float* d_x, int cols, int p, const ActQ8& a, hipStream
     if (cols <= 0 || cols % 256 || p <= 0) return fail(GLLM_EINVAL, "q8k: cols %d p %d", cols, p);
     dim3 grid(cols / 256, p);
     hipLaunchKernelGGL(q8k_prep_kernel, grid, dim3(256), 0, s, d_x, cols, a, (int8_t*)nullptr,
-                       (float*)nullptr);
+                       (float*)nullptr, (const float*)nullptr);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+int launch_q8k_prep_silu(const float* d_gate, const float* d_up, int cols, int p, const ActQ8& a,
+                         hipStream_t s) {
+    if (cols <= 0 || cols % 256 || p <= 0) return fail(GLLM_EINVAL, "q8k: cols %d p %d", cols, p);
+    dim3 grid(cols / 256, p);
+    hipLaunchKernelGGL(q8k_prep_kernel, grid, dim3(256), 0, s, d_gate, cols, a, (int8_t*)nullptr,
+                       (float*)nullptr, d_up);
     GLLM_HIP(hipGetLastError());
     return GLLM_OK;
 }
@@ -106,7 +120,7 @@ extern "C" int gllm_hip_q8k_quantize_dev(const float* d_x, int cols, int p, int8
     ActQ8 a{};
     dim3 grid(cols / 256, p);
     hipLaunchKernelGGL(q8k_prep_kernel, grid, dim3(256), 0, (hipStream_t)stream, d_x, cols, a,
-                       d_q8, d_scales);
+                       d_q8, d_scales, (const float*)nullptr);
     GLLM_HIP(hipGetLastError());
     return GLLM_OK;
 }
