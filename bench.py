@@ -279,6 +279,110 @@ def decode_bench(args):
     return out
 
 
+def suite(args):
+    """One JSON line per measured workload of the other configs:
+    configs[1] GEMVs (Q4_K / Q6_K / Q8_0, gate/up and down shapes, batch 1
+    and 8), configs[2] batched prefill (p = 512 activation rows), configs[3]
+    decode attention (ctx 4096 and 32768, exact and split-K).  Weights rotate
+    over >= 300 MB; every timing is a HIP-graph replay on the launch stream."""
+    import torch
+
+    import gopherllm_amd as g
+
+    g.load()
+    qnames = {g.TYPE_Q4_K: "Q4_K", g.TYPE_Q6_K: "Q6_K", g.TYPE_Q8_0: "Q8_0"}
+
+    def graph_time(body, reps):
+        graph = timed_graph(torch, body, 1)
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3  # us per replay
+
+    def weights_for(qtype, rows, cols, min_bytes=300e6):
+        wb = rows * g.row_bytes(qtype, cols)
+        copies = max(2, math.ceil(min_bytes / wb))
+        tmp = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+        raw = torch.empty(wb, dtype=torch.uint8, device="cuda")
+        ws = []
+        for c in range(copies):
+            g.fill_normal_dev(tmp, 2000 + c, 0.02)
+            g.quantize_rows_dev(qtype, tmp, raw)
+            ws.append(g.Weight.from_device(raw, qtype, rows, cols))
+        torch.cuda.synchronize()
+        return ws, wb
+
+    for qtype in (g.TYPE_Q4_K, g.TYPE_Q6_K, g.TYPE_Q8_0):
+        for rows, cols in ((14336, 4096), (4096, 14336)):
+            ws, wb = weights_for(qtype, rows, cols)
+            for p in (1, 8):
+                x = torch.empty((p, cols), dtype=torch.float32, device="cuda")
+                g.fill_normal_dev(x, 7, 1.0)
+                out = torch.empty((p, rows), dtype=torch.float32, device="cuda")
+
+                def body():
+                    for w in ws:
+                        w.matvec_dev(x, out)
+
+                us = graph_time(body, 20) / len(ws)
+                nbytes = wb + p * (4 * cols + 4 * rows)
+                print(json.dumps({"suite": "configs[1] gemv", "type": qnames[qtype], "rows": rows,
+                                  "cols": cols, "batch": p, "us": round(us, 3),
+                                  "GB_s": round(nbytes / us / 1e3, 1),
+                                  "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
+            del ws
+
+    for rows, cols in ((4096, 4096), (14336, 4096)):
+        ws, wb = weights_for(g.TYPE_Q4_K, rows, cols, min_bytes=0)
+        P = 512
+        x = torch.empty((P, cols), dtype=torch.float32, device="cuda")
+        g.fill_normal_dev(x, 9, 1.0)
+        out = torch.empty((P, rows), dtype=torch.float32, device="cuda")
+
+        def body():
+            ws[0].matvec_dev(x, out)
+
+        us = graph_time(body, 5)
+        ops = 2.0 * P * rows * cols
+        print(json.dumps({"suite": "configs[2] prefill", "type": "Q4_K", "rows": rows,
+                          "cols": cols, "tokens": P, "us": round(us, 1),
+                          "TOPS": round(ops / us / 1e6, 2),
+                          "frac_int8_mfma": round(ops / us / 1e6 / 5000.0, 4)}), flush=True)
+        del ws
+
+    n_heads, n_kv, hd = 32, 8, 128
+    for ctx in (4096, 32768):
+        kv = g.KVCacheF16(1, n_kv * hd, n_kv * hd, ctx)
+        k = torch.empty(ctx * n_kv * hd, dtype=torch.float32, device="cuda")
+        v = torch.empty_like(k)
+        g.fill_normal_dev(k, 11, 1.0)
+        g.fill_normal_dev(v, 12, 1.0)
+        kd = n_kv * hd
+        for pos in range(ctx):
+            kv.store_kv_dev(0, pos, k[pos * kd:(pos + 1) * kd], v[pos * kd:(pos + 1) * kd])
+        torch.cuda.synchronize()
+        q = torch.empty(n_heads * hd, dtype=torch.float32, device="cuda")
+        g.fill_normal_dev(q, 13, 1.0)
+        out = torch.empty(n_heads * hd, dtype=torch.float32, device="cuda")
+        nbytes = ctx * n_kv * hd * 2 * 2
+        for mode, name in ((g.ATTN_SPLITK, "split-K"), (g.ATTN_EXACT, "exact")):
+            def body():
+                kv.attend_dev(0, q, n_heads, n_kv, hd, 0, ctx - 1, 1.0 / math.sqrt(hd), out,
+                              mode=mode)
+
+            us = graph_time(body, 20)
+            print(json.dumps({"suite": "configs[3] attention", "ctx": ctx, "mode": name,
+                              "us": round(us, 2), "GB_s": round(nbytes / us / 1e3, 1),
+                              "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
+        kv.release()
+
+
 def profile_run():
     """Eager launches for rocprofv3 counter passes (no graphs, no timing):
     20 row-kernel launches over the rotating copies, then 5 plain device
@@ -310,6 +414,8 @@ def profile_run():
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--suite", action="store_true",
+                    help="measure the other configs (GEMV types/shapes/batch 8, prefill, attention)")
     ap.add_argument("--profile-run", action="store_true",
                     help="eager launches for rocprofv3 counter collection")
     ap.add_argument("--gpus", type=int, default=1)
@@ -323,6 +429,9 @@ def main():
     args = ap.parse_args()
     if args.profile_run:
         profile_run()
+        return
+    if args.suite:
+        suite(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "

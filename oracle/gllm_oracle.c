@@ -1060,6 +1060,8 @@ static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
         ref_rope_apply(s->k, hd, m->n_kv_heads, hd / 2, s->sinv, s->cosv);
         ref_f32_to_f16_row(s->k, s->kc[l] + (long)pos * kvd, kvd);
         ref_f32_to_f16_row(s->v, s->vc[l] + (long)pos * kvd, kvd);
+        /* kv groups are independent; each keeps its own sequential order */
+#pragma omp parallel for schedule(static) num_threads(s->threads > 0 ? s->threads : ref_num_threads()) if (pos >= 64)
         for (int g = 0; g < m->n_kv_heads; g++)
             ref_attend_group_f16(s->q + (long)g * kvmul * hd, s->kc[l] + (long)g * hd,
                                  s->vc[l] + (long)g * hd, kvmul, kvd, kvd, hd, hd, 0, pos, scale,
