@@ -19,6 +19,8 @@
 
 namespace gllm {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 // fastExpF32 (fastmath.go:47-77), operation for operation.
 __device__ __forceinline__ float fast_exp(float x) {
     if (x > 88.02969f) return __int_as_float(0x7f800000);
@@ -202,7 +204,9 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
         ((a0 + a1) + (a2 + a3)) * scale;
 }
 
-__global__ __launch_bounds__(256) void attn_softmax_values_kernel(
+// (four waves per SIMD are plenty for one workgroup per head: the 128-VGPR
+// budget keeps the V prefetch registers out of scratch)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void attn_softmax_values_kernel(
     const float* __restrict__ scores, const uint16_t* __restrict__ V, int kv_dim, int kvmul,
     int start, int span0, int span_max, float* __restrict__ out, const int* __restrict__ d_end) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -220,13 +224,16 @@ __global__ __launch_bounds__(256) void attn_softmax_values_kernel(
     const uint16_t* Vg = V + (size_t)start * kv_dim + (size_t)g * kFusedHD;
     const int lp = tid >> 2, lc = tid & 3;
     const int ntiles = (span + kVTile - 1) / kVTile;
-    uint4 pre[kVPrefetch][4];
+    u32x4 pre0[4], pre1[4], pre2[4], pre3[4];
+    auto first = [&](int i, u32x4 (&pr)[4]) __attribute__((always_inline)) {
+        const u32x4* src = (const u32x4*)(Vg + (size_t)min(i * kVTile + lp, span - 1) * kv_dim + 32 * lc);
 #pragma unroll
-    for (int i = 0; i < kVPrefetch; i++) {
-        const uint4* src = (const uint4*)(Vg + (size_t)min(i * kVTile + lp, span - 1) * kv_dim + 32 * lc);
-#pragma unroll
-        for (int u = 0; u < 4; u++) pre[i][u] = src[u];
-    }
+        for (int u = 0; u < 4; u++) pr[u] = src[u];
+    };
+    first(0, pre0);
+    first(1, pre1);
+    first(2, pre2);
+    first(3, pre3);
     const float* srow = scores + ((size_t)tok * n_heads + h) * span_max;
     float m = -__int_as_float(0x7f800000);
     for (int t = tid; t < span; t += 256) {
@@ -247,49 +254,53 @@ __global__ __launch_bounds__(256) void attn_softmax_values_kernel(
     const bool chain = tid < kFusedHD;
     const bool summer = tid == kFusedHD;
     float acc = 0.0f, denom = 0.0f;
-    for (int it0 = 0; it0 < ntiles; it0 += kVPrefetch) {
+    // one V tile: stage it from registers, refill those registers kVPrefetch
+    // tiles ahead, then run the chains over it
+    auto tile = [&](int it, u32x4 (&pr)[4]) __attribute__((always_inline)) {
+        uint16_t* buf = vt + (size_t)(it & 1) * kVTile * kFusedHD;
+        u32x4* dst = (u32x4*)(buf + lp * kFusedHD + 32 * lc);
 #pragma unroll
-        for (int ii = 0; ii < kVPrefetch; ii++) {
-            const int it = it0 + ii;
-            if (it >= ntiles) break;  // uniform
-            uint16_t* buf = vt + (size_t)(it & 1) * kVTile * kFusedHD;
-            uint4* dst = (uint4*)(buf + lp * kFusedHD + 32 * lc);
+        for (int u = 0; u < 4; u++) dst[u] = pr[u];
+        if (it + kVPrefetch < ntiles) {
+            const u32x4* src = (const u32x4*)(Vg + (size_t)min((it + kVPrefetch) * kVTile + lp, span - 1) * kv_dim + 32 * lc);
 #pragma unroll
-            for (int u = 0; u < 4; u++) dst[u] = pre[ii][u];
-            if (it + kVPrefetch < ntiles) {
-                const uint4* src = (const uint4*)(Vg + (size_t)min((it + kVPrefetch) * kVTile + lp, span - 1) * kv_dim + 32 * lc);
-#pragma unroll
-                for (int u = 0; u < 4; u++) pre[ii][u] = src[u];
-            }
-            wait_lgkm0();
-            lds_barrier();
-            const int base = it * kVTile;
-            const int n = min(kVTile, span - base);
-            if (chain) {
-                int p = 0;
-                for (; p + 16 <= n; p += 16) {
-                    float wv[16], vv[16];
-#pragma unroll
-                    for (int u = 0; u < 16; u++) {
-                        wv[u] = w[base + p + u];
-                        vv[u] = f16_bits_to_f32(buf[(p + u) * kFusedHD + d]);
-                    }
-#pragma unroll
-                    for (int u = 0; u < 16; u++) acc = fmaf(wv[u], vv[u], acc);
-                }
-                for (; p < n; p++) acc = fmaf(w[base + p], f16_bits_to_f32(buf[p * kFusedHD + d]), acc);
-            } else if (summer) {
-                int p = 0;
-                for (; p + 16 <= n; p += 16) {
-                    float wb[16];
-#pragma unroll
-                    for (int u = 0; u < 16; u++) wb[u] = w[base + p + u];
-#pragma unroll
-                    for (int u = 0; u < 16; u++) denom = denom + wb[u];
-                }
-                for (; p < n; p++) denom = denom + w[base + p];
-            }
+            for (int u = 0; u < 4; u++) pr[u] = src[u];
         }
+        wait_lgkm0();
+        lds_barrier();
+        const int base = it * kVTile;
+        const int n = min(kVTile, span - base);
+        if (chain) {
+            int p = 0;
+            for (; p + 16 <= n; p += 16) {
+                float wv[16], vv[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) {
+                    wv[u] = w[base + p + u];
+                    vv[u] = f16_bits_to_f32(buf[(p + u) * kFusedHD + d]);
+                }
+#pragma unroll
+                for (int u = 0; u < 16; u++) acc = fmaf(wv[u], vv[u], acc);
+            }
+            for (; p < n; p++) acc = fmaf(w[base + p], f16_bits_to_f32(buf[p * kFusedHD + d]), acc);
+        } else if (summer) {
+            int p = 0;
+            for (; p + 16 <= n; p += 16) {
+                float wb[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) wb[u] = w[base + p + u];
+#pragma unroll
+                for (int u = 0; u < 16; u++) denom = denom + wb[u];
+            }
+            for (; p < n; p++) denom = denom + w[base + p];
+        }
+    };
+    static_assert(kVPrefetch == 4, "tile calls below name each prefetch slot");
+    for (int it0 = 0; it0 < ntiles; it0 += kVPrefetch) {
+        tile(it0, pre0);  // it0 < ntiles
+        if (it0 + 1 < ntiles) tile(it0 + 1, pre1);
+        if (it0 + 2 < ntiles) tile(it0 + 2, pre2);
+        if (it0 + 3 < ntiles) tile(it0 + 3, pre3);
     }
     if (summer) red[4] = denom > 0.0f ? 1.0f / denom : 1.0f;
     __syncthreads();
@@ -400,6 +411,213 @@ __global__ __launch_bounds__(256) void attn_splitk_kernel(const float* __restric
     }
 }
 
+// Split-K kernel for head_dim 128 and 4 query heads per kv head (Llama-3
+// GQA).  Workgroup = 4 waves on one (kv head g, chunk of positions); each wave
+// streams its own contiguous run of 16-position tiles:
+//   lane = 16*rg + seg: rows rg, rg+4, rg+8, rg+12 of a tile, dims 8*seg..+7
+//   (one 16-byte load per row, a 256-byte K or V row per 16 lanes), with the
+//   next tile's K and V loads in flight while the current one is used;
+//   q for the lane's 8 dims and 4 heads stays in registers;
+//   the 16 (row, head) partial dots of a lane are transpose-reduced over its
+//   16-lane row group with DPP (ror 8, half mirror, quad perms), leaving lane
+//   seg with the score of row 4*(seg>>2)+rg, head seg&3;
+//   online softmax per head, weights broadcast to the row group through LDS;
+//   o[4 heads][8 dims] accumulated per lane, reduced over rg at the end.
+// The 4 waves' (max, sum, o) are merged in LDS into one partial per chunk.
+constexpr int kSkTile = 16;
+constexpr int kSkWaves = 4;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ void f16x8_to_f32(const uint4 r, float* f) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        f[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+        f[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+    }
+}
+
+// one halving step of the 16-lane transpose-reduce: lanes whose `bit` is set
+// keep the upper half of v, the DPP partner (which has the bit clear) the
+// lower half
+template <int N, int CTRL>
+__device__ __forceinline__ void tr_step(float* v, bool upper) {
+#pragma unroll
+    for (int j = 0; j < N / 2; j++) {
+        const float keep = upper ? v[j + N / 2] : v[j];
+        const float send = upper ? v[j] : v[j + N / 2];
+        v[j] = keep + dpp_f<CTRL>(send);
+    }
+}
+
+__device__ __forceinline__ float wave_head_max(float x) {
+    x = fmaxf(x, dpp_f<0x124>(x));  // row_ror:4
+    x = fmaxf(x, dpp_f<0x128>(x));  // row_ror:8
+    x = fmaxf(x, __shfl_xor(x, 16));
+    return fmaxf(x, __shfl_xor(x, 32));
+}
+
+__device__ __forceinline__ float wave_head_sum(float x) {
+    x += dpp_f<0x124>(x);
+    x += dpp_f<0x128>(x);
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
+}
+
+__global__ __launch_bounds__(256) void attn_splitk_g4_kernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    int kv_dim, int start, int span, int chunk, float scale, float* __restrict__ part_m,
+    float* __restrict__ part_l, float* __restrict__ part_o) {
+    constexpr int HD = 128, KM = 4;
+    const float ninf = -__int_as_float(0x7f800000);
+    const int g = blockIdx.y, c = blockIdx.x, nchunks = gridDim.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rg = lane >> 4, seg = lane & 15;
+    const int wspan = chunk / kSkWaves;
+    const int p0 = c * chunk + wave * wspan;  // relative to start
+    const int p1 = min(span, p0 + wspan);
+    __shared__ __align__(16) float wl[kSkWaves][64];
+    __shared__ float sm[kSkWaves][KM], sl[kSkWaves][KM];
+    __shared__ __align__(16) float so[kSkWaves][KM][HD];
+
+    float qv[KM][8];
+#pragma unroll
+    for (int h = 0; h < KM; h++) {
+        const float4* qp = (const float4*)(q + ((size_t)g * KM + h) * HD + 8 * seg);
+        const float4 a = qp[0], b = qp[1];
+        qv[h][0] = a.x; qv[h][1] = a.y; qv[h][2] = a.z; qv[h][3] = a.w;
+        qv[h][4] = b.x; qv[h][5] = b.y; qv[h][6] = b.z; qv[h][7] = b.w;
+    }
+    float o[KM][8];
+#pragma unroll
+    for (int h = 0; h < KM; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[h][e] = 0.0f;
+    float m_run = ninf, l_run = 0.0f;  // head seg & 3
+
+    const size_t col = (size_t)g * HD + 8 * seg;
+    auto load_tile = [&](int pb, uint4* kr, uint4* vr) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int pos = pb + 4 * i + rg;
+            const size_t row = (size_t)start + (pos < p1 ? pos : p0);
+            kr[i] = *(const uint4*)(K + row * kv_dim + col);
+            vr[i] = *(const uint4*)(V + row * kv_dim + col);
+        }
+    };
+    if (p0 < p1) {
+        uint4 kc[4], vc[4];
+        load_tile(p0, kc, vc);
+        for (int pb = p0; pb < p1; pb += kSkTile) {
+            uint4 kn[4], vn[4];
+            const bool more = pb + kSkTile < p1;
+            if (more) load_tile(pb + kSkTile, kn, vn);
+            // partial dots: v[4*i + h] = sum over this lane's 8 dims
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float kf[8];
+                f16x8_to_f32(kc[i], kf);
+#pragma unroll
+                for (int h = 0; h < KM; h++) {
+                    float acc = qv[h][0] * kf[0];
+#pragma unroll
+                    for (int e = 1; e < 8; e++) acc = fmaf(qv[h][e], kf[e], acc);
+                    v[4 * i + h] = acc;
+                }
+            }
+            tr_step<16, 0x128>(v, seg & 8);  // row_ror:8       (partner seg ^ 8)
+            tr_step<8, 0x141>(v, seg & 4);   // row_half_mirror (partner seg ^ 7)
+            tr_step<4, 0x1B>(v, seg & 2);    // quad_perm 3210  (partner seg ^ 3)
+            tr_step<2, 0xB1>(v, seg & 1);    // quad_perm 1032  (partner seg ^ 1)
+            const int pos = pb + 4 * (seg >> 2) + rg;
+            const float sc = pos < p1 ? v[0] * scale : ninf;
+            const float m_new = fmaxf(m_run, wave_head_max(sc));
+            const float alpha = m_run == ninf ? 0.0f : fast_exp(m_run - m_new);
+            const float w = m_new == ninf ? 0.0f : fast_exp(sc - m_new);
+            l_run = fmaf(l_run, alpha, wave_head_sum(w));
+            m_run = m_new;
+            // lane h (rg 0, seg h) holds head h's rescale factor
+            float al[KM];
+#pragma unroll
+            for (int h = 0; h < KM; h++)
+                al[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), h));
+            if (!(al[0] == 1.0f && al[1] == 1.0f && al[2] == 1.0f && al[3] == 1.0f)) {
+#pragma unroll
+                for (int h = 0; h < KM; h++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) o[h][e] *= al[h];
+            }
+            wl[wave][lane] = w;
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 wi = *(const float4*)&wl[wave][16 * rg + 4 * i];
+                const float wh[KM] = {wi.x, wi.y, wi.z, wi.w};
+                float vf[8];
+                f16x8_to_f32(vc[i], vf);
+#pragma unroll
+                for (int h = 0; h < KM; h++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) o[h][e] = fmaf(wh[h], vf[e], o[h][e]);
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (more) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    kc[i] = kn[i];
+                    vc[i] = vn[i];
+                }
+            }
+        }
+    }
+    // reduce o over the four row groups
+#pragma unroll
+    for (int h = 0; h < KM; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float x = o[h][e];
+            x += __shfl_xor(x, 16);
+            x += __shfl_xor(x, 32);
+            o[h][e] = x;
+        }
+    if (rg == 0) {
+#pragma unroll
+        for (int h = 0; h < KM; h++) {
+            *(float4*)&so[wave][h][8 * seg] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+            *(float4*)&so[wave][h][8 * seg + 4] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+        }
+    }
+    if (lane < KM) {
+        sm[wave][lane] = m_run;
+        sl[wave][lane] = l_run;
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    const int h = t >> 6, d = 2 * (t & 63);
+    float M = ninf;
+#pragma unroll
+    for (int w = 0; w < kSkWaves; w++) M = fmaxf(M, sm[w][h]);
+    float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kSkWaves; w++) {
+        const float f = sl[w][h] > 0.0f ? fast_exp(sm[w][h] - M) : 0.0f;
+        L = fmaf(sl[w][h], f, L);
+        O0 = fmaf(so[w][h][d], f, O0);
+        O1 = fmaf(so[w][h][d + 1], f, O1);
+    }
+    const size_t hc = ((size_t)g * KM + h) * nchunks + c;
+    *(float2*)&part_o[hc * HD + d] = make_float2(O0, O1);
+    if ((t & 63) == 0) {
+        part_m[hc] = M;
+        part_l[hc] = L;
+    }
+}
+
 __global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict__ part_m,
                                                          const float* __restrict__ part_l,
                                                          const float* __restrict__ part_o,
@@ -419,6 +637,60 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict
         O = fmaf(part_o[((size_t)h * nchunks + c) * hd + d], a, O);
     }
     out[(size_t)h * hd + d] = O * (1.0f / L);
+}
+
+// Merge of split-K partials, one workgroup per (head, 32-dim quarter): the
+// chunk factors exp(m_c - M) are computed once into LDS, then 8 thread groups
+// each sum every 8th chunk (independent loads in flight) and are combined.
+constexpr int kMergeMaxChunks = 2048;
+
+__global__ __launch_bounds__(256) void attn_merge2_kernel(const float* __restrict__ part_m,
+                                                          const float* __restrict__ part_l,
+                                                          const float* __restrict__ part_o,
+                                                          int nchunks, int hd,
+                                                          float* __restrict__ out) {
+    const float ninf = -__int_as_float(0x7f800000);
+    const int h = blockIdx.x, t = threadIdx.x;
+    const float* pm = part_m + (size_t)h * nchunks;
+    const float* pl = part_l + (size_t)h * nchunks;
+    __shared__ float f[kMergeMaxChunks];
+    __shared__ float red[8];
+    __shared__ float acc[8][32];
+    float m = ninf;
+    for (int c = t; c < nchunks; c += 256) m = fmaxf(m, pm[c]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((t & 63) == 0) red[t >> 6] = m;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float lsum = 0.0f;
+    for (int c = t; c < nchunks; c += 256) {
+        const float l = pl[c];
+        const float fc = l > 0.0f ? fast_exp(pm[c] - M) : 0.0f;
+        f[c] = fc;
+        lsum = fmaf(l, fc, lsum);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
+    __syncthreads();
+    if ((t & 63) == 0) red[4 + (t >> 6)] = lsum;
+    __syncthreads();
+    const float L = (red[4] + red[5]) + (red[6] + red[7]);
+    const int d = blockIdx.y * 32 + (t & 31), cg = t >> 5;
+    float o = 0.0f;
+    if (d < hd) {
+        const float* po = part_o + (size_t)h * nchunks * hd + d;
+#pragma unroll 8
+        for (int c = cg; c < nchunks; c += 8) o = fmaf(po[(size_t)c * hd], f[c], o);
+    }
+    acc[cg][t & 31] = o;
+    __syncthreads();
+    if (t < 32 && d < hd) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) sum += acc[j][t];
+        out[(size_t)h * hd + d] = sum * (1.0f / L);
+    }
 }
 
 // Exact attention for p consecutive query tokens: token t attends
@@ -478,6 +750,27 @@ int attend_splitk(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, i
     if (hd != 128) return fail(GLLM_EUNSUP, "split-K attention is built for head_dim 128");
     const int span = end - start + 1;
     const int kvmul = n_heads / n_kv;
+    if (kvmul == 4 && kv->kv_dim_k == kv->kv_dim_v) {
+        // about four workgroups per CU, chunks a multiple of 4 waves x 16 rows
+        const int quantum = kSkWaves * kSkTile;
+        const int target = std::min(kMergeMaxChunks, std::max(1, 4 * device_cus() / n_kv));
+        int chunk = (span + target - 1) / target;
+        chunk = std::max(quantum, (chunk + quantum - 1) / quantum * quantum);
+        const int nchunks = (span + chunk - 1) / chunk;  // <= target <= kMergeMaxChunks
+        const size_t nh = (size_t)n_heads;
+        float* scr = (float*)thread_scratch(6, (nh * nchunks * (2 + hd) + 64) * 4);
+        if (!scr) return GLLM_ENOMEM;
+        float* pm = scr;
+        float* pl = pm + nh * nchunks;
+        float* po = pl + nh * nchunks;
+        hipLaunchKernelGGL(attn_splitk_g4_kernel, dim3(nchunks, n_kv), dim3(256), 0, s, d_q,
+                           kv->k[l], kv->v[l], kv->kv_dim_k, start, span, chunk, scale, pm, pl, po);
+        GLLM_HIP(hipGetLastError());
+        hipLaunchKernelGGL(attn_merge2_kernel, dim3(n_heads, (hd + 31) / 32), dim3(256), 0, s, pm,
+                           pl, po, nchunks, hd, d_out);
+        GLLM_HIP(hipGetLastError());
+        return GLLM_OK;
+    }
     // chunk so that n_kv * nchunks covers the device several times over
     int nchunks = std::max(1, std::min(512 / std::max(1, n_kv), (span + kSplitTile - 1) / kSplitTile));
     int chunk = (span + nchunks - 1) / nchunks;

@@ -716,20 +716,6 @@ static void launch_q4k_nl(const GemvJob& j, dim3 grid, dim3 block, size_t stage,
 // Blocks per lane with a compiled row kernel (and its prefetch depth).
 static bool q4k_has_nl(int nl) { return nl == 4 || nl == 8 || nl == 14 || nl == 16 || nl == 28; }
 
-// Compute units of the current device (cached per device).
-static int device_cus() {
-    static int cus[64];
-    int d = 0;
-    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 256;
-    if (!cus[d]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || n <= 0)
-            n = 256;
-        cus[d] = n;
-    }
-    return cus[d];
-}
-
 // Launch shape of the Q4_K row kernel: one workgroup per compute unit, so a
 // CU's activation staging is the first memory traffic it issues (a second
 // workgroup's small activation reads would queue behind the first one's

@@ -33,6 +33,8 @@ int check(hipError_t e, const char* what);
 
 // Per-thread stream used by the blocking host entry points.
 hipStream_t thread_stream();
+// Compute units of the current device (cached per device).
+int device_cus();
 // Per-thread growable device scratch (slot 0..7).
 void* thread_scratch(int slot, size_t bytes);
 // Per-thread pinned host staging buffer.

@@ -68,6 +68,20 @@ void reset_if_device_changed() {
 
 }  // namespace
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+    static int cus[64];
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 256;
+    if (!cus[d]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || n <= 0)
+            n = 256;
+        cus[d] = n;
+    }
+    return cus[d];
+}
+
 hipStream_t thread_stream() {
     reset_if_device_changed();
     if (!t_res.stream) {
