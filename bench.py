@@ -291,6 +291,7 @@ def suite(args):
 
     g.load()
     qnames = {g.TYPE_Q4_K: "Q4_K", g.TYPE_Q6_K: "Q6_K", g.TYPE_Q8_0: "Q8_0"}
+    only = set(args.only.split(",")) if args.only else {"gemv", "prefill", "attention"}
 
     def graph_time(body, reps):
         graph = timed_graph(torch, body, 1)
@@ -318,7 +319,7 @@ def suite(args):
         torch.cuda.synchronize()
         return ws, wb
 
-    for qtype in (g.TYPE_Q4_K, g.TYPE_Q6_K, g.TYPE_Q8_0):
+    for qtype in (g.TYPE_Q4_K, g.TYPE_Q6_K, g.TYPE_Q8_0) if "gemv" in only else ():
         for rows, cols in ((14336, 4096), (4096, 14336)):
             ws, wb = weights_for(qtype, rows, cols)
             for p in (1, 8):
@@ -338,7 +339,7 @@ def suite(args):
                                   "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
             del ws
 
-    for rows, cols in ((4096, 4096), (14336, 4096)):
+    for rows, cols in ((4096, 4096), (14336, 4096)) if "prefill" in only else ():
         ws, wb = weights_for(g.TYPE_Q4_K, rows, cols, min_bytes=0)
         P = 512
         x = torch.empty((P, cols), dtype=torch.float32, device="cuda")
@@ -357,7 +358,9 @@ def suite(args):
         del ws
 
     n_heads, n_kv, hd = 32, 8, 128
-    for ctx in (4096, 32768):
+    for ctx in (4096, 32768) if "attention" in only else ():
+        if args.ctx and ctx != args.ctx:
+            continue
         kv = g.KVCacheF16(1, n_kv * hd, n_kv * hd, ctx)
         k = torch.empty(ctx * n_kv * hd, dtype=torch.float32, device="cuda")
         v = torch.empty_like(k)
@@ -416,6 +419,9 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--suite", action="store_true",
                     help="measure the other configs (GEMV types/shapes/batch 8, prefill, attention)")
+    ap.add_argument("--only", default="",
+                    help="suite parts to run: comma list of gemv, prefill, attention")
+    ap.add_argument("--ctx", type=int, default=0, help="suite attention: only this context")
     ap.add_argument("--profile-run", action="store_true",
                     help="eager launches for rocprofv3 counter collection")
     ap.add_argument("--gpus", type=int, default=1)

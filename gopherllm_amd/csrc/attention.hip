@@ -751,9 +751,19 @@ int attend_splitk(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, i
     const int span = end - start + 1;
     const int kvmul = n_heads / n_kv;
     if (kvmul == 4 && kv->kv_dim_k == kv->kv_dim_v) {
-        // about four workgroups per CU, chunks a multiple of 4 waves x 16 rows
+        // one round of resident workgroups (no ragged second round), chunks a
+        // multiple of 4 waves x 16 rows
+        static int per_cu = 0;
+        if (!per_cu) {
+            int n = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_splitk_g4_kernel, 256, 0) !=
+                    hipSuccess || n <= 0)
+                n = 2;
+            per_cu = n;
+        }
         const int quantum = kSkWaves * kSkTile;
-        const int target = std::min(kMergeMaxChunks, std::max(1, 4 * device_cus() / n_kv));
+        const int target =
+            std::min(kMergeMaxChunks, std::max(1, per_cu * device_cus() / n_kv));
         int chunk = (span + target - 1) / target;
         chunk = std::max(quantum, (chunk + quantum - 1) / quantum * quantum);
         const int nchunks = (span + chunk - 1) / chunk;  // <= target <= kMergeMaxChunks

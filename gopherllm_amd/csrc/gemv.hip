@@ -18,6 +18,7 @@ namespace gllm {
 
 constexpr int kRowsPerWG = 32;  // 256 threads / 8 lanes per row
 constexpr int kMaxTok = 8;      // activation rows per launch
+constexpr int kMfmaMinTok = 16; // Q4_K batches from this size run on the matrix cores
 
 struct GemvJob {
     const uint8_t* w[3];
@@ -826,6 +827,13 @@ int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* 
     }
     j.wg_begin[n] = wg;
     if (wg == 0) return GLLM_OK;
+    if (w0->type == GLLM_TYPE_Q4_K && p >= kMfmaMinTok) {
+        // batched prefill: matrix-core products, same bits as the row kernel
+        for (int i = 0; i < n; i++)
+            GLLM_TRY(launch_q4k_mfma(ws[i]->d_data, ws[i]->row_bytes, ws[i]->rows, ws[i]->blocks,
+                                     act, p, outs[i], j.out_stride[i], s));
+        return GLLM_OK;
+    }
     for (int t0 = 0; t0 < p; t0 += kMaxTok) {
         j.tok0 = t0;
         j.ntok = std::min(kMaxTok, p - t0);

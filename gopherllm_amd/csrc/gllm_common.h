@@ -51,6 +51,10 @@ struct ActQ8 {
 size_t act_bytes(int cols, int p);
 void act_carve(void* base, int cols, int p, ActQ8* a);
 int launch_q8k_prep(const float* d_x, int cols, int p, const ActQ8& a, hipStream_t s);
+// Batched Q4_K x Q8_K on the matrix cores (bit-identical to the row kernel):
+// out[t * out_stride + r] for p activation rows.
+int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
+                    float* out, int out_stride, hipStream_t s);
 // Same, for the activation siluMulF32(gate, up) computed on the fly.
 int launch_q8k_prep_silu(const float* d_gate, const float* d_up, int cols, int p, const ActQ8& a,
                          hipStream_t s);

@@ -1,0 +1,270 @@
+// prefill.hip -- batched Q4_K x Q8_K products on the matrix cores.
+//
+// matvecBatchQ8 (kernels_amd64.go:470-581) runs the batch-1 row kernel
+// q4kDotQ8KRow (kernels_amd64.s:437-543) once per (row, token), so a batched
+// result must equal the per-token one bit for bit.  That kernel keeps eight
+// AVX2 lanes per row; lane k owns the 32 elements {32j + 4k + i : j < 8,
+// i < 4} of every 256-element block b and runs two float chains over b:
+//   accF[k] = fma(float(I_bk), d_b * xscale_b, accF[k])
+//   accM[k] = fma(dmin_b, float(m_bk) * xsum_bk, accM[k])
+// with the exact integer I_bk = sum over its 32 elements of sc_j * q4 * q8,
+// and ends with tree8(accF - accM).
+//
+// Here I_bk comes from v_mfma_f32_16x16x32_f16: the A operand holds
+// sc_j * q4 (<= 63 * 15 = 945, exact in f16), the B operand q8 (exact in
+// f16), and every partial sum of 32 products stays below 2^24, so the fp32
+// accumulation is exact in any order and equals the int32 lane sum.  The
+// float chains then run per (row, token, lane) in VALU registers in the
+// reference's order.
+//
+// K order: lane k's elements are numbered kappa = 4j + i, which is the order
+// of the lane-permuted Q8K activations (q8perm_offset) and, for the weights,
+// of the upload repack: lane k's 16 nibble bytes sit at 16 + 16k, byte
+// 4s + i holding elements kappa = 8s + i (low nibble, sub-block 2s) and
+// 8s + 4 + i (high nibble, sub-block 2s + 1).  MFMA lane L supplies
+// kappa = 8(L/16) .. 8(L/16) + 7 of both operands, i.e. one weight dword.
+//
+// Workgroup: 8 waves, 64 weight rows x 32 tokens; wave w owns the 16x16
+// tile of rows 16 (w % 4) .. + 15 and tokens 16 (w / 4) .. + 15.  Per block the workgroup
+// stages the 32 tokens' q8 (as f16), xsums and xscales and the 64 rows'
+// decoded scales/mins in LDS (double-buffered); each wave reads its own
+// weight dwords from global memory.
+#include "gllm_common.h"
+
+namespace gllm {
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+constexpr int kPfRows = 64;
+constexpr int kPfTok = 32;
+constexpr int kPfBStride = 528;  // bytes per token row of the f16 q8 tile: 512 + 16 (no bank conflicts)
+
+struct PfStage {
+    uint8_t b16[kPfTok * kPfBStride];
+    float xsum[8][kPfTok];     // [lane k][token]
+    float xsc[kPfTok];
+    uint32_t sch[kPfRows][8];  // half2(sc_j, sc_j)
+    uint32_t scn[kPfRows][8];  // half2(-1024 sc_j, -1024 sc_j)
+    float m[8][kPfRows];       // [lane k][row]
+    float d[kPfRows];
+    float dmin[kPfRows];
+};
+
+// four signed bytes -> two half2 words holding the same integers
+__device__ __forceinline__ void i8x4_to_h(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const uint32_t u = w ^ 0x80808080u;  // c + 128, as unsigned bytes
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x05010400u);  // 1024 + u0, 1024 + u1
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x05030402u);  // 1024 + u2, 1024 + u3
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    const h2v bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    h2v ha = __builtin_bit_cast(h2v, a) + bias;  // exact: integers below 2048
+    h2v hb = __builtin_bit_cast(h2v, b) + bias;
+    lo = __builtin_bit_cast(uint32_t, ha);
+    hi = __builtin_bit_cast(uint32_t, hb);
+}
+
+// one weight dword (4 nibble bytes of one lane and sub-block pair) -> the
+// 8 f16 A values sc_lo * low nibbles, sc_hi * high nibbles
+__device__ __forceinline__ h8v dequant_a(uint32_t w, uint32_t sch_lo, uint32_t scn_lo,
+                                         uint32_t sch_hi, uint32_t scn_hi) {
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+    const h2v p0 = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, lo, 0x05010400u));
+    const h2v p1 = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, lo, 0x05030402u));
+    const h2v p2 = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, hi, 0x05010400u));
+    const h2v p3 = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, hi, 0x05030402u));
+    const h2v sl = __builtin_bit_cast(h2v, sch_lo), nl = __builtin_bit_cast(h2v, scn_lo);
+    const h2v sh = __builtin_bit_cast(h2v, sch_hi), nh = __builtin_bit_cast(h2v, scn_hi);
+    // (1024 + q) * sc - 1024 * sc == q * sc exactly: one rounding of an exact
+    // value below 2048
+    const h2v a0 = __builtin_elementwise_fma(p0, sl, nl);
+    const h2v a1 = __builtin_elementwise_fma(p1, sl, nl);
+    const h2v a2 = __builtin_elementwise_fma(p2, sh, nh);
+    const h2v a3 = __builtin_elementwise_fma(p3, sh, nh);
+    h8v r;
+    r[0] = a0[0]; r[1] = a0[1]; r[2] = a1[0]; r[3] = a1[1];
+    r[4] = a2[0]; r[5] = a2[1]; r[6] = a3[0]; r[7] = a3[1];
+    return r;
+}
+
+struct PfArgs {
+    const uint8_t* w;  // repacked Q4_K rows
+    size_t rb;         // bytes per row
+    int rows, blocks;
+    ActQ8 act;         // p tokens of Q8K activations
+    int p;
+    float* out;        // out[t * out_stride + r]
+    int out_stride;
+};
+
+// staging registers of one block (512 threads): thread (token tid/16, part
+// tid%16) carries 16 q8 bytes; threads 0..63 one xsum quad; threads 0..31 one
+// xscale; thread (row tid/8, sub-block tid%8) its row's 16-byte block header.
+struct PfRegs {
+    u4v q;
+    f4v xs;
+    float xc;
+    u4v h;
+};
+
+__device__ __forceinline__ void pf_load(const PfArgs& a, int row0, int tok0, int b, PfRegs& r) {
+    const int tid = threadIdx.x;
+    const int cols = a.blocks * 256;
+    {
+        const int t = min(tok0 + (tid >> 4), a.p - 1);
+        r.q = *(const u4v*)(a.act.q8perm + (size_t)t * cols + (size_t)b * 256 + 16 * (tid & 15));
+    }
+    if (tid < 64) {
+        const int t = min(tok0 + (tid >> 1), a.p - 1);
+        r.xs = *(const f4v*)(a.act.xs32 + (size_t)t * (cols / 32) + b * 8 + 4 * (tid & 1));
+    }
+    if (tid < kPfTok) r.xc = a.act.xscale[(size_t)min(tok0 + tid, a.p - 1) * a.blocks + b];
+    {
+        const int row = min(row0 + (tid >> 3), a.rows - 1);
+        r.h = *(const u4v*)(a.w + (size_t)row * a.rb + (size_t)b * 144);
+    }
+}
+
+__device__ __forceinline__ void pf_store(const PfRegs& r, PfStage& st) {
+    const int tid = threadIdx.x;
+    {
+        uint32_t v[8];
+        i8x4_to_h(r.q.x, v[0], v[1]);
+        i8x4_to_h(r.q.y, v[2], v[3]);
+        i8x4_to_h(r.q.z, v[4], v[5]);
+        i8x4_to_h(r.q.w, v[6], v[7]);
+        u4v* dst = (u4v*)(st.b16 + (tid >> 4) * kPfBStride + 32 * (tid & 15));
+        dst[0] = u4v{v[0], v[1], v[2], v[3]};
+        dst[1] = u4v{v[4], v[5], v[6], v[7]};
+    }
+    if (tid < 64) {
+        const int t = tid >> 1, k0 = 4 * (tid & 1);
+        st.xsum[k0][t] = r.xs.x;
+        st.xsum[k0 + 1][t] = r.xs.y;
+        st.xsum[k0 + 2][t] = r.xs.z;
+        st.xsum[k0 + 3][t] = r.xs.w;
+    }
+    if (tid < kPfTok) st.xsc[tid] = r.xc;
+    {
+        // getScaleMinK4 (simd.go:1672-1677) for sub-block j
+        const int row = tid >> 3, j = tid & 7;
+        const uint32_t s03 = r.h.y, s47 = r.h.z, s811 = r.h.w;
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = (s03 >> (8 * j)) & 63u;
+            mn = (s47 >> (8 * j)) & 63u;
+        } else {
+            const int jj = j - 4;
+            const uint32_t b8 = (s811 >> (8 * jj)) & 0xffu;
+            sc = (b8 & 15u) | (((s03 >> (8 * jj + 6)) & 3u) << 4);
+            mn = (b8 >> 4) | (((s47 >> (8 * jj + 6)) & 3u) << 4);
+        }
+        const _Float16 hs = (_Float16)(float)sc, hn = (_Float16)(-1024.0f * (float)sc);
+        const uint32_t bs = __builtin_bit_cast(uint16_t, hs), bn = __builtin_bit_cast(uint16_t, hn);
+        st.sch[row][j] = bs | (bs << 16);
+        st.scn[row][j] = bn | (bn << 16);
+        st.m[j][row] = (float)mn;
+        if (j == 0) {
+            st.d[row] = f16_bits_to_f32(r.h.x & 0xffffu);
+            st.dmin[row] = f16_bits_to_f32(r.h.x >> 16);
+        }
+    }
+}
+
+__global__ __launch_bounds__(512, 2) void prefill_q4k_mfma_kernel(PfArgs a) {
+    __shared__ __align__(16) PfStage stage[2];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int rw = wave & 3, tw = wave >> 2;  // 16-row group, 16-token column
+    const int row0 = blockIdx.x * kPfRows, tok0 = blockIdx.y * kPfTok;
+    // this lane's A row (MFMA row c of the wave's 16) and its weight dwords
+    const int arow = min(row0 + 16 * rw + c, a.rows - 1);
+    const uint8_t* wrow = a.w + (size_t)arow * a.rb + 16 + 4 * g;
+    // D layout: rows 4g + i of the wave's 16, token c of its column
+    const int lr = 16 * rw + 4 * g;
+    const int lt = 16 * tw + c;
+
+    float accF[4][8], accM[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int k = 0; k < 8; k++) accF[i][k] = accM[i][k] = 0.0f;
+
+    PfRegs regs;
+    pf_load(a, row0, tok0, 0, regs);
+    uint32_t wq[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) wq[k] = *(const uint32_t*)(wrow + 16 * k);
+    pf_store(regs, stage[0]);
+    __syncthreads();
+
+    for (int b = 0; b < a.blocks; b++) {
+        const PfStage& st = stage[b & 1];
+        const bool more = b + 1 < a.blocks;
+        uint32_t wn[8];
+        if (more) {
+            pf_load(a, row0, tok0, b + 1, regs);
+#pragma unroll
+            for (int k = 0; k < 8; k++) wn[k] = *(const uint32_t*)(wrow + (size_t)(b + 1) * 144 + 16 * k);
+        }
+        const uint32_t sh_lo = st.sch[16 * rw + c][2 * g], sn_lo = st.scn[16 * rw + c][2 * g];
+        const uint32_t sh_hi = st.sch[16 * rw + c][2 * g + 1], sn_hi = st.scn[16 * rw + c][2 * g + 1];
+        // F chain factors d * xscale per D row
+        const f4v dv = *(const f4v*)&st.d[lr];
+        const f4v dm = *(const f4v*)&st.dmin[lr];
+        const float xc = st.xsc[lt];
+        float dxs[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) dxs[i] = dv[i] * xc;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const h8v av = dequant_a(wq[k], sh_lo, sn_lo, sh_hi, sn_hi);
+            const h8v bv = *(const h8v*)(st.b16 + lt * kPfBStride + 64 * k + 16 * g);
+            const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+            const f4v dI = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, z, 0, 0, 0);
+            // M chain operands: mins of the lane's 4 D rows, xsum of its token
+            const f4v mk = *(const f4v*)&st.m[k][lr];
+            const float xk = st.xsum[k][lt];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                accF[i][k] = fmaf(dI[i], dxs[i], accF[i][k]);
+                const float mx = mk[i] * xk;
+                accM[i][k] = fmaf(dm[i], mx, accM[i][k]);
+            }
+        }
+        if (more) {
+            pf_store(regs, stage[(b + 1) & 1]);
+#pragma unroll
+            for (int k = 0; k < 8; k++) wq[k] = wn[k];
+        }
+        __syncthreads();
+    }
+    // tree8 of the reference's horizontal sum, then the (row, token) store
+    const int t = tok0 + lt;
+    if (t < a.p) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = row0 + lr + i;
+            if (r >= a.rows) continue;
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = accF[i][k] - accM[i][k];
+            const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+            a.out[(size_t)t * a.out_stride + r] = (s0 + s1) + (s2 + s3);
+        }
+    }
+}
+
+int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
+                    float* out, int out_stride, hipStream_t s) {
+    if (rows <= 0 || blocks <= 0 || p <= 0) return GLLM_OK;
+    PfArgs a{d_w, rb, rows, blocks, act, p, out, out_stride};
+    dim3 grid((rows + kPfRows - 1) / kPfRows, (p + kPfTok - 1) / kPfTok);
+    hipLaunchKernelGGL(prefill_q4k_mfma_kernel, grid, dim3(512), 0, s, a);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+}  // namespace gllm
