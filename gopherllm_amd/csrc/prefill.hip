@@ -27,8 +27,8 @@
 // Workgroup: 8 waves, 64 weight rows x 32 tokens; wave w owns the 16x16
 // tile of rows 16 (w % 4) .. + 15 and tokens 16 (w / 4) .. + 15.  Per block the workgroup
 // stages the 32 tokens' q8 (as f16), xsums and xscales and the 64 rows'
-// decoded scales/mins in LDS (double-buffered); each wave reads its own
-// weight dwords from global memory.
+// decoded scales/mins and nibble bytes in LDS (double-buffered, loaded one
+// block ahead).
 #include "gllm_common.h"
 
 namespace gllm {
@@ -40,16 +40,21 @@ typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 constexpr int kPfRows = 64;
 constexpr int kPfTok = 32;
 constexpr int kPfBStride = 528;  // bytes per token row of the f16 q8 tile: 512 + 16 (no bank conflicts)
+constexpr int kPfWStride = 36;   // dwords per row of the staged weight nibbles: 32 + 4
 
 struct PfStage {
     uint8_t b16[kPfTok * kPfBStride];
     float xsum[8][kPfTok];     // [lane k][token]
     float xsc[kPfTok];
-    uint32_t sch[kPfRows][8];  // half2(sc_j, sc_j)
-    uint32_t scn[kPfRows][8];  // half2(-1024 sc_j, -1024 sc_j)
+    uint32_t sch[8][kPfRows];  // [sub-block j][row] half2(sc_j, sc_j)
+    uint32_t scn[8][kPfRows];  // [sub-block j][row] half2(-1024 sc_j, -1024 sc_j)
     float m[8][kPfRows];       // [lane k][row]
     float d[kPfRows];
     float dmin[kPfRows];
+    // nibble dwords per row as [group s][lane k] (lane (g, c) of a wave reads
+    // its 8 dwords as 32 contiguous bytes); 36-dword rows keep the 16 rows'
+    // 16-byte reads on distinct banks
+    uint32_t wa[kPfRows][kPfWStride];
 };
 
 // four signed bytes -> two half2 words holding the same integers
@@ -99,14 +104,19 @@ struct PfArgs {
     int out_stride;
 };
 
-// staging registers of one block (512 threads): thread (token tid/16, part
-// tid%16) carries 16 q8 bytes; threads 0..63 one xsum quad; threads 0..31 one
-// xscale; thread (row tid/8, sub-block tid%8) its row's 16-byte block header.
+// staging registers of one block (512 threads), mapped so that every LDS
+// store of a wave hits distinct banks:
+//   q8: thread (token tid/16, part tid%16) carries q8 bytes 8 part .. + 7
+//       and 128 + 8 part .. + 7, written as f16 at 16 part and 256 + 16 part;
+//   threads 0..63 one xsum quad, threads 0..31 one xscale;
+//   thread (sub-block j = tid/64, row tid%64) its row's block header and the
+//   16 nibble bytes of lane k = j.
 struct PfRegs {
-    u4v q;
+    uint32_t q[4];
     f4v xs;
     float xc;
     u4v h;
+    u4v w;
 };
 
 __device__ __forceinline__ void pf_load(const PfArgs& a, int row0, int tok0, int b, PfRegs& r) {
@@ -114,7 +124,9 @@ __device__ __forceinline__ void pf_load(const PfArgs& a, int row0, int tok0, int
     const int cols = a.blocks * 256;
     {
         const int t = min(tok0 + (tid >> 4), a.p - 1);
-        r.q = *(const u4v*)(a.act.q8perm + (size_t)t * cols + (size_t)b * 256 + 16 * (tid & 15));
+        const int8_t* src = a.act.q8perm + (size_t)t * cols + (size_t)b * 256 + 8 * (tid & 15);
+        const uint2 lo = *(const uint2*)src, hi = *(const uint2*)(src + 128);
+        r.q[0] = lo.x; r.q[1] = lo.y; r.q[2] = hi.x; r.q[3] = hi.y;
     }
     if (tid < 64) {
         const int t = min(tok0 + (tid >> 1), a.p - 1);
@@ -122,8 +134,10 @@ __device__ __forceinline__ void pf_load(const PfArgs& a, int row0, int tok0, int
     }
     if (tid < kPfTok) r.xc = a.act.xscale[(size_t)min(tok0 + tid, a.p - 1) * a.blocks + b];
     {
-        const int row = min(row0 + (tid >> 3), a.rows - 1);
-        r.h = *(const u4v*)(a.w + (size_t)row * a.rb + (size_t)b * 144);
+        const int row = min(row0 + (tid & 63), a.rows - 1);
+        const uint8_t* blk = a.w + (size_t)row * a.rb + (size_t)b * 144;
+        r.h = *(const u4v*)blk;
+        r.w = *(const u4v*)(blk + 16 + 16 * (tid >> 6));
     }
 }
 
@@ -131,13 +145,13 @@ __device__ __forceinline__ void pf_store(const PfRegs& r, PfStage& st) {
     const int tid = threadIdx.x;
     {
         uint32_t v[8];
-        i8x4_to_h(r.q.x, v[0], v[1]);
-        i8x4_to_h(r.q.y, v[2], v[3]);
-        i8x4_to_h(r.q.z, v[4], v[5]);
-        i8x4_to_h(r.q.w, v[6], v[7]);
-        u4v* dst = (u4v*)(st.b16 + (tid >> 4) * kPfBStride + 32 * (tid & 15));
-        dst[0] = u4v{v[0], v[1], v[2], v[3]};
-        dst[1] = u4v{v[4], v[5], v[6], v[7]};
+        i8x4_to_h(r.q[0], v[0], v[1]);
+        i8x4_to_h(r.q[1], v[2], v[3]);
+        i8x4_to_h(r.q[2], v[4], v[5]);
+        i8x4_to_h(r.q[3], v[6], v[7]);
+        uint8_t* row = st.b16 + (tid >> 4) * kPfBStride + 16 * (tid & 15);
+        *(u4v*)row = u4v{v[0], v[1], v[2], v[3]};
+        *(u4v*)(row + 256) = u4v{v[4], v[5], v[6], v[7]};
     }
     if (tid < 64) {
         const int t = tid >> 1, k0 = 4 * (tid & 1);
@@ -149,7 +163,7 @@ __device__ __forceinline__ void pf_store(const PfRegs& r, PfStage& st) {
     if (tid < kPfTok) st.xsc[tid] = r.xc;
     {
         // getScaleMinK4 (simd.go:1672-1677) for sub-block j
-        const int row = tid >> 3, j = tid & 7;
+        const int row = tid & 63, j = tid >> 6;
         const uint32_t s03 = r.h.y, s47 = r.h.z, s811 = r.h.w;
         uint32_t sc, mn;
         if (j < 4) {
@@ -163,13 +177,18 @@ __device__ __forceinline__ void pf_store(const PfRegs& r, PfStage& st) {
         }
         const _Float16 hs = (_Float16)(float)sc, hn = (_Float16)(-1024.0f * (float)sc);
         const uint32_t bs = __builtin_bit_cast(uint16_t, hs), bn = __builtin_bit_cast(uint16_t, hn);
-        st.sch[row][j] = bs | (bs << 16);
-        st.scn[row][j] = bn | (bn << 16);
+        st.sch[j][row] = bs | (bs << 16);
+        st.scn[j][row] = bn | (bn << 16);
         st.m[j][row] = (float)mn;
         if (j == 0) {
             st.d[row] = f16_bits_to_f32(r.h.x & 0xffffu);
             st.dmin[row] = f16_bits_to_f32(r.h.x >> 16);
         }
+        // lane k = j's dwords for groups s = 0..3
+        st.wa[row][0 * 8 + j] = r.w.x;
+        st.wa[row][1 * 8 + j] = r.w.y;
+        st.wa[row][2 * 8 + j] = r.w.z;
+        st.wa[row][3 * 8 + j] = r.w.w;
     }
 }
 
@@ -179,9 +198,6 @@ __global__ __launch_bounds__(512, 2) void prefill_q4k_mfma_kernel(PfArgs a) {
     const int g = lane >> 4, c = lane & 15;
     const int rw = wave & 3, tw = wave >> 2;  // 16-row group, 16-token column
     const int row0 = blockIdx.x * kPfRows, tok0 = blockIdx.y * kPfTok;
-    // this lane's A row (MFMA row c of the wave's 16) and its weight dwords
-    const int arow = min(row0 + 16 * rw + c, a.rows - 1);
-    const uint8_t* wrow = a.w + (size_t)arow * a.rb + 16 + 4 * g;
     // D layout: rows 4g + i of the wave's 16, token c of its column
     const int lr = 16 * rw + 4 * g;
     const int lt = 16 * tw + c;
@@ -192,25 +208,14 @@ __global__ __launch_bounds__(512, 2) void prefill_q4k_mfma_kernel(PfArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; k++) accF[i][k] = accM[i][k] = 0.0f;
 
-    PfRegs regs;
-    pf_load(a, row0, tok0, 0, regs);
-    uint32_t wq[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) wq[k] = *(const uint32_t*)(wrow + 16 * k);
-    pf_store(regs, stage[0]);
-    __syncthreads();
-
-    for (int b = 0; b < a.blocks; b++) {
-        const PfStage& st = stage[b & 1];
-        const bool more = b + 1 < a.blocks;
-        uint32_t wn[8];
-        if (more) {
-            pf_load(a, row0, tok0, b + 1, regs);
-#pragma unroll
-            for (int k = 0; k < 8; k++) wn[k] = *(const uint32_t*)(wrow + (size_t)(b + 1) * 144 + 16 * k);
-        }
-        const uint32_t sh_lo = st.sch[16 * rw + c][2 * g], sn_lo = st.scn[16 * rw + c][2 * g];
-        const uint32_t sh_hi = st.sch[16 * rw + c][2 * g + 1], sn_hi = st.scn[16 * rw + c][2 * g + 1];
+    // one block's products from a staged LDS tile
+    auto block = [&](const PfStage& st) __attribute__((always_inline)) {
+        // this lane's A row (MFMA row c of the wave's 16): its 8 nibble dwords
+        const u4v wq0 = *(const u4v*)&st.wa[16 * rw + c][8 * g];
+        const u4v wq1 = *(const u4v*)&st.wa[16 * rw + c][8 * g + 4];
+        const uint32_t wq[8] = {wq0.x, wq0.y, wq0.z, wq0.w, wq1.x, wq1.y, wq1.z, wq1.w};
+        const uint32_t sh_lo = st.sch[2 * g][16 * rw + c], sn_lo = st.scn[2 * g][16 * rw + c];
+        const uint32_t sh_hi = st.sch[2 * g + 1][16 * rw + c], sn_hi = st.scn[2 * g + 1][16 * rw + c];
         // F chain factors d * xscale per D row
         const f4v dv = *(const f4v*)&st.d[lr];
         const f4v dm = *(const f4v*)&st.dmin[lr];
@@ -234,11 +239,26 @@ __global__ __launch_bounds__(512, 2) void prefill_q4k_mfma_kernel(PfArgs a) {
                 accM[i][k] = fmaf(dm[i], mx, accM[i][k]);
             }
         }
-        if (more) {
-            pf_store(regs, stage[(b + 1) & 1]);
-#pragma unroll
-            for (int k = 0; k < 8; k++) wq[k] = wn[k];
-        }
+    };
+
+    // Two staging register sets: the global loads of block b + 2 are issued
+    // while block b is computed and land in LDS after block b + 1 is.
+    const int nb = a.blocks;
+    PfRegs r0, r1;
+    pf_load(a, row0, tok0, 0, r0);
+    pf_store(r0, stage[0]);
+    if (nb > 1) pf_load(a, row0, tok0, 1, r1);
+    __syncthreads();
+#pragma unroll 1
+    for (int b = 0; b < nb; b += 2) {
+        if (b + 2 < nb) pf_load(a, row0, tok0, b + 2, r0);
+        block(stage[0]);
+        if (b + 1 < nb) pf_store(r1, stage[1]);
+        __syncthreads();
+        if (b + 1 >= nb) break;
+        if (b + 3 < nb) pf_load(a, row0, tok0, b + 3, r1);
+        block(stage[1]);
+        if (b + 2 < nb) pf_store(r0, stage[0]);
         __syncthreads();
     }
     // tree8 of the reference's horizontal sum, then the (row, token) store
