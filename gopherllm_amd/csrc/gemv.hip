@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <vector>
 
+
 #include "gllm_common.h"
 
 namespace gllm {
@@ -108,6 +109,31 @@ __device__ __forceinline__ int mul_byte(int a, uint32_t s) {
     return __mul24(a, (int)((s >> (8 * N)) & 0xffu));
 }
 
+// Q4_K lane sum sum_j sc_j * t_j from the eight dot4 results t_j: each
+// |t_j| <= 4 * 15 * 127 = 7620 and each sc_j <= 63 fit signed 16 bits, so
+// pairs (t_j, t_j+1) and (sc_j, sc_j+1) go through v_dot2_i32_i16 (exact
+// int32, like the AVX2 VPMADDWD it replaces) instead of eight 24-bit
+// multiplies of extracted scale bytes.
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ s16x2 pack16(int lo, int hi) {
+    return __builtin_bit_cast(s16x2, __builtin_amdgcn_perm((uint32_t)hi, (uint32_t)lo, 0x05040100u));
+}
+// scale bytes (0, 1) or (2, 3) of s as two 16-bit halves
+template <int N>
+__device__ __forceinline__ s16x2 sc_pair(uint32_t s) {
+    return __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, s, N == 0 ? 0x0c010c00u : 0x0c030c02u));
+}
+__device__ __forceinline__ int q4k_lane_sum(int t0, int t1, int t2, int t3, int t4, int t5, int t6,
+                                            int t7, uint32_t sc03, uint32_t sc47) {
+    const int a = __builtin_amdgcn_sdot2(pack16(t0, t1), sc_pair<0>(sc03),
+                                         __builtin_amdgcn_sdot2(pack16(t2, t3), sc_pair<1>(sc03), 0, false),
+                                         false);
+    const int b = __builtin_amdgcn_sdot2(pack16(t4, t5), sc_pair<0>(sc47),
+                                         __builtin_amdgcn_sdot2(pack16(t6, t7), sc_pair<1>(sc47), 0, false),
+                                         false);
+    return a + b;
+}
+
 __device__ __forceinline__ uint32_t ubfe(uint32_t v, uint32_t off, uint32_t width) {
     return __builtin_amdgcn_ubfe(v, off, width);
 }
@@ -188,55 +214,64 @@ __device__ __forceinline__ void xq_load(const float* __restrict__ x, int B, XReg
     }
 }
 
-// Quantise the blocks held in xr into LDS: q8 (lane-permuted), xs32 and, for
+// Quantise one 256-element block b held as x[32m + kk + 8e] = v[e] by lane
+// (m = lane / 8, kk = lane % 8) into LDS: q8 (lane-permuted), xs32 and, for
 // Q6_K (XS16), xs16 x 32 at the given LDS arrays.
+template <bool XS16>
+__device__ __forceinline__ void xq_block(const float* xv, int b, int8_t* q8, float* xs32,
+                                         float* xs16, float* xsc) {
+    const int lane = threadIdx.x & 63;
+    const int m = lane >> 3, kk = lane & 7;
+    const float x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
+    // amax, NaN skipped: v_max_f32 is IEEE maxNum
+    float a = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    float scale = 0.0f, inv = 0.0f;
+    const bool nz = a != 0.0f && a == a;
+    if (nz) {
+        scale = a / 127.0f;
+        inv = 127.0f / a;
+    }
+    int8_t* qb = q8 + (size_t)b * 256 + 4 * m + (kk & 3) + 32 * (kk >> 2);
+    qb[0] = (int8_t)(nz ? (int)rintf(x0 * inv) : 0);
+    qb[64] = (int8_t)(nz ? (int)rintf(x1 * inv) : 0);
+    qb[128] = (int8_t)(nz ? (int)rintf(x2 * inv) : 0);
+    qb[192] = (int8_t)(nz ? (int)rintf(x3 * inv) : 0);
+    if (lane == 0) xsc[b] = scale;
+    // v_kk = ((x[kk] + x[8+kk]) + x[16+kk]) + x[24+kk]; a_k = v_k + v_{k+4};
+    // r = (a0 + a1) + (a2 + a3)
+    float v = ((x0 + x1) + x2) + x3;
+    v = v + __shfl_xor(v, 4);
+    v = v + __shfl_xor(v, 1);
+    v = v + __shfl_xor(v, 2);
+    if (kk == 0) xs32[b * 8 + m] = v;
+    if constexpr (XS16) {
+        // 16-groups 2m (x0, x1) and 2m+1 (x2, x3): v_k = x[k] + x[8+k]
+        float u = x0 + x1, w = x2 + x3;
+        u = u + __shfl_xor(u, 4);
+        w = w + __shfl_xor(w, 4);
+        u = u + __shfl_xor(u, 1);
+        w = w + __shfl_xor(w, 1);
+        u = u + __shfl_xor(u, 2);
+        w = w + __shfl_xor(w, 2);
+        if (kk == 0) {
+            xs16[b * 16 + 2 * m] = u * 32.0f;
+            xs16[b * 16 + 2 * m + 1] = w * 32.0f;
+        }
+    }
+}
+
+// Quantise the blocks held in xr (wave w holds blocks w, w + nw, ...).
 template <int QB, bool XS16>
 __device__ __forceinline__ void xq_store(const XRegs<QB>& xr, int B, int8_t* q8, float* xs32,
                                          float* xs16, float* xsc) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int m = lane >> 3, kk = lane & 7;
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
 #pragma unroll
     for (int i = 0; i < QB; i++) {
         const int b = wave + nw * i;
         if (b >= B) break;  // wave-uniform
-        const float x0 = xr.v[i][0], x1 = xr.v[i][1], x2 = xr.v[i][2], x3 = xr.v[i][3];
-        // amax, NaN skipped: v_max_f32 is IEEE maxNum
-        float a = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
-        float scale = 0.0f, inv = 0.0f;
-        const bool nz = a != 0.0f && a == a;
-        if (nz) {
-            scale = a / 127.0f;
-            inv = 127.0f / a;
-        }
-        int8_t* qb = q8 + (size_t)b * 256 + 4 * m + (kk & 3) + 32 * (kk >> 2);
-        qb[0] = (int8_t)(nz ? (int)rintf(x0 * inv) : 0);
-        qb[64] = (int8_t)(nz ? (int)rintf(x1 * inv) : 0);
-        qb[128] = (int8_t)(nz ? (int)rintf(x2 * inv) : 0);
-        qb[192] = (int8_t)(nz ? (int)rintf(x3 * inv) : 0);
-        if (lane == 0) xsc[b] = scale;
-        // v_kk = ((x[kk] + x[8+kk]) + x[16+kk]) + x[24+kk]; a_k = v_k + v_{k+4};
-        // r = (a0 + a1) + (a2 + a3)
-        float v = ((x0 + x1) + x2) + x3;
-        v = v + __shfl_xor(v, 4);
-        v = v + __shfl_xor(v, 1);
-        v = v + __shfl_xor(v, 2);
-        if (kk == 0) xs32[b * 8 + m] = v;
-        if constexpr (XS16) {
-            // 16-groups 2m (x0, x1) and 2m+1 (x2, x3): v_k = x[k] + x[8+k]
-            float u = x0 + x1, w = x2 + x3;
-            u = u + __shfl_xor(u, 4);
-            w = w + __shfl_xor(w, 4);
-            u = u + __shfl_xor(u, 1);
-            w = w + __shfl_xor(w, 1);
-            u = u + __shfl_xor(u, 2);
-            w = w + __shfl_xor(w, 2);
-            if (kk == 0) {
-                xs16[b * 16 + 2 * m] = u * 32.0f;
-                xs16[b * 16 + 2 * m + 1] = w * 32.0f;
-            }
-        }
+        xq_block<XS16>(xr.v[i], b, q8, xs32, xs16, xsc);
     }
 }
 
@@ -265,10 +300,9 @@ __device__ __forceinline__ void q4k_block(const uint4 h, const uint4 q, int b, i
             const int8_t* qp = q8b + (size_t)t * cols + b * 256 + k * 32;
             const int4 qa = *(const int4*)qp;
             const int4 qb = *(const int4*)(qp + 16);
-            const int acc = (mul_byte<0>(dot4z(l0, qa.x), sc03) + mul_byte<1>(dot4z(h0, qa.y), sc03)) +
-                            (mul_byte<2>(dot4z(l1, qa.z), sc03) + mul_byte<3>(dot4z(h1, qa.w), sc03)) +
-                            (mul_byte<0>(dot4z(l2, qb.x), sc47) + mul_byte<1>(dot4z(h2, qb.y), sc47)) +
-                            (mul_byte<2>(dot4z(l3, qb.z), sc47) + mul_byte<3>(dot4z(h3, qb.w), sc47));
+            const int acc = q4k_lane_sum(dot4z(l0, qa.x), dot4z(h0, qa.y), dot4z(l1, qa.z),
+                                         dot4z(h1, qa.w), dot4z(l2, qb.x), dot4z(h2, qb.y),
+                                         dot4z(l3, qb.z), dot4z(h3, qb.w), sc03, sc47);
             const float iv = (float)acc;
             const float dxs = d * xscb[(size_t)t * B + b];
             const float mx = mkf * xs32b[(size_t)t * (cols / 32) + b * 8 + k];
