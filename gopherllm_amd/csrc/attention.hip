@@ -271,18 +271,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
         const int base = it * kVTile;
         const int n = min(kVTile, span - base);
         if (chain) {
-            int p = 0;
-            for (; p + 16 <= n; p += 16) {
-                float wv[16], vv[16];
+            if (n == kVTile) {
+                // the whole tile's operands first (one LDS round trip), then
+                // the chain: w four positions per broadcast read
+                uint16_t vb[kVTile];
+                float4 wq[kVTile / 4];
 #pragma unroll
-                for (int u = 0; u < 16; u++) {
-                    wv[u] = w[base + p + u];
-                    vv[u] = f16_bits_to_f32(buf[(p + u) * kFusedHD + d]);
+                for (int u = 0; u < kVTile / 4; u++) wq[u] = *(const float4*)&w[base + 4 * u];
+#pragma unroll
+                for (int u = 0; u < kVTile; u++) vb[u] = buf[u * kFusedHD + d];
+#pragma unroll
+                for (int u = 0; u < kVTile / 4; u++) {
+                    acc = fmaf(wq[u].x, f16_bits_to_f32(vb[4 * u]), acc);
+                    acc = fmaf(wq[u].y, f16_bits_to_f32(vb[4 * u + 1]), acc);
+                    acc = fmaf(wq[u].z, f16_bits_to_f32(vb[4 * u + 2]), acc);
+                    acc = fmaf(wq[u].w, f16_bits_to_f32(vb[4 * u + 3]), acc);
                 }
-#pragma unroll
-                for (int u = 0; u < 16; u++) acc = fmaf(wv[u], vv[u], acc);
+            } else {
+                for (int p = 0; p < n; p++)
+                    acc = fmaf(w[base + p], f16_bits_to_f32(buf[p * kFusedHD + d]), acc);
             }
-            for (; p < n; p++) acc = fmaf(w[base + p], f16_bits_to_f32(buf[p * kFusedHD + d]), acc);
         } else if (summer) {
             int p = 0;
             for (; p + 16 <= n; p += 16) {
