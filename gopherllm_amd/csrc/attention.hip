@@ -261,7 +261,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
         u32x4* dst = (u32x4*)(buf + lp * kFusedHD + 32 * lc);
 #pragma unroll
         for (int u = 0; u < 4; u++) dst[u] = pr[u];
-        if (it + kVPrefetch < ntiles) {
+        {
+            // unconditional (clamped to the last position past the end): a
+            // load under a branch makes the compiler's vmcnt waits drain the
+            // whole prefetch
             const u32x4* src = (const u32x4*)(Vg + (size_t)min((it + kVPrefetch) * kVTile + lp, span - 1) * kv_dim + 32 * lc);
 #pragma unroll
             for (int u = 0; u < 4; u++) pr[u] = src[u];

@@ -13,13 +13,24 @@
 #include <vector>
 
 
+#include <cstdlib>
+
 #include "gllm_common.h"
 
 namespace gllm {
 
 constexpr int kRowsPerWG = 32;  // 256 threads / 8 lanes per row
 constexpr int kMaxTok = 8;      // activation rows per launch
-constexpr int kMfmaMinTok = 16; // Q4_K batches from this size run on the matrix cores
+// Q4_K batches from this many activation rows run on the matrix cores
+// (GLLM_MFMA_MIN_TOK overrides, for measurement; both paths give the same bits)
+static int mfma_min_tok() {
+    static const int n = [] {
+        const char* e = getenv("GLLM_MFMA_MIN_TOK");
+        const int v = e ? atoi(e) : 0;
+        return v > 0 ? v : 8;
+    }();
+    return n;
+}
 
 struct GemvJob {
     const uint8_t* w[3];
@@ -861,7 +872,7 @@ int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* 
     }
     j.wg_begin[n] = wg;
     if (wg == 0) return GLLM_OK;
-    if (w0->type == GLLM_TYPE_Q4_K && p >= kMfmaMinTok) {
+    if (w0->type == GLLM_TYPE_Q4_K && p >= mfma_min_tok()) {
         // batched prefill: matrix-core products, same bits as the row kernel
         for (int i = 0; i < n; i++)
             GLLM_TRY(launch_q4k_mfma(ws[i]->d_data, ws[i]->row_bytes, ws[i]->rows, ws[i]->blocks,

@@ -24,8 +24,9 @@
 // 8s + 4 + i (high nibble, sub-block 2s + 1).  MFMA lane L supplies
 // kappa = 8(L/16) .. 8(L/16) + 7 of both operands, i.e. one weight dword.
 //
-// Workgroup: 8 waves, 64 weight rows x 32 tokens; wave w owns the 16x16
-// tile of rows 16 (w % 4) .. + 15 and tokens 16 (w / 4) .. + 15.  Per block the workgroup
+// Workgroup: RW x TW waves over 16 RW weight rows x 16 TW tokens; wave w
+// owns the 16x16 tile of rows 16 (w % RW) .. + 15 and tokens
+// 16 (w / RW) .. + 15.  Per block the workgroup
 // stages the 32 tokens' q8 (as f16), xsums and xscales and the 64 rows'
 // decoded scales/mins and nibble bytes in LDS (double-buffered, loaded one
 // block ahead).
@@ -37,24 +38,26 @@ typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
-constexpr int kPfRows = 64;
-constexpr int kPfTok = 32;
 constexpr int kPfBStride = 528;  // bytes per token row of the f16 q8 tile: 512 + 16 (no bank conflicts)
 constexpr int kPfWStride = 36;   // dwords per row of the staged weight nibbles: 32 + 4
 
+// One block's staged operands for a workgroup of RW 16-row groups x TW
+// 16-token columns.
+template <int RW, int TW>
 struct PfStage {
-    uint8_t b16[kPfTok * kPfBStride];
-    float xsum[8][kPfTok];     // [lane k][token]
-    float xsc[kPfTok];
-    uint32_t sch[8][kPfRows];  // [sub-block j][row] half2(sc_j, sc_j)
-    uint32_t scn[8][kPfRows];  // [sub-block j][row] half2(-1024 sc_j, -1024 sc_j)
-    float m[8][kPfRows];       // [lane k][row]
-    float d[kPfRows];
-    float dmin[kPfRows];
+    static constexpr int kRows = 16 * RW, kTok = 16 * TW;
+    uint8_t b16[kTok * kPfBStride];
+    float xsum[8][kTok];        // [lane k][token]
+    float xsc[kTok];
+    uint32_t sch[8][kRows];     // [sub-block j][row] half2(sc_j, sc_j)
+    uint32_t scn[8][kRows];     // [sub-block j][row] half2(-1024 sc_j, -1024 sc_j)
+    float m[8][kRows];          // [lane k][row]
+    float d[kRows];
+    float dmin[kRows];
     // nibble dwords per row as [group s][lane k] (lane (g, c) of a wave reads
     // its 8 dwords as 32 contiguous bytes); 36-dword rows keep the 16 rows'
     // 16-byte reads on distinct banks
-    uint32_t wa[kPfRows][kPfWStride];
+    uint32_t wa[kRows][kPfWStride];
 };
 
 // four signed bytes -> two half2 words holding the same integers
@@ -104,67 +107,87 @@ struct PfArgs {
     int out_stride;
 };
 
-// staging registers of one block (512 threads), mapped so that every LDS
-// store of a wave hits distinct banks:
-//   q8: thread (token tid/16, part tid%16) carries q8 bytes 8 part .. + 7
-//       and 128 + 8 part .. + 7, written as f16 at 16 part and 256 + 16 part;
-//   threads 0..63 one xsum quad, threads 0..31 one xscale;
-//   thread (sub-block j = tid/64, row tid%64) its row's block header and the
-//   16 nibble bytes of lane k = j.
+// Staging registers of one block for T = 64 RW TW threads, mapped so that
+// every LDS store of a wave hits distinct banks:
+//   q8: unit u = (token u/16, part u%16), units tid, tid + T, ...: q8 bytes
+//       8 part .. + 7 and 128 + 8 part .. + 7, written as f16 at 16 part and
+//       256 + 16 part of the token's row;
+//   threads 0 .. 2 kTok - 1 one xsum quad, threads 0 .. kTok - 1 one xscale;
+//   unit u = (sub-block j = u / kRows, row u % kRows): the row's block header
+//   and the 16 nibble bytes of lane k = j.
+template <int RW, int TW>
 struct PfRegs {
-    uint32_t q[4];
+    static constexpr int T = 64 * RW * TW;
+    static constexpr int NQ = 16 * 16 * TW / T;  // q8 units per thread
+    static constexpr int NH = 8 * 16 * RW / T;   // header units per thread
+    uint32_t q[NQ][4];
     f4v xs;
     float xc;
-    u4v h;
-    u4v w;
+    u4v h[NH];
+    u4v w[NH];
 };
 
-__device__ __forceinline__ void pf_load(const PfArgs& a, int row0, int tok0, int b, PfRegs& r) {
+template <int RW, int TW>
+__device__ __forceinline__ void pf_load(const PfArgs& a, int row0, int tok0, int b,
+                                        PfRegs<RW, TW>& r) {
+    using R = PfRegs<RW, TW>;
+    constexpr int kRows = 16 * RW, kTok = 16 * TW;
     const int tid = threadIdx.x;
     const int cols = a.blocks * 256;
-    {
-        const int t = min(tok0 + (tid >> 4), a.p - 1);
-        const int8_t* src = a.act.q8perm + (size_t)t * cols + (size_t)b * 256 + 8 * (tid & 15);
+#pragma unroll
+    for (int i = 0; i < R::NQ; i++) {
+        const int u = tid + R::T * i;
+        const int t = min(tok0 + (u >> 4), a.p - 1);
+        const int8_t* src = a.act.q8perm + (size_t)t * cols + (size_t)b * 256 + 8 * (u & 15);
         const uint2 lo = *(const uint2*)src, hi = *(const uint2*)(src + 128);
-        r.q[0] = lo.x; r.q[1] = lo.y; r.q[2] = hi.x; r.q[3] = hi.y;
+        r.q[i][0] = lo.x; r.q[i][1] = lo.y; r.q[i][2] = hi.x; r.q[i][3] = hi.y;
     }
-    if (tid < 64) {
+    if (tid < 2 * kTok) {
         const int t = min(tok0 + (tid >> 1), a.p - 1);
         r.xs = *(const f4v*)(a.act.xs32 + (size_t)t * (cols / 32) + b * 8 + 4 * (tid & 1));
     }
-    if (tid < kPfTok) r.xc = a.act.xscale[(size_t)min(tok0 + tid, a.p - 1) * a.blocks + b];
-    {
-        const int row = min(row0 + (tid & 63), a.rows - 1);
+    if (tid < kTok) r.xc = a.act.xscale[(size_t)min(tok0 + tid, a.p - 1) * a.blocks + b];
+#pragma unroll
+    for (int i = 0; i < R::NH; i++) {
+        const int u = tid + R::T * i;
+        const int row = min(row0 + u % kRows, a.rows - 1);
         const uint8_t* blk = a.w + (size_t)row * a.rb + (size_t)b * 144;
-        r.h = *(const u4v*)blk;
-        r.w = *(const u4v*)(blk + 16 + 16 * (tid >> 6));
+        r.h[i] = *(const u4v*)blk;
+        r.w[i] = *(const u4v*)(blk + 16 + 16 * (u / kRows));
     }
 }
 
-__device__ __forceinline__ void pf_store(const PfRegs& r, PfStage& st) {
+template <int RW, int TW>
+__device__ __forceinline__ void pf_store(const PfRegs<RW, TW>& r, PfStage<RW, TW>& st) {
+    using R = PfRegs<RW, TW>;
+    constexpr int kRows = 16 * RW, kTok = 16 * TW;
     const int tid = threadIdx.x;
-    {
+#pragma unroll
+    for (int i = 0; i < R::NQ; i++) {
+        const int u = tid + R::T * i;
         uint32_t v[8];
-        i8x4_to_h(r.q[0], v[0], v[1]);
-        i8x4_to_h(r.q[1], v[2], v[3]);
-        i8x4_to_h(r.q[2], v[4], v[5]);
-        i8x4_to_h(r.q[3], v[6], v[7]);
-        uint8_t* row = st.b16 + (tid >> 4) * kPfBStride + 16 * (tid & 15);
+        i8x4_to_h(r.q[i][0], v[0], v[1]);
+        i8x4_to_h(r.q[i][1], v[2], v[3]);
+        i8x4_to_h(r.q[i][2], v[4], v[5]);
+        i8x4_to_h(r.q[i][3], v[6], v[7]);
+        uint8_t* row = st.b16 + (u >> 4) * kPfBStride + 16 * (u & 15);
         *(u4v*)row = u4v{v[0], v[1], v[2], v[3]};
         *(u4v*)(row + 256) = u4v{v[4], v[5], v[6], v[7]};
     }
-    if (tid < 64) {
+    if (tid < 2 * kTok) {
         const int t = tid >> 1, k0 = 4 * (tid & 1);
         st.xsum[k0][t] = r.xs.x;
         st.xsum[k0 + 1][t] = r.xs.y;
         st.xsum[k0 + 2][t] = r.xs.z;
         st.xsum[k0 + 3][t] = r.xs.w;
     }
-    if (tid < kPfTok) st.xsc[tid] = r.xc;
-    {
+    if (tid < kTok) st.xsc[tid] = r.xc;
+#pragma unroll
+    for (int i = 0; i < R::NH; i++) {
         // getScaleMinK4 (simd.go:1672-1677) for sub-block j
-        const int row = tid & 63, j = tid >> 6;
-        const uint32_t s03 = r.h.y, s47 = r.h.z, s811 = r.h.w;
+        const int u = tid + R::T * i;
+        const int row = u % kRows, j = u / kRows;
+        const uint32_t s03 = r.h[i].y, s47 = r.h[i].z, s811 = r.h[i].w;
         uint32_t sc, mn;
         if (j < 4) {
             sc = (s03 >> (8 * j)) & 63u;
@@ -181,23 +204,28 @@ __device__ __forceinline__ void pf_store(const PfRegs& r, PfStage& st) {
         st.scn[j][row] = bn | (bn << 16);
         st.m[j][row] = (float)mn;
         if (j == 0) {
-            st.d[row] = f16_bits_to_f32(r.h.x & 0xffffu);
-            st.dmin[row] = f16_bits_to_f32(r.h.x >> 16);
+            st.d[row] = f16_bits_to_f32(r.h[i].x & 0xffffu);
+            st.dmin[row] = f16_bits_to_f32(r.h[i].x >> 16);
         }
         // lane k = j's dwords for groups s = 0..3
-        st.wa[row][0 * 8 + j] = r.w.x;
-        st.wa[row][1 * 8 + j] = r.w.y;
-        st.wa[row][2 * 8 + j] = r.w.z;
-        st.wa[row][3 * 8 + j] = r.w.w;
+        st.wa[row][0 * 8 + j] = r.w[i].x;
+        st.wa[row][1 * 8 + j] = r.w[i].y;
+        st.wa[row][2 * 8 + j] = r.w[i].z;
+        st.wa[row][3 * 8 + j] = r.w[i].w;
     }
 }
 
-__global__ __launch_bounds__(512, 2) void prefill_q4k_mfma_kernel(PfArgs a) {
-    __shared__ __align__(16) PfStage stage[2];
+template <int RW, int TW>
+// (two waves per SIMD for multi-wave workgroups; a one-wave workgroup, one
+// per CU, may use the whole register file for its deeper staging)
+__global__ __launch_bounds__(64 * RW * TW) __attribute__((amdgpu_waves_per_eu(RW * TW > 1 ? 2 : 1)))
+void prefill_q4k_mfma_kernel(PfArgs a) {
+    using Stage = PfStage<RW, TW>;
+    __shared__ __align__(16) Stage stage[2];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const int rw = wave & 3, tw = wave >> 2;  // 16-row group, 16-token column
-    const int row0 = blockIdx.x * kPfRows, tok0 = blockIdx.y * kPfTok;
+    const int rw = wave % RW, tw = wave / RW;  // 16-row group, 16-token column
+    const int row0 = blockIdx.x * Stage::kRows, tok0 = blockIdx.y * Stage::kTok;
     // D layout: rows 4g + i of the wave's 16, token c of its column
     const int lr = 16 * rw + 4 * g;
     const int lt = 16 * tw + c;
@@ -209,7 +237,7 @@ __global__ __launch_bounds__(512, 2) void prefill_q4k_mfma_kernel(PfArgs a) {
         for (int k = 0; k < 8; k++) accF[i][k] = accM[i][k] = 0.0f;
 
     // one block's products from a staged LDS tile
-    auto block = [&](const PfStage& st) __attribute__((always_inline)) {
+    auto block = [&](const Stage& st) __attribute__((always_inline)) {
         // this lane's A row (MFMA row c of the wave's 16): its 8 nibble dwords
         const u4v wq0 = *(const u4v*)&st.wa[16 * rw + c][8 * g];
         const u4v wq1 = *(const u4v*)&st.wa[16 * rw + c][8 * g + 4];
@@ -242,21 +270,24 @@ __global__ __launch_bounds__(512, 2) void prefill_q4k_mfma_kernel(PfArgs a) {
     };
 
     // Two staging register sets: the global loads of block b + 2 are issued
-    // while block b is computed and land in LDS after block b + 1 is.
+    // while block b is computed and land in LDS after block b + 1 is.  The
+    // loads are unconditional (past the end they re-read the last block):
+    // under a branch the compiler's vmcnt wait for the older set would also
+    // wait for the newer one and cancel the prefetch.
     const int nb = a.blocks;
-    PfRegs r0, r1;
+    PfRegs<RW, TW> r0, r1;
     pf_load(a, row0, tok0, 0, r0);
     pf_store(r0, stage[0]);
-    if (nb > 1) pf_load(a, row0, tok0, 1, r1);
+    pf_load(a, row0, tok0, min(1, nb - 1), r1);
     __syncthreads();
 #pragma unroll 1
     for (int b = 0; b < nb; b += 2) {
-        if (b + 2 < nb) pf_load(a, row0, tok0, b + 2, r0);
+        pf_load(a, row0, tok0, min(b + 2, nb - 1), r0);
         block(stage[0]);
         if (b + 1 < nb) pf_store(r1, stage[1]);
         __syncthreads();
         if (b + 1 >= nb) break;
-        if (b + 3 < nb) pf_load(a, row0, tok0, b + 3, r1);
+        pf_load(a, row0, tok0, min(b + 3, nb - 1), r1);
         block(stage[1]);
         if (b + 2 < nb) pf_store(r0, stage[0]);
         __syncthreads();
@@ -277,12 +308,24 @@ __global__ __launch_bounds__(512, 2) void prefill_q4k_mfma_kernel(PfArgs a) {
     }
 }
 
+template <int RW, int TW>
+static void launch_pf(const PfArgs& a, hipStream_t s) {
+    dim3 grid((a.rows + 16 * RW - 1) / (16 * RW), (a.p + 16 * TW - 1) / (16 * TW));
+    hipLaunchKernelGGL((prefill_q4k_mfma_kernel<RW, TW>), grid, dim3(64 * RW * TW), 0, s, a);
+}
+
+// Workgroup shape: 64 rows x 32 tokens for real prefill batches, 64 rows x 16
+// tokens for at most 16 activation rows (a decode batch).  The per-block
+// staging (q8 to f16, scale decoding) is a fixed cost per workgroup, so 64
+// rows per workgroup beat smaller tiles that would fill more CUs (measured
+// at batch 8: 22.8 vs 28.4 us for 14336 x 4096, 58.8 vs 72.3 us for
+// 4096 x 14336).
 int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
                     float* out, int out_stride, hipStream_t s) {
     if (rows <= 0 || blocks <= 0 || p <= 0) return GLLM_OK;
     PfArgs a{d_w, rb, rows, blocks, act, p, out, out_stride};
-    dim3 grid((rows + kPfRows - 1) / kPfRows, (p + kPfTok - 1) / kPfTok);
-    hipLaunchKernelGGL(prefill_q4k_mfma_kernel, grid, dim3(512), 0, s, a);
+    if (p > 16) launch_pf<4, 2>(a, s);
+    else launch_pf<4, 1>(a, s);
     GLLM_HIP(hipGetLastError());
     return GLLM_OK;
 }
