@@ -164,11 +164,27 @@ constexpr int kVTile = 64;        // positions per staged V tile (16 KB)
 constexpr int kVPrefetch = 4;     // tiles in flight per thread (registers)
 constexpr int kSmaxSpan = 6144;   // longest span the softmax/values kernel keeps in LDS (< 64 KB)
 
+// RoPE for one decode token folded into the scores launch (rope != null,
+// one token, position `end` read from d_end): applyPreparedRope on q
+// (model.go:3051-3093, interleaved pairs, same operations as rope_kv_kernel)
+// as each workgroup stages its query heads, and the workgroup whose chunk holds
+// the new position rotates the raw k row, rounds it to f16 and stores it and
+// the v row in the cache, using the stored f16 values for its own dot.
+struct AttnRope {
+    const float* sin_tab;  // [max_len][hd/2]
+    const float* cos_tab;
+    const float* k;        // raw (unrotated) k of the token, n_kv * hd
+    const float* v;
+    uint16_t* kc;          // this layer's caches
+    uint16_t* vc;
+};
+
 __global__ __launch_bounds__(256) void attn_scores128_kernel(
-    const float* __restrict__ q, const uint16_t* __restrict__ K, int kv_dim, int n_kv, int kvmul,
+    const float* __restrict__ q, const uint16_t* K, int kv_dim, int n_kv, int kvmul,
     int start, int span0, int span_max, float scale, float* __restrict__ scores,
-    const int* __restrict__ d_end) {
+    const int* __restrict__ d_end, AttnRope rope) {
     __shared__ float qs[4 * kFusedHD];
+    __shared__ __align__(16) uint16_t kcur[kFusedHD];
     const int g = blockIdx.x, chunk = blockIdx.y, tok = blockIdx.z;
     const int tid = threadIdx.x;
     if (d_end) span0 = *d_end - start + 1;  // position read on the device (graph replay)
@@ -176,14 +192,52 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
     if (chunk * kScoreChunk >= span) return;  // uniform
     const int n_heads = n_kv * kvmul;
     const float* qg = q + ((size_t)tok * n_heads + (size_t)g * kvmul) * kFusedHD;
-    for (int i = tid; i < kvmul * kFusedHD; i += 256) qs[i] = qg[i];
+    const int tcur = span - 1;  // the new position (rope mode: one token)
+    const bool has_cur = rope.sin_tab && tcur / kScoreChunk == chunk;
+    if (rope.sin_tab) {
+        const int pos = start + tcur, pairs = kFusedHD / 2;
+        for (int i = tid; i < kvmul * pairs; i += 256) {
+            const int pr = i % pairs;
+            const float sn = rope.sin_tab[(size_t)pos * pairs + pr];
+            const float cs = rope.cos_tab[(size_t)pos * pairs + pr];
+            const float v0 = qg[2 * i], v1 = qg[2 * i + 1];
+            qs[2 * i] = v0 * cs - v1 * sn;
+            qs[2 * i + 1] = v0 * sn + v1 * cs;
+        }
+        if (has_cur && tid < pairs) {
+            const float sn = rope.sin_tab[(size_t)pos * pairs + tid];
+            const float cs = rope.cos_tab[(size_t)pos * pairs + tid];
+            const float* e = rope.k + (size_t)g * kFusedHD + 2 * tid;
+            const float v0 = e[0], v1 = e[1];
+            const uint16_t r0 = f32_to_f16_bits(v0 * cs - v1 * sn);
+            const uint16_t r1 = f32_to_f16_bits(v0 * sn + v1 * cs);
+            kcur[2 * tid] = r0;
+            kcur[2 * tid + 1] = r1;
+            uint16_t* kc = rope.kc + (size_t)pos * kv_dim + (size_t)g * kFusedHD + 2 * tid;
+            kc[0] = r0;
+            kc[1] = r1;
+        } else if (has_cur && tid < 2 * pairs) {
+            const int i = tid - pairs;
+            const float* vr = rope.v + (size_t)g * kFusedHD + 2 * i;
+            uint16_t* vc = rope.vc + (size_t)pos * kv_dim + (size_t)g * kFusedHD + 2 * i;
+            vc[0] = f32_to_f16_bits(vr[0]);
+            vc[1] = f32_to_f16_bits(vr[1]);
+        }
+    } else {
+        for (int i = tid; i < kvmul * kFusedHD; i += 256) qs[i] = qg[i];
+    }
     __syncthreads();
     const int h = tid / kScoreChunk, t = chunk * kScoreChunk + tid % kScoreChunk;
     if (h >= kvmul || t >= span) return;
-    const uint4* krow = (const uint4*)(K + (size_t)(start + t) * kv_dim + (size_t)g * kFusedHD);
     uint4 kr[kFusedHD / 8];
+    if (has_cur && t == tcur) {
 #pragma unroll
-    for (int c = 0; c < kFusedHD / 8; c++) kr[c] = krow[c];
+        for (int c = 0; c < kFusedHD / 8; c++) kr[c] = *(const uint4*)&kcur[8 * c];
+    } else {
+        const uint4* krow = (const uint4*)(K + (size_t)(start + t) * kv_dim + (size_t)g * kFusedHD);
+#pragma unroll
+        for (int c = 0; c < kFusedHD / 8; c++) kr[c] = krow[c];
+    }
     const float* qh = qs + h * kFusedHD;
     float acc[8];
 #pragma unroll
@@ -717,12 +771,16 @@ bool attend_exact_graphable(const gllm_hip_kv* kv, int n_heads, int n_kv, int hd
 // on the position (a captured decode step replays for every position).
 int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
                  int start, int end0, int p, float scale, float* d_out, hipStream_t s,
-                 float* scratch, const int* d_end, int span_cap) {
+                 float* scratch, const int* d_end, int span_cap, const float* rope_sin,
+                 const float* rope_cos, const float* d_knew, const float* d_vnew) {
     const int span0 = end0 - start + 1;
     const int span_max = d_end ? span_cap : span0 + p - 1;
     const int kvmul = n_heads / n_kv;
     if (d_end && (p != 1 || !attend_exact_graphable(kv, n_heads, n_kv, hd, span_cap)))
         return fail(GLLM_EUNSUP, "attend: device-side positions need the head_dim 128 path");
+    if (rope_sin && (!d_end || !d_knew || !d_vnew))
+        return fail(GLLM_EINVAL, "attend: RoPE folding needs one token and its raw k / v rows");
+    const AttnRope rope{rope_sin, rope_cos, d_knew, d_vnew, kv->k[l], kv->v[l]};
     if (hd == kFusedHD && kvmul <= 4 && kv->kv_dim_k == kv->kv_dim_v && span_max <= kSmaxSpan) {
         float* sc = scratch ? scratch
                             : (float*)thread_scratch(5, (size_t)p * n_heads * span_max * 4 + 256);
@@ -730,7 +788,7 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
         const int nchunk = (span_max + kScoreChunk - 1) / kScoreChunk;
         hipLaunchKernelGGL(attn_scores128_kernel, dim3(n_kv, nchunk, p), dim3(256), 0, s, d_q,
                            kv->k[l], kv->kv_dim_k, n_kv, kvmul, start, span0, span_max, scale, sc,
-                           d_end);
+                           d_end, rope);
         GLLM_HIP(hipGetLastError());
         hipLaunchKernelGGL(attn_softmax_values_kernel, dim3(n_heads, p), dim3(256),
                            smax_lds_bytes(span_max), s, sc, kv->v[l], kv->kv_dim_v, kvmul, start,
@@ -824,7 +882,7 @@ int attend_dev_impl(gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n
     if (mode == GLLM_ATTN_SPLITK)
         return attend_splitk(kv, l, d_q, n_heads, n_kv, hd, start, end, scale, d_out, s);
     return attend_exact(kv, l, d_q, n_heads, n_kv, hd, start, end, 1, scale, d_out, s, nullptr,
-                        nullptr, 0);
+                        nullptr, 0, nullptr, nullptr, nullptr, nullptr);
 }
 
 int kv_store_dev_impl(gllm_hip_kv* kv, int l, int pos, const float* d_k, const float* d_v,
@@ -972,7 +1030,8 @@ int gllm_hip_attend_group(gllm_hip_kv* kv, int l, int kvh, const float* q, int q
     view.v = vp;
     view.layers = 1;
     GLLM_TRY(attend_exact(&view, 0, d, q_heads, 1, hd, start, end, 1, scale,
-                          d + (size_t)q_heads * hd, s, nullptr, nullptr, 0));
+                          d + (size_t)q_heads * hd, s, nullptr, nullptr, 0, nullptr, nullptr,
+                          nullptr, nullptr));
     GLLM_HIP(hipMemcpyAsync(out, d + (size_t)q_heads * hd, (size_t)q_heads * vd * 4,
                             hipMemcpyDeviceToHost, s));
     GLLM_HIP(hipStreamSynchronize(s));

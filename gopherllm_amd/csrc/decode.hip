@@ -26,7 +26,8 @@ int gemv_silu_f32(gllm_hip_weight* w, const float* gate, const float* up, int p,
                   void* act_buf, float* hidden, hipStream_t s);
 int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
                  int start, int end0, int p, float scale, float* d_out, hipStream_t s,
-                 float* scratch, const int* d_end, int span_cap);
+                 float* scratch, const int* d_end, int span_cap, const float* rope_sin,
+                 const float* rope_cos, const float* d_knew, const float* d_vnew);
 bool attend_exact_graphable(const gllm_hip_kv* kv, int n_heads, int n_kv, int hd, int span_cap);
 int attend_splitk(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
                   int start, int end, float scale, float* d_out, hipStream_t s);
@@ -298,13 +299,23 @@ static int forward(gllm_hip_model* m, int pos0, int p, const int* d_pos = nullpt
             float* outs[3] = {m->q, m->k, m->v};
             GLLM_TRY(matvec(m, 3, ws, m->xn, p, outs));
         }
-        const int pairs = std::max(c.n_heads, c.n_kv_heads) * (hd / 2);
-        hipLaunchKernelGGL(rope_kv_kernel, dim3(grid1((size_t)pairs, 256), p), dim3(256), 0, s, m->q,
-                           m->k, m->v, c.n_heads, c.n_kv_heads, hd, pos0, m->d_sin, m->d_cos,
-                           gllm_hip_kv_k_dev(m->kv, l), gllm_hip_kv_v_dev(m->kv, l), d_pos);
-        GLLM_HIP(hipGetLastError());
-        GLLM_TRY(attend_exact(m->kv, l, m->q, c.n_heads, c.n_kv_heads, hd, 0, pos0, p, scale,
-                              m->attn, s, m->scores, d_pos, c.max_len));
+        if (d_pos) {
+            // captured decode step: RoPE and the K/V store run inside the
+            // attention scores launch
+            GLLM_TRY(attend_exact(m->kv, l, m->q, c.n_heads, c.n_kv_heads, hd, 0, pos0, p, scale,
+                                  m->attn, s, m->scores, d_pos, c.max_len, m->d_sin, m->d_cos,
+                                  m->k, m->v));
+        } else {
+            const int pairs = std::max(c.n_heads, c.n_kv_heads) * (hd / 2);
+            hipLaunchKernelGGL(rope_kv_kernel, dim3(grid1((size_t)pairs, 256), p), dim3(256), 0, s,
+                               m->q, m->k, m->v, c.n_heads, c.n_kv_heads, hd, pos0, m->d_sin,
+                               m->d_cos, gllm_hip_kv_k_dev(m->kv, l), gllm_hip_kv_v_dev(m->kv, l),
+                               d_pos);
+            GLLM_HIP(hipGetLastError());
+            GLLM_TRY(attend_exact(m->kv, l, m->q, c.n_heads, c.n_kv_heads, hd, 0, pos0, p, scale,
+                                  m->attn, s, m->scores, d_pos, c.max_len, nullptr, nullptr,
+                                  nullptr, nullptr));
+        }
         {
             gllm_hip_weight* ws[1] = {W[GLLM_T_WO]};
             float* outs[1] = {m->proj};
