@@ -44,7 +44,7 @@ struct GemvJob {
     size_t rb;
     ActQ8 act;        // pre-quantised activations (unfused kernels)
     const float* xf;  // f32 activations when the kernel quantises them itself
-    int rows_per_wg;  // rows per workgroup (gemv_q4k_kernel: blockDim.x / (8 * G))
+    int rows_per_wg;  // rows per workgroup: blockDim.x / (8 * G)
     int tok0;         // first activation row of this launch
     int ntok;         // activation rows in this launch (<= NT)
 };
@@ -52,20 +52,20 @@ struct GemvJob {
 __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
 __device__ __forceinline__ int ubyte(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xffu); }
 
+// Blocks per lane in flight in the Q6_K / Q8_0 row kernels.  Batch 1 keeps
+// four (its activation operands ride in the same registers); larger batches
+// read the activations per token and keep two, which holds the VGPR count at
+// the occupancy the memory stream needs.
 template <int NT>
-__device__ __forceinline__ void store_rows(const GemvJob& j, int wi, int r, int k, const float* v) {
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        float s = tree8(v[t]);
-        if (k == 0 && t < j.ntok) j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = s;
-    }
-}
+constexpr int kQ6Depth = NT == 1 ? 4 : 2;
+template <int NT>
+constexpr int kQ8Depth = NT == 1 ? 4 : 2;
 
 __device__ __forceinline__ int locate(const GemvJob& j, int wg, int* wi) {
     int i = 0;
     while (i + 1 < j.n && wg >= j.wg_begin[i + 1]) i++;
     *wi = i;
-    return (wg - j.wg_begin[i]) * kRowsPerWG;
+    return (wg - j.wg_begin[i]) * j.rows_per_wg;
 }
 
 // ---------------------------------------------------------------------------
@@ -442,13 +442,20 @@ __global__ __launch_bounds__(256) void gemv_q4k_any_kernel(GemvJob j) {
 // covers bytes 4k..4k+3 of each 32-byte quad (Q6KQ8QUAD,
 // kernels_amd64.s:1130-1142); lanes 0-3 use scale 8h+2c, lanes 4-7 8h+2c+1.
 // ---------------------------------------------------------------------------
-template <int NT>
+//
+// G lanes share one AVX2 lane (G = 2, 4 for short matrices, so that a launch
+// still fills the chip): lane gi takes blocks gi, gi + G, ... and the
+// reference's sequential per-lane chain visits the G lanes in block order
+// through rot_prev, ending in lane gi = G - 1 after every group of G blocks.
+template <int NT, int G>
 __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
+    constexpr int D = kQ6Depth<NT>;
     int wi;
-    const int r = locate(j, blockIdx.x, &wi) + (threadIdx.x >> 3);
-    const int k = threadIdx.x & 7;
-    if (r >= j.rows[wi]) return;
-    const int B = j.blocks;
+    const int tid = threadIdx.x;
+    const int gi = tid % G, k = (tid / G) & 7;
+    const int r = locate(j, blockIdx.x, &wi) + tid / (8 * G);
+    if (r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    const int B = j.blocks, NB = B / G;
     const uint8_t* row = j.w[wi] + (size_t)r * j.rb;
     const uint16_t* dv = (const uint16_t*)(row + (size_t)B * 208);
     const int hk = k >> 2;
@@ -458,29 +465,52 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
     const int8_t* q8 = j.act.q8perm + (size_t)j.tok0 * j.cols + k * 32;
     const float* xsc = j.act.xscale + (size_t)j.tok0 * B;
     const float* xs16 = j.act.xs16 + (size_t)j.tok0 * (j.cols / 16) + k;
-#pragma unroll 2
-    for (int b = 0; b < B; b++) {
-        const uint8_t* blk = row + (size_t)b * 208;
-        const uint32_t ql0 = *(const uint32_t*)(blk + 4 * k);
-        const uint32_t ql1 = *(const uint32_t*)(blk + 32 + 4 * k);
-        const uint32_t ql2 = *(const uint32_t*)(blk + 64 + 4 * k);
-        const uint32_t ql3 = *(const uint32_t*)(blk + 96 + 4 * k);
-        const uint32_t qh0 = *(const uint32_t*)(blk + 128 + 4 * k);
-        const uint32_t qh1 = *(const uint32_t*)(blk + 160 + 4 * k);
-        const uint4 sv = *(const uint4*)(blk + 192);
-        const float d = f16_bits_to_f32(dv[b]);
+    // D blocks of this lane's bytes in flight, loaded in block order; the
+    // loads are unconditional (clamped to the lane's last block) so the
+    // compiler's vmcnt waits never drain the ring.  At batch 1 the block's
+    // activation operands ride in the ring too: loaded later than the
+    // weights, they would make every wait a full drain.
+    struct Blk {
+        uint32_t ql[4], qh[2];
+        uint4 sv;
+        uint32_t d;
+        int4 qa, qb;
+        float x0, x8, xs;
+    };
+    auto load = [&](int i, Blk& o) __attribute__((always_inline)) {
+        const int bb = min(i, NB - 1) * G + gi;
+        const uint8_t* blk = row + (size_t)bb * 208;
+        o.ql[0] = *(const uint32_t*)(blk + 4 * k);
+        o.ql[1] = *(const uint32_t*)(blk + 32 + 4 * k);
+        o.ql[2] = *(const uint32_t*)(blk + 64 + 4 * k);
+        o.ql[3] = *(const uint32_t*)(blk + 96 + 4 * k);
+        o.qh[0] = *(const uint32_t*)(blk + 128 + 4 * k);
+        o.qh[1] = *(const uint32_t*)(blk + 160 + 4 * k);
+        o.sv = *(const uint4*)(blk + 192);
+        o.d = dv[bb];
+        if constexpr (NT == 1) {
+            o.qa = *(const int4*)(q8 + bb * 256);
+            o.qb = *(const int4*)(q8 + bb * 256 + 16);
+            o.x0 = xs16[bb * 16];
+            o.x8 = xs16[bb * 16 + 8];
+            o.xs = xsc[bb];
+        }
+    };
+    auto compute = [&](int i, const Blk& o) __attribute__((always_inline)) {
+        const int b = i * G + gi;
+        const float d = f16_bits_to_f32(o.d);
         // codes of quad (h, c), c = 0..3 (m = 4h + c)
         int code[8];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const uint32_t y0 = h ? ql2 : ql0, y1 = h ? ql3 : ql1, qh = h ? qh1 : qh0;
+            const uint32_t y0 = h ? o.ql[2] : o.ql[0], y1 = h ? o.ql[3] : o.ql[1], qh = o.qh[h];
             code[4 * h + 0] = (int)((y0 & 0x0f0f0f0fu) | ((qh & 0x03030303u) << 4));
             code[4 * h + 1] = (int)((y1 & 0x0f0f0f0fu) | (((qh >> 2) & 0x03030303u) << 4));
             code[4 * h + 2] = (int)(((y0 >> 4) & 0x0f0f0f0fu) | (((qh >> 4) & 0x03030303u) << 4));
             code[4 * h + 3] = (int)(((y1 >> 4) & 0x0f0f0f0fu) | (((qh >> 6) & 0x03030303u) << 4));
         }
         // scale of quad m: byte 8h + 2c + hk of the 16 scale bytes
-        const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+        const uint32_t sw[4] = {o.sv.x, o.sv.y, o.sv.z, o.sv.w};
         int scl[8];
 #pragma unroll
         for (int m = 0; m < 8; m++) {
@@ -491,9 +521,10 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
         const float sk8 = (float)sbyte(sw[2 + (k >> 2)], k & 3);
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            if (t < j.ntok) {
-                const int4 qa = *(const int4*)(q8 + (size_t)t * j.cols + b * 256);
-                const int4 qb = *(const int4*)(q8 + (size_t)t * j.cols + b * 256 + 16);
+            if (NT == 1 || t < j.ntok) {
+                const int4 qa = NT == 1 ? o.qa : *(const int4*)(q8 + (size_t)t * j.cols + b * 256);
+                const int4 qb =
+                    NT == 1 ? o.qb : *(const int4*)(q8 + (size_t)t * j.cols + b * 256 + 16);
                 int acc = scl[0] * sdot4(code[0], qa.x, 0);
                 acc += scl[1] * sdot4(code[1], qa.y, 0);
                 acc += scl[2] * sdot4(code[2], qa.z, 0);
@@ -503,18 +534,45 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
                 acc += scl[6] * sdot4(code[6], qb.z, 0);
                 acc += scl[7] * sdot4(code[7], qb.w, 0);
                 const float* xs = xs16 + (size_t)t * (j.cols / 16) + b * 16;
-                float o = sk * xs[0];                                  // VMULPS
-                o = fmaf(sk8, xs[8], o);                                // VFMADD231PS
-                accM[t] = fmaf(d, o, accM[t]);                          // VFMADD231PS
-                const float dxs = d * xsc[(size_t)t * B + b];           // VMULSS
-                accF[t] = fmaf((float)acc, dxs, accF[t]);               // VFMADD231PS
+                float o2 = sk * (NT == 1 ? o.x0 : xs[0]);               // VMULPS
+                o2 = fmaf(sk8, NT == 1 ? o.x8 : xs[8], o2);             // VFMADD231PS
+                const float dxs = d * (NT == 1 ? o.xs : xsc[(size_t)t * B + b]);  // VMULSS
+                const float iv = (float)acc;
+#pragma unroll
+                for (int step = 0; step < G; step++) {
+                    accM[t] = fmaf(d, o2, rot_prev<G>(accM[t]));        // VFMADD231PS
+                    accF[t] = fmaf(iv, dxs, rot_prev<G>(accF[t]));      // VFMADD231PS
+                }
             }
         }
-    }
-    float v[NT];
+    };
+    Blk ring[D];
 #pragma unroll
-    for (int t = 0; t < NT; t++) v[t] = accF[t] - accM[t];
-    store_rows<NT>(j, wi, r, k, v);
+    for (int i = 0; i < D; i++) {
+        load(i, ring[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // whole groups straight-line (a guarded compute would turn the waits
+    // at its join into drains), then the tail
+    int i0 = 0;
+    for (; i0 + D <= NB; i0 += D) {
+#pragma unroll
+        for (int ii = 0; ii < D; ii++) {
+            compute(i0 + ii, ring[ii]);
+            __builtin_amdgcn_sched_barrier(0);  // keep the loads in block order
+            load(i0 + ii + D, ring[ii]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int ii = 0; ii < D - 1; ii++)
+        if (i0 + ii < NB) compute(i0 + ii, ring[ii]);  // uniform
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const float v = tree8_strided<G>(accF[t] - accM[t]);  // VSUBPS + tree
+        if (k == 0 && gi == G - 1 && t < j.ntok)
+            j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -522,44 +580,88 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
 // (272 bytes, 16-byte aligned).  AVX2 lane k covers bytes 4k..4k+3 of each
 // 32-value block (Q80CHUNK, kernels_amd64.s:1321-1345).
 // ---------------------------------------------------------------------------
-template <int NT>
+// G lanes per AVX2 lane as in gemv_q6k_kernel.
+template <int NT, int G>
 __global__ __launch_bounds__(256) void gemv_q8_0_kernel(GemvJob j) {
+    constexpr int D = kQ8Depth<NT>;
     int wi;
-    const int r = locate(j, blockIdx.x, &wi) + (threadIdx.x >> 3);
-    const int k = threadIdx.x & 7;
-    if (r >= j.rows[wi]) return;
-    const int B = j.blocks;
+    const int tid = threadIdx.x;
+    const int gi = tid % G, k = (tid / G) & 7;
+    const int r = locate(j, blockIdx.x, &wi) + tid / (8 * G);
+    if (r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    const int B = j.blocks, NB = B / G;
     const uint8_t* row = j.w[wi] + (size_t)r * j.rb;
     float acc11[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) acc11[t] = 0.0f;
     const int8_t* q8 = j.act.q8perm + (size_t)j.tok0 * j.cols + k * 32;
     const float* xsc = j.act.xscale + (size_t)j.tok0 * B;
-#pragma unroll 2
-    for (int b = 0; b < B; b++) {
-        const uint8_t* blk = row + (size_t)b * 272;
-        const uint4 dh = *(const uint4*)blk;
+    // D blocks of this lane's bytes in flight (see gemv_q6k_kernel)
+    struct Blk {
+        uint4 dh;
+        int wv[8];
+        int4 qa, qb;
+        float xs;
+    };
+    auto load = [&](int i, Blk& o) __attribute__((always_inline)) {
+        const int bb = min(i, NB - 1) * G + gi;
+        const uint8_t* blk = row + (size_t)bb * 272;
+        o.dh = *(const uint4*)blk;
+#pragma unroll
+        for (int q = 0; q < 8; q++) o.wv[q] = *(const int*)(blk + 16 + 32 * q + 4 * k);
+        if constexpr (NT == 1) {
+            o.qa = *(const int4*)(q8 + bb * 256);
+            o.qb = *(const int4*)(q8 + bb * 256 + 16);
+            o.xs = xsc[bb];
+        }
+    };
+    auto compute = [&](int i, const Blk& o) __attribute__((always_inline)) {
+        const int b = i * G + gi;
         float dj[8];
-        const uint32_t dw[4] = {dh.x, dh.y, dh.z, dh.w};
+        const uint32_t dw[4] = {o.dh.x, o.dh.y, o.dh.z, o.dh.w};
 #pragma unroll
         for (int q = 0; q < 8; q++) dj[q] = f16_bits_to_f32((dw[q >> 1] >> (16 * (q & 1))) & 0xffffu);
-        int wv[8];
-#pragma unroll
-        for (int q = 0; q < 8; q++) wv[q] = *(const int*)(blk + 16 + 32 * q + 4 * k);
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            if (t < j.ntok) {
-                const int4 qa = *(const int4*)(q8 + (size_t)t * j.cols + b * 256);
-                const int4 qb = *(const int4*)(q8 + (size_t)t * j.cols + b * 256 + 16);
+            if (NT == 1 || t < j.ntok) {
+                const int4 qa = NT == 1 ? o.qa : *(const int4*)(q8 + (size_t)t * j.cols + b * 256);
+                const int4 qb =
+                    NT == 1 ? o.qb : *(const int4*)(q8 + (size_t)t * j.cols + b * 256 + 16);
                 const int xq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
                 float acc12 = 0.0f;
 #pragma unroll
-                for (int q = 0; q < 8; q++) acc12 = fmaf((float)sdot4(wv[q], xq[q], 0), dj[q], acc12);
-                acc11[t] = fmaf(acc12, xsc[(size_t)t * B + b], acc11[t]);
+                for (int q = 0; q < 8; q++) acc12 = fmaf((float)sdot4(o.wv[q], xq[q], 0), dj[q], acc12);
+                const float xs = NT == 1 ? o.xs : xsc[(size_t)t * B + b];
+#pragma unroll
+                for (int step = 0; step < G; step++) acc11[t] = fmaf(acc12, xs, rot_prev<G>(acc11[t]));
             }
         }
+    };
+    Blk ring[D];
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+        load(i, ring[i]);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    store_rows<NT>(j, wi, r, k, acc11);
+    int i0 = 0;
+    for (; i0 + D <= NB; i0 += D) {
+#pragma unroll
+        for (int ii = 0; ii < D; ii++) {
+            compute(i0 + ii, ring[ii]);
+            __builtin_amdgcn_sched_barrier(0);  // keep the loads in block order
+            load(i0 + ii + D, ring[ii]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int ii = 0; ii < D - 1; ii++)
+        if (i0 + ii < NB) compute(i0 + ii, ring[ii]);  // uniform
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const float v = tree8_strided<G>(acc11[t]);
+        if (k == 0 && gi == G - 1 && t < j.ntok)
+            j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
+    }
 }
 
 // Debug: the exact int32 lane sums of every (row, block).
@@ -821,6 +923,31 @@ int launch_q4k(GemvJob& j, const int* rows, int n, const Q4KShape& sh, hipStream
     return GLLM_OK;
 }
 
+// Lanes per AVX2 lane (G) of the Q6_K / Q8_0 row kernels (G divides the
+// block count).  Batch 1 splits a row only when the matrix gives fewer than
+// half the compute units a workgroup: the G-step rotation costs more than the
+// extra workgroups bring once the launch has 128 of them.  Batches (per-token
+// activation reads make each block several times longer) take the largest G
+// that keeps the launch at two workgroups per compute unit or fewer.
+// GLLM_ROW_G overrides, for measurement; every G gives the same bits.
+static int row_lanes_g(int total_rows, int blocks, int ntok) {
+    static const int forced = [] {
+        const char* e = getenv("GLLM_ROW_G");
+        const int v = e ? atoi(e) : 0;
+        return v == 1 || v == 2 || v == 4 ? v : 0;
+    }();
+    if (forced && blocks % forced == 0) return forced;
+    const int ncu = device_cus();
+    auto wgs = [&](int g) { return (total_rows * g + kRowsPerWG - 1) / kRowsPerWG; };
+    int g = 1;
+    if (ntok == 1) {
+        while (g < 4 && blocks % (2 * g) == 0 && wgs(g) < ncu / 2) g *= 2;
+    } else {
+        while (g < 4 && blocks % (2 * g) == 0 && wgs(2 * g) <= 2 * ncu) g *= 2;
+    }
+    return g;
+}
+
 template <int NT>
 int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t s) {
     if (type == GLLM_TYPE_Q4_K) {
@@ -831,11 +958,24 @@ int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t 
              : sh.g == 2 ? launch_q4k<NT, 2>(j, rows, j.n, sh, s)
                          : launch_q4k<NT, 4>(j, rows, j.n, sh, s);
     }
-    switch (type) {
-    case GLLM_TYPE_Q6_K: hipLaunchKernelGGL(gemv_q6k_kernel<NT>, dim3(grid), dim3(256), 0, s, j); break;
-    case GLLM_TYPE_Q8_0: hipLaunchKernelGGL(gemv_q8_0_kernel<NT>, dim3(grid), dim3(256), 0, s, j); break;
-    default: return fail(GLLM_EUNSUP, "gemv: unsupported type %d", type);
+    if (type != GLLM_TYPE_Q6_K && type != GLLM_TYPE_Q8_0)
+        return fail(GLLM_EUNSUP, "gemv: unsupported type %d", type);
+    int total = 0;
+    for (int i = 0; i < j.n; i++) total += rows[i];
+    const int g = row_lanes_g(total, j.blocks, j.ntok);
+    j.rows_per_wg = kRowsPerWG / g;
+    int wg = 0;
+    for (int i = 0; i < j.n; i++) {
+        j.wg_begin[i] = wg;
+        wg += (rows[i] + j.rows_per_wg - 1) / j.rows_per_wg;
     }
+    j.wg_begin[j.n] = wg;
+    void (*kern)(GemvJob);
+    if (type == GLLM_TYPE_Q6_K)
+        kern = g == 1 ? gemv_q6k_kernel<NT, 1> : g == 2 ? gemv_q6k_kernel<NT, 2> : gemv_q6k_kernel<NT, 4>;
+    else
+        kern = g == 1 ? gemv_q8_0_kernel<NT, 1> : g == 2 ? gemv_q8_0_kernel<NT, 2> : gemv_q8_0_kernel<NT, 4>;
+    hipLaunchKernelGGL(kern, dim3(wg), dim3(256), 0, s, j);
     GLLM_HIP(hipGetLastError());
     return GLLM_OK;
 }

@@ -110,15 +110,22 @@ def test_matvec_ffn_shapes(hip, name):
         assert_parity(got8, xs, qtype, data, rows, cols, generic=False)
 
 
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("rows,cols", [(300, 1024), (37, 512), (1000, 14336)])
 @pytest.mark.parametrize("p", [2, 5, 8, 13])
-def test_batch_equals_per_token(hip, p):
-    rows, cols = 300, 1024
-    data, _ = quant_matrix(ref.Q4_K, rows, cols, 90 + p)
-    w = hip.Weight.from_host(data, ref.Q4_K, rows, cols)
+def test_batch_equals_per_token(hip, name, rows, cols, p):
+    """matvecBatchQ8 == per-token row kernel (forward_batch_test.go); the
+    shapes give the Q6_K / Q8_0 kernels 1, 2 and 4 lanes per AVX2 lane at
+    batch 1 and in batches."""
+    qtype = TYPES[name]
+    data, _ = quant_matrix(qtype, rows, cols, 90 + p + rows)
+    w = hip.Weight.from_host(data, qtype, rows, cols)
     xs = normal(91 + p, (p, cols))
+    print(f"batch {name} {rows}x{cols} p={p}", flush=True)
     batch = w.matvec_batch(xs)
     for t in range(p):
         assert np.array_equal(bits(batch[t]), bits(w.matvec_into(xs[t])))
+    assert_parity(batch, xs, qtype, data, rows, cols, generic=False)
 
 
 @pytest.mark.parametrize("qtype", [ref.Q4_K, ref.Q6_K])
