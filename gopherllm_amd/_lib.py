@@ -49,6 +49,8 @@ SIGNATURES = {
     "gllm_hip_matvec3": (i32, [vp, vp, vp, vp, vp, vp, vp]),
     "gllm_hip_matvec_batch": (i32, [vp, vp, i32, vp]),
     "gllm_hip_argmax": (i32, [vp, vp, vp]),
+    "gllm_hip_argmax_penalized": (i32, [vp, vp, vp, i32, f32, vp]),
+    "gllm_hip_argmax_penalized_dev": (i32, [vp, vp, vp, i32, f32, vp, vp]),
     "gllm_hip_matvec_dev": (i32, [vp, vp, i32, vp, i32, vp]),
     "gllm_hip_matvec_multi_dev": (i32, [i32, vp, vp, i32, vp, vp, vp]),
     "gllm_hip_argmax_dev": (i32, [vp, vp, vp, vp]),
@@ -75,6 +77,7 @@ SIGNATURES = {
     "gllm_hip_model_decode": (i32, [vp, u32, i32, vp]),
     "gllm_hip_model_prefill": (i32, [vp, vp, i32, i32, vp, vp]),
     "gllm_hip_model_hidden": (i32, [vp, vp]),
+    "gllm_hip_model_set_repeat_penalty": (i32, [vp, f32, i32]),
     "gllm_hip_model_kv": (vp, [vp]),
 }
 

@@ -101,10 +101,18 @@ class Weight:
         call("gllm_hip_matvec_batch", self.handle, _np_ptr(xs), xs.shape[0], _np_ptr(out))
         return out
 
-    def argmax_matvec(self, x) -> int:
+    def argmax_matvec(self, x, recent=None, penalty: float = 1.0) -> int:
+        """Greedy token of W.x; with recent / penalty, after applyRepeatPenalty
+        (sampling.go:136-153), as ArgmaxQ6KPenalized (internal/metal/
+        metal_darwin.go:1175) takes them."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         tok = C.c_uint32(0)
-        call("gllm_hip_argmax", self.handle, _np_ptr(x), C.byref(tok))
+        if recent is None and penalty == 1.0:
+            call("gllm_hip_argmax", self.handle, _np_ptr(x), C.byref(tok))
+        else:
+            rec = np.ascontiguousarray(recent if recent is not None else [], dtype=np.uint32)
+            call("gllm_hip_argmax_penalized", self.handle, _np_ptr(x),
+                 _np_ptr(rec) if rec.size else None, rec.size, float(penalty), C.byref(tok))
         return int(tok.value)
 
     # device forms ------------------------------------------------------------
@@ -122,8 +130,16 @@ class Weight:
              out.shape[-1], _stream(stream))
         return out
 
-    def argmax_dev(self, x, token_out, stream=None):
-        call("gllm_hip_argmax_dev", self.handle, _dev_ptr(x), _dev_ptr(token_out), _stream(stream))
+    def argmax_dev(self, x, token_out, stream=None, recent=None, penalty: float = 1.0):
+        """recent: uint32/int32 device tensor of token ids, or None."""
+        if recent is None and penalty == 1.0:
+            call("gllm_hip_argmax_dev", self.handle, _dev_ptr(x), _dev_ptr(token_out),
+                 _stream(stream))
+        else:
+            n = 0 if recent is None else recent.numel()
+            call("gllm_hip_argmax_penalized_dev", self.handle, _dev_ptr(x),
+                 _dev_ptr(recent) if n else None, n, float(penalty), _dev_ptr(token_out),
+                 _stream(stream))
         return token_out
 
     def lane_ints_dev(self, x, out, stream=None):

@@ -34,7 +34,7 @@ int attend_splitk(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, i
 int kv_store_dev_impl(gllm_hip_kv* kv, int l, int pos, const float* d_k, const float* d_v,
                       hipStream_t s);
 int launch_argmax(const float* logits, int n, uint32_t* token, unsigned long long* keys,
-                  hipStream_t s);
+                  hipStream_t s, const uint32_t* recent, int n_recent, float penalty);
 size_t argmax_keys(int n);
 }  // namespace gllm
 
@@ -61,6 +61,13 @@ struct gllm_hip_model {
     int* h_pos = nullptr;          // pinned staging for it
     hipGraphExec_t decode_graph = nullptr;  // one decode step, captured after a first eager step
     int last_p = 0;
+    // repeat penalty over the trailing token window (runtime.go:1035 and
+    // 1089-1093): ids of the last `window` tokens seen, oldest first
+    float penalty = 1.0f;
+    int window = 0;
+    std::vector<uint32_t> recent;
+    uint32_t* d_recent = nullptr;  // window ids, unused slots 0xffffffff (ignored ids)
+    uint32_t* h_recent = nullptr;  // pinned staging for it
 };
 
 namespace gllm {
@@ -237,6 +244,8 @@ __global__ void rope_kv_kernel(float* __restrict__ q, float* __restrict__ k,
 
 static inline int grid1(size_t n, int block) { return (int)((n + block - 1) / block); }
 
+constexpr int kMaxRepeatWindow = 4096;  // the reference uses 64 (runtime.go:27)
+
 static void drop_decode_graph(gllm_hip_model* m) {
     if (m->decode_graph) (void)hipGraphExecDestroy(m->decode_graph);
     m->decode_graph = nullptr;
@@ -340,14 +349,40 @@ static int forward(gllm_hip_model* m, int pos0, int p, const int* d_pos = nullpt
     return GLLM_OK;
 }
 
+static bool penalty_on(const gllm_hip_model* m) { return m->penalty != 1.0f && m->window > 0; }
+
+// emitToken's window update (runtime.go:1089-1093)
+static void push_recent(gllm_hip_model* m, uint32_t tok) {
+    if (m->window <= 0) return;
+    if ((int)m->recent.size() == m->window) m->recent.erase(m->recent.begin());
+    m->recent.push_back(tok);
+}
+
+// The window as the argmax reads it: always `window` ids, so a captured
+// decode step stays valid while the window fills.
+static int upload_recent(gllm_hip_model* m) {
+    if (!penalty_on(m)) return GLLM_OK;
+    for (int i = 0; i < m->window; i++)
+        m->h_recent[i] = i < (int)m->recent.size() ? m->recent[i] : 0xffffffffu;
+    GLLM_HIP(hipMemcpyAsync(m->d_recent, m->h_recent, (size_t)m->window * 4, hipMemcpyHostToDevice,
+                            m->stream));
+    return GLLM_OK;
+}
+
+static int model_argmax(gllm_hip_model* m, uint32_t* d_token) {
+    const bool on = penalty_on(m);
+    return launch_argmax(m->logits, m->cfg.vocab, d_token, m->argmax_keys, m->stream,
+                         on ? m->d_recent : nullptr, on ? m->window : 0, m->penalty);
+}
+
 // One greedy decode step on the token in d_tokens[0]: forward, the output
-// projection (full logits), then argmax into d_tokens[1].
+// projection (full logits), then the (penalised) argmax into d_tokens[1].
 static int decode_step(gllm_hip_model* m, int pos, const int* d_pos) {
     GLLM_TRY(forward(m, pos, 1, d_pos));
     gllm_hip_weight* ws[1] = {m->output};
     float* outs[1] = {m->logits};
     GLLM_TRY(matvec(m, 1, ws, m->xn, 1, outs));
-    return launch_argmax(m->logits, m->cfg.vocab, m->d_tokens + 1, m->argmax_keys, m->stream);
+    return model_argmax(m, m->d_tokens + 1);
 }
 
 static int check_ready(const gllm_hip_model* m) {
@@ -435,6 +470,8 @@ void gllm_hip_model_release(gllm_hip_model* m) {
     if (m->d_pos) (void)hipFree(m->d_pos);
     if (m->h_pos) (void)hipHostFree(m->h_pos);
     if (m->kv) gllm_hip_kv_release(m->kv);
+    if (m->d_recent) (void)hipFree(m->d_recent);
+    if (m->h_recent) (void)hipHostFree(m->h_recent);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
 }
@@ -487,6 +524,8 @@ int gllm_hip_model_decode(gllm_hip_model* m, uint32_t token, int pos, uint32_t* 
     if (pos < 0 || pos >= m->cfg.max_len) return fail(GLLM_EINVAL, "position %d out of range", pos);
     if (token >= (uint32_t)m->cfg.vocab) return fail(GLLM_EINVAL, "token %u out of range", token);
     hipStream_t s = m->stream;
+    push_recent(m, token);
+    GLLM_TRY(upload_recent(m));
     m->h_tokens[0] = token;
     m->h_pos[0] = pos;
     GLLM_HIP(hipMemcpyAsync(m->d_tokens, m->h_tokens, 4, hipMemcpyHostToDevice, s));
@@ -532,6 +571,8 @@ int gllm_hip_model_prefill(gllm_hip_model* m, const uint32_t* tokens, int n, int
     const int chunk = 64;
     GLLM_TRY(ensure_buffers(m, std::min(n, chunk)));
     hipStream_t s = m->stream;
+    for (int i = 0; i < n; i++) push_recent(m, tokens[i]);
+    GLLM_TRY(upload_recent(m));
     for (int c0 = 0; c0 < n; c0 += chunk) {
         const int p = std::min(chunk, n - c0);
         memcpy(m->h_tokens, tokens + c0, (size_t)p * 4);
@@ -548,10 +589,10 @@ int gllm_hip_model_prefill(gllm_hip_model* m, const uint32_t* tokens, int n, int
         float* outs[1] = {m->logits};
         GLLM_TRY(matvec(m, 1, ws, last, 1, outs));
     }
-    GLLM_TRY(launch_argmax(m->logits, m->cfg.vocab, m->d_tokens + m->max_p, m->argmax_keys, s));
-    GLLM_HIP(hipMemcpyAsync(m->h_tokens + m->max_p, m->d_tokens + m->max_p, 4, hipMemcpyDeviceToHost, s));
-    if (logits)
+    if (logits)  // the projection, before the penalty
         GLLM_HIP(hipMemcpyAsync(logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost, s));
+    GLLM_TRY(model_argmax(m, m->d_tokens + m->max_p));
+    GLLM_HIP(hipMemcpyAsync(m->h_tokens + m->max_p, m->d_tokens + m->max_p, 4, hipMemcpyDeviceToHost, s));
     GLLM_HIP(hipStreamSynchronize(s));
     *first = m->h_tokens[m->max_p];
     // keep the last token's hidden state where gllm_hip_model_hidden reads it
@@ -566,6 +607,30 @@ int gllm_hip_model_hidden(gllm_hip_model* m, float* out) {
     const float* last = m->xn + (size_t)(std::max(1, m->last_p) - 1) * m->cfg.dim;
     GLLM_HIP(hipMemcpyAsync(out, last, (size_t)m->cfg.dim * 4, hipMemcpyDeviceToHost, m->stream));
     GLLM_HIP(hipStreamSynchronize(m->stream));
+    return GLLM_OK;
+}
+
+int gllm_hip_model_set_repeat_penalty(gllm_hip_model* m, float penalty, int window) {
+    if (!m) return fail(GLLM_EINVAL, "gllm_hip_model_set_repeat_penalty: null model");
+    if (!(penalty > 0.0f) || penalty == INFINITY)
+        return fail(GLLM_EINVAL, "repeat penalty must be finite and positive");
+    if (window < 0 || window > kMaxRepeatWindow)
+        return fail(GLLM_EINVAL, "repeat window %d outside 0..%d", window, kMaxRepeatWindow);
+    GLLM_HIP(hipStreamSynchronize(m->stream));
+    if (m->d_recent) (void)hipFree(m->d_recent);
+    if (m->h_recent) (void)hipHostFree(m->h_recent);
+    m->d_recent = nullptr;
+    m->h_recent = nullptr;
+    m->recent.clear();
+    m->penalty = 1.0f;
+    m->window = 0;
+    drop_decode_graph(m);  // it captured the old window arguments
+    if (window > 0) {
+        GLLM_HIP(hipMalloc(&m->d_recent, (size_t)window * 4));
+        GLLM_HIP(hipHostMalloc(&m->h_recent, (size_t)window * 4, hipHostMallocDefault));
+    }
+    m->penalty = penalty;
+    m->window = window;
     return GLLM_OK;
 }
 

@@ -746,14 +746,45 @@ __device__ __forceinline__ unsigned long long wg_max_key(unsigned long long best
     return b;
 }
 
+// applyRepeatPenalty (sampling.go:136-153) on logit i, whose id appears
+// `count` times in the recent window: every occurrence applies the rule once
+// more, to the value the previous one left (non-finite -> -inf, positive /=
+// penalty, else *= penalty).  The rule reads only logit i, so applying it
+// count times equals the reference's in-order walk over the window.
+__device__ __forceinline__ float repeat_penalty(float v, int count, float penalty) {
+    for (int c = 0; c < count; c++) {
+        if (!finite_logit(v)) v = -INFINITY;
+        else if (v > 0.0f) v = v / penalty;
+        else v = v * penalty;
+    }
+    return v;
+}
+
+// First stage; with n_recent > 0 and penalty != 1 the workgroup counts the
+// window's ids that fall in its chunk (ids >= n are ignored, as in the
+// reference) and penalises those logits before the finite-argmax rule.
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ logits,
                                                              int n,
-                                                             unsigned long long* __restrict__ keys) {
+                                                             unsigned long long* __restrict__ keys,
+                                                             const uint32_t* __restrict__ recent,
+                                                             int n_recent, float penalty) {
+    __shared__ int hits[kArgmaxChunk];
     const int lo = blockIdx.x * kArgmaxChunk;
     const int hi = min(n, lo + kArgmaxChunk);
+    const bool pen = n_recent > 0 && penalty != 1.0f;
+    if (pen) {
+        for (int i = threadIdx.x; i < kArgmaxChunk; i += 256) hits[i] = 0;
+        __syncthreads();
+        for (int i = threadIdx.x; i < n_recent; i += 256) {
+            const uint32_t id = recent[i];
+            if (id >= (uint32_t)lo && id < (uint32_t)hi) atomicAdd(&hits[id - lo], 1);
+        }
+        __syncthreads();
+    }
     unsigned long long best = 0;
     for (int i = lo + threadIdx.x; i < hi; i += 256) {
-        const float v = logits[i];
+        float v = logits[i];
+        if (pen) v = repeat_penalty(v, hits[i - lo], penalty);
         if (finite_logit(v)) {
             const unsigned long long key = argmax_key(v, i);
             best = key > best ? key : best;
@@ -779,11 +810,17 @@ __global__ void silu_mul_rows_kernel(const float* __restrict__ gate, const float
 
 size_t argmax_keys(int n) { return (size_t)(n + kArgmaxChunk - 1) / kArgmaxChunk; }
 
-// keys: device scratch of argmax_keys(n) entries.
+// keys: device scratch of argmax_keys(n) entries; recent: n_recent device
+// token ids for the repeat penalty (none when n_recent == 0 or penalty == 1).
 int launch_argmax(const float* logits, int n, uint32_t* token, unsigned long long* keys,
-                  hipStream_t s) {
+                  hipStream_t s, const uint32_t* recent, int n_recent, float penalty) {
+    if (n_recent < 0 || (n_recent > 0 && !recent))
+        return fail(GLLM_EINVAL, "argmax: bad recent-token window (%d ids)", n_recent);
+    if (!(penalty > 0.0f) || penalty == INFINITY)
+        return fail(GLLM_EINVAL, "argmax: repeat penalty must be finite and positive");
     const int nk = (int)argmax_keys(n);
-    hipLaunchKernelGGL(argmax_partial_kernel, dim3(nk), dim3(256), 0, s, logits, n, keys);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(nk), dim3(256), 0, s, logits, n, keys, recent,
+                       n_recent, penalty);
     GLLM_HIP(hipGetLastError());
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1024), 0, s, keys, nk, token);
     GLLM_HIP(hipGetLastError());
@@ -1314,7 +1351,8 @@ int gllm_hip_matvec_batch(gllm_hip_weight* w, const float* xs, int p, float* out
     return matvec_host(1, ws, xs, p, o);
 }
 
-int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token, void* stream) {
+int gllm_hip_argmax_penalized_dev(gllm_hip_weight* w, const float* d_x, const uint32_t* d_recent,
+                                  int n_recent, float penalty, uint32_t* d_token, void* stream) {
     GLLM_TRY(validate_weight(w));
     if (!d_x || !d_token) return fail(GLLM_EINVAL, "gllm_hip_argmax_dev: null pointer");
     hipStream_t s = (hipStream_t)stream;
@@ -1326,24 +1364,41 @@ int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token,
     GLLM_TRY(matvec_multi(1, ws, d_x, 1, outs, strides, s, 0));
     auto* keys = (unsigned long long*)thread_scratch(7, argmax_keys(w->rows) * 8);
     if (!keys) return GLLM_ENOMEM;
-    return launch_argmax(logits, w->rows, d_token, keys, s);
+    return launch_argmax(logits, w->rows, d_token, keys, s, d_recent, n_recent, penalty);
 }
 
-int gllm_hip_argmax(gllm_hip_weight* w, const float* x, uint32_t* token) {
+int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token, void* stream) {
+    return gllm_hip_argmax_penalized_dev(w, d_x, nullptr, 0, 1.0f, d_token, stream);
+}
+
+int gllm_hip_argmax_penalized(gllm_hip_weight* w, const float* x, const uint32_t* recent,
+                              int n_recent, float penalty, uint32_t* token) {
     GLLM_TRY(validate_weight(w));
     if (!x || !token) return fail(GLLM_EINVAL, "gllm_hip_argmax: null pointer");
+    if (n_recent < 0 || (n_recent > 0 && !recent))
+        return fail(GLLM_EINVAL, "gllm_hip_argmax_penalized: bad recent-token window");
     hipStream_t s = thread_stream();
     if (!s) return GLLM_EDEVICE;
     float* d_x = (float*)thread_scratch(1, (size_t)w->cols * 4);
     uint32_t* d_tok = (uint32_t*)thread_scratch(4, 64);
     uint32_t* h_tok = (uint32_t*)thread_pinned(0, 64);
     if (!d_x || !d_tok || !h_tok) return GLLM_ENOMEM;
+    uint32_t* d_recent = nullptr;
+    if (n_recent > 0) {
+        d_recent = (uint32_t*)thread_scratch(8, (size_t)n_recent * 4);
+        if (!d_recent) return GLLM_ENOMEM;
+        GLLM_HIP(hipMemcpyAsync(d_recent, recent, (size_t)n_recent * 4, hipMemcpyHostToDevice, s));
+    }
     GLLM_HIP(hipMemcpyAsync(d_x, x, (size_t)w->cols * 4, hipMemcpyHostToDevice, s));
-    GLLM_TRY(gllm_hip_argmax_dev(w, d_x, d_tok, s));
+    GLLM_TRY(gllm_hip_argmax_penalized_dev(w, d_x, d_recent, n_recent, penalty, d_tok, s));
     GLLM_HIP(hipMemcpyAsync(h_tok, d_tok, 4, hipMemcpyDeviceToHost, s));
     GLLM_HIP(hipStreamSynchronize(s));
     *token = *h_tok;
     return GLLM_OK;
+}
+
+int gllm_hip_argmax(gllm_hip_weight* w, const float* x, uint32_t* token) {
+    return gllm_hip_argmax_penalized(w, x, nullptr, 0, 1.0f, token);
 }
 
 int gllm_hip_lane_ints_dev(gllm_hip_weight* w, const float* d_x, int32_t* d_ints, void* stream) {

@@ -39,13 +39,15 @@ int check(hipError_t e, const char* what) {
 
 namespace {
 
+constexpr int kScratchSlots = 12;
+
 struct ThreadRes {
     int device = -1;
     hipStream_t stream = nullptr;
-    void* scratch[8] = {};
-    size_t scratch_n[8] = {};
-    void* pinned[8] = {};
-    size_t pinned_n[8] = {};
+    void* scratch[kScratchSlots] = {};
+    size_t scratch_n[kScratchSlots] = {};
+    void* pinned[kScratchSlots] = {};
+    size_t pinned_n[kScratchSlots] = {};
 };
 
 thread_local ThreadRes t_res;
@@ -95,7 +97,7 @@ hipStream_t thread_stream() {
 
 void* thread_scratch(int slot, size_t bytes) {
     reset_if_device_changed();
-    if (slot < 0 || slot >= 8) return nullptr;
+    if (slot < 0 || slot >= kScratchSlots) return nullptr;
     if (t_res.scratch_n[slot] < bytes) {
         if (t_res.scratch[slot]) {
             // Another stream of this thread may still read the old buffer.
@@ -119,7 +121,7 @@ void* thread_scratch(int slot, size_t bytes) {
 
 void* thread_pinned(int slot, size_t bytes) {
     reset_if_device_changed();
-    if (slot < 0 || slot >= 8) return nullptr;
+    if (slot < 0 || slot >= kScratchSlots) return nullptr;
     if (t_res.pinned_n[slot] < bytes) {
         if (t_res.pinned[slot]) (void)hipHostFree(t_res.pinned[slot]);
         size_t n = bytes < 4096 ? 4096 : bytes + bytes / 4;

@@ -105,6 +105,12 @@ class LlamaDecoder:
              logits.ctypes.data_as(C.c_void_p) if logits is not None else None)
         return (int(first.value), logits) if want_logits else int(first.value)
 
+    def set_repeat_penalty(self, penalty: float, window: int = 64):
+        """Repeat penalty on every greedy choice, over the last `window`
+        tokens given to prefill / decode (runtime.go repeatPenaltyWindow = 64,
+        forwardGreedyToken runtime.go:1607).  Clears the window."""
+        call("gllm_hip_model_set_repeat_penalty", self.handle, float(penalty), int(window))
+
     def hidden(self):
         out = np.empty(self.config["dim"], np.float32)
         call("gllm_hip_model_hidden", self.handle, out.ctypes.data_as(C.c_void_p))

@@ -109,6 +109,16 @@ int gllm_hip_matvec_batch(gllm_hip_weight* w, const float* xs, int p, float* out
 /* Greedy token: argmax over finite W.x, lowest row on ties
  * (Weight.ArgmaxMatvec model.go:754 -> argmaxQ6KRowsQ8 kernels_amd64.go:294). */
 int gllm_hip_argmax(gllm_hip_weight* w, const float* x, uint32_t* token);
+/* The same after the repeat penalty (applyRepeatPenalty sampling.go:136-153,
+ * as argmaxOutputTokenPenalizedInto model.go:2574-2610 and
+ * ArgmaxQ6KPenalized internal/metal/metal_darwin.go:1175-1190 apply it; Metal
+ * caps the window at 64 ids, this call takes any length): each of the
+ * n_recent ids (duplicates count again, ids >= rows are ignored) divides a
+ * positive logit by penalty and multiplies any other by it; non-finite
+ * logits drop out.  penalty must be finite and > 0 (GLLM_EINVAL otherwise);
+ * penalty 1 is the plain argmax. */
+int gllm_hip_argmax_penalized(gllm_hip_weight* w, const float* x, const uint32_t* recent,
+                              int n_recent, float penalty, uint32_t* token);
 
 /* Device-pointer forms.  d_xs: p rows of cols floats (row stride cols);
  * d_outs: p rows of out_stride floats (out_stride >= rows). */
@@ -119,6 +129,9 @@ int gllm_hip_matvec_dev(gllm_hip_weight* w, const float* d_xs, int p, float* d_o
 int gllm_hip_matvec_multi_dev(int n, gllm_hip_weight* const* ws, const float* d_xs, int p,
                               float* const* d_outs, const int* out_strides, void* stream);
 int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token, void* stream);
+/* d_recent: n_recent device token ids. */
+int gllm_hip_argmax_penalized_dev(gllm_hip_weight* w, const float* d_x, const uint32_t* d_recent,
+                                  int n_recent, float penalty, uint32_t* d_token, void* stream);
 
 /* Split form of the same call, for callers that quantise once and dot many
  * matrices (acquireQ8 + fillQ4KXSums/fillQ6KXSums16, kernels_amd64.go:246,
@@ -222,9 +235,20 @@ int gllm_hip_model_set_norm(gllm_hip_model* m, int layer, int slot, const float*
 /* One decode step at position pos; *next = greedy token. */
 int gllm_hip_model_decode(gllm_hip_model* m, uint32_t token, int pos, uint32_t* next);
 /* Prefill n tokens from start_pos; *first = greedy token from the last
- * position's logits; logits (vocab host floats) may be NULL. */
+ * position's logits; logits (vocab host floats, the projection before any
+ * repeat penalty) may be NULL. */
 int gllm_hip_model_prefill(gllm_hip_model* m, const uint32_t* tokens, int n, int start_pos,
                            uint32_t* first, float* logits);
+/* Repeat penalty for the greedy choices of prefill and decode
+ * (forwardGreedyToken runtime.go:1607 with recent / repeatPenalty): the
+ * window holds the last `window` tokens the model has been given (prefill
+ * tokens in order, then each decode step's input token, as
+ * recentTokenWindowInto runtime.go:1225 and emitToken runtime.go:1089-1093
+ * keep it; the reference's window is 64), and every choice applies
+ * applyRepeatPenalty (sampling.go:136-153) to the logits before the finite
+ * argmax.  penalty must be finite and > 0, window 0..4096; penalty 1 or
+ * window 0 turn it off.  Clears the window. */
+int gllm_hip_model_set_repeat_penalty(gllm_hip_model* m, float penalty, int window);
 /* Normed final hidden state of the last step (dim host floats). */
 int gllm_hip_model_hidden(gllm_hip_model* m, float* out);
 gllm_hip_kv* gllm_hip_model_kv(gllm_hip_model* m);

@@ -547,6 +547,23 @@ uint32_t ref_argmax_finite(const float* logits, long n) {
     return (uint32_t)best;
 }
 
+/* sampling.go:136-153 applyRepeatPenalty, in place: walk the window in order;
+ * an id inside the vocabulary turns a non-finite logit into -inf, divides a
+ * positive one by the penalty and multiplies any other by it (a repeated id
+ * applies the rule again).  penalty 1 leaves the logits untouched. */
+void ref_apply_repeat_penalty(float* logits, long n, const uint32_t* recent, int n_recent,
+                              float penalty) {
+    if (penalty == 1.0f) return;
+    for (int i = 0; i < n_recent; i++) {
+        uint32_t tok = recent[i];
+        if ((long)tok >= n) continue;
+        float v = logits[tok];
+        if (!finite_logit(v)) logits[tok] = -INFINITY;
+        else if (v > 0) logits[tok] = v / penalty;
+        else logits[tok] = v * penalty;
+    }
+}
+
 /* kernels_amd64.go:294-331 argmaxQ6KRowsQ8 (and the Q4_K / Q8_0 twins):
  * skip non-finite, strict >, lowest row on ties, 0 if nothing finite. */
 uint32_t ref_argmax_matvec(int type, const uint8_t* data, const float* x, int rows, int cols,
@@ -986,12 +1003,36 @@ struct ref_llama_state {
     uint16_t** vc;
     float* inv_freq;
     float *x, *xn, *q, *k, *v, *attn, *proj, *gate, *up, *hidden, *logits, *sinv, *cosv;
+    /* repeat penalty and the trailing token window it reads (runtime.go:
+     * recentTokenWindowInto 1225-1228, appended per emitted token 1089-1093) */
+    float penalty;
+    int window, n_recent;
+    uint32_t* recent;
 };
+
+/* append to the window, keeping its last `window` ids in order */
+static void llama_push_recent(ref_llama_state* s, uint32_t tok) {
+    if (s->window <= 0) return;
+    if (s->n_recent == s->window) {
+        memmove(s->recent, s->recent + 1, sizeof(uint32_t) * (size_t)(s->window - 1));
+        s->n_recent--;
+    }
+    s->recent[s->n_recent++] = tok;
+}
+
+void ref_llama_set_repeat_penalty(ref_llama_state* s, float penalty, int window) {
+    free(s->recent);
+    s->penalty = penalty;
+    s->window = window > 0 ? window : 0;
+    s->n_recent = 0;
+    s->recent = (uint32_t*)calloc((size_t)(s->window > 0 ? s->window : 1), sizeof(uint32_t));
+}
 
 ref_llama_state* ref_llama_state_new(const ref_llama* m, int threads) {
     ref_llama_state* s = (ref_llama_state*)calloc(1, sizeof *s);
     s->m = *m;
     s->threads = threads;
+    s->penalty = 1.0f;
     int kvd = m->n_kv_heads * m->head_dim;
     s->kc = (uint16_t**)calloc((size_t)m->n_layers, sizeof(uint16_t*));
     s->vc = (uint16_t**)calloc((size_t)m->n_layers, sizeof(uint16_t*));
@@ -1024,7 +1065,7 @@ void ref_llama_state_free(ref_llama_state* s) {
     free(s->kc); free(s->vc); free(s->inv_freq);
     free(s->x); free(s->xn); free(s->q); free(s->k); free(s->v); free(s->attn);
     free(s->proj); free(s->gate); free(s->up); free(s->hidden); free(s->logits);
-    free(s->sinv); free(s->cosv);
+    free(s->sinv); free(s->cosv); free(s->recent);
     free(s);
 }
 
@@ -1082,6 +1123,14 @@ static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
 uint32_t ref_llama_decode(ref_llama_state* s, uint32_t token, int pos, float* hidden_out) {
     llama_body(s, token, pos);
     if (hidden_out) memcpy(hidden_out, s->xn, sizeof(float) * s->m.dim);
+    llama_push_recent(s, token);  /* emitToken appends before the next choice */
+    if (s->penalty != 1.0f) {
+        /* forwardGreedyToken with penalty != 1: ProjectLogitsInto, then
+         * SampleWithScratch's greedy branch (sampling.go:86-89) */
+        llama_matvec(s, s->m.out_type, s->m.output, s->xn, s->m.vocab, s->m.dim, s->logits);
+        ref_apply_repeat_penalty(s->logits, s->m.vocab, s->recent, s->n_recent, s->penalty);
+        return ref_argmax_finite(s->logits, s->m.vocab);
+    }
     if (s->fast) {
         /* argmax(W.x) over finite logits, lowest index on ties, equals
          * argmaxQ6KRowsQ8's result (kernels_amd64.go:294-331) */
@@ -1100,9 +1149,14 @@ uint32_t ref_llama_decode(ref_llama_state* s, uint32_t token, int pos, float* hi
 uint32_t ref_llama_prefill(ref_llama_state* s, const uint32_t* tokens, int n, int start_pos,
                            int chunk, float* logits_out) {
     (void)chunk;
-    for (int t = 0; t < n; t++) llama_body(s, tokens[t], start_pos + t);
+    for (int t = 0; t < n; t++) {
+        llama_body(s, tokens[t], start_pos + t);
+        llama_push_recent(s, tokens[t]);
+    }
     llama_matvec(s, s->m.out_type, s->m.output, s->xn, s->m.vocab, s->m.dim, s->logits);
     if (logits_out) memcpy(logits_out, s->logits, sizeof(float) * s->m.vocab);
+    /* the first generated token: SampleWithScratch over the prompt window */
+    ref_apply_repeat_penalty(s->logits, s->m.vocab, s->recent, s->n_recent, s->penalty);
     return ref_argmax_finite(s->logits, s->m.vocab);
 }
 

@@ -72,6 +72,8 @@ int ref_matvec_batch(int type, const uint8_t* data, const float* xs, int p,
 uint32_t ref_argmax_matvec(int type, const uint8_t* data, const float* x, int rows,
                            int cols, int order, int threads);
 uint32_t ref_argmax_finite(const float* logits, long n);
+void ref_apply_repeat_penalty(float* logits, long n, const uint32_t* recent, int n_recent,
+                              float penalty);
 
 /* ---- RTN encoders and decoders (quantize_rtn.go, simd.go:1488-1643) ---- */
 void ref_quantize_rows(int type, const float* src, long rows, int cols, uint8_t* dst,
@@ -119,6 +121,9 @@ void ref_llama_set_fast(ref_llama_state* s, int on);
 /* one decode step at position pos; writes the normed final hidden state into
  * hidden_out (dim floats, may be NULL) and returns the greedy token */
 uint32_t ref_llama_decode(ref_llama_state* s, uint32_t token, int pos, float* hidden_out);
+/* repeat penalty over the last `window` tokens seen by prefill / decode
+ * (window 0: none); resets the window */
+void ref_llama_set_repeat_penalty(ref_llama_state* s, float penalty, int window);
 /* prefill n tokens starting at start_pos in chunks; returns the greedy token
  * from the last position's full logits (logits_out: vocab floats or NULL) */
 uint32_t ref_llama_prefill(ref_llama_state* s, const uint32_t* tokens, int n, int start_pos,

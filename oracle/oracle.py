@@ -62,6 +62,7 @@ def lib():
             "ref_matvec_batch_fast": (i, [i, vp, vp, i, i, i, vp, i]),
             "ref_argmax_matvec": (C.c_uint32, [i, vp, vp, i, i, i, i]),
             "ref_argmax_finite": (C.c_uint32, [vp, l]),
+            "ref_apply_repeat_penalty": (None, [vp, l, vp, i, f]),
             "ref_quantize_rows": (None, [i, vp, l, i, vp, i]),
             "ref_dequant_row": (None, [i, vp, i, vp]),
             "ref_dot_f32": (f, [vp, vp, l]),
@@ -76,6 +77,7 @@ def lib():
             "ref_llama_state_new": (vp, [vp, i]),
             "ref_llama_state_free": (None, [vp]),
             "ref_llama_set_fast": (None, [vp, i]),
+            "ref_llama_set_repeat_penalty": (None, [vp, f, i]),
             "ref_llama_decode": (C.c_uint32, [vp, C.c_uint32, i, vp]),
             "ref_llama_prefill": (C.c_uint32, [vp, vp, i, i, i, vp]),
             "ref_llama_generate": (None, [vp, vp, i, i, i, vp]),
@@ -212,6 +214,20 @@ def argmax_matvec(qtype, data, x, rows, cols, order=AMD64, threads=0):
 def argmax_finite(logits):
     logits = _f32(logits)
     return int(lib().ref_argmax_finite(_p(logits), logits.size))
+
+
+def apply_repeat_penalty(logits, recent, penalty):
+    """applyRepeatPenalty (sampling.go:136-153) on a copy of logits."""
+    out = np.array(logits, np.float32, copy=True)
+    rec = np.ascontiguousarray(recent, np.uint32)
+    lib().ref_apply_repeat_penalty(_p(out), out.size, _p(rec), rec.size, np.float32(penalty))
+    return out
+
+
+def argmax_penalized(logits, recent, penalty):
+    """SampleWithScratch's greedy branch (sampling.go:86-89): penalty, then
+    argmaxFiniteToken."""
+    return argmax_finite(apply_repeat_penalty(logits, recent, penalty))
 
 
 # ---- RTN encoders / decoders ---------------------------------------------
@@ -355,6 +371,11 @@ class Llama:
             self.state = None
 
     __del__ = close
+
+    def set_repeat_penalty(self, penalty, window=64):
+        """Repeat penalty over the last `window` tokens the state has seen
+        (runtime.go repeatPenaltyWindow = 64); clears the window."""
+        lib().ref_llama_set_repeat_penalty(self.state, np.float32(penalty), window)
 
     def decode(self, token, pos):
         hid = np.empty(self.cfg["dim"], np.float32)

@@ -165,6 +165,39 @@ def test_argmax_matches_oracle(hip, qtype):
     assert zero.argmax_matvec(normal(5, cols)) == 0
 
 
+@pytest.mark.parametrize("qtype", [ref.Q6_K, ref.Q4_K, ref.Q8_0])
+def test_argmax_penalized_matches_oracle(hip, qtype):
+    """applyRepeatPenalty + argmaxFiniteToken (sampling.go:136-153, 399-418)
+    over the device logits, as ArgmaxQ6KPenalized takes them: the winner
+    twice plus an id past the vocabulary (metal_darwin_test.go:302-309), a
+    64-id window with repeats, a boosting penalty and one that overflows."""
+    import torch
+    rows, cols = 9000, 1024  # three argmax chunks, the last one ragged
+    data, _ = quant_matrix(qtype, rows, cols, 410)
+    w = hip.Weight.from_host(data, qtype, rows, cols)
+    x = normal(411, cols) * 4
+    logits = ref.matvec(qtype, data, x, rows, cols)
+    win = ref.argmax_finite(logits)
+    rng = np.random.default_rng(412)
+    top = np.argsort(-logits)[:40]
+    window = np.concatenate([top[:30], top[:10], rng.integers(0, rows, 24)]).astype(np.uint32)
+    cases = [([win, win, rows + 7], 4.0), (window, 1.7), (window, 0.6), (top[:5], 1e-37),
+             ([], 2.0), (window, 1.0)]
+    for recent, pen in cases:
+        want = ref.argmax_penalized(logits, recent, pen)
+        print(f"penalized argmax qtype={qtype} n={len(recent)} penalty={pen}", flush=True)
+        assert w.argmax_matvec(x, recent=recent, penalty=pen) == want, (len(recent), pen)
+        dx = torch.from_numpy(x).cuda()
+        tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+        rec = torch.from_numpy(np.asarray(recent, np.uint32).astype(np.int32)).cuda()
+        w.argmax_dev(dx, tok, recent=rec if len(recent) else None, penalty=pen)
+        torch.cuda.synchronize()
+        assert int(tok.item()) == want
+    for bad in (0.0, -1.0, float("inf"), float("nan")):
+        with pytest.raises(hip.GllmError):
+            w.argmax_matvec(x, recent=[1], penalty=bad)
+
+
 @pytest.mark.parametrize("name", list(TYPES))
 def test_extremes_closed_form_on_gpu(hip, name):
     qtype = TYPES[name]

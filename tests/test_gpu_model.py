@@ -61,3 +61,33 @@ def test_prefill_logits_match_oracle(hip):
     ct, cl = cpu.prefill(prompt)
     assert gt == ct
     assert np.array_equal(bits(gl), bits(cl))
+
+
+def test_generate_with_repeat_penalty(hip):
+    """forwardGreedyToken with recent / repeatPenalty (runtime.go:1607): the
+    window holds the last tokens seen (prompt, then each emitted token,
+    runtime.go:1035, 1089-1093) and every greedy choice applies
+    applyRepeatPenalty (sampling.go:136-153).  Plain greedy on this model
+    repeats one token; the penalties break that, and a window of 8 lets the
+    token return once it has slid out.  Decode steps after the first replay
+    the captured step graph, so the window reaches it through device memory."""
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = tiny_llama(seed=4, n_layers=3, dim=512, hidden=1536, n_heads=8, n_kv_heads=2, head_dim=64,
+                   vocab=3000)
+    prompt = np.random.default_rng(5).integers(0, 3000, 70)
+    gpu = LlamaDecoder.from_host_model(m, 128)
+    plain = ref.Llama(m, 128).generate(prompt, 24)
+    for pen, win in ((1.8, 64), (4.0, 8), (0.7, 16), (1.0, 64)):
+        print(f"repeat penalty {pen} window {win}", flush=True)
+        cpu = ref.Llama(m, 128)
+        cpu.set_repeat_penalty(pen, win)
+        want = cpu.generate(prompt, 24)
+        gpu.set_repeat_penalty(pen, win)
+        got = gpu.generate(prompt, 24)
+        assert np.array_equal(got, want), (pen, win, got, want)
+        if pen > 1.0:
+            assert not np.array_equal(got, plain)
+    with pytest.raises(hip.GllmError):
+        gpu.set_repeat_penalty(0.0, 64)
+    with pytest.raises(hip.GllmError):
+        gpu.set_repeat_penalty(1.5, -1)

@@ -350,6 +350,67 @@ def test_argmax_rules(oracle_lib):
     assert ref.argmax_finite(np.array([np.nan, np.inf], np.float32)) == 0
 
 
+def test_repeat_penalty_reference_cases(oracle_lib):
+    # TestRepeatPenaltyDownweightsRecentTokens (sampling_test.go:118-131):
+    # greedy over [5, 4, 0] with token 0 recent; penalty 1 keeps 0, 4 hands
+    # the win to 1
+    assert ref.argmax_penalized([5, 4, 0], [0], 1.0) == 0
+    assert ref.argmax_penalized([5, 4, 0], [0], 4.0) == 1
+    # TestMetalQ6KMatvecAndArgmax (metal_darwin_test.go:302-309): the winner
+    # listed twice plus an id past the vocabulary, penalty 4
+    lg = normal(12, 3000) * 3
+    win = ref.argmax_finite(lg)
+    rec = [win, win, lg.size + 7]
+    pen = ref.apply_repeat_penalty(lg, rec, 4.0)
+    assert ref.argmax_penalized(lg, rec, 4.0) == ref.argmax_finite(pen)
+
+
+def test_repeat_penalty_closed_forms(oracle_lib):
+    """applyRepeatPenalty (sampling.go:136-153): each occurrence divides a
+    positive logit and multiplies any other; non-finite -> -inf; ids past the
+    vocabulary are skipped; penalty 1 changes nothing."""
+    lg = np.array([8.0, -2.0, np.inf, np.nan, 3.0, 0.0, -0.0, 6.0], np.float32)
+    out = ref.apply_repeat_penalty(lg, [0, 0, 1, 2, 3, 5, 6, 99, 7, 7, 7], 2.0)
+    want = np.array([2.0, -4.0, -np.inf, -np.inf, 3.0, 0.0, -0.0, 0.75], np.float32)
+    assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
+    # a positive logit turned non-positive never flips sign; the rule then
+    # multiplies: 1e-45 (smallest subnormal) / 4 rounds to 0, then 0 * 4
+    tiny = ref.apply_repeat_penalty(np.array([1e-45], np.float32), [0, 0], 4.0)
+    assert tiny[0] == 0.0
+    # penalty below 1 boosts positives and can overflow to +inf, which the
+    # finite argmax then skips
+    big = np.array([3e38, 1.0, 2.0], np.float32)
+    assert ref.argmax_penalized(big, [0], 0.5) == 2
+    assert ref.argmax_penalized(big, [0], 1.0) == 0
+    # penalty 1 leaves even non-finite values alone (the argmax skips them)
+    odd = np.array([np.nan, 1.0], np.float32)
+    assert np.isnan(ref.apply_repeat_penalty(odd, [0], 1.0)[0])
+    assert ref.argmax_penalized(odd, [0, 1], 1.0) == 1
+    # ties after the penalty keep the lowest index
+    assert ref.argmax_penalized([4.0, 2.0, 2.0], [0], 2.0) == 0
+    assert ref.argmax_penalized([4.0, 2.0, 2.0], [0, 0], 2.0) == 1
+
+
+def test_tiny_llama_repeat_window(oracle_lib):
+    """The generation loop's window (runtime.go:1035, 1089-1093): penalty 1
+    matches plain greedy; a window of 0 as well; any penalty keeps the tokens
+    in the vocabulary and replays deterministically."""
+    m = tiny_llama(seed=21, n_layers=1, dim=256, hidden=512, n_heads=4, n_kv_heads=1, head_dim=64,
+                   vocab=300)
+    prompt = np.random.default_rng(22).integers(0, 300, 20)
+    plain = ref.Llama(m, 64).generate(prompt, 12)
+    for pen, win in ((1.0, 64), (3.0, 0)):
+        c = ref.Llama(m, 64)
+        c.set_repeat_penalty(pen, win)
+        assert np.array_equal(c.generate(prompt, 12), plain)
+    runs = []
+    for _ in range(2):
+        c = ref.Llama(m, 64)
+        c.set_repeat_penalty(1.8, 8)
+        runs.append(c.generate(prompt, 12))
+    assert np.array_equal(runs[0], runs[1]) and runs[0].max() < 300
+
+
 # ------------------------------------------------------------ encoders ----
 
 def test_q4k_dequant_known(oracle_lib):
