@@ -78,6 +78,27 @@ SIGNATURES = {
     "gllm_hip_model_prefill": (i32, [vp, vp, i32, i32, vp, vp]),
     "gllm_hip_model_hidden": (i32, [vp, vp]),
     "gllm_hip_model_set_repeat_penalty": (i32, [vp, f32, i32]),
+    "gllm_hip_gguf_open": (vp, [C.c_char_p]),
+    "gllm_hip_gguf_parse": (vp, [vp, sz]),
+    "gllm_hip_gguf_close": (None, [vp]),
+    "gllm_hip_gguf_version": (u32, [vp]),
+    "gllm_hip_gguf_data_offset": (sz, [vp]),
+    "gllm_hip_gguf_n_tensors": (i32, [vp]),
+    "gllm_hip_gguf_n_metadata": (i32, [vp]),
+    "gllm_hip_gguf_metadata_key": (C.c_char_p, [vp, i32]),
+    "gllm_hip_gguf_tensor": (i32, [vp, i32, vp, vp, vp, vp, vp, vp]),
+    "gllm_hip_gguf_find_tensor": (i32, [vp, C.c_char_p]),
+    "gllm_hip_gguf_tensor_data": (vp, [vp, i32]),
+    "gllm_hip_gguf_meta_kind": (i32, [vp, C.c_char_p, vp, vp, vp]),
+    "gllm_hip_gguf_get_u32": (i32, [vp, C.c_char_p, i32, vp]),
+    "gllm_hip_gguf_get_u64": (i32, [vp, C.c_char_p, i32, vp]),
+    "gllm_hip_gguf_get_f32": (i32, [vp, C.c_char_p, i32, vp]),
+    "gllm_hip_gguf_get_f64": (i32, [vp, C.c_char_p, i32, vp]),
+    "gllm_hip_gguf_get_bool": (i32, [vp, C.c_char_p, i32, vp]),
+    "gllm_hip_gguf_get_str": (i32, [vp, C.c_char_p, i32, vp, vp]),
+    "gllm_hip_ggml_data_size": (u64, [i32, u64]),
+    "gllm_hip_gguf_load_weight": (vp, [vp, C.c_char_p]),
+    "gllm_hip_model_from_gguf": (vp, [vp, i32]),
     "gllm_hip_model_kv": (vp, [vp]),
 }
 

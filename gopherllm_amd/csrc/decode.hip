@@ -41,6 +41,7 @@ size_t argmax_keys(int n);
 struct gllm_hip_model {
     gllm_hip_model_config cfg;
     std::vector<gllm_hip_weight*> w;  // [layer * 7 + slot] for slots 0..6
+    std::vector<gllm_hip_weight*> owned;  // weights the model releases (loaded from a file)
     gllm_hip_weight* tok_embd = nullptr;
     gllm_hip_weight* output = nullptr;
     float* d_norms = nullptr;  // [2 * n_layers + 1][dim]: attn, ffn per layer, then output
@@ -349,6 +350,13 @@ static int forward(gllm_hip_model* m, int pos0, int p, const int* d_pos = nullpt
     return GLLM_OK;
 }
 
+// The model takes over w: released with the model.
+int model_adopt_weight(gllm_hip_model* m, gllm_hip_weight* w) {
+    if (!m || !w) return fail(GLLM_EINVAL, "model_adopt_weight: null argument");
+    m->owned.push_back(w);
+    return GLLM_OK;
+}
+
 static bool penalty_on(const gllm_hip_model* m) { return m->penalty != 1.0f && m->window > 0; }
 
 // emitToken's window update (runtime.go:1089-1093)
@@ -473,6 +481,7 @@ void gllm_hip_model_release(gllm_hip_model* m) {
     if (m->d_recent) (void)hipFree(m->d_recent);
     if (m->h_recent) (void)hipHostFree(m->h_recent);
     if (m->stream) (void)hipStreamDestroy(m->stream);
+    for (gllm_hip_weight* w : m->owned) gllm_hip_weight_release(w);
     delete m;
 }
 

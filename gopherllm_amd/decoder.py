@@ -67,6 +67,32 @@ class LlamaDecoder:
         return self._norms[(layer, slot)]
 
     @classmethod
+    def from_gguf(cls, source, max_len: int = 0) -> "LlamaDecoder":
+        """LoadModel (model.go:1872-1930) for a llama GGUF: source is a path
+        or a gguf.GGUFFile.  The weights are read from the file mapping and
+        owned by the model; max_len <= 0 takes llama.context_length."""
+        from .gguf import GGUFFile
+        f = source if isinstance(source, GGUFFile) else GGUFFile(source)
+        h = call_ptr("gllm_hip_model_from_gguf", f.handle, int(max_len))
+        d = cls.__new__(cls)
+        arch = "llama."
+        d.config = {
+            "n_layers": f.get_u32(arch + "block_count"), "dim": f.get_u32(arch + "embedding_length"),
+            "hidden": f.get_u32(arch + "feed_forward_length"),
+            "n_heads": f.get_u32(arch + "attention.head_count"),
+            "n_kv_heads": f.get_u32(arch + "attention.head_count_kv"),
+            "vocab": f.tensors()[f.find("token_embd.weight")].dims[1],
+        }
+        d.config["head_dim"] = d.config["dim"] // d.config["n_heads"]
+        d.max_len = max_len if max_len > 0 else f.get_u32(arch + "context_length")
+        d._cfg = None
+        d.handle = h
+        d._weights, d._by_slot, d._norms = [], {}, {}
+        if f is not source:
+            f.close()  # the model holds device copies; the mapping can go
+        return d
+
+    @classmethod
     def from_host_model(cls, model: dict, max_len: int) -> "LlamaDecoder":
         """model: {"config", "tok_embd", "output", "out_norm", "wq".."w3" lists,
         "attn_norm"/"ffn_norm" lists} with GGUF-layout bytes."""

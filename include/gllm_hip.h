@@ -253,6 +253,65 @@ int gllm_hip_model_set_repeat_penalty(gllm_hip_model* m, float penalty, int wind
 int gllm_hip_model_hidden(gllm_hip_model* m, float* out);
 gllm_hip_kv* gllm_hip_model_kv(gllm_hip_model* m);
 
+/* ---------------------------------------------------------------------- */
+/* GGUF files (ParseGGUF gguf.go:493-568, OpenMmap mmap.go:11-14,          */
+/* loadWeight model.go:2357-2476, LoadModel model.go:1872-1930)            */
+/* ---------------------------------------------------------------------- */
+
+typedef struct gllm_hip_gguf gllm_hip_gguf;
+
+/* Map path read-only (a read copy where mapping fails) and parse its header:
+ * metadata, tensor table, DataOffset = aligned end of the header
+ * (general.alignment, default 32).  NULL on a malformed or truncated file,
+ * with gllm_hip_last_error() naming the problem.  Host-only; no device use. */
+gllm_hip_gguf* gllm_hip_gguf_open(const char* path);
+/* The same over a caller buffer, which must outlive the handle. */
+gllm_hip_gguf* gllm_hip_gguf_parse(const void* data, size_t len);
+void gllm_hip_gguf_close(gllm_hip_gguf* g);
+uint32_t gllm_hip_gguf_version(const gllm_hip_gguf* g);
+size_t gllm_hip_gguf_data_offset(const gllm_hip_gguf* g);
+int gllm_hip_gguf_n_tensors(const gllm_hip_gguf* g);
+int gllm_hip_gguf_n_metadata(const gllm_hip_gguf* g);
+/* Metadata keys in file order (a repeated key keeps its last value). */
+const char* gllm_hip_gguf_metadata_key(const gllm_hip_gguf* g, int i);
+/* Tensor i: name, dims (GGUF order, dims[0] fastest; up to 8), ggml type id
+ * (ids the reference does not know read 255), offset relative to the data
+ * offset, and byte size (GGMLType.DataSize, else the gap to the next tensor
+ * as inferTensorSizes model.go:2272 derives it).  Outputs may be NULL. */
+int gllm_hip_gguf_tensor(const gllm_hip_gguf* g, int i, const char** name, int* n_dims,
+                         uint64_t* dims, int* type, uint64_t* offset, uint64_t* bytes);
+int gllm_hip_gguf_find_tensor(const gllm_hip_gguf* g, const char* name); /* -1 if absent */
+const void* gllm_hip_gguf_tensor_data(const gllm_hip_gguf* g, int i);     /* borrowed */
+/* Metadata value kind (GGUF wire kind 0..12); for an array also its element
+ * kind and length (elem -1 and count 1 for a scalar). */
+int gllm_hip_gguf_meta_kind(const gllm_hip_gguf* g, const char* key, int* kind, int* elem,
+                            uint64_t* count);
+/* Typed reads of key (idx < 0) or of element idx of the array under key,
+ * with MetaValue's conversions (gguf.go:308-350): get_u32 accepts every
+ * integer kind (cast to 32 bits), get_f32 f32 and f64.  GLLM_EINVAL when the
+ * key is absent or the kind does not convert.  Strings are borrowed from the
+ * file and not NUL-terminated. */
+int gllm_hip_gguf_get_u32(const gllm_hip_gguf* g, const char* key, int idx, uint32_t* out);
+int gllm_hip_gguf_get_u64(const gllm_hip_gguf* g, const char* key, int idx, uint64_t* out);
+int gllm_hip_gguf_get_f32(const gllm_hip_gguf* g, const char* key, int idx, float* out);
+int gllm_hip_gguf_get_f64(const gllm_hip_gguf* g, const char* key, int idx, double* out);
+int gllm_hip_gguf_get_bool(const gllm_hip_gguf* g, const char* key, int idx, int* out);
+int gllm_hip_gguf_get_str(const gllm_hip_gguf* g, const char* key, int idx, const char** out,
+                          size_t* len);
+/* GGMLType.DataSize (gguf.go:241-297): bytes of n elements, 0 if unsized. */
+uint64_t gllm_hip_ggml_data_size(int type, uint64_t n);
+/* loadWeight for the row-kernel types: tensor name -> device weight with
+ * rows = dims[1], cols = dims[0] (model.go:2393-2396), read straight from
+ * the mapping; a tensor cut short by the end of the file is zero-padded. */
+gllm_hip_weight* gllm_hip_gguf_load_weight(const gllm_hip_gguf* g, const char* name);
+/* LoadModel for general.architecture = llama: the llama.* hyperparameters
+ * (ConfigFromGGUF model.go:328-420; vocab = token_embd rows), token_embd,
+ * output (tied to token_embd when absent), output_norm and blk.N.{attn_q,
+ * attn_k, attn_v, attn_output, ffn_gate, ffn_down, ffn_up, attn_norm,
+ * ffn_norm}.  The model owns the weights it loads.  max_len <= 0 takes
+ * llama.context_length. */
+gllm_hip_model* gllm_hip_model_from_gguf(const gllm_hip_gguf* g, int max_len);
+
 #ifdef __cplusplus
 }
 #endif
