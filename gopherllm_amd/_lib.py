@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgllm_hip.so")
 
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 8, 12, 14
+TYPE_Q4_0, TYPE_Q4_1, TYPE_Q2_K, TYPE_Q3_K, TYPE_Q5_K, TYPE_MXFP4 = 2, 3, 10, 11, 13, 39
 OK, EINVAL, EDEVICE, ENOMEM, EUNSUP = 0, -1, -2, -3, -4
 ATTN_EXACT, ATTN_SPLITK = 0, 1
 (T_WQ, T_WK, T_WV, T_WO, T_W1, T_W2, T_W3, T_TOK_EMBD, T_OUTPUT, T_ATTN_NORM, T_FFN_NORM,

@@ -26,14 +26,11 @@ from . import _lib
 from ._lib import (TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, ATTN_EXACT, ATTN_SPLITK, call, call_ptr,
                    load)
 
-BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210}
 
 
 def row_bytes(qtype: int, cols: int) -> int:
-    """GGMLType.DataSize for one row (gguf.go:241-266)."""
-    if qtype == TYPE_Q8_0:
-        return (cols // 32) * 34
-    return (cols // 256) * BLOCK_BYTES[qtype]
+    """GGMLType.DataSize for one row (gguf.go:241-297)."""
+    return int(load().gllm_hip_ggml_data_size(int(qtype), int(cols)))
 
 
 def _np_ptr(a):

@@ -169,6 +169,8 @@ struct MinSel {
     }
 };
 
+#include "gemv_formats.h"
+
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Stage this launch's activations (q8, xs32, xscale of ntok tokens) into LDS
@@ -227,7 +229,7 @@ __device__ __forceinline__ void xq_load(const float* __restrict__ x, int B, XReg
 
 // Quantise one 256-element block b held as x[32m + kk + 8e] = v[e] by lane
 // (m = lane / 8, kk = lane % 8) into LDS: q8 (lane-permuted), xs32 and, for
-// Q6_K (XS16), xs16 x 32 at the given LDS arrays.
+// Q6_K / Q2_K (XS16), the per-16 sums xs16 at the given LDS arrays.
 template <bool XS16>
 __device__ __forceinline__ void xq_block(const float* xv, int b, int8_t* q8, float* xs32,
                                          float* xs16, float* xsc) {
@@ -267,8 +269,8 @@ __device__ __forceinline__ void xq_block(const float* xv, int b, int8_t* q8, flo
         u = u + __shfl_xor(u, 2);
         w = w + __shfl_xor(w, 2);
         if (kk == 0) {
-            xs16[b * 16 + 2 * m] = u * 32.0f;
-            xs16[b * 16 + 2 * m + 1] = w * 32.0f;
+            xs16[b * 16 + 2 * m] = u;
+            xs16[b * 16 + 2 * m + 1] = w;
         }
     }
 }
@@ -491,8 +493,8 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
         if constexpr (NT == 1) {
             o.qa = *(const int4*)(q8 + bb * 256);
             o.qb = *(const int4*)(q8 + bb * 256 + 16);
-            o.x0 = xs16[bb * 16];
-            o.x8 = xs16[bb * 16 + 8];
+            o.x0 = xs16[bb * 16] * 32.0f;      // ScaleF32(xs, 32)
+            o.x8 = xs16[bb * 16 + 8] * 32.0f;
             o.xs = xsc[bb];
         }
     };
@@ -534,8 +536,8 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
                 acc += scl[6] * sdot4(code[6], qb.z, 0);
                 acc += scl[7] * sdot4(code[7], qb.w, 0);
                 const float* xs = xs16 + (size_t)t * (j.cols / 16) + b * 16;
-                float o2 = sk * (NT == 1 ? o.x0 : xs[0]);               // VMULPS
-                o2 = fmaf(sk8, NT == 1 ? o.x8 : xs[8], o2);             // VFMADD231PS
+                float o2 = sk * (NT == 1 ? o.x0 : xs[0] * 32.0f);       // VMULPS
+                o2 = fmaf(sk8, NT == 1 ? o.x8 : xs[8] * 32.0f, o2);     // VFMADD231PS
                 const float dxs = d * (NT == 1 ? o.xs : xsc[(size_t)t * B + b]);  // VMULSS
                 const float iv = (float)acc;
 #pragma unroll
@@ -849,9 +851,53 @@ __global__ void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restri
         } else if (type == GLLM_TYPE_Q6_K) {
             const size_t b = o / 210, e = o % 210;
             n = e < 208 ? b * 208 + e : (size_t)B * 208 + b * 2 + (e - 208);
-        } else {  // Q8_0
+        } else if (type == GLLM_TYPE_Q8_0) {
             const size_t g = o / 272, e = o % 272, q = e / 34, f = e % 34;
             n = g * 272 + (f < 2 ? q * 2 + f : 16 + q * 32 + (f - 2));
+        } else if (type == GLLM_TYPE_Q5_K) {
+            // [header 16][qh 32][nibbles 128] -> [header][lane k: 4 chunk dwords][lane k: qh dword]
+            const size_t b = o / 176, e = o % 176;
+            if (e < 16) {
+                n = o;
+            } else if (e < 48) {
+                n = b * 176 + 144 + (e - 16);
+            } else {
+                const size_t qi = e - 48, s4 = qi / 32, l = qi % 32;
+                n = b * 176 + 16 + (l / 4) * 16 + s4 * 4 + (l % 4);
+            }
+        } else if (type == GLLM_TYPE_Q2_K) {
+            // [scales 16][qs 64][d][dmin] -> [d][dmin][scales][lane k: qs dwords n = 0, 1]
+            const size_t b = o / 84, e = o % 84;
+            if (e < 16) {
+                n = b * 84 + 4 + e;
+            } else if (e < 80) {
+                const size_t qi = e - 16, h = qi / 32, l = qi % 32;
+                n = b * 84 + 20 + (l / 4) * 8 + h * 4 + (l % 4);
+            } else {
+                n = b * 84 + (e - 80);
+            }
+        } else if (type == GLLM_TYPE_Q3_K) {
+            // [hmask 32][qs 64][scales 12][d] -> [d][scales][lane k: hmask, qs n=0, qs n=1 dwords]
+            const size_t b = o / 110, e = o % 110;
+            if (e < 32) {
+                n = b * 110 + 14 + (e / 4) * 12 + (e % 4);
+            } else if (e < 96) {
+                const size_t qi = e - 32, h = qi / 32, l = qi % 32;
+                n = b * 110 + 14 + (l / 4) * 12 + 4 + h * 4 + (l % 4);
+            } else if (e < 108) {
+                n = b * 110 + 2 + (e - 96);
+            } else {
+                n = b * 110 + (e - 108);
+            }
+        } else if (type == GLLM_TYPE_Q4_0 || type == GLLM_TYPE_Q4_1) {
+            // 8 blocks [d (m) | 16 nibble bytes] -> [8 x d (m)][lane group kk: 8 dwords]
+            const size_t hb = type == GLLM_TYPE_Q4_0 ? 2 : 4, bb = hb + 16, sb = 8 * bb;
+            const size_t S = o / sb, e = o % sb, g = e / bb, f = e % bb;
+            n = S * sb + (f < hb ? g * hb + f : 8 * hb + ((f - hb) / 4) * 32 + g * 4 + (f - hb) % 4);
+        } else {  // MXFP4
+            // 8 blocks [16 code bytes | e] -> [8 x e][lane k: 8 code ushorts]
+            const size_t S = o / 136, e = o % 136, g = e / 17, f = e % 17;
+            n = S * 136 + (f == 16 ? g : 8 + (f / 2) * 16 + g * 2 + (f % 2));
         }
         if (inverse) dst[r * rb + o] = src[r * rb + n];
         else dst[r * rb + n] = src[r * rb + o];
@@ -868,11 +914,24 @@ int launch_repack(const uint8_t* src, uint8_t* dst, int type, int rows, int B, s
     return GLLM_OK;
 }
 
+// Types with a row kernel.
+bool row_kernel_type(int t) {
+    return t == GLLM_TYPE_Q4_K || t == GLLM_TYPE_Q6_K || t == GLLM_TYPE_Q8_0 || t == GLLM_TYPE_Q5_K ||
+           t == GLLM_TYPE_Q2_K || t == GLLM_TYPE_Q3_K || t == GLLM_TYPE_Q4_0 || t == GLLM_TYPE_Q4_1 ||
+           t == GLLM_TYPE_MXFP4;
+}
+
 size_t ref_row_bytes(int type, int cols) {
     switch (type) {
     case GLLM_TYPE_Q4_K: return (size_t)(cols / 256) * 144;
     case GLLM_TYPE_Q6_K: return (size_t)(cols / 256) * 210;
     case GLLM_TYPE_Q8_0: return (size_t)(cols / 32) * 34;
+    case GLLM_TYPE_Q5_K: return (size_t)(cols / 256) * 176;
+    case GLLM_TYPE_Q2_K: return (size_t)(cols / 256) * 84;
+    case GLLM_TYPE_Q3_K: return (size_t)(cols / 256) * 110;
+    case GLLM_TYPE_Q4_0: return (size_t)(cols / 32) * 18;
+    case GLLM_TYPE_Q4_1: return (size_t)(cols / 32) * 20;
+    case GLLM_TYPE_MXFP4: return (size_t)(cols / 32) * 17;
     default: return 0;
     }
 }
@@ -986,6 +1045,15 @@ static int row_lanes_g(int total_rows, int blocks, int ntok) {
 }
 
 template <int NT>
+static void (*pick_g(int g, void (*k1)(GemvJob), void (*k2)(GemvJob), void (*k4)(GemvJob)))(GemvJob) {
+    return g == 1 ? k1 : g == 2 ? k2 : k4;
+}
+template <class F, int NT>
+static void (*fmt_kernel(int g))(GemvJob) {
+    return pick_g<NT>(g, gemv_fmt_kernel<F, NT, 1>, gemv_fmt_kernel<F, NT, 2>, gemv_fmt_kernel<F, NT, 4>);
+}
+
+template <int NT>
 int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t s) {
     if (type == GLLM_TYPE_Q4_K) {
         int total = 0;
@@ -995,8 +1063,7 @@ int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t 
              : sh.g == 2 ? launch_q4k<NT, 2>(j, rows, j.n, sh, s)
                          : launch_q4k<NT, 4>(j, rows, j.n, sh, s);
     }
-    if (type != GLLM_TYPE_Q6_K && type != GLLM_TYPE_Q8_0)
-        return fail(GLLM_EUNSUP, "gemv: unsupported type %d", type);
+    if (!row_kernel_type(type)) return fail(GLLM_EUNSUP, "gemv: unsupported type %d", type);
     int total = 0;
     for (int i = 0; i < j.n; i++) total += rows[i];
     const int g = row_lanes_g(total, j.blocks, j.ntok);
@@ -1008,10 +1075,16 @@ int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t 
     }
     j.wg_begin[j.n] = wg;
     void (*kern)(GemvJob);
-    if (type == GLLM_TYPE_Q6_K)
-        kern = g == 1 ? gemv_q6k_kernel<NT, 1> : g == 2 ? gemv_q6k_kernel<NT, 2> : gemv_q6k_kernel<NT, 4>;
-    else
-        kern = g == 1 ? gemv_q8_0_kernel<NT, 1> : g == 2 ? gemv_q8_0_kernel<NT, 2> : gemv_q8_0_kernel<NT, 4>;
+    switch (type) {
+    case GLLM_TYPE_Q6_K: kern = pick_g<NT>(g, gemv_q6k_kernel<NT, 1>, gemv_q6k_kernel<NT, 2>, gemv_q6k_kernel<NT, 4>); break;
+    case GLLM_TYPE_Q8_0: kern = pick_g<NT>(g, gemv_q8_0_kernel<NT, 1>, gemv_q8_0_kernel<NT, 2>, gemv_q8_0_kernel<NT, 4>); break;
+    case GLLM_TYPE_Q5_K: kern = fmt_kernel<fmt::Q5K, NT>(g); break;
+    case GLLM_TYPE_Q2_K: kern = fmt_kernel<fmt::Q2K, NT>(g); break;
+    case GLLM_TYPE_Q3_K: kern = fmt_kernel<fmt::Q3K, NT>(g); break;
+    case GLLM_TYPE_Q4_0: kern = fmt_kernel<fmt::Q401<false>, NT>(g); break;
+    case GLLM_TYPE_Q4_1: kern = fmt_kernel<fmt::Q401<true>, NT>(g); break;
+    default: kern = fmt_kernel<fmt::MXFP4, NT>(g); break;
+    }
     hipLaunchKernelGGL(kern, dim3(wg), dim3(256), 0, s, j);
     GLLM_HIP(hipGetLastError());
     return GLLM_OK;
@@ -1019,7 +1092,7 @@ int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t 
 
 int validate_weight(const gllm_hip_weight* w) {
     if (!w || !w->d_data) return fail(GLLM_EINVAL, "null weight handle");
-    if (w->type != GLLM_TYPE_Q4_K && w->type != GLLM_TYPE_Q6_K && w->type != GLLM_TYPE_Q8_0)
+    if (!row_kernel_type(w->type))
         return fail(GLLM_EUNSUP, "weight type %d has no row kernel", w->type);
     return GLLM_OK;
 }
@@ -1125,8 +1198,9 @@ int matvec_multi(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, fl
         if (ws[i]->cols != ws[0]->cols || ws[i]->type != ws[0]->type)
             return fail(GLLM_EINVAL, "fused matvec needs one type and one cols (%d/%d vs %d/%d)",
                         ws[i]->type, ws[i]->cols, ws[0]->type, ws[0]->cols);
-    if (n > 1 && ws[0]->type == GLLM_TYPE_Q8_0)
-        return fail(GLLM_EUNSUP, "fused Q8_0 matvec: the reference uses its float kernel here");
+    if (n > 1 && ws[0]->type != GLLM_TYPE_Q4_K && ws[0]->type != GLLM_TYPE_Q6_K)
+        return fail(GLLM_EUNSUP, "fused matvec of type %d: the reference uses its float kernel "
+                                 "here (matvecSameType2/3Into, model.go:3213-3254)", ws[0]->type);
     if (p <= 0) return fail(GLLM_EINVAL, "p = %d", p);
     for (int i = 0; i < n; i++)
         if (strides && strides[i] < ws[i]->rows) return fail(GLLM_EINVAL, "out stride < rows");
@@ -1145,7 +1219,7 @@ using namespace gllm;
 extern "C" {
 
 static gllm_hip_weight* weight_alloc(int ggml_type, int rows, int cols, size_t len) {
-    if (ggml_type != GLLM_TYPE_Q4_K && ggml_type != GLLM_TYPE_Q6_K && ggml_type != GLLM_TYPE_Q8_0) {
+    if (!row_kernel_type(ggml_type)) {
         fail(GLLM_EUNSUP, "weight type %d not supported", ggml_type);
         return nullptr;
     }

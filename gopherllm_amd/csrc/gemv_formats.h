@@ -1,0 +1,341 @@
+// gemv_formats.h -- row kernels for Q5_K, Q4_0, Q4_1, MXFP4, Q2_K and Q3_K
+// against Q8K activations, bit-exact to kernels_amd64.s:550-1128 (included
+// by gemv.hip, which supplies GemvJob, locate, rot_prev, tree8_strided,
+// dot4z, q4k_lane_sum and MinSel).
+//
+// Every format keeps the AVX2 lane structure of its reference kernel: lane k
+// of a row owns elements 32m + 4k .. 32m + 4k + 3 of every 32-element group
+// m of a 256-element block, which is exactly the lane-permuted q8 layout the
+// activations use.  Per block (or per 32-element block for the legacy
+// formats) each lane forms its exact int32 and advances its fp32 chains with
+// the reference's operations in the reference's order; the row ends with the
+// same 8 -> 4 -> 2 -> 1 tree (plus the scalar offset chain of Q4_0 / Q4_1).
+//
+// Upload repacks (same byte count per 256 elements; see repack_kernel):
+//   Q5_K  176 B: [16 header][lane k: 16 nibble bytes at 16+16k][lane k: qh dword at 144+4k]
+//   Q2_K   84 B: [d, dmin][16 scale bytes at 4][lane k: qs dwords n=0,1 at 20+8k]
+//   Q3_K  110 B: [d][12 scale bytes at 2][lane k: hmask, qs n=0, qs n=1 dwords at 14+12k]
+//   Q4_0  144 B per 8 blocks: [8 x f16 d][lane group kk: 8 nibble dwords at 16+32kk]
+//   Q4_1  160 B per 8 blocks: [8 x (d, m)][lane group kk: 8 nibble dwords at 32+32kk]
+//   MXFP4 136 B per 8 blocks: [8 exponent bytes][lane k: 8 code ushorts at 8+16k]
+// Q3_K blocks are only 2-byte aligned, so its lanes read 16-bit halves.
+
+namespace fmt {
+
+// Which activation sums a format reads, and whether its chains exist.
+enum Sums { kNone = 0, kX32 = 1, kX16 = 2 };
+
+__device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint32_t*)p; }
+// two aligned 16-bit halves (p is 2-byte aligned)
+__device__ __forceinline__ uint32_t ld32h(const uint8_t* p) {
+    const uint16_t* h = (const uint16_t*)p;
+    return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+}
+
+// Activation operands of one lane, one token, one 256-element block.
+struct Act {
+    int4 qa, qb;        // groups 0..3 and 4..7, lane k's 4 bytes each
+    float xs;           // Q8K scale of the block
+    const float* x32;   // per-32 sums of the block (8), or null
+    const float* x16;   // per-16 sums of the block (16, unscaled), or null
+    __device__ __forceinline__ int q(int m) const {
+        const int v[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        return v[m];
+    }
+};
+
+// ---- Q5_K -----------------------------------------------------------------
+struct Q5K {
+    static constexpr int kBytes = 176, kSums = kX32;
+    static constexpr bool kHasM = true, kHasS = false;
+    struct Regs {
+        uint4 h, q;
+        uint32_t qh;
+    };
+    __device__ static void load(const uint8_t* blk, int k, Regs& r) {
+        r.h = *(const uint4*)blk;
+        r.q = *(const uint4*)(blk + 16 + 16 * k);
+        r.qh = ld32(blk + 144 + 4 * k);
+    }
+    // q5kDotQ8KRow (kernels_amd64.s:578-663): Q4_K's chains, codes with the
+    // fifth bit of qh ORed in (bit 2s for low nibbles, 2s+1 for high).
+    template <int G>
+    __device__ static void step(const Regs& r, int k, const Act& a, float& accF, float& accM,
+                                float&) {
+        const float d = f16_bits_to_f32(r.h.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(r.h.x >> 16);
+        const uint32_t sc03 = r.h.y & 0x3f3f3f3fu;
+        const uint32_t sc47 = (r.h.w & 0x0f0f0f0fu) | ((r.h.y >> 2) & 0x30303030u);
+        const float mkf = (float)MinSel(k).get(r.h.z, r.h.w);
+        const uint32_t qs[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        int t[8];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int lo = (int)((qs[s] & 0x0f0f0f0fu) | (((r.qh >> (2 * s)) & 0x01010101u) << 4));
+            const int hi = (int)(((qs[s] >> 4) & 0x0f0f0f0fu) | (((r.qh >> (2 * s + 1)) & 0x01010101u) << 4));
+            t[2 * s] = dot4z(lo, a.q(2 * s));
+            t[2 * s + 1] = dot4z(hi, a.q(2 * s + 1));
+        }
+        const int acc = q4k_lane_sum(t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7], sc03, sc47);
+        const float iv = (float)acc;
+        const float dxs = d * a.xs;                 // VMULSS
+        const float mx = mkf * a.x32[k];            // VMULPS
+#pragma unroll
+        for (int st = 0; st < G; st++) {
+            accF = fmaf(iv, dxs, rot_prev<G>(accF));     // VFMADD231PS
+            accM = fmaf(dmin, mx, rot_prev<G>(accM));    // VFMADD231PS
+        }
+    }
+};
+
+// ---- Q2_K -----------------------------------------------------------------
+struct Q2K {
+    static constexpr int kBytes = 84, kSums = kX16;
+    static constexpr bool kHasM = true, kHasS = false;
+    struct Regs {
+        uint32_t dd, sc[4], q0, q1;
+    };
+    __device__ static void load(const uint8_t* blk, int k, Regs& r) {
+        r.dd = ld32(blk);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.sc[i] = ld32(blk + 4 + 4 * i);
+        r.q0 = ld32(blk + 20 + 8 * k);
+        r.q1 = ld32(blk + 24 + 8 * k);
+    }
+    __device__ static int scb(const Regs& r, int i) { return (int)((r.sc[i >> 2] >> (8 * (i & 3))) & 0xffu); }
+    // q2kDotQ8KRow (kernels_amd64.s:816-887): group m's codes at shift
+    // 2(m%4) of qs dword m/4, weighted by the d-scale nibble of sub-block
+    // 2m + k/4; min term t = fma(min_{8+k}, xsum_{8+k}, min_k * xsum_k).
+    template <int G>
+    __device__ static void step(const Regs& r, int k, const Act& a, float& accF, float& accM,
+                                float&) {
+        const float d = f16_bits_to_f32(r.dd & 0xffffu);
+        const float dmin = f16_bits_to_f32(r.dd >> 16);
+        int acc = 0;
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const uint32_t qn = m < 4 ? r.q0 : r.q1;
+            const int code = (int)((qn >> (2 * (m & 3))) & 0x03030303u);
+            acc += (scb(r, 2 * m + (k >> 2)) & 15) * dot4z(code, a.q(m));
+        }
+        float t = (float)(scb(r, k) >> 4) * a.x16[k];             // VMULPS
+        t = fmaf((float)(scb(r, 8 + k) >> 4), a.x16[8 + k], t);   // VFMADD231PS
+        const float iv = (float)acc;
+        const float dxs = d * a.xs;
+#pragma unroll
+        for (int st = 0; st < G; st++) {
+            accF = fmaf(dxs, iv, rot_prev<G>(accF));
+            accM = fmaf(dmin, t, rot_prev<G>(accM));
+        }
+    }
+};
+
+// ---- Q3_K -----------------------------------------------------------------
+struct Q3K {
+    static constexpr int kBytes = 110, kSums = kNone;
+    static constexpr bool kHasM = false, kHasS = false;
+    struct Regs {
+        uint32_t d, s0, s1, s2, hm, q0, q1;
+    };
+    __device__ static void load(const uint8_t* blk, int k, Regs& r) {
+        r.d = *(const uint16_t*)blk;
+        r.s0 = ld32h(blk + 2);
+        r.s1 = ld32h(blk + 6);
+        r.s2 = ld32h(blk + 10);
+        r.hm = ld32h(blk + 14 + 12 * k);
+        r.q0 = ld32h(blk + 18 + 12 * k);
+        r.q1 = ld32h(blk + 22 + 12 * k);
+    }
+    // q3kDotQ8KRow (kernels_amd64.s:945-1063): w = code + 4 * (hmask bit m),
+    // lane dot w.a - 4 * sum(a) (== the signed values times a), weighted by
+    // dl = scale - 32 of sub-block 2m + k/4 (q3KScales, quant_extra.go:315).
+    template <int G>
+    __device__ static void step(const Regs& r, int k, const Act& a, float& accF, float&, float&) {
+        const uint32_t sc[4] = {
+            (r.s0 & 0x0f0f0f0fu) | ((r.s2 << 4) & 0x30303030u),
+            (r.s1 & 0x0f0f0f0fu) | ((r.s2 << 2) & 0x30303030u),
+            ((r.s0 >> 4) & 0x0f0f0f0fu) | (r.s2 & 0x30303030u),
+            ((r.s1 >> 4) & 0x0f0f0f0fu) | ((r.s2 >> 2) & 0x30303030u)};
+        int acc = 0;
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const uint32_t qn = m < 4 ? r.q0 : r.q1;
+            const uint32_t w = ((qn >> (2 * (m & 3))) & 0x03030303u) + (((r.hm >> m) & 0x01010101u) << 2);
+            const int am = a.q(m);
+            const int dot = dot4z((int)w, am) - 4 * dot4z(0x01010101, am);
+            const int i = 2 * m + (k >> 2);
+            const int dl = (int)((sc[i >> 2] >> (8 * (i & 3))) & 0xffu) - 32;
+            acc += dl * dot;
+        }
+        const float iv = (float)acc;
+        const float dxs = f16_bits_to_f32(r.d) * a.xs;
+#pragma unroll
+        for (int st = 0; st < G; st++) accF = fmaf(dxs, iv, rot_prev<G>(accF));
+    }
+};
+
+// ---- Q4_0 / Q4_1 ------------------------------------------------------------
+template <bool Q41>
+struct Q401 {
+    static constexpr int kBytes = Q41 ? 160 : 144, kSums = kX32;
+    static constexpr bool kHasM = false, kHasS = true;
+    struct Regs {
+        uint4 h0, h1;  // Q4_0: h0 = 8 f16 d; Q4_1: h0, h1 = 8 (d | m << 16)
+        uint4 n0, n1;  // nibble dword of blocks 0..7 for this lane group
+    };
+    __device__ static void load(const uint8_t* blk, int k, Regs& r) {
+        r.h0 = *(const uint4*)blk;
+        if constexpr (Q41) r.h1 = *(const uint4*)(blk + 16);
+        const uint8_t* nb = blk + (Q41 ? 32 : 16) + 32 * (k & 3);
+        r.n0 = *(const uint4*)nb;
+        r.n1 = *(const uint4*)(nb + 16);
+    }
+    // q4_0DotQ8KRow / q4_1DotQ8KRow (kernels_amd64.s:679-793): per 32-block
+    // g, lane k's unsigned codes (low nibbles for k < 4, high for k >= 4),
+    // accF = fma(d*xs, float(I), accF); the offset chain is
+    // fma(-8, d*xsum_g, s) (Q4_0) or s + m*xsum_g (Q4_1).
+    template <int G>
+    __device__ static void step(const Regs& r, int k, const Act& a, float& accF, float&,
+                                float& accS) {
+        const uint32_t nib[8] = {r.n0.x, r.n0.y, r.n0.z, r.n0.w, r.n1.x, r.n1.y, r.n1.z, r.n1.w};
+        const uint32_t hd[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+        const int sh = 4 * (k >> 2);
+        float iv[8], dxs[8], off[8];
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const int code = (int)((nib[g] >> sh) & 0x0f0f0f0fu);
+            iv[g] = (float)dot4z(code, a.q(g));
+            float d, m = 0.0f;
+            if constexpr (Q41) {
+                d = f16_bits_to_f32(hd[g] & 0xffffu);
+                m = f16_bits_to_f32(hd[g] >> 16);
+            } else {
+                d = f16_bits_to_f32((hd[g >> 1] >> (16 * (g & 1))) & 0xffffu);
+            }
+            dxs[g] = d * a.xs;                               // VMULSS X9, X0
+            off[g] = (Q41 ? m : d) * a.x32[g];               // VMULSS (R9)
+        }
+#pragma unroll
+        for (int st = 0; st < G; st++) {
+            float f = rot_prev<G>(accF), s = rot_prev<G>(accS);
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                f = fmaf(dxs[g], iv[g], f);                  // VFMADD231PS
+                if constexpr (Q41) s = s + off[g];           // VADDSS
+                else s = fmaf(-8.0f, off[g], s);             // VFMADD231SS
+            }
+            accF = f;
+            accS = s;
+        }
+    }
+};
+
+// ---- MXFP4 ------------------------------------------------------------------
+struct MXFP4 {
+    static constexpr int kBytes = 136, kSums = kNone;
+    static constexpr bool kHasM = false, kHasS = false;
+    struct Regs {
+        uint2 e;   // exponent bytes of blocks 0..7
+        uint4 c;   // code ushort of blocks 0..7 (two per dword)
+    };
+    __device__ static void load(const uint8_t* blk, int k, Regs& r) {
+        r.e = *(const uint2*)blk;
+        const uint2 lo = *(const uint2*)(blk + 8 + 16 * k);
+        const uint2 hi = *(const uint2*)(blk + 16 + 16 * k);
+        r.c = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+    // twice the e2m1 value of code c (mxfp4DoubledLUT), as a signed byte
+    __device__ static uint32_t dbl(uint32_t c) {
+        const uint32_t mag = (uint32_t)(0x0c08060403020100ull >> (8 * (c & 7))) & 0xffu;
+        return (c & 8) ? ((0u - mag) & 0xffu) : mag;
+    }
+    // mxfp4DotQ8KRow (kernels_amd64.s:1065-1128): hx = 0.5 * xs, then per
+    // 32-block accF = fma(bits(e << 23) * hx, float(I), accF).
+    template <int G>
+    __device__ static void step(const Regs& r, int, const Act& a, float& accF, float&, float&) {
+        const uint32_t cw[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
+        const float hx = 0.5f * a.xs;                             // VMULSS (R8), X7
+        float iv[8], sc[8];
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const uint32_t u = (cw[g >> 1] >> (16 * (g & 1))) & 0xffffu;
+            const uint32_t v = dbl(u & 15) | (dbl((u >> 4) & 15) << 8) | (dbl((u >> 8) & 15) << 16) |
+                               (dbl(u >> 12) << 24);
+            iv[g] = (float)dot4z((int)v, a.q(g));
+            const uint32_t eb = (g < 4 ? r.e.x >> (8 * g) : r.e.y >> (8 * (g - 4))) & 0xffu;
+            sc[g] = __uint_as_float(eb << 23) * hx;                // VMULSS X10, X0
+        }
+#pragma unroll
+        for (int st = 0; st < G; st++) {
+            float f = rot_prev<G>(accF);
+#pragma unroll
+            for (int g = 0; g < 8; g++) f = fmaf(sc[g], iv[g], f);  // VFMADD231PS
+            accF = f;
+        }
+    }
+};
+
+}  // namespace fmt
+
+// One row kernel for every format above: lane (k, gi) of row r walks blocks
+// gi, gi + G, ... with two blocks of weight bytes in flight.
+template <class F, int NT, int G>
+__global__ __launch_bounds__(256) void gemv_fmt_kernel(GemvJob j) {
+    constexpr int D = 2;
+    int wi;
+    const int tid = threadIdx.x;
+    const int gi = tid % G, k = (tid / G) & 7;
+    const int r = locate(j, blockIdx.x, &wi) + tid / (8 * G);
+    if (r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    const int B = j.blocks, NB = B / G;
+    const uint8_t* row = j.w[wi] + (size_t)r * j.rb;
+    float accF[NT], accM[NT], accS[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) accF[t] = accM[t] = accS[t] = 0.0f;
+    typename F::Regs ring[D];
+    auto load = [&](int i, typename F::Regs& o) __attribute__((always_inline)) {
+        F::load(row + (size_t)(min(i, NB - 1) * G + gi) * F::kBytes, k, o);
+    };
+    auto compute = [&](int i, const typename F::Regs& o) __attribute__((always_inline)) {
+        const int b = i * G + gi;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (NT == 1 || t < j.ntok) {
+                const size_t tok = (size_t)(j.tok0 + t);
+                const int8_t* q8 = j.act.q8perm + tok * j.cols + (size_t)b * 256 + k * 32;
+                fmt::Act a;
+                a.qa = *(const int4*)q8;
+                a.qb = *(const int4*)(q8 + 16);
+                a.xs = j.act.xscale[tok * B + b];
+                a.x32 = F::kSums == fmt::kX32 ? j.act.xs32 + tok * (j.cols / 32) + (size_t)b * 8 : nullptr;
+                a.x16 = F::kSums == fmt::kX16 ? j.act.xs16 + tok * (j.cols / 16) + (size_t)b * 16 : nullptr;
+                F::template step<G>(o, k, a, accF[t], accM[t], accS[t]);
+            }
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+        load(i, ring[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    int i0 = 0;
+    for (; i0 + D <= NB; i0 += D) {
+#pragma unroll
+        for (int ii = 0; ii < D; ii++) {
+            compute(i0 + ii, ring[ii]);
+            __builtin_amdgcn_sched_barrier(0);
+            load(i0 + ii + D, ring[ii]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int ii = 0; ii < D - 1; ii++)
+        if (i0 + ii < NB) compute(i0 + ii, ring[ii]);  // uniform
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        float v = tree8_strided<G>(F::kHasM ? accF[t] - accM[t] : accF[t]);  // VSUBPS + tree
+        if constexpr (F::kHasS) v = v + accS[t];                               // VADDSS
+        if (k == 0 && gi == G - 1 && t < j.ntok)
+            j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
+    }
+}

@@ -45,7 +45,7 @@ struct ActQ8 {
     int8_t* q8perm;  // [p][cols] lane-permuted int8 (see q8perm_offset)
     float* xscale;   // [p][cols/256]
     float* xs32;     // [p][cols/32]   per-32 sums (amd64 order)
-    float* xs16;     // [p][cols/16]   per-16 sums x 32 (amd64 order)
+    float* xs16;     // [p][cols/16]   per-16 sums (amd64 order; Q6_K scales them by 32)
     int cols, p;
 };
 size_t act_bytes(int cols, int p);

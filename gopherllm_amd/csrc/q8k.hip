@@ -3,7 +3,8 @@
 // One workgroup per (256-element block, activation row).  Reproduces
 //   q8kQuantizePortable  quant_q8k_portable.go:36-62 (== kernels_amd64.s:348-436)
 //   sumF32Groups32       kernels_amd64.s:208-230  (Q4_K dmin term)
-//   sumF32Groups16 x 32  kernels_amd64.s:234-254 + ScaleF32(xs, 32) (Q6_K offset)
+//   sumF32Groups16       kernels_amd64.s:234-254 (Q2_K min term; Q6_K's offset term
+//                        applies ScaleF32(xs, 32) where it reads them)
 // bit for bit, and writes q8 in the lane-permuted layout the row kernels read
 // (q8perm_offset in gllm_common.h).
 #include "gllm_common.h"
@@ -86,7 +87,7 @@ __global__ __launch_bounds__(256) void q8k_prep_kernel(const float* __restrict__
 #pragma unroll
         for (int k = 0; k < 8; k++) s[k] = g[k] + g[8 + k];
         const float a0 = s[0] + s[4], a1 = s[1] + s[5], a2 = s[2] + s[6], a3 = s[3] + s[7];
-        a.xs16[(size_t)t * (cols / 16) + b * 16 + gi] = ((a0 + a1) + (a2 + a3)) * 32.0f;
+        a.xs16[(size_t)t * (cols / 16) + b * 16 + gi] = (a0 + a1) + (a2 + a3);
     }
 }
 

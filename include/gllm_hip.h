@@ -37,9 +37,15 @@ extern "C" {
 
 /* GGML tensor types accepted by the row kernels (gguf.go:27-60). */
 #define GLLM_TYPE_F32 0
+#define GLLM_TYPE_Q4_0 2
+#define GLLM_TYPE_Q4_1 3
 #define GLLM_TYPE_Q8_0 8
+#define GLLM_TYPE_Q2_K 10
+#define GLLM_TYPE_Q3_K 11
 #define GLLM_TYPE_Q4_K 12
+#define GLLM_TYPE_Q5_K 13
 #define GLLM_TYPE_Q6_K 14
+#define GLLM_TYPE_MXFP4 39
 
 #define GLLM_OK 0
 #define GLLM_EINVAL (-1)   /* bad argument or shape */

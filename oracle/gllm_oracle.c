@@ -193,6 +193,12 @@ long ref_row_bytes(int type, int cols) {
     case REF_Q4_K: return (long)(cols / 256) * 144;
     case REF_Q6_K: return (long)(cols / 256) * 210;
     case REF_Q8_0: return (long)(cols / 32) * 34;
+    case REF_Q4_0: return (long)(cols / 32) * 18;
+    case REF_Q4_1: return (long)(cols / 32) * 20;
+    case REF_MXFP4: return (long)(cols / 32) * 17;
+    case REF_Q2_K: return (long)(cols / 256) * 84;
+    case REF_Q3_K: return (long)(cols / 256) * 110;
+    case REF_Q5_K: return (long)(cols / 256) * 176;
     case REF_F32: return (long)cols * 4;
     case REF_F16: return (long)cols * 2;
     default: return -1;
@@ -423,6 +429,349 @@ static float q8_0_dot_amd64(const uint8_t* row, const int8_t* q8, const float* x
     return tree8(acc11);
 }
 
+/* ---- Q5_K: Q4_K plus a fifth bit from the 32-byte qh plane ------------- */
+
+/* quant_q8k_portable.go:132-167 q5kDotQ8KRowPortable */
+static float q5k_dot_generic(const uint8_t* row, const int8_t* q8, const float* xscale,
+                             const float* xsums, int blocks) {
+    float sum = 0.0f;
+    for (int b = 0; b < blocks; b++) {
+        const uint8_t* blk = row + (long)b * 176;
+        float d = ref_f16_to_f32(le16(blk)), dmin = ref_f16_to_f32(le16(blk + 2));
+        const uint8_t* qh = blk + 16;
+        const uint8_t* q = blk + 48;
+        int32_t block_int = 0;
+        for (int s = 0; s < 4; s++) {
+            int sc1, sc2, mm;
+            scale_min_k4(2 * s, blk + 4, &sc1, &mm);
+            scale_min_k4(2 * s + 1, blk + 4, &sc2, &mm);
+            int32_t lo = 0, hi = 0;
+            for (int l = 0; l < 32; l++) {
+                int qv = q[s * 32 + l];
+                int h1 = (qh[l] >> (2 * s)) & 1, h2 = (qh[l] >> (2 * s + 1)) & 1;
+                lo += ((qv & 0x0f) + h1 * 16) * (int32_t)q8[b * 256 + s * 64 + l];
+                hi += ((qv >> 4) + h2 * 16) * (int32_t)q8[b * 256 + s * 64 + 32 + l];
+            }
+            block_int += sc1 * lo + sc2 * hi;
+        }
+        sum += d * xscale[b] * (float)block_int;
+        float min_term = 0.0f;
+        for (int j = 0; j < 8; j++) {
+            int sc, m;
+            scale_min_k4(j, blk + 4, &sc, &m);
+            min_term += (float)m * xsums[b * 8 + j];
+        }
+        sum -= dmin * min_term;
+    }
+    return sum;
+}
+
+/* kernels_amd64.s:550-570 Q5KQ8CHUNK lanes: Q4_K's, with bit 2s (low
+ * nibbles) / 2s+1 (high nibbles) of qh[e] ORed in as bit 4. */
+static void q5k_lane_ints(const uint8_t* blk, const int8_t* q8b, int32_t acc[8]) {
+    const uint8_t* qh = blk + 16;
+    const uint8_t* q = blk + 48;
+    int sc[8], mm;
+    for (int j = 0; j < 8; j++) scale_min_k4(j, blk + 4, &sc[j], &mm);
+    for (int k = 0; k < 8; k++) acc[k] = 0;
+    for (int s = 0; s < 4; s++)
+        for (int k = 0; k < 8; k++) {
+            int32_t lo = 0, hi = 0;
+            for (int e = 4 * k; e < 4 * k + 4; e++) {
+                int qv = q[32 * s + e];
+                lo += ((qv & 0x0f) | (((qh[e] >> (2 * s)) & 1) << 4)) * (int32_t)q8b[64 * s + e];
+                hi += ((qv >> 4) | (((qh[e] >> (2 * s + 1)) & 1) << 4)) * (int32_t)q8b[64 * s + 32 + e];
+            }
+            acc[k] += sc[2 * s] * lo + sc[2 * s + 1] * hi;
+        }
+}
+
+/* kernels_amd64.s:578-663 q5kDotQ8KRow (q4kDotQ8KRow's float order) */
+static float q5k_dot_amd64(const uint8_t* row, const int8_t* q8, const float* xscale,
+                           const float* xsums, int blocks) {
+    float accF[8] = {0}, accM[8] = {0};
+    for (int b = 0; b < blocks; b++) {
+        const uint8_t* blk = row + (long)b * 176;
+        float d = ref_f16_to_f32(le16(blk)), dmin = ref_f16_to_f32(le16(blk + 2));
+        for (int k = 0; k < 8; k++) {
+            int sc, m;
+            scale_min_k4(k, blk + 4, &sc, &m);
+            float mx = (float)m * xsums[b * 8 + k];           /* VMULPS */
+            accM[k] = fmaf(dmin, mx, accM[k]);                  /* VFMADD231PS */
+        }
+        int32_t acc[8];
+        q5k_lane_ints(blk, q8 + (long)b * 256, acc);
+        float dxs = d * xscale[b];                              /* VMULSS */
+        for (int k = 0; k < 8; k++) accF[k] = fmaf((float)acc[k], dxs, accF[k]);
+    }
+    float t[8];
+    for (int k = 0; k < 8; k++) t[k] = accF[k] - accM[k];     /* VSUBPS */
+    return tree8(t);
+}
+
+/* ---- Q4_0 / Q4_1: legacy 32-element blocks, 8 per Q8K block ------------ */
+
+/* code of element e (0..31) of a 16-byte nibble block: low nibbles are
+ * elements 0..15, high nibbles 16..31 */
+static inline int nib32(const uint8_t* nib, int e) { return e < 16 ? nib[e] & 0x0f : nib[e - 16] >> 4; }
+
+/* quant_q8k_portable.go:233-249 q4_0DotQ8KRowPortable */
+static float q4_0_dot_generic(const uint8_t* row, const int8_t* q8, const float* xscale,
+                              const float* xsums, int blocks) {
+    float sum = 0.0f;
+    for (int g = 0; g < blocks * 8; g++) {
+        const uint8_t* blk = row + (long)g * 18;
+        float d = ref_f16_to_f32(le16(blk));
+        int32_t intdot = 0;
+        for (int i = 0; i < 16; i++) {
+            intdot += (blk[2 + i] & 0x0f) * (int32_t)q8[g * 32 + i];
+            intdot += (blk[2 + i] >> 4) * (int32_t)q8[g * 32 + 16 + i];
+        }
+        sum += d * (xscale[g / 8] * (float)intdot - 8.0f * xsums[g]);
+    }
+    return sum;
+}
+
+/* quant_q8k_portable.go:251-271 q4_1DotQ8KRowPortable */
+static float q4_1_dot_generic(const uint8_t* row, const int8_t* q8, const float* xscale,
+                              const float* xsums, int blocks) {
+    float sum = 0.0f;
+    for (int g = 0; g < blocks * 8; g++) {
+        const uint8_t* blk = row + (long)g * 20;
+        float d = ref_f16_to_f32(le16(blk)), m = ref_f16_to_f32(le16(blk + 2));
+        int32_t intdot = 0;
+        for (int i = 0; i < 16; i++) {
+            intdot += (blk[4 + i] & 0x0f) * (int32_t)q8[g * 32 + i];
+            intdot += (blk[4 + i] >> 4) * (int32_t)q8[g * 32 + 16 + i];
+        }
+        sum += d * xscale[g / 8] * (float)intdot + m * xsums[g];
+    }
+    return sum;
+}
+
+/* kernels_amd64.s:679-732 q4_0DotQ8KRow / 734-793 q4_1DotQ8KRow: per
+ * 32-block g, lane k holds the unsigned-code dot of elements 4k..4k+3
+ * (Q40Q41EXPAND puts low nibbles in lanes 0-3, high in 4-7);
+ * accF_k = fma(d*xs, float(I_k), accF_k); a scalar chain carries the offset:
+ * Q4_0 fma(-8, d*xsum_g, s), Q4_1 s + m*xsum_g; result tree8(accF) + s. */
+static float q4_01_dot_amd64(int type, const uint8_t* row, const int8_t* q8,
+                             const float* xscale, const float* xsums, int blocks) {
+    const int bb = type == REF_Q4_0 ? 18 : 20, no = type == REF_Q4_0 ? 2 : 4;
+    float accF[8] = {0}, accS = 0.0f;
+    for (int b = 0; b < blocks; b++) {
+        const float xs = xscale[b];
+        for (int g = 0; g < 8; g++) {
+            const uint8_t* blk = row + (long)(b * 8 + g) * bb;
+            const int8_t* q8g = q8 + (long)b * 256 + g * 32;
+            float d = ref_f16_to_f32(le16(blk));
+            float dxs = d * xs;                                 /* VMULSS X9, X0 */
+            for (int k = 0; k < 8; k++) {
+                int32_t I = 0;
+                for (int e = 4 * k; e < 4 * k + 4; e++) I += nib32(blk + no, e) * (int32_t)q8g[e];
+                accF[k] = fmaf(dxs, (float)I, accF[k]);         /* VFMADD231PS */
+            }
+            if (type == REF_Q4_0) {
+                float t = d * xsums[b * 8 + g];                 /* VMULSS (R9), X0 */
+                accS = fmaf(-8.0f, t, accS);                    /* VFMADD231SS */
+            } else {
+                float m = ref_f16_to_f32(le16(blk + 2));
+                float t = m * xsums[b * 8 + g];                 /* VMULSS (R9), X6 */
+                accS = accS + t;                                /* VADDSS */
+            }
+        }
+    }
+    return tree8(accF) + accS;                                  /* VADDSS X10, X11 */
+}
+
+/* ---- MXFP4: 17-byte blocks, e2m1 codes, E8M0 scale --------------------- */
+
+/* quant_q8k_portable.go:271-274 mxfp4DoubledLUT: twice the e2m1 value */
+static const int mxfp4_dbl[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+static inline int mxfp4_code(const uint8_t* blk, int e) {
+    return (e & 1) ? blk[e >> 1] >> 4 : blk[e >> 1] & 0x0f;
+}
+
+/* quant_q8k_portable.go:274-303 mxfp4DotQ8KRowPortable */
+static float mxfp4_dot_generic(const uint8_t* row, const int8_t* q8, const float* xscale,
+                               int blocks) {
+    float sum = 0.0f;
+    for (int g = 0; g < blocks * 8; g++) {
+        const uint8_t* blk = row + (long)g * 17;
+        uint32_t e = blk[16];
+        float scale = e > 0 ? bits_f32(e << 23) : 0.0f;
+        int32_t intdot = 0;
+        for (int i = 0; i < 32; i++) intdot += mxfp4_dbl[mxfp4_code(blk, i)] * (int32_t)q8[g * 32 + i];
+        sum += scale * 0.5f * xscale[g / 8] * (float)intdot;
+    }
+    return sum;
+}
+
+/* kernels_amd64.s:1065-1128 mxfp4DotQ8KRow: lane k holds elements 4k..4k+3
+ * (VPUNPCK restores element order); hx = 0.5*xs per Q8K block, then
+ * accF_k = fma(bits(e << 23) * hx, float(I_k), accF_k); tree8. */
+static float mxfp4_dot_amd64(const uint8_t* row, const int8_t* q8, const float* xscale,
+                             int blocks) {
+    float accF[8] = {0};
+    for (int b = 0; b < blocks; b++) {
+        float hx = 0.5f * xscale[b];                             /* VMULSS (R8), X7 */
+        for (int g = 0; g < 8; g++) {
+            const uint8_t* blk = row + (long)(b * 8 + g) * 17;
+            const int8_t* q8g = q8 + (long)b * 256 + g * 32;
+            float sc = bits_f32((uint32_t)blk[16] << 23) * hx; /* VMULSS X10, X0 */
+            for (int k = 0; k < 8; k++) {
+                int32_t I = 0;
+                for (int e = 4 * k; e < 4 * k + 4; e++)
+                    I += mxfp4_dbl[mxfp4_code(blk, e)] * (int32_t)q8g[e];
+                accF[k] = fmaf(sc, (float)I, accF[k]);          /* VFMADD231PS */
+            }
+        }
+    }
+    return tree8(accF);
+}
+
+/* ---- Q2_K: 16 sub-blocks of 16, 2-bit codes, 4-bit scale / min -------- */
+
+/* element e (0..255) of a Q2_K / Q3_K block: 32-element group m = e / 32
+ * reads qs byte 32 * (m / 4) + e % 32 at shift 2 * (m % 4) */
+static inline int q2_code(const uint8_t* qs, int e) {
+    const int m = e / 32;
+    return (qs[32 * (m / 4) + e % 32] >> (2 * (m % 4))) & 3;
+}
+
+/* quant_q8k_portable.go:305-347 q2kDotQ8KRowPortable */
+static float q2k_dot_generic(const uint8_t* row, const int8_t* q8, const float* xscale,
+                             const float* xsums16, int blocks) {
+    float sum = 0.0f;
+    for (int b = 0; b < blocks; b++) {
+        const uint8_t* blk = row + (long)b * 84;
+        float d = ref_f16_to_f32(le16(blk + 80)), dmin = ref_f16_to_f32(le16(blk + 82));
+        int32_t block_int = 0;
+        float min_term = 0.0f;
+        for (int is = 0; is < 16; is++) {
+            int32_t qdot = 0;
+            for (int l = 0; l < 16; l++)
+                qdot += q2_code(blk + 16, is * 16 + l) * (int32_t)q8[b * 256 + is * 16 + l];
+            block_int += (blk[is] & 0x0f) * qdot;
+            min_term += (float)(blk[is] >> 4) * xsums16[b * 16 + is];
+        }
+        sum += d * xscale[b] * (float)block_int - dmin * min_term;
+    }
+    return sum;
+}
+
+/* Q2KQ8CHUNK lanes (kernels_amd64.s:795-803): group m, lane k = elements
+ * 32m + 4k..+3, weighted by the d-scale nibble of sub-block 2m + k/4. */
+static void q2k_lane_ints(const uint8_t* blk, const int8_t* q8b, int32_t acc[8]) {
+    for (int k = 0; k < 8; k++) acc[k] = 0;
+    for (int m = 0; m < 8; m++)
+        for (int k = 0; k < 8; k++) {
+            int32_t I = 0;
+            for (int e = 32 * m + 4 * k; e < 32 * m + 4 * k + 4; e++)
+                I += q2_code(blk + 16, e) * (int32_t)q8b[e];
+            acc[k] += (blk[2 * m + k / 4] & 0x0f) * I;
+        }
+}
+
+/* kernels_amd64.s:816-887 q2kDotQ8KRow: lane k's min term pairs sub-blocks
+ * k and 8 + k: t = fma(min_{8+k}, xsum_{8+k}, min_k * xsum_k),
+ * accM_k = fma(dmin, t, accM_k); accF as Q4_K; tree8(accF - accM). */
+static float q2k_dot_amd64(const uint8_t* row, const int8_t* q8, const float* xscale,
+                           const float* xsums16, int blocks) {
+    float accF[8] = {0}, accM[8] = {0};
+    for (int b = 0; b < blocks; b++) {
+        const uint8_t* blk = row + (long)b * 84;
+        float d = ref_f16_to_f32(le16(blk + 80)), dmin = ref_f16_to_f32(le16(blk + 82));
+        for (int k = 0; k < 8; k++) {
+            float t = (float)(blk[k] >> 4) * xsums16[b * 16 + k];               /* VMULPS */
+            t = fmaf((float)(blk[8 + k] >> 4), xsums16[b * 16 + 8 + k], t);      /* VFMADD231PS */
+            accM[k] = fmaf(dmin, t, accM[k]);                                    /* VFMADD231PS */
+        }
+        int32_t acc[8];
+        q2k_lane_ints(blk, q8 + (long)b * 256, acc);
+        float dxs = d * xscale[b];
+        for (int k = 0; k < 8; k++) accF[k] = fmaf(dxs, (float)acc[k], accF[k]);
+    }
+    float t[8];
+    for (int k = 0; k < 8; k++) t[k] = accF[k] - accM[k];
+    return tree8(t);
+}
+
+/* ---- Q3_K: 2-bit codes with a high-bit mask, 6-bit signed scales ------- */
+
+/* quant_extra.go:315-334 q3KScales: 16 six-bit scales from 12 bytes */
+static void q3k_scales(const uint8_t* p, int out[16]) {
+    uint32_t a0, a1, tmp;
+    memcpy(&a0, p, 4);
+    memcpy(&a1, p + 4, 4);
+    memcpy(&tmp, p + 8, 4);
+    uint32_t aux[4];
+    aux[2] = ((a0 >> 4) & 0x0f0f0f0fu) | (((tmp >> 4) & 0x03030303u) << 4);
+    aux[3] = ((a1 >> 4) & 0x0f0f0f0fu) | (((tmp >> 6) & 0x03030303u) << 4);
+    aux[0] = (a0 & 0x0f0f0f0fu) | (((tmp >> 0) & 0x03030303u) << 4);
+    aux[1] = (a1 & 0x0f0f0f0fu) | (((tmp >> 2) & 0x03030303u) << 4);
+    for (int i = 0; i < 16; i++) out[i] = (int)((aux[i / 4] >> (8 * (i % 4))) & 0xff);
+}
+
+/* signed Q3_K value of element e: code - 4 unless hmask bit m = e / 32 of
+ * byte e % 32 is set */
+static inline int q3_value(const uint8_t* blk, int e) {
+    const int h = (blk[e % 32] >> (e / 32)) & 1;
+    return q2_code(blk + 32, e) - (h ? 0 : 4);
+}
+
+/* quant_q8k_portable.go:349-390 q3kDotQ8KRowPortable */
+static float q3k_dot_generic(const uint8_t* row, const int8_t* q8, const float* xscale,
+                             int blocks) {
+    float sum = 0.0f;
+    for (int b = 0; b < blocks; b++) {
+        const uint8_t* blk = row + (long)b * 110;
+        int sc[16];
+        q3k_scales(blk + 96, sc);
+        float d = ref_f16_to_f32(le16(blk + 108));
+        int32_t block_int = 0;
+        for (int is = 0; is < 16; is++) {
+            int32_t qdot = 0;
+            for (int l = 0; l < 16; l++)
+                qdot += q3_value(blk, is * 16 + l) * (int32_t)q8[b * 256 + is * 16 + l];
+            block_int += (sc[is] - 32) * qdot;
+        }
+        sum += d * xscale[b] * (float)block_int;
+    }
+    return sum;
+}
+
+/* Q3KQ8CHUNK lanes (kernels_amd64.s:915-943): w = code + 4h, pair sums
+ * w.a - 4.(sum a) (== the signed value times a), weighted by dl = sc - 32 of
+ * sub-block 2m + k/4. */
+static void q3k_lane_ints(const uint8_t* blk, const int8_t* q8b, int32_t acc[8]) {
+    int sc[16];
+    q3k_scales(blk + 96, sc);
+    for (int k = 0; k < 8; k++) acc[k] = 0;
+    for (int m = 0; m < 8; m++)
+        for (int k = 0; k < 8; k++) {
+            int32_t I = 0;
+            for (int e = 32 * m + 4 * k; e < 32 * m + 4 * k + 4; e++)
+                I += q3_value(blk, e) * (int32_t)q8b[e];
+            acc[k] += (sc[2 * m + k / 4] - 32) * I;
+        }
+}
+
+/* kernels_amd64.s:945-1063 q3kDotQ8KRow: accF_k = fma(d*xs, float(I_k),
+ * accF_k); tree8 (no min term). */
+static float q3k_dot_amd64(const uint8_t* row, const int8_t* q8, const float* xscale,
+                           int blocks) {
+    float accF[8] = {0};
+    for (int b = 0; b < blocks; b++) {
+        const uint8_t* blk = row + (long)b * 110;
+        int32_t acc[8];
+        q3k_lane_ints(blk, q8 + (long)b * 256, acc);
+        float dxs = ref_f16_to_f32(le16(blk + 108)) * xscale[b];
+        for (int k = 0; k < 8; k++) accF[k] = fmaf(dxs, (float)acc[k], accF[k]);
+    }
+    return tree8(accF);
+}
+
 float ref_q4k_dot(const uint8_t* row, const int8_t* q8, const float* xscale,
                   const float* xsums32, int blocks, int order) {
     return order == REF_ORDER_AMD64 ? q4k_dot_amd64(row, q8, xscale, xsums32, blocks)
@@ -444,6 +793,26 @@ void ref_lane_ints(int type, const uint8_t* row, const int8_t* q8, int blocks, i
         int32_t acc[8];
         if (type == REF_Q4_K) {
             q4k_lane_ints(row + (long)b * 144, q8 + (long)b * 256, acc);
+        } else if (type == REF_Q5_K) {
+            q5k_lane_ints(row + (long)b * 176, q8 + (long)b * 256, acc);
+        } else if (type == REF_Q2_K) {
+            q2k_lane_ints(row + (long)b * 84, q8 + (long)b * 256, acc);
+        } else if (type == REF_Q3_K) {
+            q3k_lane_ints(row + (long)b * 110, q8 + (long)b * 256, acc);
+        } else if (type == REF_Q4_0 || type == REF_Q4_1 || type == REF_MXFP4) {
+            /* per 32-block pieces, summed over the 8 blocks per lane (exact) */
+            const int bb = type == REF_Q4_0 ? 18 : type == REF_Q4_1 ? 20 : 17;
+            for (int k = 0; k < 8; k++) acc[k] = 0;
+            for (int g = 0; g < 8; g++) {
+                const uint8_t* blk = row + (long)(b * 8 + g) * bb;
+                const int8_t* q8g = q8 + (long)b * 256 + g * 32;
+                for (int k = 0; k < 8; k++)
+                    for (int e = 4 * k; e < 4 * k + 4; e++) {
+                        const int c = type == REF_MXFP4 ? mxfp4_dbl[mxfp4_code(blk, e)]
+                                                        : nib32(blk + (type == REF_Q4_0 ? 2 : 4), e);
+                        acc[k] += c * (int32_t)q8g[e];
+                    }
+            }
         } else if (type == REF_Q6_K) {
             q6k_lane_ints(row + (long)b * 210, q8 + (long)b * 256, acc);
         } else {
@@ -484,16 +853,43 @@ typedef struct {
 static void prepare_act(int type, const float* x, int cols, int order, act_q8* a) {
     int blocks = cols / 256;
     ref_q8k_quantize(x, a->q8, a->xscale, blocks);
-    if (type == REF_Q4_K) ref_xsums32(x, a->xsums, cols / 32, order);
+    if (type == REF_Q4_K || type == REF_Q5_K || type == REF_Q4_0 || type == REF_Q4_1)
+        ref_xsums32(x, a->xsums, cols / 32, order);  /* fillQ4KXSums */
     else if (type == REF_Q6_K) ref_xsums16(x, a->xsums, cols / 16, order, 1);
+    else if (type == REF_Q2_K) ref_xsums16(x, a->xsums, cols / 16, order, 0); /* unscaled */
+}
+
+float ref_row_dot_any(int type, const uint8_t* row, const int8_t* q8, const float* xscale,
+                      const float* xsums, int blocks, int order) {
+    const int amd = order == REF_ORDER_AMD64;
+    switch (type) {
+    case REF_Q4_K: return ref_q4k_dot(row, q8, xscale, xsums, blocks, order);
+    case REF_Q6_K: return ref_q6k_dot(row, q8, xscale, xsums, blocks, order);
+    case REF_Q8_0: return ref_q8_0_dot(row, q8, xscale, blocks, order);
+    case REF_Q5_K: return amd ? q5k_dot_amd64(row, q8, xscale, xsums, blocks)
+                              : q5k_dot_generic(row, q8, xscale, xsums, blocks);
+    case REF_Q4_0: return amd ? q4_01_dot_amd64(REF_Q4_0, row, q8, xscale, xsums, blocks)
+                              : q4_0_dot_generic(row, q8, xscale, xsums, blocks);
+    case REF_Q4_1: return amd ? q4_01_dot_amd64(REF_Q4_1, row, q8, xscale, xsums, blocks)
+                              : q4_1_dot_generic(row, q8, xscale, xsums, blocks);
+    case REF_MXFP4: return amd ? mxfp4_dot_amd64(row, q8, xscale, blocks)
+                               : mxfp4_dot_generic(row, q8, xscale, blocks);
+    case REF_Q2_K: return amd ? q2k_dot_amd64(row, q8, xscale, xsums, blocks)
+                              : q2k_dot_generic(row, q8, xscale, xsums, blocks);
+    case REF_Q3_K: return amd ? q3k_dot_amd64(row, q8, xscale, blocks)
+                              : q3k_dot_generic(row, q8, xscale, blocks);
+    default: return 0.0f;
+    }
 }
 
 static float row_dot(int type, const uint8_t* row, const act_q8* a, int blocks, int order) {
-    switch (type) {
-    case REF_Q4_K: return ref_q4k_dot(row, a->q8, a->xscale, a->xsums, blocks, order);
-    case REF_Q6_K: return ref_q6k_dot(row, a->q8, a->xscale, a->xsums, blocks, order);
-    default: return ref_q8_0_dot(row, a->q8, a->xscale, blocks, order);
-    }
+    return ref_row_dot_any(type, row, a->q8, a->xscale, a->xsums, blocks, order);
+}
+
+int ref_type_supported(int type) {
+    return type == REF_Q4_K || type == REF_Q6_K || type == REF_Q8_0 || type == REF_Q5_K ||
+           type == REF_Q4_0 || type == REF_Q4_1 || type == REF_MXFP4 || type == REF_Q2_K ||
+           type == REF_Q3_K;
 }
 
 static int act_alloc(act_q8* a, int cols) {
@@ -507,7 +903,7 @@ static void act_free(act_q8* a) { free(a->q8); free(a->xscale); free(a->xsums); 
 int ref_matvec_batch(int type, const uint8_t* data, const float* xs, int p, int rows,
                      int cols, float* outs, int order, int threads) {
     if (cols <= 0 || cols % 256 || rows < 0 || p <= 0) return -1;
-    if (type != REF_Q4_K && type != REF_Q6_K && type != REF_Q8_0) return -1;
+    if (!ref_type_supported(type)) return -1;
     int blocks = cols / 256;
     long rb = ref_row_bytes(type, cols);
     act_q8* acts = (act_q8*)calloc((size_t)p, sizeof(act_q8));
@@ -815,6 +1211,84 @@ void ref_dequant_row(int type, const uint8_t* row, int cols, float* out) {
                 ql += 64;
                 qh += 32;
                 sc += 8;
+            }
+        }
+    } else if (type == REF_Q5_K) {
+        /* simd.go:1567-1605 DequantRowQ5KInto */
+        for (int b = 0; b < cols / 256; b++) {
+            const uint8_t* blk = row + (long)b * 176;
+            float d = ref_f16_to_f32(le16(blk)), dmin = ref_f16_to_f32(le16(blk + 2));
+            const uint8_t* qh = blk + 16;
+            const uint8_t* q = blk + 48;
+            int is = 0, u1 = 1, u2 = 2;
+            for (int j = 0; j < 256; j += 64) {
+                int sc1, m1, sc2, m2;
+                scale_min_k4(is, blk + 4, &sc1, &m1);
+                scale_min_k4(is + 1, blk + 4, &sc2, &m2);
+                float d1 = d * (float)sc1, d2 = d * (float)sc2;
+                float min1 = dmin * (float)m1, min2 = dmin * (float)m2;
+                for (int l = 0; l < 32; l++) {
+                    int hi1 = (qh[l] & u1) ? 16 : 0, hi2 = (qh[l] & u2) ? 16 : 0;
+                    out[b * 256 + j + l] = d1 * (float)((q[l] & 0x0f) + hi1) - min1;
+                    out[b * 256 + j + 32 + l] = d2 * (float)((q[l] >> 4) + hi2) - min2;
+                }
+                q += 32;
+                is += 2;
+                u1 <<= 2;
+                u2 <<= 2;
+            }
+        }
+    } else if (type == REF_Q4_0 || type == REF_Q4_1) {
+        /* simd.go:1509-1522 DequantRowQ4_0Into, quant_extra.go:20-34 Q4_1 */
+        const int bb = type == REF_Q4_0 ? 18 : 20;
+        for (int b = 0; b < cols / 32; b++) {
+            const uint8_t* blk = row + (long)b * bb;
+            float d = ref_f16_to_f32(le16(blk));
+            for (int i = 0; i < 16; i++) {
+                if (type == REF_Q4_0) {
+                    out[b * 32 + i] = d * (float)((blk[2 + i] & 0x0f) - 8);
+                    out[b * 32 + 16 + i] = d * (float)(((blk[2 + i] >> 4) & 0x0f) - 8);
+                } else {
+                    float m = ref_f16_to_f32(le16(blk + 2));
+                    out[b * 32 + i] = d * (float)(blk[4 + i] & 0x0f) + m;
+                    out[b * 32 + 16 + i] = d * (float)(blk[4 + i] >> 4) + m;
+                }
+            }
+        }
+    } else if (type == REF_MXFP4) {
+        /* simd.go:1653-1670 DequantRowMXFP4Into: 2^(e-127) * e2m1 value */
+        static const float lut[16] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f,
+                                      -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+        for (int b = 0; b < cols / 32; b++) {
+            const uint8_t* blk = row + (long)b * 17;
+            float scale = (float)ldexp(1.0, (int)blk[16] - 127);
+            for (int i = 0; i < 16; i++) {
+                out[b * 32 + 2 * i] = scale * lut[blk[i] & 0x0f];
+                out[b * 32 + 2 * i + 1] = scale * lut[blk[i] >> 4];
+            }
+        }
+    } else if (type == REF_Q2_K) {
+        /* quant_extra.go:233-263 DequantRowQ2KInto */
+        for (int b = 0; b < cols / 256; b++) {
+            const uint8_t* blk = row + (long)b * 84;
+            float d = ref_f16_to_f32(le16(blk + 80)), dmin = ref_f16_to_f32(le16(blk + 82));
+            for (int is = 0; is < 16; is++) {
+                float dl = d * (float)(blk[is] & 0x0f), ml = dmin * (float)(blk[is] >> 4);
+                for (int l = 0; l < 16; l++)
+                    out[b * 256 + is * 16 + l] = dl * (float)q2_code(blk + 16, is * 16 + l) - ml;
+            }
+        }
+    } else if (type == REF_Q3_K) {
+        /* quant_extra.go:336-368 DequantRowQ3KInto */
+        for (int b = 0; b < cols / 256; b++) {
+            const uint8_t* blk = row + (long)b * 110;
+            int sc[16];
+            q3k_scales(blk + 96, sc);
+            float d = ref_f16_to_f32(le16(blk + 108));
+            for (int is = 0; is < 16; is++) {
+                float dl = d * (float)(sc[is] - 32);
+                for (int l = 0; l < 16; l++)
+                    out[b * 256 + is * 16 + l] = dl * (float)q3_value(blk, is * 16 + l);
             }
         }
     } else if (type == REF_F32) {

@@ -26,7 +26,10 @@ extern "C" {
 #endif
 
 /* GGML type ids (gguf.go:27-60). */
-enum { REF_F32 = 0, REF_F16 = 1, REF_Q8_0 = 8, REF_Q4_K = 12, REF_Q6_K = 14 };
+enum {
+    REF_F32 = 0, REF_F16 = 1, REF_Q4_0 = 2, REF_Q4_1 = 3, REF_Q8_0 = 8, REF_Q2_K = 10,
+    REF_Q3_K = 11, REF_Q4_K = 12, REF_Q5_K = 13, REF_Q6_K = 14, REF_MXFP4 = 39
+};
 enum { REF_ORDER_GENERIC = 0, REF_ORDER_AMD64 = 1 };
 
 /* ---- f16 (simd.go:88-109, kv_f16.go:17-49) ---- */
@@ -53,6 +56,12 @@ float ref_q8_0_dot(const uint8_t* row, const int8_t* q8, const float* xscale,
                    int blocks, int order);
 /* amd64 int32 lane accumulators (the exact integer part) for each block:
  * out[b*8 + k] = accI_k of block b. */
+/* Any supported type: one row against prepared activations (xsums as the
+ * type needs them: 32-group sums for Q4_K/Q5_K/Q4_0/Q4_1, 16-group sums x32
+ * for Q6_K, unscaled 16-group sums for Q2_K, none otherwise). */
+float ref_row_dot_any(int type, const uint8_t* row, const int8_t* q8, const float* xscale,
+                      const float* xsums, int blocks, int order);
+int ref_type_supported(int type);
 void ref_lane_ints(int type, const uint8_t* row, const int8_t* q8, int blocks,
                    int32_t* out);
 

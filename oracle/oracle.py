@@ -17,6 +17,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
+Q4_0, Q4_1, Q2_K, Q3_K, Q5_K, MXFP4 = 2, 3, 10, 11, 13, 39
+EXTRA_TYPES = (Q5_K, Q4_0, Q4_1, MXFP4, Q2_K, Q3_K)
 GENERIC, AMD64 = 0, 1
 
 _lib = None
@@ -56,6 +58,8 @@ def lib():
             "ref_q6k_dot_avx2": (f, [vp, vp, vp, vp, i]),
             "ref_q8_0_dot_avx2": (f, [vp, vp, vp, i]),
             "ref_lane_ints": (None, [i, vp, vp, i, vp]),
+            "ref_row_dot_any": (f, [i, vp, vp, vp, vp, i, i]),
+            "ref_type_supported": (i, [i]),
             "ref_row_bytes": (l, [i, i]),
             "ref_matvec": (i, [i, vp, vp, i, i, vp, i, i]),
             "ref_matvec_batch": (i, [i, vp, vp, i, i, i, vp, i, i]),
@@ -155,7 +159,10 @@ def row_dot(qtype, row, q8, xscale, xsums, order=AMD64):
         return L.ref_q4k_dot(_p(row), _p(q8), _p(xscale), _p(_f32(xsums)), blocks, order)
     if qtype == Q6_K:
         return L.ref_q6k_dot(_p(row), _p(q8), _p(xscale), _p(_f32(xsums)), blocks, order)
-    return L.ref_q8_0_dot(_p(row), _p(q8), _p(xscale), blocks, order)
+    if qtype == Q8_0:
+        return L.ref_q8_0_dot(_p(row), _p(q8), _p(xscale), blocks, order)
+    xs = _f32(xsums if xsums is not None else np.zeros(1, np.float32))
+    return L.ref_row_dot_any(qtype, _p(row), _p(q8), _p(xscale), _p(xs), blocks, order)
 
 
 def row_dot_avx2(qtype, row, q8, xscale, xsums):

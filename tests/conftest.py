@@ -75,3 +75,56 @@ def hip():
     if not g.available():
         pytest.fail("libgllm_hip loaded but no gfx950 device: " + g._lib.last_error())
     return g
+
+
+# ---- rows of the formats beyond Q4_K / Q6_K / Q8_0 ----------------------
+BLOCK = {ref.Q5_K: (176, 256), ref.Q4_0: (18, 32), ref.Q4_1: (20, 32), ref.MXFP4: (17, 32),
+         ref.Q2_K: (84, 256), ref.Q3_K: (110, 256)}
+NAMES = {ref.Q5_K: "q5k", ref.Q4_0: "q4_0", ref.Q4_1: "q4_1", ref.MXFP4: "mxfp4",
+         ref.Q2_K: "q2k", ref.Q3_K: "q3k"}
+
+
+def f16b(v):
+    return np.frombuffer(np.float16(v).tobytes(), np.uint8)
+
+
+def random_rows(qtype, rows, cols, seed):
+    """Random codes with sane scales (the reference's randomQ*Row helpers)."""
+    rng = np.random.default_rng(seed)
+    bb, be = BLOCK[qtype]
+    nb = rows * cols // be
+    blk = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
+    d = rng.uniform(0.002, 0.02, nb).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    m = rng.uniform(0.001, 0.01, nb).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    if qtype == ref.Q5_K:
+        blk[:, 0:2], blk[:, 2:4] = d, m
+    elif qtype == ref.Q4_0:
+        blk[:, 0:2] = d
+    elif qtype == ref.Q4_1:
+        blk[:, 0:2], blk[:, 2:4] = d, m
+    elif qtype == ref.MXFP4:
+        blk[:, 16] = rng.integers(118, 130, nb)
+    elif qtype == ref.Q2_K:
+        blk[:, 80:82], blk[:, 82:84] = d, m
+    elif qtype == ref.Q3_K:
+        blk[:, 108:110] = d
+    return blk.reshape(-1)
+
+
+def extreme_row(qtype, cols):
+    bb, be = BLOCK[qtype]
+    blk = np.full((cols // be, bb), 0xFF, np.uint8)
+    one = f16b(1.0)
+    if qtype == ref.Q5_K:
+        blk[:, 0:2], blk[:, 2:4] = one, one
+    elif qtype == ref.Q4_0:
+        blk[:, 0:2] = one
+    elif qtype == ref.Q4_1:
+        blk[:, 0:2], blk[:, 2:4] = one, one
+    elif qtype == ref.MXFP4:
+        blk[:, 16] = 127
+    elif qtype == ref.Q2_K:
+        blk[:, 80:82], blk[:, 82:84] = one, one
+    elif qtype == ref.Q3_K:
+        blk[:, 108:110] = one
+    return blk.reshape(-1)

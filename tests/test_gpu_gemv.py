@@ -262,4 +262,4 @@ def test_invalid_shapes_rejected(hip):
     with pytest.raises(hip.GllmError):
         hip.Weight.from_host(d[:100], ref.Q4_K, 4, 256)  # too few bytes
     with pytest.raises(hip.GllmError):
-        hip.Weight.from_host(d, 2, 4, 256)               # Q4_0: not on this path
+        hip.Weight.from_host(d, 6, 4, 256)               # Q5_0: no int8 row dot in the reference
