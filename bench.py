@@ -282,7 +282,8 @@ def decode_bench(args):
 def suite(args):
     """One JSON line per measured workload of the other configs:
     configs[1] GEMVs (Q4_K / Q6_K / Q8_0, gate/up and down shapes, batch 1
-    and 8), configs[2] batched prefill (p = 512 activation rows), configs[3]
+    and 8; Q5_K / Q4_0 / Q4_1 / MXFP4 / Q2_K / Q3_K at the gate/up shape),
+    configs[2] batched prefill (p = 512 activation rows), configs[3]
     decode attention (ctx 4096 and 32768, exact and split-K).  Weights rotate
     over >= 300 MB; every timing is a HIP-graph replay on the launch stream."""
     import torch
@@ -291,7 +292,7 @@ def suite(args):
 
     g.load()
     qnames = {g.TYPE_Q4_K: "Q4_K", g.TYPE_Q6_K: "Q6_K", g.TYPE_Q8_0: "Q8_0"}
-    only = set(args.only.split(",")) if args.only else {"gemv", "prefill", "attention"}
+    only = set(args.only.split(",")) if args.only else {"gemv", "formats", "prefill", "attention"}
 
     def graph_time(body, reps):
         graph = timed_graph(torch, body, 1)
@@ -338,6 +339,43 @@ def suite(args):
                                   "GB_s": round(nbytes / us / 1e3, 1),
                                   "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
             del ws
+
+    # formats beyond Q4_K / Q6_K / Q8_0: random codes with valid f16 scales
+    # (the block layouts of gguf.go:241-297), gate/up shape
+    fmt_layout = {g.TYPE_Q5_K: ("Q5_K", 176, 256, [(0, 2), (2, 4)], None),
+                  g.TYPE_Q4_0: ("Q4_0", 18, 32, [(0, 2)], None),
+                  g.TYPE_Q4_1: ("Q4_1", 20, 32, [(0, 2), (2, 4)], None),
+                  g.TYPE_MXFP4: ("MXFP4", 17, 32, [], 16),
+                  g.TYPE_Q2_K: ("Q2_K", 84, 256, [(80, 82), (82, 84)], None),
+                  g.TYPE_Q3_K: ("Q3_K", 110, 256, [(108, 110)], None)}
+    for qtype, (name, bb, be, halfs, ebyte) in fmt_layout.items() if "formats" in only else ():
+        import numpy as np
+        rows, cols = 14336, 4096
+        rng = np.random.default_rng(qtype)
+        nb = rows * cols // be
+        blk = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
+        for lo, hi in halfs:
+            blk[:, lo:hi] = rng.uniform(0.002, 0.02, nb).astype(np.float16).view(np.uint8).reshape(nb, 2)
+        if ebyte is not None:
+            blk[:, ebyte] = rng.integers(118, 130, nb)
+        raw = blk.reshape(-1)
+        wb = raw.size
+        ws = [g.Weight.from_host(raw, qtype, rows, cols) for _ in range(max(2, math.ceil(300e6 / wb)))]
+        for p in (1, 8):
+            x = torch.empty((p, cols), dtype=torch.float32, device="cuda")
+            g.fill_normal_dev(x, 7, 1.0)
+            out = torch.empty((p, rows), dtype=torch.float32, device="cuda")
+
+            def body():
+                for w in ws:
+                    w.matvec_dev(x, out)
+
+            us = graph_time(body, 20) / len(ws)
+            nbytes = wb + p * (4 * cols + 4 * rows)
+            print(json.dumps({"suite": "formats gemv", "type": name, "rows": rows, "cols": cols,
+                              "batch": p, "us": round(us, 3), "GB_s": round(nbytes / us / 1e3, 1),
+                              "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
+        del ws
 
     for rows, cols in ((4096, 4096), (14336, 4096)) if "prefill" in only else ():
         ws, wb = weights_for(g.TYPE_Q4_K, rows, cols, min_bytes=0)
@@ -420,7 +458,7 @@ def main():
     ap.add_argument("--suite", action="store_true",
                     help="measure the other configs (GEMV types/shapes/batch 8, prefill, attention)")
     ap.add_argument("--only", default="",
-                    help="suite parts to run: comma list of gemv, prefill, attention")
+                    help="suite parts to run: comma list of gemv, formats, prefill, attention")
     ap.add_argument("--ctx", type=int, default=0, help="suite attention: only this context")
     ap.add_argument("--profile-run", action="store_true",
                     help="eager launches for rocprofv3 counter collection")

@@ -32,21 +32,36 @@ __device__ __forceinline__ uint32_t ld32h(const uint8_t* p) {
     return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
 }
 
-// Activation operands of one lane, one token, one 256-element block.
+// Activation operands of one lane, one token, one 256-element block: the
+// q8 bytes, the Q8K scale and the kNX activation sums the format reads
+// (Q5_K: x32[k]; Q4_0 / Q4_1: x32[0..7]; Q2_K: x16[k], x16[8 + k]).
 struct Act {
     int4 qa, qb;        // groups 0..3 and 4..7, lane k's 4 bytes each
     float xs;           // Q8K scale of the block
-    const float* x32;   // per-32 sums of the block (8), or null
-    const float* x16;   // per-16 sums of the block (16, unscaled), or null
+    float xv[8];
     __device__ __forceinline__ int q(int m) const {
         const int v[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
         return v[m];
     }
 };
 
+// Fill a's sums for format F from the block's sums in memory.
+template <class F>
+__device__ __forceinline__ void load_sums(Act& a, int k, const float* x32, const float* x16) {
+    if constexpr (F::kSums == kX32 && F::kNX == 1) {
+        a.xv[0] = x32[k];
+    } else if constexpr (F::kSums == kX32) {
+#pragma unroll
+        for (int g = 0; g < 8; g++) a.xv[g] = x32[g];
+    } else if constexpr (F::kSums == kX16) {
+        a.xv[0] = x16[k];
+        a.xv[1] = x16[8 + k];
+    }
+}
+
 // ---- Q5_K -----------------------------------------------------------------
 struct Q5K {
-    static constexpr int kBytes = 176, kSums = kX32;
+    static constexpr int kBytes = 176, kSums = kX32, kNX = 1;
     static constexpr bool kHasM = true, kHasS = false;
     struct Regs {
         uint4 h, q;
@@ -79,7 +94,7 @@ struct Q5K {
         const int acc = q4k_lane_sum(t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7], sc03, sc47);
         const float iv = (float)acc;
         const float dxs = d * a.xs;                 // VMULSS
-        const float mx = mkf * a.x32[k];            // VMULPS
+        const float mx = mkf * a.xv[0];             // VMULPS
 #pragma unroll
         for (int st = 0; st < G; st++) {
             accF = fmaf(iv, dxs, rot_prev<G>(accF));     // VFMADD231PS
@@ -90,7 +105,7 @@ struct Q5K {
 
 // ---- Q2_K -----------------------------------------------------------------
 struct Q2K {
-    static constexpr int kBytes = 84, kSums = kX16;
+    static constexpr int kBytes = 84, kSums = kX16, kNX = 2;
     static constexpr bool kHasM = true, kHasS = false;
     struct Regs {
         uint32_t dd, sc[4], q0, q1;
@@ -102,7 +117,9 @@ struct Q2K {
         r.q0 = ld32(blk + 20 + 8 * k);
         r.q1 = ld32(blk + 24 + 8 * k);
     }
-    __device__ static int scb(const Regs& r, int i) { return (int)((r.sc[i >> 2] >> (8 * (i & 3))) & 0xffu); }
+    // scale byte 4q + (i & 3) where the dword q is fixed at compile time (a
+    // runtime index into sc[] would move the whole register ring to scratch)
+    __device__ static int byte_of(uint32_t w, int i) { return (int)((w >> (8 * (i & 3))) & 0xffu); }
     // q2kDotQ8KRow (kernels_amd64.s:816-887): group m's codes at shift
     // 2(m%4) of qs dword m/4, weighted by the d-scale nibble of sub-block
     // 2m + k/4; min term t = fma(min_{8+k}, xsum_{8+k}, min_k * xsum_k).
@@ -116,10 +133,13 @@ struct Q2K {
         for (int m = 0; m < 8; m++) {
             const uint32_t qn = m < 4 ? r.q0 : r.q1;
             const int code = (int)((qn >> (2 * (m & 3))) & 0x03030303u);
-            acc += (scb(r, 2 * m + (k >> 2)) & 15) * dot4z(code, a.q(m));
+            // sub-block 2m + k/4 lies in scale dword m/2
+            acc += (byte_of(r.sc[m >> 1], 2 * m + (k >> 2)) & 15) * dot4z(code, a.q(m));
         }
-        float t = (float)(scb(r, k) >> 4) * a.x16[k];             // VMULPS
-        t = fmaf((float)(scb(r, 8 + k) >> 4), a.x16[8 + k], t);   // VFMADD231PS
+        const int mk = byte_of(k < 4 ? r.sc[0] : r.sc[1], k) >> 4;
+        const int mk8 = byte_of(k < 4 ? r.sc[2] : r.sc[3], k) >> 4;
+        float t = (float)mk * a.xv[0];                            // VMULPS
+        t = fmaf((float)mk8, a.xv[1], t);                         // VFMADD231PS
         const float iv = (float)acc;
         const float dxs = d * a.xs;
 #pragma unroll
@@ -132,7 +152,7 @@ struct Q2K {
 
 // ---- Q3_K -----------------------------------------------------------------
 struct Q3K {
-    static constexpr int kBytes = 110, kSums = kNone;
+    static constexpr int kBytes = 110, kSums = kNone, kNX = 0;
     static constexpr bool kHasM = false, kHasS = false;
     struct Regs {
         uint32_t d, s0, s1, s2, hm, q0, q1;
@@ -177,7 +197,7 @@ struct Q3K {
 // ---- Q4_0 / Q4_1 ------------------------------------------------------------
 template <bool Q41>
 struct Q401 {
-    static constexpr int kBytes = Q41 ? 160 : 144, kSums = kX32;
+    static constexpr int kBytes = Q41 ? 160 : 144, kSums = kX32, kNX = 8;
     static constexpr bool kHasM = false, kHasS = true;
     struct Regs {
         uint4 h0, h1;  // Q4_0: h0 = 8 f16 d; Q4_1: h0, h1 = 8 (d | m << 16)
@@ -213,7 +233,7 @@ struct Q401 {
                 d = f16_bits_to_f32((hd[g >> 1] >> (16 * (g & 1))) & 0xffffu);
             }
             dxs[g] = d * a.xs;                               // VMULSS X9, X0
-            off[g] = (Q41 ? m : d) * a.x32[g];               // VMULSS (R9)
+            off[g] = (Q41 ? m : d) * a.xv[g];                // VMULSS (R9)
         }
 #pragma unroll
         for (int st = 0; st < G; st++) {
@@ -232,7 +252,7 @@ struct Q401 {
 
 // ---- MXFP4 ------------------------------------------------------------------
 struct MXFP4 {
-    static constexpr int kBytes = 136, kSums = kNone;
+    static constexpr int kBytes = 136, kSums = kNone, kNX = 0;
     static constexpr bool kHasM = false, kHasS = false;
     struct Regs {
         uint2 e;   // exponent bytes of blocks 0..7
@@ -244,10 +264,17 @@ struct MXFP4 {
         const uint2 hi = *(const uint2*)(blk + 16 + 16 * k);
         r.c = make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
-    // twice the e2m1 value of code c (mxfp4DoubledLUT), as a signed byte
-    __device__ static uint32_t dbl(uint32_t c) {
-        const uint32_t mag = (uint32_t)(0x0c08060403020100ull >> (8 * (c & 7))) & 0xffu;
-        return (c & 8) ? ((0u - mag) & 0xffu) : mag;
+    // Lane dot of one 32-block against mxfp4DoubledLUT values: u holds the
+    // lane's four codes (nibbles, element order).  Magnitudes come from one
+    // byte permute of the table {0,1,2,3,4,6,8,12}; the sign bit splits the
+    // dot into a positive and a negative part (VPSIGNB on the activations
+    // gives the same integer), so nothing is negated bytewise.
+    __device__ static int lane_dot(uint32_t u, int act) {
+        const uint32_t lo = u & 0x0f0fu, hi = (u >> 4) & 0x0f0fu;        // codes 0, 2 | 1, 3
+        const uint32_t codes = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // c0 c1 c2 c3
+        const uint32_t mag = __builtin_amdgcn_perm(0x0c080604u, 0x03020100u, codes & 0x07070707u);
+        const uint32_t neg = ((codes >> 3) & 0x01010101u) * 0xffu;
+        return dot4z((int)(mag & ~neg), act) - dot4z((int)(mag & neg), act);
     }
     // mxfp4DotQ8KRow (kernels_amd64.s:1065-1128): hx = 0.5 * xs, then per
     // 32-block accF = fma(bits(e << 23) * hx, float(I), accF).
@@ -259,9 +286,7 @@ struct MXFP4 {
 #pragma unroll
         for (int g = 0; g < 8; g++) {
             const uint32_t u = (cw[g >> 1] >> (16 * (g & 1))) & 0xffffu;
-            const uint32_t v = dbl(u & 15) | (dbl((u >> 4) & 15) << 8) | (dbl((u >> 8) & 15) << 16) |
-                               (dbl(u >> 12) << 24);
-            iv[g] = (float)dot4z((int)v, a.q(g));
+            iv[g] = (float)lane_dot(u, a.q(g));
             const uint32_t eb = (g < 4 ? r.e.x >> (8 * g) : r.e.y >> (8 * (g - 4))) & 0xffu;
             sc[g] = __uint_as_float(eb << 23) * hx;                // VMULSS X10, X0
         }
@@ -278,10 +303,18 @@ struct MXFP4 {
 }  // namespace fmt
 
 // One row kernel for every format above: lane (k, gi) of row r walks blocks
-// gi, gi + G, ... with two blocks of weight bytes in flight.
+// gi, gi + G, ... with D blocks of weight bytes in flight, loaded in block
+// order and unconditionally (clamped to the lane's last block) so the
+// compiler's vmcnt waits never drain the ring.  At batch 1 the block's
+// activation operands ride in the ring as well.
+template <class F, int NT>
+constexpr int fmt_depth() {
+    return NT == 1 ? (F::kNX == 8 ? 3 : 4) : 2;
+}
+
 template <class F, int NT, int G>
 __global__ __launch_bounds__(256) void gemv_fmt_kernel(GemvJob j) {
-    constexpr int D = 2;
+    constexpr int D = fmt_depth<F, NT>();
     int wi;
     const int tid = threadIdx.x;
     const int gi = tid % G, k = (tid / G) & 7;
@@ -292,24 +325,37 @@ __global__ __launch_bounds__(256) void gemv_fmt_kernel(GemvJob j) {
     float accF[NT], accM[NT], accS[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) accF[t] = accM[t] = accS[t] = 0.0f;
-    typename F::Regs ring[D];
-    auto load = [&](int i, typename F::Regs& o) __attribute__((always_inline)) {
-        F::load(row + (size_t)(min(i, NB - 1) * G + gi) * F::kBytes, k, o);
+    struct Slot {
+        typename F::Regs w;
+        fmt::Act a;  // NT == 1 only
     };
-    auto compute = [&](int i, const typename F::Regs& o) __attribute__((always_inline)) {
-        const int b = i * G + gi;
+    const size_t tok0 = (size_t)j.tok0;
+    auto act_of = [&](size_t tok, int b, fmt::Act& a) __attribute__((always_inline)) {
+        const int8_t* q8 = j.act.q8perm + tok * j.cols + (size_t)b * 256 + k * 32;
+        a.qa = *(const int4*)q8;
+        a.qb = *(const int4*)(q8 + 16);
+        a.xs = j.act.xscale[tok * B + b];
+        fmt::load_sums<F>(a, k, j.act.xs32 + tok * (j.cols / 32) + (size_t)b * 8,
+                          j.act.xs16 + tok * (j.cols / 16) + (size_t)b * 16);
+    };
+    Slot ring[D];
+    auto load = [&](int i, Slot& o) __attribute__((always_inline)) {
+        const int b = min(i, NB - 1) * G + gi;
+        F::load(row + (size_t)b * F::kBytes, k, o.w);
+        if constexpr (NT == 1) act_of(tok0, b, o.a);
+    };
+    auto compute = [&](int i, const Slot& o) __attribute__((always_inline)) {
+        if constexpr (NT == 1) {
+            F::template step<G>(o.w, k, o.a, accF[0], accM[0], accS[0]);
+        } else {
+            const int b = i * G + gi;
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            if (NT == 1 || t < j.ntok) {
-                const size_t tok = (size_t)(j.tok0 + t);
-                const int8_t* q8 = j.act.q8perm + tok * j.cols + (size_t)b * 256 + k * 32;
-                fmt::Act a;
-                a.qa = *(const int4*)q8;
-                a.qb = *(const int4*)(q8 + 16);
-                a.xs = j.act.xscale[tok * B + b];
-                a.x32 = F::kSums == fmt::kX32 ? j.act.xs32 + tok * (j.cols / 32) + (size_t)b * 8 : nullptr;
-                a.x16 = F::kSums == fmt::kX16 ? j.act.xs16 + tok * (j.cols / 16) + (size_t)b * 16 : nullptr;
-                F::template step<G>(o, k, a, accF[t], accM[t], accS[t]);
+            for (int t = 0; t < NT; t++) {
+                if (t < j.ntok) {
+                    fmt::Act a;
+                    act_of(tok0 + t, b, a);
+                    F::template step<G>(o.w, k, a, accF[t], accM[t], accS[t]);
+                }
             }
         }
     };
