@@ -158,36 +158,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float* __restrict__ x,
         }
     }
     __syncthreads();
-    const int n32 = n & ~31, n8 = n & ~7;
-    if (tid < 32) {
-        float y = 0.0f;
-        int i = 0;
-        for (; i + 16 * 32 <= n32; i += 16 * 32) {
-            float xb[16];
-#pragma unroll
-            for (int u = 0; u < 16; u++) xb[u] = xs[i + 32 * u + tid];
-#pragma unroll
-            for (int u = 0; u < 16; u++) y = fmaf(xb[u], xb[u], y);
-        }
-        for (; i < n32; i += 32) y = fmaf(xs[i + tid], xs[i + tid], y);
-        part[tid] = y;
-    }
-    __syncthreads();
-    if (tid < 8) {
-        float acc = (part[tid] + part[8 + tid]) + (part[16 + tid] + part[24 + tid]);
-        for (int i = n32; i < n8; i += 8) acc = fmaf(xs[i + tid], xs[i + tid], acc);
-        part[tid] = acc;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        const float a0 = part[0] + part[4], a1 = part[1] + part[5];
-        const float a2 = part[2] + part[6], a3 = part[3] + part[7];
-        float ss = (a0 + a1) + (a2 + a3);
-        for (int i = n8; i < n; i++) ss = ss + xs[i] * xs[i];
-        s_scale = (float)(1.0 / sqrt((double)(ss / (float)n + eps)));
-    }
-    __syncthreads();
-    const float scale = s_scale;
+    const float scale = rms_scale_lds(xs, n, eps, part, &s_scale);
     float4* o4 = (float4*)(out + (size_t)t * n);
 #pragma unroll
     for (int u = 0; u < kNormVec; u++) {

@@ -121,6 +121,47 @@ __device__ __forceinline__ float tree8(float v) {
 // siluMulF32AVX2 (kernels_amd64.s:1630-1700) for one element, lane for lane:
 // the Cephes exp of -|g| with the reference's constants, then
 // (g * (g < 0 ? e : 1) / (1 + e)) * up.
+// rmsNormInto's scale over the n floats xs[] (LDS; n % 8 == 0): the
+// sum of squares in dotF32AVX2's order (kernels_amd64.s:28-93: 4 x 8 fma
+// accumulators over 32-element strides, then the 32 -> 8 -> tree reduction)
+// and scale = float32(1 / sqrt(float64(ss / n + eps))) (model.go:2986-3011).
+// Threads 0..31 run the accumulator chains; every thread of the block calls
+// it and receives the scale.  part[32] and *s_scale are LDS scratch.
+__device__ inline float rms_scale_lds(const float* xs, int n, float eps, float* part,
+                                      float* s_scale) {
+    const int tid = threadIdx.x;
+    const int n32 = n & ~31, n8 = n & ~7;
+    if (tid < 32) {
+        float y = 0.0f;
+        int i = 0;
+        for (; i + 16 * 32 <= n32; i += 16 * 32) {
+            float xb[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) xb[u] = xs[i + 32 * u + tid];
+#pragma unroll
+            for (int u = 0; u < 16; u++) y = fmaf(xb[u], xb[u], y);
+        }
+        for (; i < n32; i += 32) y = fmaf(xs[i + tid], xs[i + tid], y);
+        part[tid] = y;
+    }
+    __syncthreads();
+    if (tid < 8) {
+        float acc = (part[tid] + part[8 + tid]) + (part[16 + tid] + part[24 + tid]);
+        for (int i = n32; i < n8; i += 8) acc = fmaf(xs[i + tid], xs[i + tid], acc);
+        part[tid] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const float a0 = part[0] + part[4], a1 = part[1] + part[5];
+        const float a2 = part[2] + part[6], a3 = part[3] + part[7];
+        float ss = (a0 + a1) + (a2 + a3);
+        for (int i = n8; i < n; i++) ss = ss + xs[i] * xs[i];
+        *s_scale = (float)(1.0 / sqrt((double)(ss / (float)n + eps)));
+    }
+    __syncthreads();
+    return *s_scale;
+}
+
 __device__ __forceinline__ float silu_mul(float g, float up) {
     const float lo_clamp = __uint_as_float(0xc2b0c0a5u);  // -88.376
     const float log2e = __uint_as_float(0x3fb8aa3bu);

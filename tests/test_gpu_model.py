@@ -91,3 +91,34 @@ def test_generate_with_repeat_penalty(hip):
         gpu.set_repeat_penalty(0.0, 64)
     with pytest.raises(hip.GllmError):
         gpu.set_repeat_penalty(1.5, -1)
+
+
+def test_decode_8b_layer_shapes_bit_exact(hip):
+    """Two layers at the 8B shapes (dim 4096, hidden 14336, 32 / 8 heads of
+    128), the row kernels the full model runs (fused-quantiser Q4_K at 4096
+    columns, 14336-column down projection), non-trivial norm weights: hidden
+    states and greedy tokens identical to the oracle's ForwardBodyInto
+    through prefill and the captured, replayed decode step."""
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = tiny_llama(seed=12, n_layers=2, dim=4096, hidden=14336, n_heads=32, n_kv_heads=8,
+                   head_dim=128, vocab=1200)
+    rng = np.random.default_rng(13)
+    m["out_norm"] = (1 + 0.2 * rng.standard_normal(4096)).astype(np.float32)
+    m["attn_norm"] = [(1 + 0.2 * rng.standard_normal(4096)).astype(np.float32) for _ in range(2)]
+    m["ffn_norm"] = [(1 + 0.2 * rng.standard_normal(4096)).astype(np.float32) for _ in range(2)]
+    max_len = 64
+    gpu = LlamaDecoder.from_host_model(m, max_len)
+    cpu = ref.Llama(m, max_len, fast=True)
+    prompt = rng.integers(0, 1200, 9)
+    gt = gpu.prefill(prompt)
+    ct, _ = cpu.prefill(prompt)
+    assert gt == ct
+    tok = gt
+    for i in range(12):
+        pos = len(prompt) + i
+        print(f"8b-shape decode pos {pos}", flush=True)
+        want, hid = cpu.decode(tok, pos)
+        got = gpu.decode(tok, pos)
+        assert np.array_equal(bits(gpu.hidden()), bits(hid)), pos
+        assert got == want, pos
+        tok = want
