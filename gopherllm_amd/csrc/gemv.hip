@@ -169,8 +169,6 @@ struct MinSel {
     }
 };
 
-#include "gemv_formats.h"
-
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Stage this launch's activations (q8, xs32, xscale of ntok tokens) into LDS
@@ -287,6 +285,30 @@ __device__ __forceinline__ void xq_store(const XRegs<QB>& xr, int B, int8_t* q8,
         xq_block<XS16>(xr.v[i], b, q8, xs32, xs16, xsc);
     }
 }
+
+// LDS image of one quantised activation row for the batch-1 Q6_K, Q8_0 and
+// other-format row kernels when they quantise x themselves (256-thread
+// workgroups, cols <= kFuseCols: four waves of four blocks each).
+constexpr int kFuseCols = 4096;
+struct FusedAct {
+    int8_t q8[kFuseCols];  // lane-permuted, as q8perm
+    float xs32[kFuseCols / 32];
+    float xs16[kFuseCols / 16];  // unscaled per-16 sums
+    float xsc[kFuseCols / 256];
+};
+constexpr int kFuseQB = kFuseCols / 256 / 4;
+
+// Fused prologue, part 2 (part 1 is xq_load<kFuseQB>, issued before the
+// weight prefetch so its registers retire first): quantise into fa and make
+// it visible to the workgroup without waiting for the weight loads.
+template <bool XS16>
+__device__ __forceinline__ void fused_act_store(const XRegs<kFuseQB>& xr, int B, FusedAct& fa) {
+    xq_store<kFuseQB, XS16>(xr, B, fa.q8, fa.xs32, fa.xs16, fa.xsc);
+    wait_lgkm0();
+    lds_barrier();
+}
+
+#include "gemv_formats.h"
 
 // One Q4_K block of one AVX2 lane for NT tokens: exact int32 lane sum
 //   accI_k = sum_j sc_j * dot4(nibbles of sub-block j in lane k, q8)
@@ -449,16 +471,25 @@ __global__ __launch_bounds__(256) void gemv_q4k_any_kernel(GemvJob j) {
 // still fills the chip): lane gi takes blocks gi, gi + G, ... and the
 // reference's sequential per-lane chain visits the G lanes in block order
 // through rot_prev, ending in lane gi = G - 1 after every group of G blocks.
-template <int NT, int G>
+//
+// FUSE (batch 1, cols <= kFuseCols): the workgroup quantises the f32
+// activation into LDS itself (x loads first, weight prefetch second), so the
+// matvec is one launch; lanes past the last row then compute a clamped row
+// and store nothing, since the whole workgroup takes part in the barrier.
+template <int NT, int G, bool FUSE = false>
 __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
+    static_assert(!FUSE || NT == 1, "fused quantisation is batch 1 only");
     constexpr int D = kQ6Depth<NT>;
+    __shared__ __attribute__((aligned(16))) uint8_t fa_raw[FUSE ? sizeof(FusedAct) : 16];
+    FusedAct& fa = *(FusedAct*)fa_raw;
     int wi;
     const int tid = threadIdx.x;
     const int gi = tid % G, k = (tid / G) & 7;
     const int r = locate(j, blockIdx.x, &wi) + tid / (8 * G);
-    if (r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    if (!FUSE && r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    const bool live = r < j.rows[wi];
     const int B = j.blocks, NB = B / G;
-    const uint8_t* row = j.w[wi] + (size_t)r * j.rb;
+    const uint8_t* row = j.w[wi] + (size_t)(live ? r : j.rows[wi] - 1) * j.rb;
     const uint16_t* dv = (const uint16_t*)(row + (size_t)B * 208);
     const int hk = k >> 2;
     float accF[NT], accM[NT];
@@ -479,7 +510,7 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
         int4 qa, qb;
         float x0, x8, xs;
     };
-    auto load = [&](int i, Blk& o) __attribute__((always_inline)) {
+    auto load_w = [&](int i, Blk& o) __attribute__((always_inline)) {
         const int bb = min(i, NB - 1) * G + gi;
         const uint8_t* blk = row + (size_t)bb * 208;
         o.ql[0] = *(const uint32_t*)(blk + 4 * k);
@@ -490,13 +521,26 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
         o.qh[1] = *(const uint32_t*)(blk + 160 + 4 * k);
         o.sv = *(const uint4*)(blk + 192);
         o.d = dv[bb];
-        if constexpr (NT == 1) {
+    };
+    auto load_a = [&](int i, Blk& o) __attribute__((always_inline)) {
+        const int bb = min(i, NB - 1) * G + gi;
+        if constexpr (FUSE) {
+            o.qa = *(const int4*)(fa.q8 + bb * 256 + k * 32);
+            o.qb = *(const int4*)(fa.q8 + bb * 256 + k * 32 + 16);
+            o.x0 = fa.xs16[bb * 16 + k] * 32.0f;  // ScaleF32(xs, 32)
+            o.x8 = fa.xs16[bb * 16 + 8 + k] * 32.0f;
+            o.xs = fa.xsc[bb];
+        } else if constexpr (NT == 1) {
             o.qa = *(const int4*)(q8 + bb * 256);
             o.qb = *(const int4*)(q8 + bb * 256 + 16);
             o.x0 = xs16[bb * 16] * 32.0f;      // ScaleF32(xs, 32)
             o.x8 = xs16[bb * 16 + 8] * 32.0f;
             o.xs = xsc[bb];
         }
+    };
+    auto load = [&](int i, Blk& o) __attribute__((always_inline)) {
+        load_w(i, o);
+        load_a(i, o);
     };
     auto compute = [&](int i, const Blk& o) __attribute__((always_inline)) {
         const int b = i * G + gi;
@@ -549,10 +593,24 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
         }
     };
     Blk ring[D];
+    XRegs<kFuseQB> xr;
+    if constexpr (FUSE) {
+        xq_load<kFuseQB>(j.xf, B, xr);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int i = 0; i < D; i++) {
-        load(i, ring[i]);
+        if constexpr (FUSE) {
+            load_w(i, ring[i]);
+        } else {
+            load(i, ring[i]);
+        }
         __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (FUSE) {
+        fused_act_store<true>(xr, B, fa);
+#pragma unroll
+        for (int i = 0; i < D; i++) load_a(i, ring[i]);
     }
     // whole groups straight-line (a guarded compute would turn the waits
     // at its join into drains), then the tail
@@ -572,7 +630,7 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const float v = tree8_strided<G>(accF[t] - accM[t]);  // VSUBPS + tree
-        if (k == 0 && gi == G - 1 && t < j.ntok)
+        if (live && k == 0 && gi == G - 1 && t < j.ntok)
             j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
     }
 }
@@ -582,17 +640,21 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
 // (272 bytes, 16-byte aligned).  AVX2 lane k covers bytes 4k..4k+3 of each
 // 32-value block (Q80CHUNK, kernels_amd64.s:1321-1345).
 // ---------------------------------------------------------------------------
-// G lanes per AVX2 lane as in gemv_q6k_kernel.
-template <int NT, int G>
+// G lanes per AVX2 lane and FUSE as in gemv_q6k_kernel.
+template <int NT, int G, bool FUSE = false>
 __global__ __launch_bounds__(256) void gemv_q8_0_kernel(GemvJob j) {
+    static_assert(!FUSE || NT == 1, "fused quantisation is batch 1 only");
     constexpr int D = kQ8Depth<NT>;
+    __shared__ __attribute__((aligned(16))) uint8_t fa_raw[FUSE ? sizeof(FusedAct) : 16];
+    FusedAct& fa = *(FusedAct*)fa_raw;
     int wi;
     const int tid = threadIdx.x;
     const int gi = tid % G, k = (tid / G) & 7;
     const int r = locate(j, blockIdx.x, &wi) + tid / (8 * G);
-    if (r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    if (!FUSE && r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    const bool live = r < j.rows[wi];
     const int B = j.blocks, NB = B / G;
-    const uint8_t* row = j.w[wi] + (size_t)r * j.rb;
+    const uint8_t* row = j.w[wi] + (size_t)(live ? r : j.rows[wi] - 1) * j.rb;
     float acc11[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) acc11[t] = 0.0f;
@@ -605,17 +667,28 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(GemvJob j) {
         int4 qa, qb;
         float xs;
     };
-    auto load = [&](int i, Blk& o) __attribute__((always_inline)) {
+    auto load_w = [&](int i, Blk& o) __attribute__((always_inline)) {
         const int bb = min(i, NB - 1) * G + gi;
         const uint8_t* blk = row + (size_t)bb * 272;
         o.dh = *(const uint4*)blk;
 #pragma unroll
         for (int q = 0; q < 8; q++) o.wv[q] = *(const int*)(blk + 16 + 32 * q + 4 * k);
-        if constexpr (NT == 1) {
+    };
+    auto load_a = [&](int i, Blk& o) __attribute__((always_inline)) {
+        const int bb = min(i, NB - 1) * G + gi;
+        if constexpr (FUSE) {
+            o.qa = *(const int4*)(fa.q8 + bb * 256 + k * 32);
+            o.qb = *(const int4*)(fa.q8 + bb * 256 + k * 32 + 16);
+            o.xs = fa.xsc[bb];
+        } else if constexpr (NT == 1) {
             o.qa = *(const int4*)(q8 + bb * 256);
             o.qb = *(const int4*)(q8 + bb * 256 + 16);
             o.xs = xsc[bb];
         }
+    };
+    auto load = [&](int i, Blk& o) __attribute__((always_inline)) {
+        load_w(i, o);
+        load_a(i, o);
     };
     auto compute = [&](int i, const Blk& o) __attribute__((always_inline)) {
         const int b = i * G + gi;
@@ -640,10 +713,24 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(GemvJob j) {
         }
     };
     Blk ring[D];
+    XRegs<kFuseQB> xr;
+    if constexpr (FUSE) {
+        xq_load<kFuseQB>(j.xf, B, xr);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int i = 0; i < D; i++) {
-        load(i, ring[i]);
+        if constexpr (FUSE) {
+            load_w(i, ring[i]);
+        } else {
+            load(i, ring[i]);
+        }
         __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (FUSE) {
+        fused_act_store<false>(xr, B, fa);
+#pragma unroll
+        for (int i = 0; i < D; i++) load_a(i, ring[i]);
     }
     int i0 = 0;
     for (; i0 + D <= NB; i0 += D) {
@@ -661,7 +748,7 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(GemvJob j) {
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const float v = tree8_strided<G>(acc11[t]);
-        if (k == 0 && gi == G - 1 && t < j.ntok)
+        if (live && k == 0 && gi == G - 1 && t < j.ntok)
             j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
     }
 }
@@ -1030,9 +1117,11 @@ int launch_q4k(GemvJob& j, const int* rows, int n, const Q4KShape& sh, hipStream
 }
 
 // Lanes per AVX2 lane (G) of the Q6_K / Q8_0 row kernels (G divides the
-// block count).  Batch 1 splits a row only when the matrix gives fewer than
-// half the compute units a workgroup: the G-step rotation costs more than the
-// extra workgroups bring once the launch has 128 of them.  Batches (per-token
+// block count).  Batch 1 splits a row only while the launch has fewer
+// workgroups than the device has compute units: with every CU busy the G-step
+// rotation costs more than extra workgroups bring (Q6_K 14336x4096 measured
+// 16.7 / 21.2 / 29.5 us at G = 1 / 2 / 4), with half of them idle it is the
+// other way round (Q6_K 4096x14336: 44.9 / 27.8 / 24.8 us).  Batches (per-token
 // activation reads make each block several times longer) take the largest G
 // that keeps the launch at two workgroups per compute unit or fewer.
 // GLLM_ROW_G overrides, for measurement; every G gives the same bits.
@@ -1047,7 +1136,7 @@ static int row_lanes_g(int total_rows, int blocks, int ntok) {
     auto wgs = [&](int g) { return (total_rows * g + kRowsPerWG - 1) / kRowsPerWG; };
     int g = 1;
     if (ntok == 1) {
-        while (g < 4 && blocks % (2 * g) == 0 && wgs(g) < ncu / 2) g *= 2;
+        while (g < 4 && blocks % (2 * g) == 0 && wgs(g) < ncu) g *= 2;
     } else {
         while (g < 4 && blocks % (2 * g) == 0 && wgs(2 * g) <= 2 * ncu) g *= 2;
     }
@@ -1058,9 +1147,30 @@ template <int NT>
 static void (*pick_g(int g, void (*k1)(GemvJob), void (*k2)(GemvJob), void (*k4)(GemvJob)))(GemvJob) {
     return g == 1 ? k1 : g == 2 ? k2 : k4;
 }
-template <class F, int NT>
+template <class F, int NT, bool FUSE>
 static void (*fmt_kernel(int g))(GemvJob) {
-    return pick_g<NT>(g, gemv_fmt_kernel<F, NT, 1>, gemv_fmt_kernel<F, NT, 2>, gemv_fmt_kernel<F, NT, 4>);
+    return pick_g<NT>(g, gemv_fmt_kernel<F, NT, 1, FUSE>, gemv_fmt_kernel<F, NT, 2, FUSE>,
+                      gemv_fmt_kernel<F, NT, 4, FUSE>);
+}
+
+// The Q6_K, Q8_0 and other-format row kernel for this type, batch tile NT
+// and G; FUSE selects the variant that quantises x itself.
+template <int NT, bool FUSE>
+static void (*row_kernel(int type, int g))(GemvJob) {
+    switch (type) {
+    case GLLM_TYPE_Q6_K:
+        return pick_g<NT>(g, gemv_q6k_kernel<NT, 1, FUSE>, gemv_q6k_kernel<NT, 2, FUSE>,
+                          gemv_q6k_kernel<NT, 4, FUSE>);
+    case GLLM_TYPE_Q8_0:
+        return pick_g<NT>(g, gemv_q8_0_kernel<NT, 1, FUSE>, gemv_q8_0_kernel<NT, 2, FUSE>,
+                          gemv_q8_0_kernel<NT, 4, FUSE>);
+    case GLLM_TYPE_Q5_K: return fmt_kernel<fmt::Q5K, NT, FUSE>(g);
+    case GLLM_TYPE_Q2_K: return fmt_kernel<fmt::Q2K, NT, FUSE>(g);
+    case GLLM_TYPE_Q3_K: return fmt_kernel<fmt::Q3K, NT, FUSE>(g);
+    case GLLM_TYPE_Q4_0: return fmt_kernel<fmt::Q401<false>, NT, FUSE>(g);
+    case GLLM_TYPE_Q4_1: return fmt_kernel<fmt::Q401<true>, NT, FUSE>(g);
+    default: return fmt_kernel<fmt::MXFP4, NT, FUSE>(g);
+    }
 }
 
 template <int NT>
@@ -1074,6 +1184,8 @@ int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t 
                          : launch_q4k<NT, 4>(j, rows, j.n, sh, s);
     }
     if (!row_kernel_type(type)) return fail(GLLM_EUNSUP, "gemv: unsupported type %d", type);
+    if (j.xf && (NT != 1 || j.cols > kFuseCols))
+        return fail(GLLM_EINVAL, "gemv: fused quantisation needs batch 1 and cols <= %d", kFuseCols);
     int total = 0;
     for (int i = 0; i < j.n; i++) total += rows[i];
     const int g = row_lanes_g(total, j.blocks, j.ntok);
@@ -1084,16 +1196,9 @@ int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t 
         wg += (rows[i] + j.rows_per_wg - 1) / j.rows_per_wg;
     }
     j.wg_begin[j.n] = wg;
-    void (*kern)(GemvJob);
-    switch (type) {
-    case GLLM_TYPE_Q6_K: kern = pick_g<NT>(g, gemv_q6k_kernel<NT, 1>, gemv_q6k_kernel<NT, 2>, gemv_q6k_kernel<NT, 4>); break;
-    case GLLM_TYPE_Q8_0: kern = pick_g<NT>(g, gemv_q8_0_kernel<NT, 1>, gemv_q8_0_kernel<NT, 2>, gemv_q8_0_kernel<NT, 4>); break;
-    case GLLM_TYPE_Q5_K: kern = fmt_kernel<fmt::Q5K, NT>(g); break;
-    case GLLM_TYPE_Q2_K: kern = fmt_kernel<fmt::Q2K, NT>(g); break;
-    case GLLM_TYPE_Q3_K: kern = fmt_kernel<fmt::Q3K, NT>(g); break;
-    case GLLM_TYPE_Q4_0: kern = fmt_kernel<fmt::Q401<false>, NT>(g); break;
-    case GLLM_TYPE_Q4_1: kern = fmt_kernel<fmt::Q401<true>, NT>(g); break;
-    default: kern = fmt_kernel<fmt::MXFP4, NT>(g); break;
+    void (*kern)(GemvJob) = row_kernel<NT, false>(type, g);
+    if constexpr (NT == 1) {
+        if (j.xf) kern = row_kernel<1, true>(type, g);
     }
     hipLaunchKernelGGL(kern, dim3(wg), dim3(256), 0, s, j);
     GLLM_HIP(hipGetLastError());
@@ -1152,13 +1257,13 @@ int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* 
 
 // True when the batch-1 row kernels for these weights quantise x themselves.
 bool fused_quant(int n, gllm_hip_weight* const* ws) {
-    if (ws[0]->type != GLLM_TYPE_Q4_K) return false;
-    int total = 0;
-    for (int i = 0; i < n; i++) total += ws[i]->rows;
     // every workgroup quantises the whole of x: worth it for rows up to 4096
     // wide (one launch instead of two); wider rows pay more in-kernel work
     // than the separate launch costs
-    if (ws[0]->cols > 4096) return false;
+    if (ws[0]->cols > kFuseCols) return false;
+    if (ws[0]->type != GLLM_TYPE_Q4_K) return true;
+    int total = 0;
+    for (int i = 0; i < n; i++) total += ws[i]->rows;
     const Q4KShape sh = q4k_shape(total, ws[0]->blocks);
     return sh.threads >= 256 && q4k_has_nl(ws[0]->blocks / sh.g) &&
            q4k_stage_bytes(1, ws[0]->cols) <= kMaxStage;

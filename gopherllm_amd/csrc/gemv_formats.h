@@ -1,7 +1,7 @@
 // gemv_formats.h -- row kernels for Q5_K, Q4_0, Q4_1, MXFP4, Q2_K and Q3_K
 // against Q8K activations, bit-exact to kernels_amd64.s:550-1128 (included
 // by gemv.hip, which supplies GemvJob, locate, rot_prev, tree8_strided,
-// dot4z, q4k_lane_sum and MinSel).
+// dot4z, q4k_lane_sum, MinSel and the fused-quantisation helpers).
 //
 // Every format keeps the AVX2 lane structure of its reference kernel: lane k
 // of a row owns elements 32m + 4k .. 32m + 4k + 3 of every 32-element group
@@ -312,16 +312,23 @@ constexpr int fmt_depth() {
     return NT == 1 ? (F::kNX == 8 ? 3 : 4) : 2;
 }
 
-template <class F, int NT, int G>
+//
+// FUSE (batch 1, cols <= kFuseCols) quantises x into LDS inside the
+// workgroup, as gemv_q6k_kernel does.
+template <class F, int NT, int G, bool FUSE = false>
 __global__ __launch_bounds__(256) void gemv_fmt_kernel(GemvJob j) {
+    static_assert(!FUSE || NT == 1, "fused quantisation is batch 1 only");
     constexpr int D = fmt_depth<F, NT>();
+    __shared__ __attribute__((aligned(16))) uint8_t fa_raw[FUSE ? sizeof(FusedAct) : 16];
+    FusedAct& fa = *(FusedAct*)fa_raw;
     int wi;
     const int tid = threadIdx.x;
     const int gi = tid % G, k = (tid / G) & 7;
     const int r = locate(j, blockIdx.x, &wi) + tid / (8 * G);
-    if (r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    if (!FUSE && r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    const bool live = r < j.rows[wi];
     const int B = j.blocks, NB = B / G;
-    const uint8_t* row = j.w[wi] + (size_t)r * j.rb;
+    const uint8_t* row = j.w[wi] + (size_t)(live ? r : j.rows[wi] - 1) * j.rb;
     float accF[NT], accM[NT], accS[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) accF[t] = accM[t] = accS[t] = 0.0f;
@@ -331,18 +338,27 @@ __global__ __launch_bounds__(256) void gemv_fmt_kernel(GemvJob j) {
     };
     const size_t tok0 = (size_t)j.tok0;
     auto act_of = [&](size_t tok, int b, fmt::Act& a) __attribute__((always_inline)) {
-        const int8_t* q8 = j.act.q8perm + tok * j.cols + (size_t)b * 256 + k * 32;
-        a.qa = *(const int4*)q8;
-        a.qb = *(const int4*)(q8 + 16);
-        a.xs = j.act.xscale[tok * B + b];
-        fmt::load_sums<F>(a, k, j.act.xs32 + tok * (j.cols / 32) + (size_t)b * 8,
-                          j.act.xs16 + tok * (j.cols / 16) + (size_t)b * 16);
+        if constexpr (FUSE) {
+            a.qa = *(const int4*)(fa.q8 + b * 256 + k * 32);
+            a.qb = *(const int4*)(fa.q8 + b * 256 + k * 32 + 16);
+            a.xs = fa.xsc[b];
+            fmt::load_sums<F>(a, k, fa.xs32 + b * 8, fa.xs16 + b * 16);
+        } else {
+            const int8_t* q8 = j.act.q8perm + tok * j.cols + (size_t)b * 256 + k * 32;
+            a.qa = *(const int4*)q8;
+            a.qb = *(const int4*)(q8 + 16);
+            a.xs = j.act.xscale[tok * B + b];
+            fmt::load_sums<F>(a, k, j.act.xs32 + tok * (j.cols / 32) + (size_t)b * 8,
+                              j.act.xs16 + tok * (j.cols / 16) + (size_t)b * 16);
+        }
     };
     Slot ring[D];
+    auto load_w = [&](int i, Slot& o) __attribute__((always_inline)) {
+        F::load(row + (size_t)(min(i, NB - 1) * G + gi) * F::kBytes, k, o.w);
+    };
     auto load = [&](int i, Slot& o) __attribute__((always_inline)) {
-        const int b = min(i, NB - 1) * G + gi;
-        F::load(row + (size_t)b * F::kBytes, k, o.w);
-        if constexpr (NT == 1) act_of(tok0, b, o.a);
+        load_w(i, o);
+        if constexpr (NT == 1) act_of(tok0, min(i, NB - 1) * G + gi, o.a);
     };
     auto compute = [&](int i, const Slot& o) __attribute__((always_inline)) {
         if constexpr (NT == 1) {
@@ -359,10 +375,24 @@ __global__ __launch_bounds__(256) void gemv_fmt_kernel(GemvJob j) {
             }
         }
     };
+    XRegs<kFuseQB> xr;
+    if constexpr (FUSE) {
+        xq_load<kFuseQB>(j.xf, B, xr);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int i = 0; i < D; i++) {
-        load(i, ring[i]);
+        if constexpr (FUSE) {
+            load_w(i, ring[i]);
+        } else {
+            load(i, ring[i]);
+        }
         __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (FUSE) {
+        fused_act_store<F::kSums == fmt::kX16>(xr, B, fa);
+#pragma unroll
+        for (int i = 0; i < D; i++) act_of(tok0, min(i, NB - 1) * G + gi, ring[i].a);
     }
     int i0 = 0;
     for (; i0 + D <= NB; i0 += D) {
@@ -381,7 +411,7 @@ __global__ __launch_bounds__(256) void gemv_fmt_kernel(GemvJob j) {
     for (int t = 0; t < NT; t++) {
         float v = tree8_strided<G>(F::kHasM ? accF[t] - accM[t] : accF[t]);  // VSUBPS + tree
         if constexpr (F::kHasS) v = v + accS[t];                               // VADDSS
-        if (k == 0 && gi == G - 1 && t < j.ntok)
+        if (live && k == 0 && gi == G - 1 && t < j.ntok)
             j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
     }
 }

@@ -2,11 +2,13 @@
 for bit against the amd64-order oracle (kernels_amd64.s:550-1128) through the
 C ABI, at batch 1 and in batches, with 1, 2 and 4 lanes per AVX2 lane (the
 shapes choose them), ragged row counts, the all-0xff extremes and the
-upload repack's inverse."""
+upload repack's inverse; and, for these formats, Q6_K and Q8_0, the batch-1
+kernels that quantise x themselves against the same kernels fed by the
+separate quantiser launch."""
 import numpy as np
 import pytest
 
-from conftest import BLOCK, NAMES, extreme_row, normal, random_rows
+from conftest import BLOCK, NAMES, extreme_row, normal, quant_matrix, random_rows
 from oracle import oracle as ref
 
 pytestmark = pytest.mark.gpu
@@ -87,3 +89,32 @@ def test_fused_matvec_of_other_types_rejected(hip):
     a = hip.Weight.from_host(data, ref.Q5_K, 64, 256)
     with pytest.raises(hip.GllmError):
         hip.matvec2_into(a, a, normal(2, 256))
+
+
+@pytest.mark.parametrize("qtype", [ref.Q6_K, ref.Q8_0] + FORMATS,
+                         ids=["q6k", "q8_0"] + [NAMES[q] for q in FORMATS])
+@pytest.mark.parametrize("rows,cols", [(37, 512), (1000, 4096), (4100, 4096)])
+def test_fused_quantisation_matches_prequantised(hip, qtype, rows, cols):
+    """At batch 1 with cols <= 4096 the row kernels quantise x in LDS
+    themselves; the same kernels fed by the separate Q8K-prep launch
+    (gllm_hip_q8k_prepare_dev + gllm_hip_matvec_q8_dev) and the oracle agree
+    bit for bit, ragged last workgroup included."""
+    import torch
+    if qtype in BLOCK:
+        data = random_rows(qtype, rows, cols, 3 * rows + qtype)
+    else:
+        data, _ = quant_matrix(qtype, rows, cols, 5 * rows + qtype)
+    x = normal(rows + 17, cols)
+    x[100:140] = 0.0
+    w = hip.Weight.from_host(data, qtype, rows, cols)
+    print(f"fused vs prequantised type {qtype} {rows}x{cols}", flush=True)
+    fused = w.matvec_into(x)
+    xd = torch.from_numpy(x).cuda()
+    act = torch.empty(hip.act_bytes(cols, 1), dtype=torch.uint8, device="cuda")
+    hip.q8k_prepare_dev(xd, act)
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    w.matvec_q8_dev(act, 1, out)
+    torch.cuda.synchronize()
+    want = ref.matvec(qtype, data, x, rows, cols)
+    assert_bits(fused, want, "fused")
+    assert_bits(out.cpu().numpy(), want, "prequantised")
