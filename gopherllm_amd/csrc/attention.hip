@@ -194,6 +194,17 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
     const float* qg = q + ((size_t)tok * n_heads + (size_t)g * kvmul) * kFusedHD;
     const int tcur = span - 1;  // the new position (rope mode: one token)
     const bool has_cur = rope.sin_tab && tcur / kScoreChunk == chunk;
+    // this thread's K row first, so its latency overlaps the query staging
+    // (clamped to span_max - 1, inside the cache; rows past the span are
+    // loaded and dropped; the new position's row comes from kcur below)
+    const int h = tid / kScoreChunk, t = chunk * kScoreChunk + tid % kScoreChunk;
+    uint4 kr[kFusedHD / 8];
+    {
+        const uint4* krow = (const uint4*)(K + (size_t)(start + min(t, span_max - 1)) * kv_dim +
+                                           (size_t)g * kFusedHD);
+#pragma unroll
+        for (int c = 0; c < kFusedHD / 8; c++) kr[c] = krow[c];
+    }
     if (rope.sin_tab) {
         const int pos = start + tcur, pairs = kFusedHD / 2;
         for (int i = tid; i < kvmul * pairs; i += 256) {
@@ -227,16 +238,10 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
         for (int i = tid; i < kvmul * kFusedHD; i += 256) qs[i] = qg[i];
     }
     __syncthreads();
-    const int h = tid / kScoreChunk, t = chunk * kScoreChunk + tid % kScoreChunk;
     if (h >= kvmul || t >= span) return;
-    uint4 kr[kFusedHD / 8];
     if (has_cur && t == tcur) {
 #pragma unroll
         for (int c = 0; c < kFusedHD / 8; c++) kr[c] = *(const uint4*)&kcur[8 * c];
-    } else {
-        const uint4* krow = (const uint4*)(K + (size_t)(start + t) * kv_dim + (size_t)g * kFusedHD);
-#pragma unroll
-        for (int c = 0; c < kFusedHD / 8; c++) kr[c] = krow[c];
     }
     const float* qh = qs + h * kFusedHD;
     float acc[8];
@@ -258,36 +263,50 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
         ((a0 + a1) + (a2 + a3)) * scale;
 }
 
-// (four waves per SIMD are plenty for one workgroup per head: the 128-VGPR
-// budget keeps the V prefetch registers out of scratch)
+// DS workgroups share one (query head, token): workgroup slice c runs the
+// value chains of elements c*DW .. c*DW+DW-1 (DW = 128 / DS) and stages only
+// that slice of each V row, so a decode token spreads its V stream over
+// n_heads * DS compute units.  Every slice recomputes the same max, weights
+// and sequential denominator, so each chain sees the same operands in the
+// same position order whatever DS is.
+// (four waves per SIMD are plenty: the 128-VGPR budget keeps the V prefetch
+// registers out of scratch)
+template <int DS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void attn_softmax_values_kernel(
     const float* __restrict__ scores, const uint16_t* __restrict__ V, int kv_dim, int kvmul,
     int start, int span0, int span_max, float* __restrict__ out, const int* __restrict__ d_end) {
+    static_assert(DS == 1 || DS == 2 || DS == 4, "slices of 128, 64 or 32 elements");
+    constexpr int DW = kFusedHD / DS;   // elements per workgroup
+    constexpr int U = 4 / DS;           // 16-byte pieces per thread per tile row
+    constexpr int P = DS == 1 ? kVPrefetch : 8;  // tiles in flight (P * U <= 16 registers of 16 bytes)
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    const int h = blockIdx.x, tok = blockIdx.y, n_heads = gridDim.x;
+    const int h = blockIdx.x / DS, slice = blockIdx.x % DS, tok = blockIdx.y;
+    const int n_heads = gridDim.x / DS;
     const int tid = threadIdx.x;
-    if (d_end) span0 = *d_end - start + 1;
-    const int span = span0 + tok;
     const int g = h / kvmul;
     const int wlen = (span_max + 3) & ~3;             // keeps the V tiles 16-byte aligned
     float* w = lds;                                   // [wlen]
     float* red = w + wlen;                            // [8]
-    uint16_t* vt = (uint16_t*)(red + 8);              // [2][kVTile][128] f16
-    // V prefetch first: thread (position lp, quarter lc) owns 64 bytes of a
-    // tile row, kVPrefetch tiles ahead
-    const uint16_t* Vg = V + (size_t)start * kv_dim + (size_t)g * kFusedHD;
+    uint16_t* vt = (uint16_t*)(red + 8);              // [2][kVTile][DW] f16
+    // V prefetch first: thread (position lp, piece lc) owns U * 16 bytes of
+    // the slice of a tile row, P tiles ahead.  Loads are unconditional and
+    // clamped to span_max - 1 (rows start .. start + span_max - 1 lie inside
+    // the cache), so they neither wait for the device-side position nor sit
+    // under a branch (which would make the compiler's vmcnt waits drain the
+    // prefetch); rows past the span are never read from LDS.
+    const uint16_t* Vg = V + (size_t)start * kv_dim + (size_t)g * kFusedHD + slice * DW;
     const int lp = tid >> 2, lc = tid & 3;
-    const int ntiles = (span + kVTile - 1) / kVTile;
-    u32x4 pre0[4], pre1[4], pre2[4], pre3[4];
-    auto first = [&](int i, u32x4 (&pr)[4]) __attribute__((always_inline)) {
-        const u32x4* src = (const u32x4*)(Vg + (size_t)min(i * kVTile + lp, span - 1) * kv_dim + 32 * lc);
+    u32x4 pre[P][U];
+    auto fetch = [&](int i, u32x4 (&pr)[U]) __attribute__((always_inline)) {
+        const u32x4* src = (const u32x4*)(Vg + (size_t)min(i * kVTile + lp, span_max - 1) * kv_dim + 8 * U * lc);
 #pragma unroll
-        for (int u = 0; u < 4; u++) pr[u] = src[u];
+        for (int u = 0; u < U; u++) pr[u] = src[u];
     };
-    first(0, pre0);
-    first(1, pre1);
-    first(2, pre2);
-    first(3, pre3);
+#pragma unroll
+    for (int q = 0; q < P; q++) fetch(q, pre[q]);
+    if (d_end) span0 = *d_end - start + 1;
+    const int span = span0 + tok;
+    const int ntiles = (span + kVTile - 1) / kVTile;
     const float* srow = scores + ((size_t)tok * n_heads + h) * span_max;
     float m = -__int_as_float(0x7f800000);
     for (int t = tid; t < span; t += 256) {
@@ -302,27 +321,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     for (int t = tid; t < span; t += 256) w[t] = fast_exp(w[t] - mx);
     // (the first tile barrier orders the exp writes before their readers)
-    // values: threads 0..127 own one element each; thread 128 (a wave that
-    // only stages V) sums the denominator tile by tile, in position order
+    // values: threads 0..DW-1 own one element each; the first thread of the
+    // next wave (a wave that otherwise only stages V) sums the denominator
+    // tile by tile, in position order
+    constexpr int kSummer = (DW + 63) / 64 * 64;
     const int d = tid;
-    const bool chain = tid < kFusedHD;
-    const bool summer = tid == kFusedHD;
+    const bool chain = tid < DW;
+    const bool summer = tid == kSummer;
     float acc = 0.0f, denom = 0.0f;
-    // one V tile: stage it from registers, refill those registers kVPrefetch
-    // tiles ahead, then run the chains over it
-    auto tile = [&](int it, u32x4 (&pr)[4]) __attribute__((always_inline)) {
-        uint16_t* buf = vt + (size_t)(it & 1) * kVTile * kFusedHD;
-        u32x4* dst = (u32x4*)(buf + lp * kFusedHD + 32 * lc);
+    // one V tile: stage it from registers, refill those registers P tiles
+    // ahead, then run the chains over it
+    auto tile = [&](int it, u32x4 (&pr)[U]) __attribute__((always_inline)) {
+        uint16_t* buf = vt + (size_t)(it & 1) * kVTile * DW;
+        u32x4* dst = (u32x4*)(buf + lp * DW + 8 * U * lc);
 #pragma unroll
-        for (int u = 0; u < 4; u++) dst[u] = pr[u];
-        {
-            // unconditional (clamped to the last position past the end): a
-            // load under a branch makes the compiler's vmcnt waits drain the
-            // whole prefetch
-            const u32x4* src = (const u32x4*)(Vg + (size_t)min((it + kVPrefetch) * kVTile + lp, span - 1) * kv_dim + 32 * lc);
-#pragma unroll
-            for (int u = 0; u < 4; u++) pr[u] = src[u];
-        }
+        for (int u = 0; u < U; u++) dst[u] = pr[u];
+        fetch(it + P, pr);
         wait_lgkm0();
         lds_barrier();
         const int base = it * kVTile;
@@ -336,7 +350,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 #pragma unroll
                 for (int u = 0; u < kVTile / 4; u++) wq[u] = *(const float4*)&w[base + 4 * u];
 #pragma unroll
-                for (int u = 0; u < kVTile; u++) vb[u] = buf[u * kFusedHD + d];
+                for (int u = 0; u < kVTile; u++) vb[u] = buf[u * DW + d];
 #pragma unroll
                 for (int u = 0; u < kVTile / 4; u++) {
                     acc = fmaf(wq[u].x, f16_bits_to_f32(vb[4 * u]), acc);
@@ -346,7 +360,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
                 }
             } else {
                 for (int p = 0; p < n; p++)
-                    acc = fmaf(w[base + p], f16_bits_to_f32(buf[p * kFusedHD + d]), acc);
+                    acc = fmaf(w[base + p], f16_bits_to_f32(buf[p * DW + d]), acc);
             }
         } else if (summer) {
             int p = 0;
@@ -360,20 +374,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
             for (; p < n; p++) denom = denom + w[base + p];
         }
     };
-    static_assert(kVPrefetch == 4, "tile calls below name each prefetch slot");
-    for (int it0 = 0; it0 < ntiles; it0 += kVPrefetch) {
-        tile(it0, pre0);  // it0 < ntiles
-        if (it0 + 1 < ntiles) tile(it0 + 1, pre1);
-        if (it0 + 2 < ntiles) tile(it0 + 2, pre2);
-        if (it0 + 3 < ntiles) tile(it0 + 3, pre3);
+    for (int it0 = 0; it0 < ntiles; it0 += P) {
+#pragma unroll
+        for (int q = 0; q < P; q++)
+            if (it0 + q < ntiles) tile(it0 + q, pre[q]);  // uniform
     }
     if (summer) red[4] = denom > 0.0f ? 1.0f / denom : 1.0f;
     __syncthreads();
-    if (chain) out[((size_t)tok * n_heads + h) * kFusedHD + d] = acc * red[4];
+    if (chain) out[((size_t)tok * n_heads + h) * kFusedHD + slice * DW + d] = acc * red[4];
 }
 
+template <int DS>
 static size_t smax_lds_bytes(int span_max) {
-    return ((size_t)((span_max + 3) & ~3) + 8) * 4 + 2 * (size_t)kVTile * kFusedHD * 2;
+    return ((size_t)((span_max + 3) & ~3) + 8) * 4 + 2 * (size_t)kVTile * (kFusedHD / DS) * 2;
 }
 
 // --- split-K path ------------------------------------------------------------
@@ -776,6 +789,10 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
     const int span0 = end0 - start + 1;
     const int span_max = d_end ? span_cap : span0 + p - 1;
     const int kvmul = n_heads / n_kv;
+    // the kernels load rows up to start + span_max - 1 before they know the span
+    if (start < 0 || span_max < 1 || start + span_max > kv->max_len)
+        return fail(GLLM_EINVAL, "attend: rows %d..%d outside the cache (%d)", start,
+                    start + span_max - 1, kv->max_len);
     if (d_end && (p != 1 || !attend_exact_graphable(kv, n_heads, n_kv, hd, span_cap)))
         return fail(GLLM_EUNSUP, "attend: device-side positions need the head_dim 128 path");
     if (rope_sin && (!d_end || !d_knew || !d_vnew))
@@ -790,9 +807,17 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
                            kv->k[l], kv->kv_dim_k, n_kv, kvmul, start, span0, span_max, scale, sc,
                            d_end, rope);
         GLLM_HIP(hipGetLastError());
-        hipLaunchKernelGGL(attn_softmax_values_kernel, dim3(n_heads, p), dim3(256),
-                           smax_lds_bytes(span_max), s, sc, kv->v[l], kv->kv_dim_v, kvmul, start,
-                           span0, span_max, d_out, d_end);
+        // one token: four workgroups per head (a quarter of each V row apiece);
+        // prefill tokens already give n_heads * p workgroups
+        if (p == 1) {
+            hipLaunchKernelGGL(attn_softmax_values_kernel<4>, dim3(n_heads * 4, p), dim3(256),
+                               smax_lds_bytes<4>(span_max), s, sc, kv->v[l], kv->kv_dim_v, kvmul,
+                               start, span0, span_max, d_out, d_end);
+        } else {
+            hipLaunchKernelGGL(attn_softmax_values_kernel<1>, dim3(n_heads, p), dim3(256),
+                               smax_lds_bytes<1>(span_max), s, sc, kv->v[l], kv->kv_dim_v, kvmul,
+                               start, span0, span_max, d_out, d_end);
+        }
         GLLM_HIP(hipGetLastError());
         return GLLM_OK;
     }
