@@ -368,8 +368,16 @@ static int check_ready(const gllm_hip_model* m) {
     if (!m) return fail(GLLM_EINVAL, "null model");
     if (!m->tok_embd || !m->output) return fail(GLLM_EINVAL, "model: embedding/output not set");
     if (m->tok_embd->type != GLLM_TYPE_Q4_K) return fail(GLLM_EUNSUP, "model: embedding must be Q4_K");
-    for (size_t i = 0; i < m->w.size(); i++)
+    for (size_t i = 0; i < m->w.size(); i++) {
         if (!m->w[i]) return fail(GLLM_EINVAL, "model: layer %zu slot %zu not set", i / 7, i % 7);
+        // the layer's fused projections (Q/K/V, gate/up) are int8 row dots in
+        // the reference only for these two formats (tryMatvecAttentionInto,
+        // model.go:3156-3190); other formats go through its float kernels
+        const int t = m->w[i]->type;
+        if (t != GLLM_TYPE_Q4_K && t != GLLM_TYPE_Q6_K)
+            return fail(GLLM_EUNSUP, "model: layer %zu slot %zu has type %d (layers must be "
+                                     "Q4_K or Q6_K)", i / 7, i % 7, t);
+    }
     return GLLM_OK;
 }
 

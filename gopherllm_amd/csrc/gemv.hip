@@ -1269,20 +1269,38 @@ bool fused_quant(int n, gllm_hip_weight* const* ws) {
            q4k_stage_bytes(1, ws[0]->cols) <= kMaxStage;
 }
 
-// W.x for p rows of f32 activations: one fused launch at batch 1 when the
-// shape has one, else q8kQuantize + xsums into `act` (act_bytes(cols, p)
-// bytes of device scratch) followed by the row kernels.
+// W.x for p rows of f32 activations and n weights of one cols: each run of
+// consecutive weights of one type is one row-kernel launch (the run's
+// kernel quantises x itself at batch 1 when its shape allows), and every run
+// that reads pre-quantised activations shares one q8kQuantize + xsums into
+// `act` (act_bytes(cols, p) bytes of device scratch).  Runs of different
+// types are what the reference's mixed groups compute: one int8 row dot per
+// projection (tryMatvecAttentionInto, model.go:3156-3190;
+// matvecBatchQ8Fused, kernels_portable_tunables.go:304-408).
 int gemv_f32(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float* const* outs,
              const int* strides, void* act_buf, hipStream_t s) {
     const int cols = ws[0]->cols;
-    if (p == 1 && fused_quant(n, ws)) {
-        ActQ8 none{};
-        return run_gemv(n, ws, none, 1, outs, strides, s, d_xs);
+    ActQ8 act{};
+    bool quantised = false;
+    for (int i = 0; i < n;) {
+        int e = i + 1;
+        while (e < n && ws[e]->type == ws[i]->type) e++;
+        const int m = e - i;
+        const int* st = strides ? strides + i : nullptr;
+        if (p == 1 && fused_quant(m, ws + i)) {
+            ActQ8 none{};
+            GLLM_TRY(run_gemv(m, ws + i, none, 1, outs + i, st, s, d_xs));
+        } else {
+            if (!quantised) {
+                act_carve(act_buf, cols, p, &act);
+                GLLM_TRY(launch_q8k_prep(d_xs, cols, p, act, s));
+                quantised = true;
+            }
+            GLLM_TRY(run_gemv(m, ws + i, act, p, outs + i, st, s, nullptr));
+        }
+        i = e;
     }
-    ActQ8 act;
-    act_carve(act_buf, cols, p, &act);
-    GLLM_TRY(launch_q8k_prep(d_xs, cols, p, act, s));
-    return run_gemv(n, ws, act, p, outs, strides, s, nullptr);
+    return GLLM_OK;
 }
 
 // W.siluMulF32(gate, up) for p rows (the FFN down projection): the SwiGLU is
@@ -1310,13 +1328,21 @@ int matvec_multi(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, fl
                  const int* strides, hipStream_t s, int scratch_slot) {
     for (int i = 0; i < n; i++) GLLM_TRY(validate_weight(ws[i]));
     for (int i = 1; i < n; i++)
-        if (ws[i]->cols != ws[0]->cols || ws[i]->type != ws[0]->type)
-            return fail(GLLM_EINVAL, "fused matvec needs one type and one cols (%d/%d vs %d/%d)",
-                        ws[i]->type, ws[i]->cols, ws[0]->type, ws[0]->cols);
-    if (n > 1 && ws[0]->type != GLLM_TYPE_Q4_K && ws[0]->type != GLLM_TYPE_Q6_K)
-        return fail(GLLM_EUNSUP, "fused matvec of type %d: the reference uses its float kernel "
-                                 "here (matvecSameType2/3Into, model.go:3213-3254)", ws[0]->type);
+        if (ws[i]->cols != ws[0]->cols)
+            return fail(GLLM_EINVAL, "fused matvec needs one cols (%d vs %d)", ws[i]->cols,
+                        ws[0]->cols);
     if (p <= 0) return fail(GLLM_EINVAL, "p = %d", p);
+    // batch 1: groups of Q4_K / Q6_K, mixed or not, are int8 row dots in the
+    // reference (MatvecQ4K2/3IntoWithXSums, MatvecQ6K2/3Into,
+    // MatvecQ4K2Q6KIntoWithXSums); groups of the other formats go through its
+    // float kernels (matvecSameType2/3Into, model.go:3213-3254).  Batches
+    // share the int8 activations across any formats (matvecBatchQ8Fused).
+    if (n > 1 && p == 1)
+        for (int i = 0; i < n; i++)
+            if (ws[i]->type != GLLM_TYPE_Q4_K && ws[i]->type != GLLM_TYPE_Q6_K)
+                return fail(GLLM_EUNSUP, "fused batch-1 matvec of type %d: the reference uses "
+                                         "its float kernel here (matvecSameType2/3Into, "
+                                         "model.go:3213-3254)", ws[i]->type);
     for (int i = 0; i < n; i++)
         if (strides && strides[i] < ws[i]->rows) return fail(GLLM_EINVAL, "out stride < rows");
     void* sc = thread_scratch(scratch_slot, act_bytes(ws[0]->cols, p));

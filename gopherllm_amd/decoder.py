@@ -95,7 +95,8 @@ class LlamaDecoder:
     @classmethod
     def from_host_model(cls, model: dict, max_len: int) -> "LlamaDecoder":
         """model: {"config", "tok_embd", "output", "out_norm", "wq".."w3" lists,
-        "attn_norm"/"ffn_norm" lists} with GGUF-layout bytes."""
+        "attn_norm"/"ffn_norm" lists, optional "types" [n_layers][7] in wq wk
+        wv wo w1 w2 w3 order} with GGUF-layout bytes."""
         cfg = model["config"]
         d = cls(cfg, max_len)
         dim, hidden = cfg["dim"], cfg["hidden"]
@@ -108,10 +109,13 @@ class LlamaDecoder:
         d.set_weight(0, _lib.T_OUTPUT, Weight.from_host(model["output"], cfg["out_type"],
                                                         cfg["vocab"], dim))
         d.set_norm(0, _lib.T_OUT_NORM, model["out_norm"])
+        types = model.get("types")  # optional [n_layers][7], wq wk wv wo w1 w2 w3
+        order = ("wq", "wk", "wv", "wo", "w1", "w2", "w3")
         for l in range(cfg["n_layers"]):
             for k, slot in LAYER_SLOTS.items():
                 r, c = shapes[k]
-                d.set_weight(l, slot, Weight.from_host(model[k][l], lt, r, c))
+                t = types[l][order.index(k)] if types is not None else lt
+                d.set_weight(l, slot, Weight.from_host(model[k][l], t, r, c))
             d.set_norm(l, _lib.T_ATTN_NORM, model["attn_norm"][l])
             d.set_norm(l, _lib.T_FFN_NORM, model["ffn_norm"][l])
         return d

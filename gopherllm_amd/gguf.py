@@ -305,10 +305,13 @@ def write_llama_gguf(path, model: dict, alignment: int = 32, name: str = "synthe
     shapes = {"attn_q": ("wq", qd, dim), "attn_k": ("wk", kvd, dim), "attn_v": ("wv", kvd, dim),
               "attn_output": ("wo", dim, qd), "ffn_gate": ("w1", hidden, dim),
               "ffn_down": ("w2", dim, hidden), "ffn_up": ("w3", hidden, dim)}
+    types = model.get("types")  # optional [n_layers][7], wq wk wv wo w1 w2 w3 (mixed files)
+    order = ("wq", "wk", "wv", "wo", "w1", "w2", "w3")
     for l in range(nl):
         add(f"blk.{l}.attn_norm.weight", (dim,), F32, np.asarray(model["attn_norm"][l], np.float32))
         for tname, (key, rows, cols) in shapes.items():
-            add(f"blk.{l}.{tname}.weight", (cols, rows), cfg["layer_type"], model[key][l])
+            t = types[l][order.index(key)] if types is not None else cfg["layer_type"]
+            add(f"blk.{l}.{tname}.weight", (cols, rows), t, model[key][l])
         add(f"blk.{l}.ffn_norm.weight", (dim,), F32, np.asarray(model["ffn_norm"][l], np.float32))
     with open(path, "wb") as f:
         w = GGUFWriter(f, meta, planned, alignment)

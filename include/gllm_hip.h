@@ -130,8 +130,14 @@ int gllm_hip_argmax_penalized(gllm_hip_weight* w, const float* x, const uint32_t
  * d_outs: p rows of out_stride floats (out_stride >= rows). */
 int gllm_hip_matvec_dev(gllm_hip_weight* w, const float* d_xs, int p, float* d_outs,
                         int out_stride, void* stream);
-/* n weights (same cols, same type) against the same activations; one
- * quantisation of x is shared by all of them. */
+/* n weights (same cols) against the same activations; one quantisation of
+ * x is shared by all of them, runs of one type are one launch.  Batches
+ * (p > 1) take any mix of the int8 formats (matvecBatchQ8Fused2/3,
+ * kernels_portable_tunables.go:292-408); batch 1 with n > 1 takes Q4_K and
+ * Q6_K, mixed or not (Q4KMatvec3IntoWithXSums, MatvecQ6K2/3Into,
+ * MatvecQ4K2Q6KIntoWithXSums: model.go:3110-3190) and refuses the other
+ * formats, whose same-type groups the reference runs as floats
+ * (matvecSameType2/3Into, model.go:3213-3254). */
 int gllm_hip_matvec_multi_dev(int n, gllm_hip_weight* const* ws, const float* d_xs, int p,
                               float* const* d_outs, const int* out_strides, void* stream);
 int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token, void* stream);

@@ -1556,8 +1556,15 @@ static void llama_matvec(ref_llama_state* s, int type, const uint8_t* w, const f
     ref_matvec(type, w, x, rows, cols, out, REF_ORDER_AMD64, s->threads);
 }
 
+/* type of matrix `slot` (0..6: wq wk wv wo w1 w2 w3) of layer l */
+static int llama_type(const ref_llama* m, int l, int slot) {
+    return m->types ? m->types[l * 7 + slot] : m->layer_type;
+}
+
 /* ForwardBodyInto (model.go:2622-2820) for the plain llama graph; leaves the
- * output-normed hidden state in s->xn. */
+ * output-normed hidden state in s->xn.  Every projection is its own int8
+ * matvec, which is also what the reference's mixed Q4_K / Q6_K groups compute
+ * (tryMatvecAttentionInto, model.go:3156-3190). */
 static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
     const ref_llama* m = &s->m;
     int dim = m->dim, hd = m->head_dim, kvd = m->n_kv_heads * hd;
@@ -1568,9 +1575,9 @@ static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
     float scale = (float)(1.0 / sqrt((double)hd));
     for (int l = 0; l < m->n_layers; l++) {
         ref_rmsnorm(s->x, m->attn_norm[l], m->rms_eps, dim, s->xn);
-        llama_matvec(s, m->layer_type, m->wq[l], s->xn, m->n_heads * hd, dim, s->q);
-        llama_matvec(s, m->layer_type, m->wk[l], s->xn, kvd, dim, s->k);
-        llama_matvec(s, m->layer_type, m->wv[l], s->xn, kvd, dim, s->v);
+        llama_matvec(s, llama_type(m, l, 0), m->wq[l], s->xn, m->n_heads * hd, dim, s->q);
+        llama_matvec(s, llama_type(m, l, 1), m->wk[l], s->xn, kvd, dim, s->k);
+        llama_matvec(s, llama_type(m, l, 2), m->wv[l], s->xn, kvd, dim, s->v);
         ref_rope_apply(s->q, hd, m->n_heads, hd / 2, s->sinv, s->cosv);
         ref_rope_apply(s->k, hd, m->n_kv_heads, hd / 2, s->sinv, s->cosv);
         ref_f32_to_f16_row(s->k, s->kc[l] + (long)pos * kvd, kvd);
@@ -1581,13 +1588,13 @@ static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
             ref_attend_group_f16(s->q + (long)g * kvmul * hd, s->kc[l] + (long)g * hd,
                                  s->vc[l] + (long)g * hd, kvmul, kvd, kvd, hd, hd, 0, pos, scale,
                                  s->attn + (long)g * kvmul * hd);
-        llama_matvec(s, m->layer_type, m->wo[l], s->attn, dim, m->n_heads * hd, s->proj);
+        llama_matvec(s, llama_type(m, l, 3), m->wo[l], s->attn, dim, m->n_heads * hd, s->proj);
         for (int i = 0; i < dim; i++) s->x[i] = fmaf(s->proj[i], 1.0f, s->x[i]);
         ref_rmsnorm(s->x, m->ffn_norm[l], m->rms_eps, dim, s->xn);
-        llama_matvec(s, m->layer_type, m->w1[l], s->xn, m->hidden, dim, s->gate);
-        llama_matvec(s, m->layer_type, m->w3[l], s->xn, m->hidden, dim, s->up);
+        llama_matvec(s, llama_type(m, l, 4), m->w1[l], s->xn, m->hidden, dim, s->gate);
+        llama_matvec(s, llama_type(m, l, 6), m->w3[l], s->xn, m->hidden, dim, s->up);
         ref_silu_mul(s->gate, s->up, s->hidden, m->hidden);
-        llama_matvec(s, m->layer_type, m->w2[l], s->hidden, dim, m->hidden, s->proj);
+        llama_matvec(s, llama_type(m, l, 5), m->w2[l], s->hidden, dim, m->hidden, s->proj);
         for (int i = 0; i < dim; i++) s->x[i] = fmaf(s->proj[i], 1.0f, s->x[i]);
     }
     ref_rmsnorm(s->x, m->out_norm, m->rms_eps, dim, s->xn);

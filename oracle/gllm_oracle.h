@@ -120,6 +120,9 @@ typedef struct ref_llama {
     const uint8_t** wq; const uint8_t** wk; const uint8_t** wv; const uint8_t** wo;
     const uint8_t** w1; const uint8_t** w2; const uint8_t** w3;
     const float** attn_norm; const float** ffn_norm;
+    /* NULL, or the type of each matrix, n_layers * 7 in the order wq wk wv wo
+     * w1 w2 w3 (mixed files such as Q4_K_M, whose attn_v / ffn_down are Q6_K) */
+    const int* types;
 } ref_llama;
 
 typedef struct ref_llama_state ref_llama_state;

@@ -333,7 +333,7 @@ class _RefLlama(C.Structure):
         ("tok_embd", C.c_void_p), ("output", C.c_void_p), ("out_norm", C.c_void_p),
         ("layer_type", C.c_int),
     ] + [(n, C.c_void_p) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3",
-                                    "attn_norm", "ffn_norm")]
+                                    "attn_norm", "ffn_norm", "types")]
 
 
 class Llama:
@@ -366,6 +366,10 @@ class Llama:
             setattr(s, k, a.ctypes.data)
         for k in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "attn_norm", "ffn_norm"):
             setattr(s, k, ptr_array(model[k]))
+        if "types" in model:  # per-matrix types, [n_layers][7] (wq wk wv wo w1 w2 w3)
+            t = np.ascontiguousarray(np.asarray(model["types"], np.int32).reshape(n * 7))
+            self._keep.append(t)
+            s.types = t.ctypes.data
         self._s = s
         self.cfg = cfg
         self.state = L.ref_llama_state_new(C.byref(s), threads)

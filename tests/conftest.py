@@ -34,10 +34,15 @@ def quant_matrix(qtype, rows, cols, seed, std=0.02):
     return ref.quantize_rows(qtype, w), w
 
 
+MATRICES = ("wq", "wk", "wv", "wo", "w1", "w2", "w3")
+
+
 def tiny_llama(seed=1, n_layers=2, dim=512, hidden=1024, n_heads=8, n_kv_heads=2, head_dim=64,
-               vocab=1000, layer_type=ref.Q4_K, out_type=ref.Q6_K):
+               vocab=1000, layer_type=ref.Q4_K, out_type=ref.Q6_K, type_of=None):
     """A small llama-shaped model with the reference's tensor roles
-    (model.go:2027 loadLayer) and RMSNorm weights of 1.0."""
+    (model.go:2027 loadLayer) and RMSNorm weights of 1.0.  type_of(layer,
+    name), if given, picks each matrix's type (mixed files such as Q4_K_M)
+    and the model then carries "types" [n_layers][7] in MATRICES order."""
     cfg = dict(n_layers=n_layers, dim=dim, hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv_heads,
                head_dim=head_dim, vocab=vocab, rms_eps=1e-5, rope_theta=500000.0,
                emb_type=ref.Q4_K, out_type=out_type, layer_type=layer_type)
@@ -49,12 +54,21 @@ def tiny_llama(seed=1, n_layers=2, dim=512, hidden=1024, n_heads=8, n_kv_heads=2
     m["out_norm"] = np.ones(dim, np.float32)
     shapes = {"wq": (qd, dim), "wk": (kvd, dim), "wv": (kvd, dim), "wo": (dim, qd),
               "w1": (hidden, dim), "w2": (dim, hidden), "w3": (hidden, dim)}
+    tof = type_of or (lambda l, k: layer_type)
     for k, (r, c) in shapes.items():
-        m[k] = [quant_matrix(layer_type, r, c, s + 10 + 10 * l + list(shapes).index(k))[0]
+        m[k] = [quant_matrix(tof(l, k), r, c, s + 10 + 10 * l + list(shapes).index(k))[0]
                 for l in range(n_layers)]
+    if type_of is not None:
+        m["types"] = [[int(tof(l, k)) for k in MATRICES] for l in range(n_layers)]
     m["attn_norm"] = [np.ones(dim, np.float32) for _ in range(n_layers)]
     m["ffn_norm"] = [np.ones(dim, np.float32) for _ in range(n_layers)]
     return m
+
+
+def q4km_types(l, name):
+    """Q4_K_M-style mix for tiny_llama(type_of=...): attn_v and ffn_down in
+    Q6_K on every other layer, the rest Q4_K."""
+    return ref.Q6_K if name in ("wv", "w2") and l % 2 == 0 else ref.Q4_K
 
 
 @pytest.fixture(scope="session")

@@ -7,7 +7,7 @@ generic (portable Go) order.
 import numpy as np
 import pytest
 
-from conftest import normal, quant_matrix
+from conftest import BLOCK, normal, quant_matrix, random_rows
 from oracle import oracle as ref
 
 pytestmark = pytest.mark.gpu
@@ -263,3 +263,38 @@ def test_invalid_shapes_rejected(hip):
         hip.Weight.from_host(d[:100], ref.Q4_K, 4, 256)  # too few bytes
     with pytest.raises(hip.GllmError):
         hip.Weight.from_host(d, 6, 4, 256)               # Q5_0: no int8 row dot in the reference
+
+
+def test_mixed_type_groups_share_activations(hip):
+    """n weights of different types against the same activations: the
+    Q4_K / Q4_K / Q6_K attention group of Q4_K_M files at batch 1
+    (MatvecQ4K2Q6KIntoWithXSums) and in batches (matvecBatchQ8Fused, any
+    int8 format; p = 40 puts the Q4_K run on the matrix cores) equal the
+    oracle's per-weight matvecs bit for bit."""
+    import torch
+    cols = 1024
+    groups = [(ref.Q4_K, 512), (ref.Q4_K, 128), (ref.Q6_K, 128)]
+    others = [(ref.Q5_K, 96), (ref.Q8_0, 200), (ref.Q3_K, 64)]
+    for mix in (groups, others):
+        datas, ws = [], []
+        for i, (t, r) in enumerate(mix):
+            if t in BLOCK:
+                d = random_rows(t, r, cols, 40 + i)
+            else:
+                d, _ = quant_matrix(t, r, cols, 40 + i)
+            datas.append(d)
+            ws.append(hip.Weight.from_host(d, t, r, cols))
+        for p in ((1, 5, 40) if mix is groups else (3, 8)):
+            print(f"mixed group {[t for t, _ in mix]} p={p}", flush=True)
+            xs = normal(50 + p, (p, cols))
+            outs = [torch.empty((p, r), dtype=torch.float32, device="cuda") for _, r in mix]
+            hip.matvec_multi_dev(ws, torch.from_numpy(xs).cuda(), outs)
+            torch.cuda.synchronize()
+            for (t, r), d, o in zip(mix, datas, outs):
+                want = ref.matvec_batch(t, d, xs, r, cols)
+                assert np.array_equal(bits(o.cpu().numpy()), bits(want)), (t, p)
+    # batch 1 with a format whose fused group the reference runs as floats
+    with pytest.raises(hip.GllmError):
+        hip.matvec_multi_dev(ws, torch.from_numpy(normal(1, (1, cols))).cuda(),
+                             [torch.empty((1, r), dtype=torch.float32, device="cuda")
+                              for _, r in others])

@@ -5,7 +5,7 @@ oracle on the same tensors."""
 import numpy as np
 import pytest
 
-from conftest import normal, quant_matrix, tiny_llama
+from conftest import normal, q4km_types, quant_matrix, tiny_llama
 from oracle import oracle as ref
 
 pytestmark = pytest.mark.gpu
@@ -105,3 +105,25 @@ def test_truncated_weight_is_zero_padded(hip, tmp_path):
     want = ref.matvec(ref.Q4_K, zp, normal(39, cols), rows, cols)
     assert np.array_equal(bits(got), bits(want))
     assert np.all(got[-10:] == 0.0)
+
+
+def test_decoder_from_mixed_gguf_matches_oracle(hip, tmp_path):
+    """A Q4_K_M-style file (Q6_K attn_v / ffn_down on some layers): each
+    tensor is uploaded with its own type tag and the decoder's mixed
+    projection groups give the oracle's tokens."""
+    from gopherllm_amd import gguf
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = varied_norms(tiny_llama(seed=35, n_layers=2, dim=512, hidden=1024, n_heads=8, n_kv_heads=2,
+                                head_dim=64, vocab=900, type_of=q4km_types), 36)
+    path = gguf.write_llama_gguf(tmp_path / "mixed.gguf", m)
+    with gguf.GGUFFile(str(path)) as f:
+        types = {t.name: t.dtype for t in f.tensors()}
+    assert types["blk.0.attn_v.weight"] == ref.Q6_K and types["blk.0.ffn_down.weight"] == ref.Q6_K
+    assert types["blk.1.attn_v.weight"] == ref.Q4_K and types["blk.0.attn_q.weight"] == ref.Q4_K
+    prompt = np.random.default_rng(37).integers(0, 900, 24)
+    print("from_gguf mixed generate", flush=True)
+    dec = LlamaDecoder.from_gguf(str(path), 64)
+    got = dec.generate(prompt, 10)
+    want = ref.Llama(m, 64).generate(prompt, 10)
+    assert np.array_equal(got, want), (got, want)
+    dec.release()

@@ -4,7 +4,7 @@ ForwardBodyInto / ForwardBatchInto on the same weights."""
 import numpy as np
 import pytest
 
-from conftest import tiny_llama
+from conftest import q4km_types, tiny_llama
 from oracle import oracle as ref
 
 pytestmark = pytest.mark.gpu
@@ -122,3 +122,43 @@ def test_decode_8b_layer_shapes_bit_exact(hip):
         assert np.array_equal(bits(gpu.hidden()), bits(hid)), pos
         assert got == want, pos
         tok = want
+
+
+def test_mixed_q4k_q6k_layers_match_oracle(hip):
+    """A Q4_K_M-style model (Q6_K attn_v / ffn_down in some layers): every
+    projection is its own int8 row dot, as in the reference's mixed groups
+    (tryMatvecAttentionInto, model.go:3156-3190; matvecBatchQ8Fused for
+    prefill), so prefill logits, decode hidden states and greedy tokens are
+    bit-identical to the oracle's."""
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = tiny_llama(seed=12, n_layers=3, dim=512, hidden=1024, n_heads=8, n_kv_heads=2,
+                   head_dim=64, vocab=1200, type_of=q4km_types)
+    prompt = np.random.default_rng(13).integers(0, 1200, 40)
+    max_len = 96
+    gpu = LlamaDecoder.from_host_model(m, max_len)
+    cpu = ref.Llama(m, max_len)
+    print("mixed-type model: prefill", flush=True)
+    gt, gl = gpu.prefill(prompt, want_logits=True)
+    ct, cl = cpu.prefill(prompt)
+    assert np.array_equal(bits(gl), bits(cl))
+    assert gt == ct
+    tok = ct
+    for pos in range(len(prompt), len(prompt) + 8):
+        want, hid = cpu.decode(tok, pos)
+        got = gpu.decode(tok, pos)
+        assert np.array_equal(bits(gpu.hidden()), bits(hid)), pos
+        assert got == want, pos
+        tok = want
+
+
+def test_layers_of_float_kernel_formats_rejected(hip):
+    """The reference runs fused Q/K/V and gate/up groups of formats other
+    than Q4_K / Q6_K through float kernels (matvecSameType2/3Into), so the
+    resident decoder refuses such layers instead of returning other numbers."""
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = tiny_llama(seed=14, n_layers=1, dim=256, hidden=512, n_heads=4, n_kv_heads=1,
+                   head_dim=64, vocab=300,
+                   type_of=lambda l, k: ref.Q8_0 if k == "wk" else ref.Q4_K)
+    gpu = LlamaDecoder.from_host_model(m, 32)
+    with pytest.raises(hip.GllmError):
+        gpu.decode(1, 0)
