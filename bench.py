@@ -341,16 +341,18 @@ def suite(args):
             del ws
 
     # formats beyond Q4_K / Q6_K / Q8_0: random codes with valid f16 scales
-    # (the block layouts of gguf.go:241-297), gate/up shape
+    # (the block layouts of gguf.go:241-297), gate/up shape at batch 1 and 8,
+    # down shape at batch 1
     fmt_layout = {g.TYPE_Q5_K: ("Q5_K", 176, 256, [(0, 2), (2, 4)], None),
                   g.TYPE_Q4_0: ("Q4_0", 18, 32, [(0, 2)], None),
                   g.TYPE_Q4_1: ("Q4_1", 20, 32, [(0, 2), (2, 4)], None),
                   g.TYPE_MXFP4: ("MXFP4", 17, 32, [], 16),
                   g.TYPE_Q2_K: ("Q2_K", 84, 256, [(80, 82), (82, 84)], None),
                   g.TYPE_Q3_K: ("Q3_K", 110, 256, [(108, 110)], None)}
-    for qtype, (name, bb, be, halfs, ebyte) in fmt_layout.items() if "formats" in only else ():
+    fmt_cases = [(q, shape) for shape in ((14336, 4096), (4096, 14336)) for q in fmt_layout]
+    for qtype, (rows, cols) in fmt_cases if "formats" in only else ():
         import numpy as np
-        rows, cols = 14336, 4096
+        name, bb, be, halfs, ebyte = fmt_layout[qtype]
         rng = np.random.default_rng(qtype)
         nb = rows * cols // be
         blk = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
@@ -361,7 +363,7 @@ def suite(args):
         raw = blk.reshape(-1)
         wb = raw.size
         ws = [g.Weight.from_host(raw, qtype, rows, cols) for _ in range(max(2, math.ceil(300e6 / wb)))]
-        for p in (1, 8):
+        for p in ((1, 8) if cols == 4096 else (1,)):
             x = torch.empty((p, cols), dtype=torch.float32, device="cuda")
             g.fill_normal_dev(x, 7, 1.0)
             out = torch.empty((p, rows), dtype=torch.float32, device="cuda")

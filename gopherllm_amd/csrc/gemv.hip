@@ -1121,11 +1121,15 @@ int launch_q4k(GemvJob& j, const int* rows, int n, const Q4KShape& sh, hipStream
 // workgroups than the device has compute units: with every CU busy the G-step
 // rotation costs more than extra workgroups bring (Q6_K 14336x4096 measured
 // 16.7 / 21.2 / 29.5 us at G = 1 / 2 / 4), with half of them idle it is the
-// other way round (Q6_K 4096x14336: 44.9 / 27.8 / 24.8 us).  Batches (per-token
+// other way round (Q6_K 4096x14336: 44.9 / 27.8 / 24.8 us).  Q6_K, the
+// heaviest lane step, also splits while a lane would walk more than 16
+// blocks and the launch has fewer than two workgroups per CU (4096x14336 at
+// G = 4); the other formats measured faster at G = 2
+// there (Q5_K 16.4 / 18.7 us, Q8_0 25.5 / 26.4 us at G = 2 / 4).  Batches (per-token
 // activation reads make each block several times longer) take the largest G
 // that keeps the launch at two workgroups per compute unit or fewer.
 // GLLM_ROW_G overrides, for measurement; every G gives the same bits.
-static int row_lanes_g(int total_rows, int blocks, int ntok) {
+static int row_lanes_g(int total_rows, int blocks, int ntok, int type) {
     static const int forced = [] {
         const char* e = getenv("GLLM_ROW_G");
         const int v = e ? atoi(e) : 0;
@@ -1136,7 +1140,10 @@ static int row_lanes_g(int total_rows, int blocks, int ntok) {
     auto wgs = [&](int g) { return (total_rows * g + kRowsPerWG - 1) / kRowsPerWG; };
     int g = 1;
     if (ntok == 1) {
-        while (g < 4 && blocks % (2 * g) == 0 && wgs(g) < ncu) g *= 2;
+        const bool long_q6k = type == GLLM_TYPE_Q6_K;
+        while (g < 4 && blocks % (2 * g) == 0 &&
+               (wgs(g) < ncu || (long_q6k && blocks / g > 16 && wgs(g) < 2 * ncu)))
+            g *= 2;
     } else {
         while (g < 4 && blocks % (2 * g) == 0 && wgs(2 * g) <= 2 * ncu) g *= 2;
     }
@@ -1188,7 +1195,7 @@ int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t 
         return fail(GLLM_EINVAL, "gemv: fused quantisation needs batch 1 and cols <= %d", kFuseCols);
     int total = 0;
     for (int i = 0; i < j.n; i++) total += rows[i];
-    const int g = row_lanes_g(total, j.blocks, j.ntok);
+    const int g = row_lanes_g(total, j.blocks, j.ntok, type);
     j.rows_per_wg = kRowsPerWG / g;
     int wg = 0;
     for (int i = 0; i < j.n; i++) {
