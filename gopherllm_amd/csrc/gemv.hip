@@ -1047,11 +1047,11 @@ static void launch_q4k_nl(const GemvJob& j, dim3 grid, dim3 block, size_t stage,
 // Blocks per lane with a compiled row kernel (and its prefetch depth).
 static bool q4k_has_nl(int nl) { return nl == 4 || nl == 8 || nl == 14 || nl == 16 || nl == 28; }
 
-// Launch shape of the Q4_K row kernel: one workgroup per compute unit, so a
-// CU's activation staging is the first memory traffic it issues (a second
-// workgroup's small activation reads would queue behind the first one's
-// weight stream).  G lanes share an AVX2 lane when the rows alone give
-// fewer than four waves per workgroup.
+// Launch shape of the Q4_K row kernel: one workgroup per compute unit up to
+// the row cap below, so a CU's activation staging is the first memory
+// traffic it issues (a second workgroup's small activation reads would queue
+// behind the first one's weight stream).  G lanes share an AVX2 lane when the
+// rows alone give fewer than four waves per workgroup.
 struct Q4KShape {
     int g, rows_per_wg, threads;
 };
@@ -1066,6 +1066,21 @@ static int q4k_min_threads() {
     }();
     return n;
 }
+// Largest workgroup in rows at G = 1, and in lanes (rows x 8 x G) at any G:
+// 64 rows, 512 threads.  Matrices with more rows than that per compute unit
+// (the decode step's fused gate/up, 28672 rows) take several workgroups per
+// CU instead of one large one; measured on the 8B decode step, 438 tok/s at
+// 64 rows against 434 at 128 (1024 threads), 425 at 72, 414 at 80 and 56,
+// 404 at 96.  GLLM_Q4K_MAX_ROWS overrides, for measurement (8..128); every
+// shape gives the same bits.
+static int q4k_max_rows() {
+    static const int n = [] {
+        const char* e = getenv("GLLM_Q4K_MAX_ROWS");
+        const int v = e ? atoi(e) : 0;
+        return v >= 8 && v <= 128 ? v / 8 * 8 : 64;
+    }();
+    return n;
+}
 static Q4KShape q4k_shape(int total_rows, int blocks) {
     const int ncu = device_cus();
     Q4KShape best{0, 0, 0};
@@ -1074,7 +1089,7 @@ static Q4KShape q4k_shape(int total_rows, int blocks) {
         const int unit = 8 / g;  // rows per wave
         int rpw = (total_rows + ncu - 1) / ncu;
         rpw = (rpw + unit - 1) / unit * unit;
-        rpw = std::min(rpw, 128 / g);  // at most 1024 threads
+        rpw = std::min(rpw, std::max(unit, q4k_max_rows() / g));
         const Q4KShape sh{g, rpw, rpw * 8 * g};
         if (!q4k_has_nl(blocks / g) && best.g) continue;
         best = sh;
