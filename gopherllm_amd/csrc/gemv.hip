@@ -465,6 +465,8 @@ __global__ __launch_bounds__(256) void gemv_q4k_any_kernel(GemvJob j) {
 // [ql 128][qh 64][int8 scales 16] followed by B f16 d values.  AVX2 lane k
 // covers bytes 4k..4k+3 of each 32-byte quad (Q6KQ8QUAD,
 // kernels_amd64.s:1130-1142); lanes 0-3 use scale 8h+2c, lanes 4-7 8h+2c+1.
+// The repack stores lane k's four ql dwords together at 16k and its two qh
+// dwords at 128 + 8k, so a lane reads its share of a block in four loads.
 // ---------------------------------------------------------------------------
 //
 // G lanes share one AVX2 lane (G = 2, 4 for short matrices, so that a launch
@@ -513,12 +515,14 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
     auto load_w = [&](int i, Blk& o) __attribute__((always_inline)) {
         const int bb = min(i, NB - 1) * G + gi;
         const uint8_t* blk = row + (size_t)bb * 208;
-        o.ql[0] = *(const uint32_t*)(blk + 4 * k);
-        o.ql[1] = *(const uint32_t*)(blk + 32 + 4 * k);
-        o.ql[2] = *(const uint32_t*)(blk + 64 + 4 * k);
-        o.ql[3] = *(const uint32_t*)(blk + 96 + 4 * k);
-        o.qh[0] = *(const uint32_t*)(blk + 128 + 4 * k);
-        o.qh[1] = *(const uint32_t*)(blk + 160 + 4 * k);
+        const uint4 l4 = *(const uint4*)(blk + 16 * k);   // lane k's ql dwords q = 0..3
+        const uint2 h2 = *(const uint2*)(blk + 128 + 8 * k);  // its qh dwords h = 0, 1
+        o.ql[0] = l4.x;
+        o.ql[1] = l4.y;
+        o.ql[2] = l4.z;
+        o.ql[3] = l4.w;
+        o.qh[0] = h2.x;
+        o.qh[1] = h2.y;
         o.sv = *(const uint4*)(blk + 192);
         o.d = dv[bb];
     };
@@ -783,8 +787,8 @@ __global__ __launch_bounds__(256) void lane_ints_kernel(const uint8_t* __restric
             const int8_t* sc = (const int8_t*)(blk + 192);
             for (int m = 0; m < 8; m++) {
                 const int h = m >> 2, c = m & 3;
-                const uint32_t y = *(const uint32_t*)(blk + 64 * h + ((c & 1) ? 32 : 0) + 4 * k);
-                const uint32_t qh = *(const uint32_t*)(blk + 128 + 32 * h + 4 * k);
+                const uint32_t y = *(const uint32_t*)(blk + 16 * k + 4 * (2 * h + (c & 1)));  // repacked
+                const uint32_t qh = *(const uint32_t*)(blk + 128 + 8 * k + 4 * h);
                 const uint32_t code = ((y >> (4 * (c >> 1))) & 0x0f0f0f0fu) |
                                       (((qh >> (2 * c)) & 0x03030303u) << 4);
                 acc += (int)sc[8 * h + 2 * c + (k >> 2)] * sdot4((int)code, xq[m], 0);
@@ -936,8 +940,21 @@ __global__ void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restri
                 n = b * 144 + 16 + (l / 4) * 16 + s4 * 4 + (l % 4);
             }
         } else if (type == GLLM_TYPE_Q6_K) {
+            // ql byte 32q + 4k + j -> 16k + 4q + j, qh byte 128 + 32h + 4k + j
+            // -> 128 + 8k + 4h + j (lane k's bytes together), scales
+            // unchanged, d to the row's tail
             const size_t b = o / 210, e = o % 210;
-            n = e < 208 ? b * 208 + e : (size_t)B * 208 + b * 2 + (e - 208);
+            if (e < 128) {
+                const size_t q = e / 32, l = e % 32;
+                n = b * 208 + (l / 4) * 16 + q * 4 + (l % 4);
+            } else if (e < 192) {
+                const size_t h = (e - 128) / 32, l = (e - 128) % 32;
+                n = b * 208 + 128 + (l / 4) * 8 + h * 4 + (l % 4);
+            } else if (e < 208) {
+                n = b * 208 + e;
+            } else {
+                n = (size_t)B * 208 + b * 2 + (e - 208);
+            }
         } else if (type == GLLM_TYPE_Q8_0) {
             const size_t g = o / 272, e = o % 272, q = e / 34, f = e % 34;
             n = g * 272 + (f < 2 ? q * 2 + f : 16 + q * 32 + (f - 2));
