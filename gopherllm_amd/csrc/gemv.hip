@@ -640,9 +640,10 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0, repacked at upload: per 256-element group, [8 x f16 d][8 x 32 int8]
-// (272 bytes, 16-byte aligned).  AVX2 lane k covers bytes 4k..4k+3 of each
-// 32-value block (Q80CHUNK, kernels_amd64.s:1321-1345).
+// Q8_0, repacked at upload: per 256-element group, [8 x f16 d] then lane k's
+// dwords of the eight 32-value blocks together at 16 + 32k (272 bytes,
+// 16-byte aligned).  AVX2 lane k covers bytes 4k..4k+3 of each 32-value block
+// (Q80CHUNK, kernels_amd64.s:1321-1345), read here in two 16-byte loads.
 // ---------------------------------------------------------------------------
 // G lanes per AVX2 lane and FUSE as in gemv_q6k_kernel.
 template <int NT, int G, bool FUSE = false>
@@ -675,8 +676,16 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(GemvJob j) {
         const int bb = min(i, NB - 1) * G + gi;
         const uint8_t* blk = row + (size_t)bb * 272;
         o.dh = *(const uint4*)blk;
-#pragma unroll
-        for (int q = 0; q < 8; q++) o.wv[q] = *(const int*)(blk + 16 + 32 * q + 4 * k);
+        const uint4 w0 = *(const uint4*)(blk + 16 + 32 * k);  // lane k's dwords, blocks 0..3
+        const uint4 w1 = *(const uint4*)(blk + 32 + 32 * k);  // blocks 4..7
+        o.wv[0] = (int)w0.x;
+        o.wv[1] = (int)w0.y;
+        o.wv[2] = (int)w0.z;
+        o.wv[3] = (int)w0.w;
+        o.wv[4] = (int)w1.x;
+        o.wv[5] = (int)w1.y;
+        o.wv[6] = (int)w1.z;
+        o.wv[7] = (int)w1.w;
     };
     auto load_a = [&](int i, Blk& o) __attribute__((always_inline)) {
         const int bb = min(i, NB - 1) * G + gi;
@@ -795,7 +804,7 @@ __global__ __launch_bounds__(256) void lane_ints_kernel(const uint8_t* __restric
             }
         } else {
             const uint8_t* blk = row + (size_t)b * 272;
-            for (int q = 0; q < 8; q++) acc += sdot4(*(const int*)(blk + 16 + 32 * q + 4 * k), xq[q], 0);
+            for (int q = 0; q < 8; q++) acc += sdot4(*(const int*)(blk + 16 + 32 * k + 4 * q), xq[q], 0);
         }
         out[((size_t)r * B + b) * 8 + k] = acc;
     }
@@ -956,8 +965,10 @@ __global__ void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restri
                 n = (size_t)B * 208 + b * 2 + (e - 208);
             }
         } else if (type == GLLM_TYPE_Q8_0) {
+            // [d][32 int8] x 8 -> [8 d][lane k: its dword of blocks q = 0..7 at
+            // 16 + 32k + 4q]
             const size_t g = o / 272, e = o % 272, q = e / 34, f = e % 34;
-            n = g * 272 + (f < 2 ? q * 2 + f : 16 + q * 32 + (f - 2));
+            n = g * 272 + (f < 2 ? q * 2 + f : 16 + ((f - 2) / 4) * 32 + q * 4 + (f - 2) % 4);
         } else if (type == GLLM_TYPE_Q5_K) {
             // [header 16][qh 32][nibbles 128] -> [header][lane k: 4 chunk dwords][lane k: qh dword]
             const size_t b = o / 176, e = o % 176;
