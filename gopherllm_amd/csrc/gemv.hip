@@ -1168,7 +1168,7 @@ int launch_q4k(GemvJob& j, const int* rows, int n, const Q4KShape& sh, hipStream
 // heaviest lane step, also splits while a lane would walk more than 16
 // blocks and the launch has fewer than two workgroups per CU (4096x14336 at
 // G = 4); the other formats measured faster at G = 2
-// there (Q5_K 16.4 / 18.7 us, Q8_0 25.5 / 26.4 us at G = 2 / 4).  Batches (per-token
+// there (Q5_K 16.4 / 18.7 us, Q3_K 18.8 / 20.7 us at G = 2 / 4).  Batches (per-token
 // activation reads make each block several times longer) take the largest G
 // that keeps the launch at two workgroups per compute unit or fewer.
 // GLLM_ROW_G overrides, for measurement; every G gives the same bits.
