@@ -28,8 +28,8 @@ def assert_bits(got, want, what):
 
 
 @pytest.mark.parametrize("qtype", FORMATS, ids=[NAMES[q] for q in FORMATS])
-@pytest.mark.parametrize("rows,cols", [(1, 256), (37, 512), (300, 1024), (1000, 4096),
-                                       (4096, 4096), (600, 14336)])
+@pytest.mark.parametrize("rows,cols", [(1, 256), (37, 512), (37, 768), (21, 2304), (300, 1024),
+                                       (1000, 4096), (4096, 4096), (600, 14336)])
 def test_matvec_bit_exact(hip, qtype, rows, cols):
     data = random_rows(qtype, rows, cols, rows + cols + qtype)
     x = normal(rows * 3 + cols, cols)
@@ -40,7 +40,7 @@ def test_matvec_bit_exact(hip, qtype, rows, cols):
 
 
 @pytest.mark.parametrize("qtype", FORMATS, ids=[NAMES[q] for q in FORMATS])
-@pytest.mark.parametrize("rows,cols", [(37, 512), (300, 1024), (4096, 4096)])
+@pytest.mark.parametrize("rows,cols", [(37, 512), (37, 768), (300, 1024), (4096, 4096)])
 def test_batches_bit_exact(hip, qtype, rows, cols):
     """matvecBatchQ8 == per-token row kernel, for 4- and 8-token tiles."""
     data = random_rows(qtype, rows, cols, 7 * rows + qtype)
@@ -93,7 +93,7 @@ def test_fused_matvec_of_other_types_rejected(hip):
 
 @pytest.mark.parametrize("qtype", [ref.Q6_K, ref.Q8_0] + FORMATS,
                          ids=["q6k", "q8_0"] + [NAMES[q] for q in FORMATS])
-@pytest.mark.parametrize("rows,cols", [(37, 512), (1000, 4096), (4100, 4096)])
+@pytest.mark.parametrize("rows,cols", [(37, 512), (37, 768), (1000, 4096), (4100, 4096)])
 def test_fused_quantisation_matches_prequantised(hip, qtype, rows, cols):
     """At batch 1 with cols <= 4096 the row kernels quantise x in LDS
     themselves; the same kernels fed by the separate Q8K-prep launch

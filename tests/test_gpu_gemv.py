@@ -83,7 +83,10 @@ def test_lane_ints_bit_exact(hip, name):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
-@pytest.mark.parametrize("rows,cols", [(1, 256), (37, 512), (4096, 4096), (1000, 14336)])
+# odd block counts (768, 2304 columns) put Q6_K rows (210 bytes per block) on
+# 2-byte boundaries, so the row kernels' wide loads run unaligned there
+@pytest.mark.parametrize("rows,cols", [(1, 256), (37, 512), (37, 768), (21, 2304), (4096, 4096),
+                                       (1000, 14336)])
 def test_matvec_bit_exact(hip, name, rows, cols):
     qtype = TYPES[name]
     data, _ = quant_matrix(qtype, rows, cols, rows + cols)
@@ -111,7 +114,7 @@ def test_matvec_ffn_shapes(hip, name):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
-@pytest.mark.parametrize("rows,cols", [(300, 1024), (37, 512), (1000, 14336)])
+@pytest.mark.parametrize("rows,cols", [(300, 1024), (37, 512), (37, 768), (1000, 14336)])
 @pytest.mark.parametrize("p", [2, 5, 8, 13])
 def test_batch_equals_per_token(hip, name, rows, cols, p):
     """matvecBatchQ8 == per-token row kernel (forward_batch_test.go); the
