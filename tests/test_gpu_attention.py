@@ -67,13 +67,33 @@ def _all_heads_oracle(q, k16, v16, start, end):
     return out
 
 
+def rope_rows(x, first_pos, n_heads, theta=500000.0):
+    """Interleaved RoPE (applyPreparedRope, model.go:3051-3093) of row i at
+    position first_pos + i, through the oracle's restatement."""
+    inv = ref.rope_inv_freq(theta, HD)
+    out = np.empty_like(x)
+    for i in range(x.shape[0]):
+        s, c = ref.rope_sincos(first_pos + i, inv)
+        out[i] = ref.rope_apply(x[i], HD, n_heads, s, c)
+    return out
+
+
 @pytest.mark.parametrize("ctx", [4096, 32768])
 def test_decode_attention_configs3(hip, ctx):
     """32 q heads, 8 kv heads, head_dim 128, F16 KV at 4096 and
-    32768.  Exact path bit-exact; split-K within tolerance."""
+    32768, RoPE theta 500000 on Q (at the decode position ctx - 1) and on
+    every K row (at its own position) before the f16 store.  Exact path
+    bit-exact; split-K within 1e-5 relative / 1e-6 absolute."""
     import torch
-    kv, k16, v16 = fill_cache(hip, 1, ctx, 30)
-    q = normal(31, N_HEADS * HD)
+    kv = hip.KVCacheF16(1, KVD, KVD, ctx)
+    k = rope_rows(normal(30, (ctx, KVD)), 0, N_KV)
+    v = normal(31, (ctx, KVD))
+    dk, dv = torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda()
+    for pos in range(ctx):
+        kv.store_kv_dev(0, pos, dk[pos], dv[pos])
+    torch.cuda.synchronize()
+    k16, v16 = ref.f32_to_f16(k), ref.f32_to_f16(v)
+    q = rope_rows(normal(32, (1, N_HEADS * HD)), ctx - 1, N_HEADS)[0]
     dq = torch.from_numpy(q).cuda()
     want = _all_heads_oracle(q, k16, v16, 0, ctx - 1)
     out = torch.empty(N_HEADS * HD, dtype=torch.float32, device="cuda")
