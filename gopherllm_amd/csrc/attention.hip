@@ -800,8 +800,8 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
     const AttnRope rope{rope_sin, rope_cos, d_knew, d_vnew, kv->k[l], kv->v[l]};
     if (hd == kFusedHD && kvmul <= 4 && kv->kv_dim_k == kv->kv_dim_v && span_max <= kSmaxSpan) {
         float* sc = scratch ? scratch
-                            : (float*)thread_scratch(5, (size_t)p * n_heads * span_max * 4 + 256);
-        if (!sc) return GLLM_ENOMEM;
+                            : (float*)thread_scratch(5, (size_t)p * n_heads * span_max * 4 + 256, s);
+        if (!sc) return scratch_error();
         const int nchunk = (span_max + kScoreChunk - 1) / kScoreChunk;
         hipLaunchKernelGGL(attn_scores128_kernel, dim3(n_kv, nchunk, p), dim3(256), 0, s, d_q,
                            kv->k[l], kv->kv_dim_k, n_kv, kvmul, start, span0, span_max, scale, sc,
@@ -821,8 +821,8 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
         GLLM_HIP(hipGetLastError());
         return GLLM_OK;
     }
-    float* scr = (float*)thread_scratch(5, ((size_t)p * n_heads * (span_max + 1) + 64) * 4);
-    if (!scr) return GLLM_ENOMEM;
+    float* scr = (float*)thread_scratch(5, ((size_t)p * n_heads * (span_max + 1) + 64) * 4, s);
+    if (!scr) return scratch_error();
     float* scores = scr;
     float* inv = scr + (size_t)p * n_heads * span_max;
     const int items = span_max * n_kv;
@@ -862,8 +862,8 @@ int attend_splitk(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, i
         chunk = std::max(quantum, (chunk + quantum - 1) / quantum * quantum);
         const int nchunks = (span + chunk - 1) / chunk;  // <= target <= kMergeMaxChunks
         const size_t nh = (size_t)n_heads;
-        float* scr = (float*)thread_scratch(6, (nh * nchunks * (2 + hd) + 64) * 4);
-        if (!scr) return GLLM_ENOMEM;
+        float* scr = (float*)thread_scratch(6, (nh * nchunks * (2 + hd) + 64) * 4, s);
+        if (!scr) return scratch_error();
         float* pm = scr;
         float* pl = pm + nh * nchunks;
         float* po = pl + nh * nchunks;
@@ -881,8 +881,8 @@ int attend_splitk(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, i
     chunk = (chunk + kSplitTile - 1) / kSplitTile * kSplitTile;
     nchunks = (span + chunk - 1) / chunk;
     const size_t nh = (size_t)n_heads;
-    float* scr = (float*)thread_scratch(6, (nh * nchunks * (2 + hd) + 64) * 4);
-    if (!scr) return GLLM_ENOMEM;
+    float* scr = (float*)thread_scratch(6, (nh * nchunks * (2 + hd) + 64) * 4, s);
+    if (!scr) return scratch_error();
     float* pm = scr;
     float* pl = pm + nh * nchunks;
     float* po = pl + nh * nchunks;
@@ -1013,8 +1013,8 @@ int gllm_hip_kv_store(gllm_hip_kv* kv, int l, int pos, const float* k, const flo
     if (!kv || !k || !v) return fail(GLLM_EINVAL, "gllm_hip_kv_store: null pointer");
     hipStream_t s = thread_stream();
     if (!s) return GLLM_EDEVICE;
-    float* d = (float*)thread_scratch(1, (size_t)(kv->kv_dim_k + kv->kv_dim_v) * 4);
-    if (!d) return GLLM_ENOMEM;
+    float* d = (float*)thread_scratch(1, (size_t)(kv->kv_dim_k + kv->kv_dim_v) * 4, s);
+    if (!d) return scratch_error();
     GLLM_HIP(hipMemcpyAsync(d, k, (size_t)kv->kv_dim_k * 4, hipMemcpyHostToDevice, s));
     GLLM_HIP(hipMemcpyAsync(d + kv->kv_dim_k, v, (size_t)kv->kv_dim_v * 4, hipMemcpyHostToDevice, s));
     GLLM_TRY(kv_store_dev_impl(kv, l, pos, d, d + kv->kv_dim_k, s));
@@ -1044,8 +1044,8 @@ int gllm_hip_attend_group(gllm_hip_kv* kv, int l, int kvh, const float* q, int q
                     end, kv->max_len - 1);
     hipStream_t s = thread_stream();
     if (!s) return GLLM_EDEVICE;
-    float* d = (float*)thread_scratch(1, (size_t)q_heads * hd * 2 * 4);
-    if (!d) return GLLM_ENOMEM;
+    float* d = (float*)thread_scratch(1, (size_t)q_heads * hd * 2 * 4, s);
+    if (!d) return scratch_error();
     GLLM_HIP(hipMemcpyAsync(d, q, (size_t)q_heads * hd * 4, hipMemcpyHostToDevice, s));
     // Present the group as a one-kv-head cache view starting at head kvh.
     gllm_hip_kv view = *kv;

@@ -10,6 +10,8 @@
 // block order; the row ends with the reference's 8->4->2->1 tree.  The
 // result is therefore bit-identical to the amd64 kernels.
 #include <algorithm>
+#include <mutex>
+#include <string>
 #include <vector>
 
 
@@ -1395,8 +1397,8 @@ int matvec_multi(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, fl
                                          "model.go:3213-3254)", ws[i]->type);
     for (int i = 0; i < n; i++)
         if (strides && strides[i] < ws[i]->rows) return fail(GLLM_EINVAL, "out stride < rows");
-    void* sc = thread_scratch(scratch_slot, act_bytes(ws[0]->cols, p));
-    if (!sc) return GLLM_ENOMEM;
+    void* sc = thread_scratch(scratch_slot, act_bytes(ws[0]->cols, p), s);
+    if (!sc) return scratch_error();
     return gemv_f32(n, ws, d_xs, p, outs, strides, sc, s);
 }
 
@@ -1408,6 +1410,11 @@ using namespace gllm;
 // C ABI
 // ---------------------------------------------------------------------------
 extern "C" {
+static gllm_hip_weight* weight_upload(const void* data, size_t len, int ggml_type, int rows,
+                                      int cols);
+static int matvec_host(int n, gllm_hip_weight* const* ws, const float* x, int p,
+                       float* const* outs);
+
 
 static gllm_hip_weight* weight_alloc(int ggml_type, int rows, int cols, size_t len) {
     if (!row_kernel_type(ggml_type)) {
@@ -1450,12 +1457,8 @@ static gllm_hip_weight* weight_finish(gllm_hip_weight* w, const uint8_t* d_src, 
     return w;
 }
 
-gllm_hip_weight* gllm_hip_weight_new(const void* data, size_t len, int ggml_type, int rows,
-                                     int cols) {
-    if (!data) {
-        fail(GLLM_EINVAL, "gllm_hip_weight_new: null data");
-        return nullptr;
-    }
+static gllm_hip_weight* weight_upload(const void* data, size_t len, int ggml_type, int rows,
+                                      int cols) {
     gllm_hip_weight* w = weight_alloc(ggml_type, rows, cols, len);
     if (!w) return nullptr;
     hipStream_t s = thread_stream();
@@ -1479,12 +1482,23 @@ gllm_hip_weight* gllm_hip_weight_new(const void* data, size_t len, int ggml_type
     return out;
 }
 
+gllm_hip_weight* gllm_hip_weight_new(const void* data, size_t len, int ggml_type, int rows,
+                                     int cols) {
+    if (!data) {
+        fail(GLLM_EINVAL, "gllm_hip_weight_new: null data");
+        return nullptr;
+    }
+    if (self_check() != GLLM_OK) return nullptr;
+    return weight_upload(data, len, ggml_type, rows, cols);
+}
+
 gllm_hip_weight* gllm_hip_weight_from_device(const void* d_data, size_t len, int ggml_type,
                                              int rows, int cols, void* stream) {
     if (!d_data) {
         fail(GLLM_EINVAL, "gllm_hip_weight_from_device: null data");
         return nullptr;
     }
+    if (self_check() != GLLM_OK) return nullptr;
     gllm_hip_weight* w = weight_alloc(ggml_type, rows, cols, len);
     if (!w) return nullptr;
     // NULL is the legacy default stream, as for every _dev entry point: the
@@ -1566,9 +1580,9 @@ static int matvec_host(int n, gllm_hip_weight* const* ws, const float* x, int p,
     const int cols = ws[0]->cols;
     size_t out_total = 0;
     for (int i = 0; i < n; i++) out_total += (size_t)ws[i]->rows * p;
-    float* d_x = (float*)thread_scratch(1, (size_t)cols * p * 4);
-    float* d_out = (float*)thread_scratch(2, out_total * 4);
-    if (!d_x || !d_out) return GLLM_ENOMEM;
+    float* d_x = (float*)thread_scratch(1, (size_t)cols * p * 4, s);
+    float* d_out = (float*)thread_scratch(2, out_total * 4, s);
+    if (!d_x || !d_out) return scratch_error();
     GLLM_HIP(hipMemcpyAsync(d_x, x, (size_t)cols * p * 4, hipMemcpyHostToDevice, s));
     float* douts[3];
     int strides[3];
@@ -1621,14 +1635,14 @@ int gllm_hip_argmax_penalized_dev(gllm_hip_weight* w, const float* d_x, const ui
     GLLM_TRY(validate_weight(w));
     if (!d_x || !d_token) return fail(GLLM_EINVAL, "gllm_hip_argmax_dev: null pointer");
     hipStream_t s = (hipStream_t)stream;
-    float* logits = (float*)thread_scratch(3, (size_t)w->rows * 4);
-    if (!logits) return GLLM_ENOMEM;
+    float* logits = (float*)thread_scratch(3, (size_t)w->rows * 4, s);
+    if (!logits) return scratch_error();
     gllm_hip_weight* ws[1] = {w};
     float* outs[1] = {logits};
     int strides[1] = {w->rows};
     GLLM_TRY(matvec_multi(1, ws, d_x, 1, outs, strides, s, 0));
-    auto* keys = (unsigned long long*)thread_scratch(7, argmax_keys(w->rows) * 8);
-    if (!keys) return GLLM_ENOMEM;
+    auto* keys = (unsigned long long*)thread_scratch(7, argmax_keys(w->rows) * 8, s);
+    if (!keys) return scratch_error();
     return launch_argmax(logits, w->rows, d_token, keys, s, d_recent, n_recent, penalty);
 }
 
@@ -1644,14 +1658,14 @@ int gllm_hip_argmax_penalized(gllm_hip_weight* w, const float* x, const uint32_t
         return fail(GLLM_EINVAL, "gllm_hip_argmax_penalized: bad recent-token window");
     hipStream_t s = thread_stream();
     if (!s) return GLLM_EDEVICE;
-    float* d_x = (float*)thread_scratch(1, (size_t)w->cols * 4);
-    uint32_t* d_tok = (uint32_t*)thread_scratch(4, 64);
+    float* d_x = (float*)thread_scratch(1, (size_t)w->cols * 4, s);
+    uint32_t* d_tok = (uint32_t*)thread_scratch(4, 64, s);
     uint32_t* h_tok = (uint32_t*)thread_pinned(0, 64);
     if (!d_x || !d_tok || !h_tok) return GLLM_ENOMEM;
     uint32_t* d_recent = nullptr;
     if (n_recent > 0) {
-        d_recent = (uint32_t*)thread_scratch(8, (size_t)n_recent * 4);
-        if (!d_recent) return GLLM_ENOMEM;
+        d_recent = (uint32_t*)thread_scratch(8, (size_t)n_recent * 4, s);
+        if (!d_recent) return scratch_error();
         GLLM_HIP(hipMemcpyAsync(d_recent, recent, (size_t)n_recent * 4, hipMemcpyHostToDevice, s));
     }
     GLLM_HIP(hipMemcpyAsync(d_x, x, (size_t)w->cols * 4, hipMemcpyHostToDevice, s));
@@ -1670,8 +1684,8 @@ int gllm_hip_lane_ints_dev(gllm_hip_weight* w, const float* d_x, int32_t* d_ints
     GLLM_TRY(validate_weight(w));
     if (!d_x || !d_ints) return fail(GLLM_EINVAL, "gllm_hip_lane_ints_dev: null pointer");
     hipStream_t s = (hipStream_t)stream;
-    void* sc = thread_scratch(0, act_bytes(w->cols, 1));
-    if (!sc) return GLLM_ENOMEM;
+    void* sc = thread_scratch(0, act_bytes(w->cols, 1), s);
+    if (!sc) return scratch_error();
     ActQ8 act;
     act_carve(sc, w->cols, 1, &act);
     GLLM_TRY(launch_q8k_prep(d_x, w->cols, 1, act, s));
@@ -1683,3 +1697,183 @@ int gllm_hip_lane_ints_dev(gllm_hip_weight* w, const float* d_x, int32_t* d_ints
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Load-time known-answer check (the reference's q8kSelfCheck,
+// q8k_dot_arm64.go:146-228, which disables a kernel whose integer dots
+// disagree with a restated answer).  Once per device, before the first weight
+// is created, small Q4_K, Q6_K and Q8_0 matrices go through the same matvec
+// path every caller uses (upload and repack, Q8K quantisation, row kernel,
+// float chains, lane tree).  The inputs are chosen so that the answer is an
+// integer the float path must hit exactly:
+//   * x holds integers in [-3, 3] with one 127 per 256-block, so the Q8K
+//     scale is exactly 1 and q8 == x (kernels_amd64.s:348-436);
+//   * every f16 d / dmin is 1.0, so each row dot is sum_e w_e * x_e with the
+//     integer weight w_e = sc*q - m (Q4_K), sc*(q - 32) (Q6_K) or q (Q8_0);
+//   * pattern rows keep sum_e (|A_e| + |B_e|) |x_e| below 2^24 (A, B: the
+//     scale chain's and the min / offset chain's integer terms), so every
+//     partial sum of every lane chain and of the lane tree is exact;
+//   * the Q4_K all-0xff row with x = 127 everywhere (TestAuditQ4KDotExtremes,
+//     q4k_q8_amd64_audit_test.go:18-52) gives 28,675,584 per block:
+//     all lanes hold equal even values, so each tree addition is exact too.
+// On a mismatch no weight can be created on that device and every weight
+// constructor fails with GLLM_EUNSUP, which sends the Go seam to its CPU
+// kernels.  GLLM_SELF_CHECK_PLANT=1 adds one to a host-side expected value
+// (a planted mistake on the CPU), so the refusal path can be tested.
+// ---------------------------------------------------------------------------
+namespace gllm {
+namespace {
+
+// 8192 rows take the fused-quantiser row kernels of every format at batch
+// 1, as a full-size matrix does
+constexpr int kCheckRows = 8192;
+
+uint8_t check_byte(int i, int mul, int add) { return (uint8_t)(i * mul + add); }
+
+// getScaleMinK4 (simd.go:1672-1677)
+void scale_min_k4(int j, const uint8_t* q, int* sc, int* m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0x0f) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// Integer terms of element e of a block (GGUF layout, d = dmin = 1): the
+// scale chain's term A and the min / offset chain's term B, weight A - B.
+void check_terms(int type, const uint8_t* blk, int e, int* A, int* B) {
+    if (type == GLLM_TYPE_Q4_K) {
+        int sc, m;
+        scale_min_k4(e / 32, blk + 4, &sc, &m);
+        const int s = e / 64, l = e % 32;
+        const uint8_t qb = blk[16 + 32 * s + l];
+        *A = sc * ((e / 32) % 2 ? qb >> 4 : qb & 15);
+        *B = m;
+        return;
+    }
+    if (type == GLLM_TYPE_Q6_K) {
+        const int h = e / 128, r = e % 128, l = r % 32, quad = r / 32;
+        const uint8_t* ql = blk + 64 * h;
+        const uint8_t qh = blk[128 + 32 * h + l];
+        const int lo = quad & 1 ? ql[l + 32] : ql[l];
+        const int q = (quad < 2 ? lo & 15 : lo >> 4) | (((qh >> (2 * quad)) & 3) << 4);
+        const int sc = (int)(int8_t)blk[192 + 8 * h + l / 16 + 2 * quad];
+        *A = sc * q;
+        *B = 32 * sc;
+        return;
+    }
+    *A = (int)(int8_t)blk[(e / 32) * 34 + 2 + e % 32];  // Q8_0
+    *B = 0;
+}
+
+// One format: kCheckRows rows of pattern bytes against a pattern x of
+// integers in [-xr, xr] (one 127 per block), and for Q4_K the all-0xff row
+// against x = 127.  Returns GLLM_OK, or GLLM_EUNSUP on a wrong answer.
+int check_format(int type, int cols, int xr, bool plant) {
+    const size_t rb = ref_row_bytes(type, cols);
+    const size_t bb = rb / (cols / 256);  // bytes per 256 elements
+    std::vector<uint8_t> w(rb * kCheckRows);
+    for (int r = 0; r < kCheckRows; r++)
+        for (size_t i = 0; i < rb; i++) w[r * rb + i] = check_byte((int)i, 7 + 6 * r + type, 3 * r + 1);
+    for (int r = 0; r < kCheckRows; r++)
+        for (int b = 0; b < cols / 256; b++) {
+            uint8_t* blk = &w[r * rb + b * bb];
+            if (type == GLLM_TYPE_Q4_K) {
+                blk[0] = 0x00, blk[1] = 0x3c, blk[2] = 0x00, blk[3] = 0x3c;  // d = dmin = 1
+            } else if (type == GLLM_TYPE_Q6_K) {
+                blk[208] = 0x00, blk[209] = 0x3c;
+            } else {
+                for (int j = 0; j < 8; j++) blk[34 * j] = 0x00, blk[34 * j + 1] = 0x3c;
+            }
+        }
+    std::vector<float> x(cols);
+    for (int i = 0; i < cols; i++) x[i] = (float)((i * 37 + 11) % (2 * xr + 1) - xr);
+    for (int b = 0; b < cols / 256; b++) x[b * 256 + (b * 41) % 256] = 127.0f;
+    std::vector<float> want(kCheckRows);
+    for (int r = 0; r < kCheckRows; r++) {
+        long long acc = 0, mag = 0;
+        for (int e = 0; e < cols; e++) {
+            int A, B;
+            check_terms(type, &w[r * rb + (e / 256) * bb], e % 256, &A, &B);
+            const long long xe = (long long)x[e];
+            acc += (long long)(A - B) * xe;
+            mag += (long long)((A < 0 ? -A : A) + (B < 0 ? -B : B)) * (xe < 0 ? -xe : xe);
+        }
+        // every partial sum of either chain, and of the lane tree, is bounded
+        // by mag: below 2^24 they are all exact in float
+        if (mag >= (1LL << 24)) return fail(GLLM_EUNSUP, "self-check pattern out of range");
+        want[r] = (float)acc;
+    }
+    if (plant) want[1] += 1.0f;
+    gllm_hip_weight* h = weight_upload(w.data(), w.size(), type, kCheckRows, cols);
+    if (!h) return GLLM_EDEVICE;
+    std::vector<float> got(kCheckRows);
+    gllm_hip_weight* ws[1] = {h};
+    float* outs[1] = {got.data()};
+    int rc = matvec_host(1, ws, x.data(), 1, outs);
+    gllm_hip_weight_release(h);
+    GLLM_TRY(rc);
+    for (int r = 0; r < kCheckRows; r++)
+        if (got[r] != want[r])
+            return fail(GLLM_EUNSUP, "self-check: type %d row %d gave %.9g, known answer %.9g", type,
+                        r, got[r], want[r]);
+    if (type == GLLM_TYPE_Q4_K) {
+        std::vector<uint8_t> ext(rb, 0xff);
+        for (int b = 0; b < cols / 256; b++)
+            ext[b * bb] = 0x00, ext[b * bb + 1] = 0x3c, ext[b * bb + 2] = 0x00, ext[b * bb + 3] = 0x3c;
+        std::vector<float> x127(cols, 127.0f);
+        gllm_hip_weight* he = weight_upload(ext.data(), ext.size(), type, 1, cols);
+        if (!he) return GLLM_EDEVICE;
+        float g = 0.0f;
+        gllm_hip_weight* we[1] = {he};
+        float* oe[1] = {&g};
+        rc = matvec_host(1, we, x127.data(), 1, oe);
+        gllm_hip_weight_release(he);
+        GLLM_TRY(rc);
+        // (63*15*127*256 - 8*63*32*127) per block
+        const float ew = 28675584.0f * (float)(cols / 256);
+        if (g != ew)
+            return fail(GLLM_EUNSUP, "self-check: Q4_K extremes gave %.9g, known answer %.9g", g, ew);
+    }
+    return GLLM_OK;
+}
+
+std::mutex g_check_mu;
+int g_check_state[64];  // per device: 0 not run, 1 passed, <0 the failure code
+std::string g_check_msg[64];
+
+}  // namespace
+
+int self_check() {
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) {
+        (void)hipGetLastError();
+        return fail(GLLM_EDEVICE, "no HIP device");
+    }
+    std::lock_guard<std::mutex> lock(g_check_mu);
+    if (g_check_state[d] == 0) {
+        const char* e = getenv("GLLM_SELF_CHECK_PLANT");
+        const bool plant = e && atoi(e) == 1;
+        int rc = GLLM_OK;
+        // Q6_K's chains carry |sc| * 95 per unit of x, so it takes two blocks
+        // of x in [-1, 1] to stay below 2^24
+        if (rc == GLLM_OK) rc = check_format(GLLM_TYPE_Q4_K, 1024, 3, plant);
+        if (rc == GLLM_OK) rc = check_format(GLLM_TYPE_Q6_K, 512, 1, plant);
+        if (rc == GLLM_OK) rc = check_format(GLLM_TYPE_Q8_0, 1024, 3, plant);
+        if (rc == GLLM_OK) {
+            g_check_state[d] = 1;
+        } else {
+            g_check_state[d] = rc == GLLM_EDEVICE ? 0 : rc;  // a device error is retried
+            g_check_msg[d] = gllm_hip_last_error();
+            return rc;
+        }
+    }
+    if (g_check_state[d] < 0)
+        return fail(g_check_state[d], "device %d failed the load-time known-answer check (%s)", d,
+                    g_check_msg[d].c_str());
+    return GLLM_OK;
+}
+
+}  // namespace gllm

@@ -35,8 +35,16 @@ int check(hipError_t e, const char* what);
 hipStream_t thread_stream();
 // Compute units of the current device (cached per device).
 int device_cus();
-// Per-thread growable device scratch (slot 0..7).
-void* thread_scratch(int slot, size_t bytes);
+// Growable device scratch of the calling thread for work on `stream` (slot
+// 0..11).  Null, with the error set, when it cannot grow: allocation failed,
+// or the stream is being captured into a graph.
+void* thread_scratch(int slot, size_t bytes, hipStream_t stream);
+// Status code of the calling thread's last thread_scratch failure
+// (GLLM_EUNSUP under capture, GLLM_ENOMEM otherwise).
+int scratch_error();
+// Load-time known-answer check of the current device (run once per device,
+// before its first weight): GLLM_OK, or the failure code with the error set.
+int self_check();
 // Per-thread pinned host staging buffer.
 void* thread_pinned(int slot, size_t bytes);
 

@@ -3,8 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include <map>
-#include <mutex>
+#include <unordered_map>
+#include <vector>
 
 #include "gllm_common.h"
 
@@ -41,16 +41,29 @@ namespace {
 
 constexpr int kScratchSlots = 12;
 
+// Device scratch of one (host thread, stream) pair.  Work enqueued on one
+// stream runs in order, so slots keyed by the stream never serve two
+// concurrent kernels; two streams of one thread (a Go scheduler thread
+// running two Runners) get separate slots.
+struct StreamScratch {
+    void* p[kScratchSlots] = {};
+    size_t n[kScratchSlots] = {};
+};
+
 struct ThreadRes {
     int device = -1;
     hipStream_t stream = nullptr;
-    void* scratch[kScratchSlots] = {};
-    size_t scratch_n[kScratchSlots] = {};
+    std::unordered_map<hipStream_t, StreamScratch> scratch;
+    // Buffers replaced by a larger one.  Work already enqueued, or a graph a
+    // caller captured earlier, may still read them, so they are never freed
+    // (growth is geometric, so they total at most a few times the largest).
+    std::vector<void*> retired;
     void* pinned[kScratchSlots] = {};
     size_t pinned_n[kScratchSlots] = {};
 };
 
 thread_local ThreadRes t_res;
+thread_local int t_scratch_code = GLLM_ENOMEM;
 
 int current_device() {
     int d = 0;
@@ -63,7 +76,13 @@ int current_device() {
 void reset_if_device_changed() {
     int d = current_device();
     if (t_res.device != d) {
-        t_res = ThreadRes();
+        t_res.scratch.clear();
+        t_res.retired.clear();
+        t_res.stream = nullptr;
+        for (int i = 0; i < kScratchSlots; i++) {
+            t_res.pinned[i] = nullptr;
+            t_res.pinned_n[i] = 0;
+        }
         t_res.device = d;
     }
 }
@@ -95,29 +114,38 @@ hipStream_t thread_stream() {
     return t_res.stream;
 }
 
-void* thread_scratch(int slot, size_t bytes) {
+void* thread_scratch(int slot, size_t bytes, hipStream_t stream) {
     reset_if_device_changed();
     if (slot < 0 || slot >= kScratchSlots) return nullptr;
-    if (t_res.scratch_n[slot] < bytes) {
-        if (t_res.scratch[slot]) {
-            // Another stream of this thread may still read the old buffer.
-            (void)hipDeviceSynchronize();
-            (void)hipFree(t_res.scratch[slot]);
+    StreamScratch& sc = t_res.scratch[stream];
+    if (sc.n[slot] < bytes) {
+        // Growing allocates; under stream capture that would either fail or
+        // leave the captured graph holding a pointer this thread later
+        // replaces.  The caller sizes the slot with one uncaptured call first.
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) != hipSuccess) (void)hipGetLastError();
+        if (cs != hipStreamCaptureStatusNone) {
+            t_scratch_code = GLLM_EUNSUP;
+            set_error("scratch slot %d would grow to %zu bytes inside a stream capture; make the "
+                      "same call once outside the capture first", slot, bytes);
+            return nullptr;
         }
         size_t n = bytes < 4096 ? 4096 : bytes + bytes / 4;
         void* p = nullptr;
         if (hipMalloc(&p, n) != hipSuccess) {
             (void)hipGetLastError();
-            t_res.scratch[slot] = nullptr;
-            t_res.scratch_n[slot] = 0;
+            t_scratch_code = GLLM_ENOMEM;
             set_error("hipMalloc(%zu) for scratch failed", n);
             return nullptr;
         }
-        t_res.scratch[slot] = p;
-        t_res.scratch_n[slot] = n;
+        if (sc.p[slot]) t_res.retired.push_back(sc.p[slot]);
+        sc.p[slot] = p;
+        sc.n[slot] = n;
     }
-    return t_res.scratch[slot];
+    return sc.p[slot];
 }
+
+int scratch_error() { return t_scratch_code; }
 
 void* thread_pinned(int slot, size_t bytes) {
     reset_if_device_changed();
@@ -162,7 +190,7 @@ int gllm_hip_available(void) {
         set_error("device is %s, this build targets gfx950", prop.gcnArchName);
         return 0;
     }
-    return 1;
+    return self_check() == GLLM_OK ? 1 : 0;
 }
 
 const char* gllm_hip_last_error(void) { return t_error.c_str(); }

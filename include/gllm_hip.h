@@ -21,9 +21,22 @@
  *    (simd.go:264), weights are row-major GGUF tensors with rows = dims[1],
  *    cols = dims[0] (model.go:2393-2396).
  *  - Thread safety: handles may be used from several host threads at once;
- *    host entry points use per-thread streams and per-thread scratch.
+ *    host entry points use per-thread streams.  Device scratch (quantised
+ *    activations, logits, attention partials) is kept per (host thread,
+ *    stream), so two streams driven from one thread never share it.
  *    A KV cache or model handle must not be mutated by two threads at once
  *    (the reference serialises requests per Runner, runtime.go:816-817).
+ *  - Graph capture: a "_dev" call may be captured into a caller's HIP graph
+ *    once the same call (same shapes, same stream) has run uncaptured: the
+ *    scratch it uses then exists, and it stays allocated for the process
+ *    lifetime even after a later, larger call on that stream moves to a
+ *    bigger buffer.  A call that would have to allocate scratch while its
+ *    stream is capturing fails with GLLM_EUNSUP and enqueues nothing.
+ *  - Start-up check: before the first weight is created on a device (and in
+ *    gllm_hip_available) the library runs a known-answer check of the Q4_K,
+ *    Q6_K and Q8_0 matvec path (q8kSelfCheck, q8k_dot_arm64.go:146-228).  On
+ *    a mismatch gllm_hip_available() returns 0 and every weight constructor
+ *    fails with GLLM_EUNSUP, so the caller keeps its CPU kernels.
  */
 #ifndef GLLM_HIP_H
 #define GLLM_HIP_H
