@@ -41,6 +41,36 @@ def _dev_ptr(t):
     return C.c_void_p(t.data_ptr())
 
 
+_DTYPES = {"f32": ("float32",), "u8": ("uint8", "int8"), "u32": ("int32", "uint32"),
+           "i32": ("int32",), "u16": ("int16", "uint16")}
+
+
+def _dev(t, kind: str, numel: int, what: str):
+    """Device pointer of tensor t after checking that it is a contiguous
+    device tensor of the element kind with at least numel elements: a wrong
+    tensor would otherwise become an out-of-bounds device access."""
+    if not getattr(t, "is_cuda", False):
+        raise ValueError(f"{what}: expected a device tensor")
+    if str(t.dtype).replace("torch.", "") not in _DTYPES[kind]:
+        raise ValueError(f"{what}: dtype {t.dtype}, expected {kind}")
+    if not t.is_contiguous():
+        raise ValueError(f"{what}: tensor must be contiguous")
+    if t.numel() < numel:
+        raise ValueError(f"{what}: {t.numel()} elements, need at least {numel}")
+    return _dev_ptr(t)
+
+
+def _host_f32(a, numel: int, what: str):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    if a.size < numel:
+        raise ValueError(f"{what}: {a.size} elements, need at least {numel}")
+    return a
+
+
+def _rows(t):
+    return t.shape[0] if t.dim() == 2 else 1
+
+
 def _stream(stream=None):
     if stream is not None:
         return C.c_void_p(stream)
@@ -67,7 +97,7 @@ class Weight:
 
     @classmethod
     def from_device(cls, tensor, qtype: int, rows: int, cols: int, stream=None) -> "Weight":
-        h = call_ptr("gllm_hip_weight_from_device", _dev_ptr(tensor),
+        h = call_ptr("gllm_hip_weight_from_device", _dev(tensor, "u8", 0, "tensor"),
                      tensor.numel() * tensor.element_size(), qtype, rows, cols, _stream(stream))
         return cls(h, qtype, rows, cols)
 
@@ -84,16 +114,19 @@ class Weight:
 
     # host-pointer forms ----------------------------------------------------
     def matvec_into(self, x, out=None):
-        x = np.ascontiguousarray(x, dtype=np.float32)
-        if x.size < self.cols:
-            raise ValueError("x shorter than cols")
+        x = _host_f32(x, self.cols, "matvec_into x")
         if out is None:
             out = np.empty(self.rows, np.float32)
+        elif out.dtype != np.float32 or not out.flags.c_contiguous or out.size < self.rows:
+            raise ValueError("matvec_into out: need a contiguous float32 array of rows elements")
         call("gllm_hip_matvec", self.handle, _np_ptr(x), _np_ptr(out))
         return out
 
     def matvec_batch(self, xs):
-        xs = np.ascontiguousarray(xs, dtype=np.float32).reshape(-1, self.cols)
+        xs = np.ascontiguousarray(xs, dtype=np.float32)
+        if xs.size % self.cols:
+            raise ValueError("matvec_batch: xs is not a whole number of cols-wide rows")
+        xs = xs.reshape(-1, self.cols)
         out = np.empty((xs.shape[0], self.rows), np.float32)
         call("gllm_hip_matvec_batch", self.handle, _np_ptr(xs), xs.shape[0], _np_ptr(out))
         return out
@@ -102,7 +135,7 @@ class Weight:
         """Greedy token of W.x; with recent / penalty, after applyRepeatPenalty
         (sampling.go:136-153), as ArgmaxQ6KPenalized (internal/metal/
         metal_darwin.go:1175) takes them."""
-        x = np.ascontiguousarray(x, dtype=np.float32)
+        x = _host_f32(x, self.cols, "argmax_matvec x")
         tok = C.c_uint32(0)
         if recent is None and penalty == 1.0:
             call("gllm_hip_argmax", self.handle, _np_ptr(x), C.byref(tok))
@@ -115,46 +148,59 @@ class Weight:
     # device forms ------------------------------------------------------------
     def matvec_dev(self, xs, out, stream=None):
         """xs: (p, cols) float32 device tensor; out: (p, >= rows) float32."""
-        p = xs.shape[0] if xs.dim() == 2 else 1
+        p = _rows(xs)
         stride = out.shape[-1]
-        call("gllm_hip_matvec_dev", self.handle, _dev_ptr(xs), p, _dev_ptr(out), stride,
-             _stream(stream))
+        if xs.shape[-1] != self.cols or stride < self.rows:
+            raise ValueError(f"matvec_dev: xs (.., {xs.shape[-1]}) / out (.., {stride}) do not fit "
+                             f"{self.rows}x{self.cols}")
+        call("gllm_hip_matvec_dev", self.handle, _dev(xs, "f32", p * self.cols, "xs"), p,
+             _dev(out, "f32", p * stride, "out"), stride, _stream(stream))
         return out
 
     def matvec_q8_dev(self, act, p, out, stream=None):
         """Row kernels only, against activations quantised by q8k_prepare_dev."""
-        call("gllm_hip_matvec_q8_dev", self.handle, _dev_ptr(act), p, _dev_ptr(out),
-             out.shape[-1], _stream(stream))
+        stride = out.shape[-1]
+        if stride < self.rows:
+            raise ValueError("matvec_q8_dev: out rows shorter than the weight's rows")
+        call("gllm_hip_matvec_q8_dev", self.handle, _dev(act, "u8", act_bytes(self.cols, p), "act"),
+             p, _dev(out, "f32", p * stride, "out"), stride, _stream(stream))
         return out
 
     def argmax_dev(self, x, token_out, stream=None, recent=None, penalty: float = 1.0):
         """recent: uint32/int32 device tensor of token ids, or None."""
+        xp = _dev(x, "f32", self.cols, "x")
+        tp = _dev(token_out, "u32", 1, "token_out")
         if recent is None and penalty == 1.0:
-            call("gllm_hip_argmax_dev", self.handle, _dev_ptr(x), _dev_ptr(token_out),
-                 _stream(stream))
+            call("gllm_hip_argmax_dev", self.handle, xp, tp, _stream(stream))
         else:
             n = 0 if recent is None else recent.numel()
-            call("gllm_hip_argmax_penalized_dev", self.handle, _dev_ptr(x),
-                 _dev_ptr(recent) if n else None, n, float(penalty), _dev_ptr(token_out),
+            call("gllm_hip_argmax_penalized_dev", self.handle, xp,
+                 _dev(recent, "u32", n, "recent") if n else None, n, float(penalty), tp,
                  _stream(stream))
         return token_out
 
     def lane_ints_dev(self, x, out, stream=None):
-        call("gllm_hip_lane_ints_dev", self.handle, _dev_ptr(x), _dev_ptr(out), _stream(stream))
+        call("gllm_hip_lane_ints_dev", self.handle, _dev(x, "f32", self.cols, "x"),
+             _dev(out, "i32", self.rows * (self.cols // 256) * 8, "out"), _stream(stream))
         return out
 
     def download_dev(self, out, stream=None):
-        call("gllm_hip_weight_download_dev", self.handle, _dev_ptr(out), _stream(stream))
+        call("gllm_hip_weight_download_dev", self.handle,
+             _dev(out, "u8", self.rows * row_bytes(self.type, self.cols), "out"), _stream(stream))
         return out
 
 
 def matvec_multi_dev(weights, xs, outs, stream=None):
     n = len(weights)
+    p = _rows(xs)
+    for w, o in zip(weights, outs):
+        if xs.shape[-1] != w.cols or o.shape[-1] < w.rows:
+            raise ValueError("matvec_multi_dev: xs / out shapes do not fit a weight")
     hs = (C.c_void_p * n)(*[w.handle for w in weights])
-    ps = (C.c_void_p * n)(*[o.data_ptr() for o in outs])
+    ps = (C.c_void_p * n)(*[_dev(o, "f32", p * o.shape[-1], "out").value for o in outs])
     strides = (C.c_int * n)(*[o.shape[-1] for o in outs])
-    p = xs.shape[0] if xs.dim() == 2 else 1
-    call("gllm_hip_matvec_multi_dev", n, hs, _dev_ptr(xs), p, ps, strides, _stream(stream))
+    call("gllm_hip_matvec_multi_dev", n, hs, _dev(xs, "f32", p * weights[0].cols, "xs"), p, ps,
+         strides, _stream(stream))
 
 
 def _matvec_into(qtype, data, x, rows, cols, out):
@@ -199,27 +245,31 @@ def act_bytes(cols: int, p: int = 1) -> int:
 
 def q8k_prepare_dev(xs, act, stream=None):
     """acquireQ8 + xsums for p rows of xs into the device buffer `act`."""
-    p = xs.shape[0] if xs.dim() == 2 else 1
-    call("gllm_hip_q8k_prepare_dev", _dev_ptr(xs), xs.shape[-1], p, _dev_ptr(act), _stream(stream))
+    p = _rows(xs)
+    cols = xs.shape[-1]
+    call("gllm_hip_q8k_prepare_dev", _dev(xs, "f32", p * cols, "xs"), cols, p,
+         _dev(act, "u8", act_bytes(cols, p), "act"), _stream(stream))
     return act
 
 
 def q8k_quantize_dev(x, q8_out, scales_out, stream=None):
-    p = x.shape[0] if x.dim() == 2 else 1
+    p = _rows(x)
     cols = x.shape[-1]
-    call("gllm_hip_q8k_quantize_dev", _dev_ptr(x), cols, p, _dev_ptr(q8_out),
-         _dev_ptr(scales_out), _stream(stream))
+    call("gllm_hip_q8k_quantize_dev", _dev(x, "f32", p * cols, "x"), cols, p,
+         _dev(q8_out, "u8", p * cols, "q8_out"), _dev(scales_out, "f32", p * (cols // 256), "scales"),
+         _stream(stream))
 
 
 def quantize_rows_dev(qtype, src, dst, stream=None):
     rows, cols = src.shape
-    call("gllm_hip_quantize_rows_dev", qtype, _dev_ptr(src), rows, cols, _dev_ptr(dst),
-         _stream(stream))
+    call("gllm_hip_quantize_rows_dev", qtype, _dev(src, "f32", rows * cols, "src"), rows, cols,
+         _dev(dst, "u8", rows * row_bytes(qtype, cols), "dst"), _stream(stream))
     return dst
 
 
 def fill_normal_dev(out, seed: int, std: float, stream=None):
-    call("gllm_hip_fill_normal_dev", _dev_ptr(out), out.numel(), seed, std, _stream(stream))
+    call("gllm_hip_fill_normal_dev", _dev(out, "f32", 0, "out"), out.numel(), seed, std,
+         _stream(stream))
     return out
 
 
@@ -256,17 +306,17 @@ class KVCacheF16:
         return k, v
 
     def store_kv(self, layer, pos, k, v):
-        k = np.ascontiguousarray(k, dtype=np.float32)
-        v = np.ascontiguousarray(v, dtype=np.float32)
+        k = _host_f32(k, self.kv_dim_k, "store_kv k")
+        v = _host_f32(v, self.kv_dim_v, "store_kv v")
         call("gllm_hip_kv_store", self.handle, layer, pos, _np_ptr(k), _np_ptr(v))
 
     def store_kv_dev(self, layer, pos, k, v, stream=None):
-        call("gllm_hip_kv_store_dev", self.handle, layer, pos, _dev_ptr(k), _dev_ptr(v),
-             _stream(stream))
+        call("gllm_hip_kv_store_dev", self.handle, layer, pos, _dev(k, "f32", self.kv_dim_k, "k"),
+             _dev(v, "f32", self.kv_dim_v, "v"), _stream(stream))
 
     def attend_head_group(self, layer, kvh, queries, q_heads, hd, vd, start, end, scale,
                           softcap=0.0):
-        queries = np.ascontiguousarray(queries, dtype=np.float32)
+        queries = _host_f32(queries, q_heads * hd, "attend_head_group queries")
         out = np.empty(q_heads * vd, np.float32)
         call("gllm_hip_attend_group", self.handle, layer, kvh, _np_ptr(queries), q_heads, hd, vd,
              start, end, scale, softcap, _np_ptr(out))
@@ -274,6 +324,7 @@ class KVCacheF16:
 
     def attend_dev(self, layer, q, n_heads, n_kv_heads, hd, start, end, scale, out,
                    mode=ATTN_EXACT, stream=None):
-        call("gllm_hip_attend_dev", self.handle, layer, _dev_ptr(q), n_heads, n_kv_heads, hd,
-             start, end, scale, mode, _dev_ptr(out), _stream(stream))
+        call("gllm_hip_attend_dev", self.handle, layer, _dev(q, "f32", n_heads * hd, "q"), n_heads,
+             n_kv_heads, hd, start, end, scale, mode, _dev(out, "f32", n_heads * hd, "out"),
+             _stream(stream))
         return out

@@ -62,6 +62,7 @@ struct gllm_hip_model {
     int* h_pos = nullptr;          // pinned staging for it
     hipGraphExec_t decode_graph = nullptr;  // one decode step, captured after a first eager step
     int last_p = 0;
+    float attn_scale = 0.0f;  // llama.attention.scale; 0 = 1/sqrt(head_dim)
     // repeat penalty over the trailing token window (runtime.go:1035 and
     // 1089-1093): ids of the last `window` tokens seen, oldest first
     float penalty = 1.0f;
@@ -264,7 +265,8 @@ static int forward(gllm_hip_model* m, int pos0, int p, const int* d_pos = nullpt
     const auto& c = m->cfg;
     hipStream_t s = m->stream;
     const int hd = c.head_dim, kvd = c.n_kv_heads * hd;
-    const float scale = (float)(1.0 / sqrt((double)hd));
+    // config.AttentionScale, else float32(1/sqrt(headDim)) (model.go:2685-2688)
+    const float scale = m->attn_scale != 0.0f ? m->attn_scale : (float)(1.0 / sqrt((double)hd));
     const size_t norm_lds = (size_t)c.dim * 4;
     hipLaunchKernelGGL(embed_q4k_kernel, dim3(p), dim3(256), 0, s, m->tok_embd->d_data,
                        m->tok_embd->row_bytes, c.dim, m->d_tokens, m->x);
@@ -326,6 +328,11 @@ int model_adopt_weight(gllm_hip_model* m, gllm_hip_weight* w) {
     if (!m || !w) return fail(GLLM_EINVAL, "model_adopt_weight: null argument");
     m->owned.push_back(w);
     return GLLM_OK;
+}
+
+void model_set_attn_scale(gllm_hip_model* m, float scale) {
+    m->attn_scale = scale;
+    drop_decode_graph(m);
 }
 
 static bool penalty_on(const gllm_hip_model* m) { return m->penalty != 1.0f && m->window > 0; }
@@ -559,6 +566,10 @@ int gllm_hip_model_prefill(gllm_hip_model* m, const uint32_t* tokens, int n, int
     const int chunk = 64;
     GLLM_TRY(ensure_buffers(m, std::min(n, chunk)));
     hipStream_t s = m->stream;
+    // a prefill from position 0 starts a request: its window is the tail of
+    // this prompt (recentTokenWindowInto, runtime.go:1035), not the previous
+    // request's tokens; a later start continues the same request's window
+    if (start_pos == 0) m->recent.clear();
     for (int i = 0; i < n; i++) push_recent(m, tokens[i]);
     GLLM_TRY(upload_recent(m));
     for (int c0 = 0; c0 < n; c0 += chunk) {

@@ -30,6 +30,7 @@
 
 namespace gllm {
 int model_adopt_weight(gllm_hip_model* m, gllm_hip_weight* w);
+void model_set_attn_scale(gllm_hip_model* m, float scale);
 }
 
 namespace {
@@ -667,8 +668,53 @@ gllm_hip_model* gllm_hip_model_from_gguf(const gllm_hip_gguf* g, int max_len) {
         return nullptr;
     }
     c.vocab = (int)g->tensors[te].dims[1];
+    // ConfigFromGGUF / LoadModel (model.go:400-452, 1728-1756, 1866-1869)
+    // read further llama keys that change the graph.  This decoder runs the
+    // plain llama graph only, so a file that sets any of them to a
+    // non-default value is refused rather than decoded into other tokens.
+    auto present = [&](const char* k) { return find_meta(g, k) != nullptr; };
+    const char* why = nullptr;
+    if (present("llama.rope.dimension_count") &&
+        (int)u32("llama.rope.dimension_count", 0) != c.head_dim)
+        why = "llama.rope.dimension_count != head_dim (partial rotary)";
+    else if (present("llama.attention.value_length") &&
+             (int)u32("llama.attention.value_length", 0) != c.head_dim)
+        why = "llama.attention.value_length != head_dim";
+    else if (f32("llama.attention.temperature_scale", 0.0f) != 0.0f)
+        why = "llama.attention.temperature_scale";
+    else if (u32("llama.attention.sliding_window", 0) > 0 &&
+             (int)u32("llama.attention.sliding_window", 0) < c.max_len)
+        why = "llama.attention.sliding_window";
+    else if (f32("llama.attn_logit_softcapping", 0.0f) != 0.0f)
+        why = "llama.attn_logit_softcapping";
+    else if (f32("llama.final_logit_softcapping", 0.0f) != 0.0f)
+        why = "llama.final_logit_softcapping";
+    else if (f32("llama.embedding_scale", 0.0f) != 0.0f && f32("llama.embedding_scale", 0.0f) != 1.0f)
+        why = "llama.embedding_scale";
+    else if (f32("llama.residual_scale", 1.0f) != 0.0f && f32("llama.residual_scale", 1.0f) != 1.0f)
+        why = "llama.residual_scale";
+    else if (f32("llama.logit_scale", 1.0f) != 0.0f && f32("llama.logit_scale", 1.0f) != 1.0f)
+        why = "llama.logit_scale";
+    else if (tensor_index(g, "rope_factors_long.weight") >= 0 ||
+             tensor_index(g, "rope_factors_short.weight") >= 0)
+        why = "rope_factors_{long,short}.weight";
+    else {
+        const char* st = nullptr;
+        size_t sl = 0;
+        if (gllm_hip_gguf_get_str(g, "llama.rope.scaling.type", -1, &st, &sl) == GLLM_OK &&
+            std::string(st, sl) == "yarn" && f32("llama.rope.scaling.factor", 1.0f) > 1.0f &&
+            u32("llama.rope.scaling.original_context_length", 0) > 0)
+            why = "llama.rope.scaling.type = yarn";
+    }
+    if (why) {
+        fail(GLLM_EUNSUP, "gllm_hip_model_from_gguf: %s is not supported by this decoder", why);
+        return nullptr;
+    }
     gllm_hip_model* m = gllm_hip_model_new(&c);
     if (!m) return nullptr;
+    // llama.attention.scale replaces 1/sqrt(head_dim) when set (model.go:2685-2688)
+    if (f32("llama.attention.scale", 0.0f) != 0.0f)
+        gllm::model_set_attn_scale(m, f32("llama.attention.scale", 0.0f));
     auto load = [&](const std::string& name, int layer, int slot) -> gllm_hip_weight* {
         gllm_hip_weight* w = gllm_hip_gguf_load_weight(g, name.c_str());
         if (!w) return nullptr;

@@ -268,11 +268,14 @@ class GGUFFile:
         return Weight(h, info.dtype, rows, info.dims[0])
 
 
-def write_llama_gguf(path, model: dict, alignment: int = 32, name: str = "synthetic llama"):
+def write_llama_gguf(path, model: dict, alignment: int = 32, name: str = "synthetic llama",
+                     extra_meta: dict | None = None, extra_tensors=()):
     """Write a model dict of the tests' / benchmark's builder (GGUF-layout
     tensor bytes plus "config") as a llama GGUF file with llama.cpp's tensor
     names and hyperparameter keys (the layout ConfigFromGGUF / LoadModel
-    read, model.go:328-420, 1872-2090)."""
+    read, model.go:328-420, 1872-2090).  extra_meta ({key: MetaValue})
+    and extra_tensors ((name, dims, dtype, bytes) tuples) are added as given;
+    a config "attn_scale" is written as llama.attention.scale."""
     cfg = model["config"]
     dim, hidden, nl = cfg["dim"], cfg["hidden"], cfg["n_layers"]
     qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
@@ -291,6 +294,9 @@ def write_llama_gguf(path, model: dict, alignment: int = 32, name: str = "synthe
         "llama.attention.layer_norm_rms_epsilon": MetaValue("f32", float(cfg["rms_eps"])),
         "llama.vocab_size": MetaValue("u32", cfg["vocab"]),
     }
+    if cfg.get("attn_scale"):
+        meta["llama.attention.scale"] = MetaValue("f32", float(cfg["attn_scale"]))
+    meta.update(extra_meta or {})
     F32 = 0
     planned, blobs = [], []
 
@@ -313,6 +319,8 @@ def write_llama_gguf(path, model: dict, alignment: int = 32, name: str = "synthe
             t = types[l][order.index(key)] if types is not None else cfg["layer_type"]
             add(f"blk.{l}.{tname}.weight", (cols, rows), t, model[key][l])
         add(f"blk.{l}.ffn_norm.weight", (dim,), F32, np.asarray(model["ffn_norm"][l], np.float32))
+    for tname, dims, dtype, data in extra_tensors:
+        add(tname, dims, dtype, data)
     with open(path, "wb") as f:
         w = GGUFWriter(f, meta, planned, alignment)
         for b in blobs:

@@ -1572,7 +1572,7 @@ static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
     long er = ref_row_bytes(m->emb_type, dim);
     ref_dequant_row(m->emb_type, m->tok_embd + (long)token * er, dim, s->x);
     ref_rope_sincos(pos, s->inv_freq, hd / 2, s->sinv, s->cosv);
-    float scale = (float)(1.0 / sqrt((double)hd));
+    float scale = m->attn_scale != 0.0f ? m->attn_scale : (float)(1.0 / sqrt((double)hd));
     for (int l = 0; l < m->n_layers; l++) {
         ref_rmsnorm(s->x, m->attn_norm[l], m->rms_eps, dim, s->xn);
         llama_matvec(s, llama_type(m, l, 0), m->wq[l], s->xn, m->n_heads * hd, dim, s->q);

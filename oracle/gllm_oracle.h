@@ -123,6 +123,9 @@ typedef struct ref_llama {
     /* NULL, or the type of each matrix, n_layers * 7 in the order wq wk wv wo
      * w1 w2 w3 (mixed files such as Q4_K_M, whose attn_v / ffn_down are Q6_K) */
     const int* types;
+    /* config.AttentionScale (llama.attention.scale); 0 = 1/sqrt(head_dim)
+     * (model.go:2685-2688) */
+    float attn_scale;
 } ref_llama;
 
 typedef struct ref_llama_state ref_llama_state;

@@ -333,7 +333,8 @@ class _RefLlama(C.Structure):
         ("tok_embd", C.c_void_p), ("output", C.c_void_p), ("out_norm", C.c_void_p),
         ("layer_type", C.c_int),
     ] + [(n, C.c_void_p) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3",
-                                    "attn_norm", "ffn_norm", "types")]
+                                    "attn_norm", "ffn_norm", "types")] + [
+        ("attn_scale", C.c_float)]
 
 
 class Llama:
@@ -359,6 +360,7 @@ class Llama:
         s.max_len = max_len
         s.rms_eps = cfg["rms_eps"]
         s.rope_theta = cfg["rope_theta"]
+        s.attn_scale = cfg.get("attn_scale", 0.0)
         s.emb_type, s.out_type, s.layer_type = cfg["emb_type"], cfg["out_type"], cfg["layer_type"]
         for k in ("tok_embd", "output", "out_norm"):
             a = np.ascontiguousarray(model[k])

@@ -238,3 +238,71 @@ def test_llama_file_layout(tmp_path):
         assert np.frombuffer(g.tensor_bytes("blk.0.attn_norm.weight"), np.float32).tolist() == [1.0] * 256
     with pytest.raises(gguf.GllmError):
         GGUFFile(tmp_path / "missing.gguf")
+
+
+REFUSED = [
+    ("llama.rope.dimension_count", ("u32", 32)),
+    ("llama.attention.value_length", ("u32", 32)),
+    ("llama.attention.temperature_scale", ("f32", 0.1)),
+    ("llama.attention.sliding_window", ("u32", 16)),
+    ("llama.attn_logit_softcapping", ("f32", 30.0)),
+    ("llama.final_logit_softcapping", ("f32", 30.0)),
+    ("llama.embedding_scale", ("f32", 2.0)),
+    ("llama.residual_scale", ("f32", 0.5)),
+    ("llama.logit_scale", ("f32", 0.5)),
+    ("yarn", None),
+    ("rope_factors_long.weight", None),
+]
+
+
+@pytest.mark.parametrize("key,value", REFUSED, ids=[k for k, _ in REFUSED])
+def test_model_from_gguf_refuses_graph_changing_keys(tmp_path, key, value):
+    """Keys of ConfigFromGGUF / LoadModel (model.go:400-452, 1728-1756,
+    1866-1869) that change the llama graph away from the plain one this
+    decoder runs make gllm_hip_model_from_gguf fail with GLLM_EUNSUP, naming
+    the key, before any device work (so this runs without a GPU)."""
+    from conftest import tiny_llama
+    from gopherllm_amd import _lib, gguf
+    m = tiny_llama(seed=2, n_layers=1, dim=256, hidden=512, n_heads=4, n_kv_heads=1, head_dim=64,
+                   vocab=300)
+    extra, tensors = {}, ()
+    if key == "yarn":
+        extra = {"llama.rope.scaling.type": gguf.MetaValue("str", "yarn"),
+                 "llama.rope.scaling.factor": gguf.MetaValue("f32", 4.0),
+                 "llama.rope.scaling.original_context_length": gguf.MetaValue("u32", 1024)}
+    elif key.endswith(".weight"):
+        tensors = ((key, (32,), 0, np.ones(32, np.float32)),)
+    else:
+        extra = {key: gguf.MetaValue(*value)}
+    path = gguf.write_llama_gguf(tmp_path / "x.gguf", m, extra_meta=extra, extra_tensors=tensors)
+    f = gguf.GGUFFile(str(path))
+    L = _lib.load()
+    h = L.gllm_hip_model_from_gguf(f.handle, 64)
+    assert not h
+    msg = _lib.last_error()
+    assert "not supported" in msg and (key.split(".")[-1] in msg or key in msg), msg
+    f.close()
+
+
+def test_model_from_gguf_accepts_default_valued_keys(tmp_path):
+    """The same keys at their defaults (rope over the whole head, value
+    length = head_dim, unit scales, no window) pass the check: the call then
+    fails only where this host has no device, not on the key check."""
+    from conftest import tiny_llama
+    from gopherllm_amd import _lib, gguf
+    m = tiny_llama(seed=2, n_layers=1, dim=256, hidden=512, n_heads=4, n_kv_heads=1, head_dim=64,
+                   vocab=300)
+    extra = {"llama.rope.dimension_count": gguf.MetaValue("u32", 64),
+             "llama.attention.value_length": gguf.MetaValue("u32", 64),
+             "llama.residual_scale": gguf.MetaValue("f32", 1.0),
+             "llama.logit_scale": gguf.MetaValue("f32", 1.0),
+             "llama.attention.sliding_window": gguf.MetaValue("u32", 0)}
+    path = gguf.write_llama_gguf(tmp_path / "ok.gguf", m, extra_meta=extra)
+    f = gguf.GGUFFile(str(path))
+    L = _lib.load()
+    h = L.gllm_hip_model_from_gguf(f.handle, 64)
+    if h:
+        L.gllm_hip_model_release(h)
+    else:
+        assert "not supported" not in _lib.last_error()
+    f.close()

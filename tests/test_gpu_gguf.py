@@ -127,3 +127,29 @@ def test_decoder_from_mixed_gguf_matches_oracle(hip, tmp_path):
     want = ref.Llama(m, 64).generate(prompt, 10)
     assert np.array_equal(got, want), (got, want)
     dec.release()
+
+
+def test_decoder_from_gguf_attention_scale(hip, tmp_path):
+    """llama.attention.scale replaces 1/sqrt(head_dim) (config.AttentionScale,
+    model.go:2685-2688): tokens and KV rows equal the oracle run with the
+    same scale, and differ from the default-scale run."""
+    from gopherllm_amd import gguf
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = tiny_llama(seed=36, n_layers=2, dim=512, hidden=1024, n_heads=8, n_kv_heads=2,
+                   head_dim=64, vocab=1500)
+    m["config"] = dict(m["config"], attn_scale=0.5)
+    path = gguf.write_llama_gguf(tmp_path / "scale.gguf", m)
+    prompt = np.random.default_rng(37).integers(0, 1500, 30)
+    print("from_gguf attention.scale generate", flush=True)
+    dec = LlamaDecoder.from_gguf(str(path), 64)
+    got = dec.generate(prompt, 12)
+    cpu = ref.Llama(m, 64)
+    want = cpu.generate(prompt, 12)
+    assert np.array_equal(got, want), (got, want)
+    k, _ = dec.kv_cache().read(1, 0, 41)
+    assert np.array_equal(k, cpu.kcache(1, 64)[:41])
+    default = dict(m, config=dict(m["config"], attn_scale=0.0))
+    cpu0 = ref.Llama(default, 64)
+    cpu0.generate(prompt, 12)
+    assert not np.array_equal(cpu0.kcache(1, 64)[:41], k)
+    dec.release()

@@ -93,6 +93,35 @@ def test_generate_with_repeat_penalty(hip):
         gpu.set_repeat_penalty(1.5, -1)
 
 
+def test_back_to_back_requests_do_not_share_the_penalty_window(hip):
+    """Each request's window is the tail of its own prompt
+    (recentTokenWindowInto, runtime.go:1035): a second request on the same
+    model, prefilled from position 0 without another set_repeat_penalty,
+    chooses what a fresh oracle chooses for that prompt alone; a request
+    after set_repeat_penalty(1) is plain greedy."""
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = tiny_llama(seed=4, n_layers=3, dim=512, hidden=1536, n_heads=8, n_kv_heads=2, head_dim=64,
+                   vocab=3000)
+    rng = np.random.default_rng(15)
+    pa, pb = rng.integers(0, 3000, 50), rng.integers(0, 3000, 40)
+    gpu = LlamaDecoder.from_host_model(m, 128)
+
+    def fresh(prompt, pen, win):
+        cpu = ref.Llama(m, 128)
+        if pen != 1.0:
+            cpu.set_repeat_penalty(pen, win)
+        return cpu.generate(prompt, 20)
+
+    gpu.set_repeat_penalty(2.5, 16)
+    print("request A, penalty 2.5 window 16", flush=True)
+    assert np.array_equal(gpu.generate(pa, 20), fresh(pa, 2.5, 16))
+    print("request B, same setting, no reset", flush=True)
+    assert np.array_equal(gpu.generate(pb, 20), fresh(pb, 2.5, 16))
+    gpu.set_repeat_penalty(1.0, 64)
+    print("request A again, penalty 1", flush=True)
+    assert np.array_equal(gpu.generate(pa, 20), fresh(pa, 1.0, 64))
+
+
 def test_decode_8b_layer_shapes_bit_exact(hip):
     """Two layers at the 8B shapes (dim 4096, hidden 14336, 32 / 8 heads of
     128), the row kernels the full model runs (fused-quantiser Q4_K at 4096
