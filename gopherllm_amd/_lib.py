@@ -53,6 +53,7 @@ SIGNATURES = {
     "gllm_hip_argmax_penalized": (i32, [vp, vp, vp, i32, f32, vp]),
     "gllm_hip_argmax_penalized_dev": (i32, [vp, vp, vp, i32, f32, vp, vp]),
     "gllm_hip_matvec_dev": (i32, [vp, vp, i32, vp, i32, vp]),
+    "gllm_hip_matvec_dev_noalloc": (i32, [vp, vp, i32, vp, i32, vp]),
     "gllm_hip_matvec_multi_dev": (i32, [i32, vp, vp, i32, vp, vp, vp]),
     "gllm_hip_argmax_dev": (i32, [vp, vp, vp, vp]),
     "gllm_hip_act_bytes": (sz, [i32, i32]),

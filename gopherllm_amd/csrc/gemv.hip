@@ -1376,8 +1376,8 @@ int gemv_silu_f32(gllm_hip_weight* w, const float* gate, const float* up, int p,
     return run_gemv(1, ws, act, p, outs, nullptr, s, nullptr);
 }
 
-int matvec_multi(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float* const* outs,
-                 const int* strides, hipStream_t s, int scratch_slot) {
+// Argument checks shared by every device matvec entry point.
+int validate_matvec(int n, gllm_hip_weight* const* ws, int p, const int* strides) {
     for (int i = 0; i < n; i++) GLLM_TRY(validate_weight(ws[i]));
     for (int i = 1; i < n; i++)
         if (ws[i]->cols != ws[0]->cols)
@@ -1397,6 +1397,12 @@ int matvec_multi(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, fl
                                          "model.go:3213-3254)", ws[i]->type);
     for (int i = 0; i < n; i++)
         if (strides && strides[i] < ws[i]->rows) return fail(GLLM_EINVAL, "out stride < rows");
+    return GLLM_OK;
+}
+
+int matvec_multi(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float* const* outs,
+                 const int* strides, hipStream_t s, int scratch_slot) {
+    GLLM_TRY(validate_matvec(n, ws, p, strides));
     void* sc = thread_scratch(scratch_slot, act_bytes(ws[0]->cols, p), s);
     if (!sc) return scratch_error();
     return gemv_f32(n, ws, d_xs, p, outs, strides, sc, s);

@@ -158,6 +158,18 @@ int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token,
 int gllm_hip_argmax_penalized_dev(gllm_hip_weight* w, const float* d_x, const uint32_t* d_recent,
                                   int n_recent, float penalty, uint32_t* d_token, void* stream);
 
+/* gllm_hip_matvec_dev for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, results and
+ * errors as gllm_hip_matvec_dev; the quantised activations go to a fixed
+ * 4 MiB buffer in the library's device image (one per GPU, held until the
+ * process ends) instead of allocated scratch, so the call allocates
+ * nothing.  GLLM_EINVAL when gllm_hip_act_bytes(cols, p) exceeds 4 MiB.
+ * Every call on one GPU shares that buffer: calls that overlap on one GPU
+ * (other streams or host threads) race, and callers serialise them. */
+int gllm_hip_matvec_dev_noalloc(gllm_hip_weight* w, const float* d_xs, int p, float* d_outs,
+                                int out_stride, void* stream);
+
 /* Split form of the same call, for callers that quantise once and dot many
  * matrices (acquireQ8 + fillQ4KXSums/fillQ6KXSums16, kernels_amd64.go:246,
  * then dotQ4KRowsQ8 / dotQ6KRowsQ8 / dotQ8_0RowsQ8, kernels_amd64.go:268-285,
