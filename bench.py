@@ -58,9 +58,10 @@ def make_weights(g, torch, rows, cols, copies, seed):
     return ws
 
 
-def timed_graph(torch, body, reps):
-    """Capture body() once, replay it `reps` times between events; returns
-    (ms per replay)."""
+def timed_graph(torch, body, reps=1):
+    """Capture body() into a HIP graph on a side stream and return it.  The
+    eager warm-up runs on the same stream the capture uses, so any per-stream
+    scratch the library sizes on first use exists before the capture."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -68,11 +69,31 @@ def timed_graph(torch, body, reps):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=s):
         body()
     graph.replay()
     torch.cuda.synchronize()
     return graph
+
+
+def cpu_identity():
+    """Host CPU model, L3 size and usable cores, for the cpu_baseline record."""
+    model, l3 = "unknown", None
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        base = "/sys/devices/system/cpu/cpu0/cache"
+        for ent in sorted(os.listdir(base)):
+            if open(os.path.join(base, ent, "level")).read().strip() == "3":
+                l3 = open(os.path.join(base, ent, "size")).read().strip()
+    except OSError:
+        pass
+    return {"cpu": model, "l3": l3, "cores_usable": len(os.sched_getaffinity(0))}
 
 
 def run(args):
@@ -100,41 +121,46 @@ def run(args):
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
-    def full_steps():  # `copies` whole MatvecQ4KInto steps (gllm_hip_matvec_dev)
-        for w in weights:
-            w.matvec_dev(x.view(1, -1), out.view(1, -1))
+    def launches(ws):
+        def body():
+            for w in ws:
+                w.matvec_dev(x.view(1, -1), out.view(1, -1))
+        return body
 
-    # At this shape the row kernel quantises x itself (one launch per step),
-    # so the dominant kernel's launches are the steps themselves.
-    full = timed_graph(torch, full_steps, 1)
-    kern = full
+    # At this shape the row kernel quantises x itself: one step (one whole
+    # MatvecQ4KInto) is one launch of the dominant kernel.  A graph holds one
+    # rotation over the weight copies; a second graph holds the remainder, so
+    # exactly --warmup and --steps steps run.
+    rot = timed_graph(torch, launches(weights))
+    rem_graphs = {}
 
-    reps = max(1, math.ceil(args.steps / copies))
-    wreps = max(1, math.ceil(args.warmup / copies)) if args.warmup > 0 else 0
-    steps = reps * copies
-    for _ in range(wreps):
-        full.replay()
+    def run_steps(n):
+        for _ in range(n // copies):
+            rot.replay()
+        r = n % copies
+        if r:
+            if r not in rem_graphs:
+                rem_graphs[r] = timed_graph(torch, launches(weights[:r]))
+            rem_graphs[r].replay()
+
+    steps, warm = args.steps, args.warmup
+    if args.steps % copies:
+        rem_graphs[args.steps % copies] = timed_graph(torch, launches(weights[:args.steps % copies]))
+    run_steps(warm)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
-        full.replay()
+    run_steps(steps)
     e1.record()
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / steps
-
-    for _ in range(wreps):
-        kern.replay()
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(reps):
-        kern.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    kernel_us = e0.elapsed_time(e1) / steps * 1e3
+    # one launch per step: the kernel's average launch duration over the
+    # timed region (HIP events on the launch stream; includes the dispatch
+    # gap between back-to-back launches)
+    kernel_us = ms_per_step * 1e3
 
     # replayed graphs still produce the eager result
-    full.replay()
+    rot.replay()
     torch.cuda.synchronize()
     last = weights[-1].matvec_into(xh)
     assert np.array_equal(out.cpu().numpy().view(np.uint32), last.view(np.uint32))
@@ -152,7 +178,7 @@ def run(args):
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": wreps * copies,
+        "warmup": warm,
         "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -175,6 +201,9 @@ def run(args):
             "traffic": traffic,
             "kernel": "gemv_q4k_kernel (fused Q8K quantisation, one launch per step)",
             "kernel_avg_us": round(kernel_us, 3),
+            "kernel_timing": "HIP events on the launch stream around the timed region: "
+                             f"{steps} back-to-back launches replayed from HIP graphs "
+                             "(dispatch gaps included); launches per step = 1",
             "bytes_per_launch": nbytes,
         },
     }
@@ -209,9 +238,11 @@ def cpu_baseline(weights, xh, rows, cols, seconds, torch):
         if el >= seconds:
             break
     gbs = alg_bytes(rows, cols) * n / el / 1e9
-    return {"value": round(gbs, 2), "unit": "GB/s", "cores": cores, "kind": kind,
-            "sample": f"{n} MatvecQ4KInto calls (14336x4096 Q4_K, AVX2 port of kernels_amd64.s, "
-                      f"{len(host)} rotating weight copies) in {el:.1f} s"}
+    rec = {"value": round(gbs, 2), "unit": "GB/s", "cores": cores, "kind": kind,
+           "sample": f"{n} MatvecQ4KInto calls (14336x4096 Q4_K, AVX2 port of kernels_amd64.s, "
+                     f"{len(host)} rotating weight copies) in {el:.1f} s"}
+    rec.update(cpu_identity())
+    return rec
 
 
 def decode_bench(args):
@@ -260,23 +291,50 @@ def decode_bench(args):
         "model_build_s": round(build_s, 2),
     }
     if not args.no_cpu_baseline:
-        from oracle import oracle as ref
-
-        m = synth.host_model(d)
+        out["cpu_baseline"] = decode_cpu_baseline(d, prompt, toks, P, N, args.cpu_seconds)
+    else:
         d.release()
-        cpu = ref.Llama(m, P + N, fast=True)
-        cores = len(os.sched_getaffinity(0))
-        tok = cpu.prefill(prompt[:1])[0]
-        steps, c0 = 0, time.perf_counter()
-        while steps < 64 and (steps < 4 or time.perf_counter() - c0 < args.cpu_seconds):
-            tok = cpu.decode(tok, 1 + steps)[0]
-            steps += 1
-        el = time.perf_counter() - c0
-        out["cpu_baseline"] = {"value": round(steps / el, 3), "unit": "tok/s", "cores": cores,
-                               "kind": "port",
-                               "sample": f"{steps} greedy decode steps at positions 1..{steps} "
-                                         f"(AVX2 port of kernels_amd64.s, same weights) in {el:.1f} s"}
     return out
+
+
+def decode_cpu_baseline(d, prompt, toks, P, N, seconds):
+    """The oracle's decoder (row dots through the AVX2 port of
+    kernels_amd64.s) at the positions the GPU decode was timed at.  Its KV
+    cache for positions 0..P-1 is the device's (bit-identical to the
+    oracle's own prefill, which the GPU tests check), so the CPU starts at
+    position P without a 512-token CPU prefill; each CPU step must return
+    the GPU's token."""
+    import numpy as np
+
+    from gopherllm_amd import synth
+    from oracle import oracle as ref
+
+    m = synth.host_model(d)
+    kv = d.kv_cache()
+    ks = [kv.read(l, 0, P) for l in range(d.config["n_layers"])]
+    d.release()
+    cpu = ref.Llama(m, P + N, fast=True)
+    for l, (k16, v16) in enumerate(ks):
+        cpu.set_kv(l, 0, k16, v16)
+    del ks
+    cores = len(os.sched_getaffinity(0))
+    steps, c0 = 0, time.perf_counter()
+    tok = int(toks[0])
+    while steps < N - 1 and (steps < 4 or time.perf_counter() - c0 < seconds):
+        tok = cpu.decode(tok, P + steps)[0]
+        if tok != int(toks[steps + 1]):
+            raise SystemExit(f"CPU decode step at position {P + steps} returned {tok}, "
+                             f"GPU {int(toks[steps + 1])}")
+        steps += 1
+    el = time.perf_counter() - c0
+    rec = {"value": round(steps / el, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+           "sample": f"{steps} greedy decode steps at positions {P}..{P + steps - 1} after the "
+                     f"{P}-token prompt (oracle decoder, AVX2 port of kernels_amd64.s, same "
+                     f"weights, KV rows 0..{P - 1} from the device), each step's token equal to "
+                     f"the GPU's, in {el:.1f} s"}
+    rec.update(cpu_identity())
+    cpu.close()
+    return rec
 
 
 def suite(args):
@@ -320,25 +378,28 @@ def suite(args):
         torch.cuda.synchronize()
         return ws, wb
 
-    for qtype in (g.TYPE_Q4_K, g.TYPE_Q6_K, g.TYPE_Q8_0) if "gemv" in only else ():
-        for rows, cols in ((14336, 4096), (4096, 14336)):
-            ws, wb = weights_for(qtype, rows, cols)
-            for p in (1, 8):
-                x = torch.empty((p, cols), dtype=torch.float32, device="cuda")
-                g.fill_normal_dev(x, 7, 1.0)
-                out = torch.empty((p, rows), dtype=torch.float32, device="cuda")
+    gemv_cases = [(g.TYPE_Q4_K, 4096, 4096)]  # configs[0]
+    gemv_cases += [(q, r, c) for q in (g.TYPE_Q4_K, g.TYPE_Q6_K, g.TYPE_Q8_0)
+                   for r, c in ((14336, 4096), (4096, 14336))]  # configs[1]
+    for qtype, rows, cols in gemv_cases if "gemv" in only else ():
+        ws, wb = weights_for(qtype, rows, cols)
+        for p in (1, 8):
+            x = torch.empty((p, cols), dtype=torch.float32, device="cuda")
+            g.fill_normal_dev(x, 7, 1.0)
+            out = torch.empty((p, rows), dtype=torch.float32, device="cuda")
 
-                def body():
-                    for w in ws:
-                        w.matvec_dev(x, out)
+            def body():
+                for w in ws:
+                    w.matvec_dev(x, out)
 
-                us = graph_time(body, 20) / len(ws)
-                nbytes = wb + p * (4 * cols + 4 * rows)
-                print(json.dumps({"suite": "configs[1] gemv", "type": qnames[qtype], "rows": rows,
-                                  "cols": cols, "batch": p, "us": round(us, 3),
-                                  "GB_s": round(nbytes / us / 1e3, 1),
-                                  "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
-            del ws
+            us = graph_time(body, 20) / len(ws)
+            nbytes = wb + p * (4 * cols + 4 * rows)
+            cfg = "configs[0] gemv" if rows == cols else "configs[1] gemv"
+            print(json.dumps({"suite": cfg, "type": qnames[qtype], "rows": rows,
+                              "cols": cols, "batch": p, "us": round(us, 3),
+                              "GB_s": round(nbytes / us / 1e3, 1),
+                              "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
+        del ws
 
     # formats beyond Q4_K / Q6_K / Q8_0: random codes with valid f16 scales
     # (the block layouts of gguf.go:241-297), gate/up shape at batch 1 and 8,
@@ -426,6 +487,55 @@ def suite(args):
         kv.release()
 
 
+def launch_floor(args):
+    """Per-node cost of short launches replayed back to back from one HIP
+    graph (HIP events on the launch stream, no profiler): an empty one-thread
+    kernel, a 64 KB elementwise fill over 64 workgroups, a 16 KB copy, and the
+    smallest Q4_K matvec (256 x 256, one workgroup, quantiser fused).  This
+    is the fixed cost each launch of the decode step pays before its own
+    work."""
+    import torch
+
+    import gopherllm_amd as g
+
+    g.load()
+    n = 500
+    a = torch.zeros(16384, dtype=torch.float32, device="cuda")
+    b = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    c = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    raw = torch.empty(256 * 144, dtype=torch.uint8, device="cuda")
+    tmp = torch.empty((256, 256), dtype=torch.float32, device="cuda")
+    g.fill_normal_dev(tmp, 5, 0.02)
+    g.quantize_rows_dev(g.TYPE_Q4_K, tmp, raw)
+    w = g.Weight.from_device(raw, g.TYPE_Q4_K, 256, 256)
+    x = torch.empty((1, 256), dtype=torch.float32, device="cuda")
+    g.fill_normal_dev(x, 6, 1.0)
+    y = torch.empty((1, 256), dtype=torch.float32, device="cuda")
+    bodies = {
+        "empty kernel (1 thread)": lambda: torch.cuda._sleep(0),
+        "fill 64 KB": lambda: a.fill_(1.0),
+        "copy 16 KB": lambda: b.copy_(c),
+        "Q4_K matvec 256x256": lambda: w.matvec_dev(x, y),
+    }
+    for name, fn in bodies.items():
+        def body():
+            for _ in range(n):
+                fn()
+        graph = timed_graph(torch, body)
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / (5 * n) * 1e3
+        print(json.dumps({"launch_floor": name, "nodes_per_graph": n, "us_per_node": round(us, 3)}),
+              flush=True)
+
+
 def profile_run():
     """Eager launches for rocprofv3 counter passes (no graphs, no timing):
     20 row-kernel launches over the rotating copies, then 5 plain device
@@ -464,6 +574,8 @@ def main():
     ap.add_argument("--ctx", type=int, default=0, help="suite attention: only this context")
     ap.add_argument("--profile-run", action="store_true",
                     help="eager launches for rocprofv3 counter collection")
+    ap.add_argument("--launch-floor", action="store_true",
+                    help="per-node cost of short launches replayed from one HIP graph")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
@@ -475,6 +587,9 @@ def main():
     args = ap.parse_args()
     if args.profile_run:
         profile_run()
+        return
+    if args.launch_floor:
+        launch_floor(args)
         return
     if args.suite:
         suite(args)

@@ -48,16 +48,42 @@ def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source into libgllm_hip.so; returns its path."""
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    """Compile every HIP source into libgllm_hip.so; returns its path.  Each
+    source is compiled to an object in parallel (no device code crosses
+    translation units), then one link step writes the library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    cc = hipcc()
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+
+    def compile_one(src):
+        obj = os.path.join(objdir, os.path.basename(src)[:-4] + ".o")
+        cmd = [cc] + compile_flags + ["-c", src, "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        return obj, res
+
+    srcs = sources()
+    jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(jobs) as ex:
+        results = list(ex.map(compile_one, srcs))
+    failed = [(o, r) for o, r in results if r.returncode != 0]
+    for o, r in failed:
+        sys.stderr.write(r.stdout + r.stderr)
+    if failed:
+        raise RuntimeError(f"hipcc failed for {[os.path.basename(o) for o, _ in failed]}")
     tmp = LIB + ".tmp"
-    cmd = [hipcc()] + FLAGS + sources() + ["-o", tmp]
+    cmd = [cc] + FLAGS + [o for o, _ in results] + ["-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
+        raise RuntimeError(f"hipcc link failed with exit code {res.returncode}")
     os.replace(tmp, LIB)
     return LIB
 

@@ -413,6 +413,17 @@ class Llama:
         ptr = lib().ref_llama_kcache(self.state, layer)
         return np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_uint16)), (max_len, kvd)).copy()
 
+    def set_kv(self, layer, pos0, k16, v16):
+        """Write f16 K/V rows (bit arrays [n][kv_dim]) into the state's cache at
+        positions pos0.. (for starting a decode from another engine's prefill)."""
+        kvd = self.cfg["n_kv_heads"] * self.cfg["head_dim"]
+        for get, rows in ((lib().ref_llama_kcache, k16), (lib().ref_llama_vcache, v16)):
+            rows = np.ascontiguousarray(rows, np.uint16)
+            assert rows.ndim == 2 and rows.shape[1] == kvd
+            assert 0 <= pos0 and pos0 + rows.shape[0] <= self._s.max_len
+            base = get(self.state, layer)
+            C.memmove(base + 2 * pos0 * kvd, rows.ctypes.data, rows.nbytes)
+
     def vcache(self, layer, max_len):
         kvd = self.cfg["n_kv_heads"] * self.cfg["head_dim"]
         ptr = lib().ref_llama_vcache(self.state, layer)

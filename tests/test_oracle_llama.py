@@ -394,3 +394,23 @@ def test_rope_dot_depends_only_on_relative_position(oracle_lib):
     for d in (1, 50, 400):
         assert abs(rot(q, 7 + d) @ rot(k, 3 + d) - base) < 2e-5 * np.abs(q).sum()
     assert abs(rot(q, 7) @ rot(k, 7) - rot(q, 7) @ rot(k, 3)) > 1e-2
+
+
+def test_oracle_decode_resumes_from_copied_cache(oracle_lib):
+    """set_kv: a second state whose cache rows 0..P-1 are copied from a state
+    that ran the prompt decodes the same tokens and hidden states from
+    position P (the benchmark's CPU baseline starts decoding that way)."""
+    m = sensitive_llama(**CONFIGS[0])
+    prompt = np.random.default_rng(9).integers(0, m["config"]["vocab"], 11)
+    max_len, P = 24, len(prompt)
+    src, dst = ref.Llama(m, max_len), ref.Llama(m, max_len)
+    tok, _ = src.prefill(prompt)
+    for l in range(m["config"]["n_layers"]):
+        dst.set_kv(l, 0, src.kcache(l, max_len)[:P], src.vcache(l, max_len)[:P])
+    ta = tb = tok
+    for i in range(5):
+        ta, ha = src.decode(ta, P + i)
+        tb, hb = dst.decode(tb, P + i)
+        assert ta == tb and np.array_equal(ha.view(np.uint32), hb.view(np.uint32)), i
+    with pytest.raises(AssertionError):
+        dst.set_kv(0, max_len - 2, src.kcache(0, max_len)[:3], src.vcache(0, max_len)[:3])
