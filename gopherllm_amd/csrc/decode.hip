@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void embed_q4k_kernel(const uint8_t* __restric
     const uint8_t* row = table + (size_t)tokens[t] * rb;
     for (int e = threadIdx.x; e < dim; e += blockDim.x) {
         const int b = e >> 8, i = e & 255;
-        const uint8_t* blk = row + (size_t)b * 144;
+        const uint8_t* blk = row + q4k_hdr_off(b);
         const int j = i >> 5;  // sub-block
         const uint8_t* sc = blk + 4;
         int s, m;
@@ -102,8 +102,9 @@ __global__ __launch_bounds__(256) void embed_q4k_kernel(const uint8_t* __restric
         const float d = f16_bits_to_f32(blk[0] | (blk[1] << 8));
         const float dmin = f16_bits_to_f32(blk[2] | (blk[3] << 8));
         const int chunk = i >> 6, l = i & 31, hi = (i >> 5) & 1;
-        // the upload repack moved nibble byte 32*chunk + l to 16*(l/4) + 4*chunk + l%4
-        const uint8_t qb = blk[16 + (l >> 2) * 16 + chunk * 4 + (l & 3)];
+        // the upload repack moved nibble byte 32*chunk + l of block b to
+        // q4k_nib_off(B, b) + 16*(l/4) + 4*chunk + l%4
+        const uint8_t qb = row[q4k_nib_off(dim >> 8, b) + (l >> 2) * 16 + chunk * 4 + (l & 3)];
         const int qv = hi ? (qb >> 4) : (qb & 0x0f);
         const float d1 = d * (float)s;
         const float min1 = dmin * (float)m;

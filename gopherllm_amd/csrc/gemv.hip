@@ -75,8 +75,10 @@ __device__ __forceinline__ int locate(const GemvJob& j, int wg, int* wi) {
 // nibbles] (simd.go:1530-1557).  AVX2 lane k covers bytes 4k..4k+3 of each of
 // the four 32-byte nibble chunks (Q4KQ8CHUNK, kernels_amd64.s:443-455).  The
 // upload repack stores those 16 bytes contiguously (nibble byte 32s + 4k + j
-// moves to 16k + 4s + j; header and block size unchanged), so a lane reads
-// its share of a block with one 16-byte load.
+// moves to 16k + 4s + j) and moves the row's headers in front of its nibble
+// blocks (q4k_hdr_off / q4k_nib_off; block size unchanged), so a lane reads
+// its share of a block with one 16-byte load and the headers of eight blocks
+// with another.
 //
 // G lanes share one AVX2 lane k of one row: lane g takes blocks g, g+G, ...
 // and every round of G blocks advances the sequential fp32 chains through
@@ -138,13 +140,11 @@ __device__ __forceinline__ s16x2 sc_pair(uint32_t s) {
 }
 __device__ __forceinline__ int q4k_lane_sum(int t0, int t1, int t2, int t3, int t4, int t5, int t6,
                                             int t7, uint32_t sc03, uint32_t sc47) {
-    const int a = __builtin_amdgcn_sdot2(pack16(t0, t1), sc_pair<0>(sc03),
-                                         __builtin_amdgcn_sdot2(pack16(t2, t3), sc_pair<1>(sc03), 0, false),
-                                         false);
-    const int b = __builtin_amdgcn_sdot2(pack16(t4, t5), sc_pair<0>(sc47),
-                                         __builtin_amdgcn_sdot2(pack16(t6, t7), sc_pair<1>(sc47), 0, false),
-                                         false);
-    return a + b;
+    // one accumulator chain (the integer sum is exact in any order)
+    int acc = __builtin_amdgcn_sdot2(pack16(t0, t1), sc_pair<0>(sc03), 0, false);
+    acc = __builtin_amdgcn_sdot2(pack16(t2, t3), sc_pair<1>(sc03), acc, false);
+    acc = __builtin_amdgcn_sdot2(pack16(t4, t5), sc_pair<0>(sc47), acc, false);
+    return __builtin_amdgcn_sdot2(pack16(t6, t7), sc_pair<1>(sc47), acc, false);
 }
 
 __device__ __forceinline__ uint32_t ubfe(uint32_t v, uint32_t off, uint32_t width) {
@@ -352,20 +352,60 @@ __device__ __forceinline__ void q4k_block(const uint4 h, const uint4 q, int b, i
     }
 }
 
+// Header of lane-local block J (mod 8) of this lane's row and G-slot: the
+// eight k-lanes of a (row, gi) group, G lanes apart, each loaded one block's
+// header; ds_swizzle (bit mode, inside 32-lane halves) reads lane k = J of
+// the group: and-mask keeps the row and gi bits, or-mask sets k.
+template <int G>
+constexpr int log2g() {
+    return G == 1 ? 0 : G == 2 ? 1 : 2;
+}
+template <int G, int J>
+__device__ __forceinline__ uint32_t hdr_bcast1(uint32_t v) {
+    constexpr int lg = log2g<G>();
+    constexpr int and_mask = 0x1f & ~(7 << lg);
+    constexpr int or_mask = J << lg;
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, and_mask | (or_mask << 5));
+}
+template <int G, int J>
+__device__ __forceinline__ uint4 hdr_bcast(uint4 v) {
+    return make_uint4(hdr_bcast1<G, J>(v.x), hdr_bcast1<G, J>(v.y), hdr_bcast1<G, J>(v.z),
+                      hdr_bcast1<G, J>(v.w));
+}
+template <int G>
+__device__ __forceinline__ uint4 hdr_of(uint4 v, int j) {  // j: compile-time after unrolling
+    switch (j & 7) {
+    case 0: return hdr_bcast<G, 0>(v);
+    case 1: return hdr_bcast<G, 1>(v);
+    case 2: return hdr_bcast<G, 2>(v);
+    case 3: return hdr_bcast<G, 3>(v);
+    case 4: return hdr_bcast<G, 4>(v);
+    case 5: return hdr_bcast<G, 5>(v);
+    case 6: return hdr_bcast<G, 6>(v);
+    default: return hdr_bcast<G, 7>(v);
+    }
+}
+
 // Row kernel for compile-time blocks per lane NL (B = NL * G) and prefetch
 // depth D (NL % D == 0): every weight load is unconditional straight-line
-// code, D blocks per lane in flight.
+// code, D blocks per lane in flight.  A lane's block headers come from the
+// row's header plane (q4k_hdr_off): lane k loads the header of its
+// (8h + k)-th block for h = 0..NL/8, one 16-byte load per eight blocks, and
+// the loop broadcasts block i's header from lane i % 8 of its group; the
+// only per-block weight load is the lane's 16 nibble bytes.
 //
 // FUSE (batch 1 only): the workgroup quantises the f32 activation itself.
-// Its x loads are issued first, the weight prefetch second, so the compiler's
-// in-order vmcnt waits hand the x registers to the quantiser while the
-// weights are still streaming.  Otherwise the pre-quantised activations are
-// copied to LDS with direct global->LDS loads issued before the prefetch.
+// Its x loads are issued first, the header and nibble prefetch second, so
+// the compiler's in-order vmcnt waits hand the x registers to the quantiser
+// while the weights are still streaming.  Otherwise the pre-quantised
+// activations are copied to LDS with direct global->LDS loads issued before
+// the prefetch.
 template <int NT, int G, int NL, int D, bool FUSE>
-__global__ __launch_bounds__(1024) void gemv_q4k_kernel(GemvJob j) {
+__global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(GemvJob j) {
     static_assert(NL % D == 0, "prefetch depth must divide the blocks per lane");
     static_assert(!FUSE || NT == 1, "fused quantisation is batch 1 only");
     constexpr int B = NL * G;
+    constexpr int NH = (NL + 7) / 8;  // header loads per lane
     constexpr int QB = FUSE ? (B + 3) / 4 : 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x;
@@ -376,7 +416,8 @@ __global__ __launch_bounds__(1024) void gemv_q4k_kernel(GemvJob j) {
     const int r = ((int)blockIdx.x - j.wg_begin[wi]) * j.rows_per_wg + rl;
     const bool live = r < j.rows[wi];
     const int rr = live ? r : j.rows[wi] - 1;  // dead lanes read a valid row, write nothing
-    const uint8_t* lane_row = j.w[wi] + (size_t)rr * j.rb + (size_t)gi * 144 + 16 * k;
+    const uint8_t* row = j.w[wi] + (size_t)rr * j.rb;
+    const uint8_t* lane_nib = row + q4k_nib_off(B, gi) + 16 * k;  // block i: + i * G * 128
     int8_t* q8b = (int8_t*)smem;
     float* xs32b = (float*)(smem + (size_t)NT * cols);
     float* xscb = xs32b + (size_t)NT * (cols / 32);
@@ -387,22 +428,26 @@ __global__ __launch_bounds__(1024) void gemv_q4k_kernel(GemvJob j) {
         stage_act_asm<NT>(j, smem);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // Loads are pinned in block order (header, then nibbles): vmcnt retires
-    // in issue order, so block i becomes usable as soon as its own data is in
-    // and the loop consumes the blocks as they arrive.
-    uint4 H[D], Q[D];
+    uint4 HG[NH];
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+        const int i = 8 * h + k < NL ? 8 * h + k : NL - 1;  // clamped lanes are never read
+        HG[h] = *(const uint4*)(row + q4k_hdr_off(i * G + gi));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // nibble loads pinned in block order: vmcnt retires in issue order, so
+    // block i is usable as soon as its own data is in
+    uint4 Q[D];
 #pragma unroll
     for (int i = 0; i < D; i++) {
-        const uint8_t* blk = lane_row + (size_t)i * G * 144;
-        H[i] = *(const uint4*)(blk - 16 * k);
-        Q[i] = *(const uint4*)(blk + 16);
+        Q[i] = *(const uint4*)(lane_nib + (size_t)i * G * 128);
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (FUSE) {
         xq_store<QB, false>(xr, B, q8b, xs32b, nullptr, xscb);
         wait_lgkm0();
     } else {
-        wait_vmem_le<2 * D>();
+        wait_vmem_le<NH + D>();
     }
     lds_barrier();
     const MinSel ms(k);
@@ -413,14 +458,12 @@ __global__ __launch_bounds__(1024) void gemv_q4k_kernel(GemvJob j) {
     for (int i0 = 0; i0 < NL; i0 += D) {
 #pragma unroll
         for (int ii = 0; ii < D; ii++) {
-            const uint4 h = H[ii], q = Q[ii];
-            if (i0 + D < NL) {
-                const uint8_t* blk = lane_row + (size_t)(i0 + D + ii) * G * 144;
-                H[ii] = *(const uint4*)(blk - 16 * k);
-                Q[ii] = *(const uint4*)(blk + 16);
-            }
-            q4k_block<NT, G>(h, q, (i0 + ii) * G + gi, k, ms, j.ntok, q8b, xs32b, xscb, cols, B,
-                             accF, accM);
+            const int i = i0 + ii;
+            const uint4 q = Q[ii];
+            const uint4 h = hdr_of<G>(HG[i / 8], i);
+            if (i0 + D < NL) Q[ii] = *(const uint4*)(lane_nib + (size_t)(i + D) * G * 128);
+            q4k_block<NT, G>(h, q, i * G + gi, k, ms, j.ntok, q8b, xs32b, xscb, cols, B, accF,
+                             accM);
         }
     }
 #pragma unroll
@@ -442,7 +485,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_any_kernel(GemvJob j) {
     while (wi + 1 < j.n && (int)blockIdx.x >= j.wg_begin[wi + 1]) wi++;
     const int r = ((int)blockIdx.x - j.wg_begin[wi]) * (32 / G) + rl;
     if (r >= j.rows[wi]) return;
-    const uint8_t* lane_row = j.w[wi] + (size_t)r * j.rb + (size_t)gi * 144;
+    const uint8_t* row = j.w[wi] + (size_t)r * j.rb;
     const int8_t* q8b = j.act.q8perm + (size_t)j.tok0 * cols;
     const float* xs32b = j.act.xs32 + (size_t)j.tok0 * (cols / 32);
     const float* xscb = j.act.xscale + (size_t)j.tok0 * B;
@@ -451,9 +494,10 @@ __global__ __launch_bounds__(256) void gemv_q4k_any_kernel(GemvJob j) {
 #pragma unroll
     for (int t = 0; t < NT; t++) accF[t] = accM[t] = 0.0f;
     for (int i = 0; i < B / G; i++) {
-        const uint8_t* blk = lane_row + (size_t)i * G * 144;
-        q4k_block<NT, G>(*(const uint4*)blk, *(const uint4*)(blk + 16 + 16 * k), i * G + gi, k, ms,
-                         j.ntok, q8b, xs32b, xscb, cols, B, accF, accM);
+        const int b = i * G + gi;
+        q4k_block<NT, G>(*(const uint4*)(row + q4k_hdr_off(b)),
+                         *(const uint4*)(row + q4k_nib_off(B, b) + 16 * k), b, k, ms, j.ntok, q8b,
+                         xs32b, xscb, cols, B, accF, accM);
     }
 #pragma unroll
     for (int t = 0; t < NT; t++) {
@@ -783,12 +827,12 @@ __global__ __launch_bounds__(256) void lane_ints_kernel(const uint8_t* __restric
         const int xq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
         int acc = 0;
         if (type == GLLM_TYPE_Q4_K) {
-            const uint8_t* blk = row + (size_t)b * 144;
-            const uint4 h = *(const uint4*)blk;
+            const uint4 h = *(const uint4*)(row + q4k_hdr_off(b));
+            const uint8_t* nib = row + q4k_nib_off(B, b);
             const uint32_t sc03 = h.y & 0x3f3f3f3fu;
             const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
             for (int s = 0; s < 4; s++) {
-                const uint32_t wd = *(const uint32_t*)(blk + 16 + 16 * k + 4 * s);  // repacked
+                const uint32_t wd = *(const uint32_t*)(nib + 16 * k + 4 * s);  // repacked
                 const uint32_t sc = s < 2 ? sc03 : sc47;
                 acc += ubyte(sc, (2 * s) & 3) * sdot4((int)(wd & 0x0f0f0f0fu), xq[2 * s], 0);
                 acc += ubyte(sc, (2 * s + 1) & 3) * sdot4((int)((wd >> 4) & 0x0f0f0f0fu), xq[2 * s + 1], 0);
@@ -942,13 +986,14 @@ __global__ void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restri
         const size_t r = i / rb, o = i % rb;  // o: offset in the reference row
         size_t n;                             // offset in the repacked row
         if (type == GLLM_TYPE_Q4_K) {
-            // nibble byte 32s + 4k + j -> 16k + 4s + j (header unchanged)
+            // headers to the front of the row (q4k_hdr_off), nibble byte
+            // 32s + 4k + j of block b -> q4k_nib_off(B, b) + 16k + 4s + j
             const size_t b = o / 144, e = o % 144;
             if (e < 16) {
-                n = o;
+                n = q4k_hdr_off((int)b) + e;
             } else {
                 const size_t qi = e - 16, s4 = qi / 32, l = qi % 32;
-                n = b * 144 + 16 + (l / 4) * 16 + s4 * 4 + (l % 4);
+                n = q4k_nib_off(B, (int)b) + (l / 4) * 16 + s4 * 4 + (l % 4);
             }
         } else if (type == GLLM_TYPE_Q6_K) {
             // ql byte 32q + 4k + j -> 16k + 4q + j, qh byte 128 + 32h + 4k + j
@@ -1065,7 +1110,7 @@ constexpr size_t kMaxStage = 48 << 10;
 
 template <int NT, int G, int NL, int D>
 static void launch_q4k_nl(const GemvJob& j, dim3 grid, dim3 block, size_t stage, hipStream_t s) {
-    if constexpr (NT == 1) {
+    if constexpr (NT == 1 && NL * G * 256 <= kFuseCols) {
         if (j.xf) {
             hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, true>), grid, block, stage, s, j);
             return;
@@ -1111,6 +1156,16 @@ static int q4k_max_rows() {
     }();
     return n;
 }
+// Largest workgroup in lanes (GLLM_Q4K_MAX_THREADS overrides, for
+// measurement, up to 1024: every shape gives the same bits).
+static int q4k_max_threads() {
+    static const int n = [] {
+        const char* e = getenv("GLLM_Q4K_MAX_THREADS");
+        const int v = e ? atoi(e) : 0;
+        return v >= 64 && v <= 1024 ? v : 512;
+    }();
+    return n;
+}
 static Q4KShape q4k_shape(int total_rows, int blocks) {
     const int ncu = device_cus();
     Q4KShape best{0, 0, 0};
@@ -1120,6 +1175,7 @@ static Q4KShape q4k_shape(int total_rows, int blocks) {
         int rpw = (total_rows + ncu - 1) / ncu;
         rpw = (rpw + unit - 1) / unit * unit;
         rpw = std::min(rpw, std::max(unit, q4k_max_rows() / g));
+        rpw = std::min(rpw, std::max(unit, q4k_max_threads() / (8 * g) / unit * unit));
         const Q4KShape sh{g, rpw, rpw * 8 * g};
         if (!q4k_has_nl(blocks / g) && best.g) continue;
         best = sh;
@@ -1133,7 +1189,7 @@ int launch_q4k(GemvJob& j, const int* rows, int n, const Q4KShape& sh, hipStream
     const int nl = j.blocks / G;
     const size_t stage = q4k_stage_bytes(NT, j.cols);
     const bool compiled = stage <= kMaxStage && q4k_has_nl(nl) && sh.threads >= 256;
-    if (j.xf && (NT != 1 || !compiled))
+    if (j.xf && (NT != 1 || !compiled || j.cols > kFuseCols))
         return fail(GLLM_EINVAL, "gemv: fused quantisation needs batch 1 and a compiled shape");
     // the generic kernel keeps 256-thread workgroups of 32 / G rows
     j.rows_per_wg = compiled ? sh.rows_per_wg : 32 / G;

@@ -76,7 +76,7 @@ struct gllm_hip_weight {
     int rows, cols;
     int blocks;          // cols / 256
     size_t row_bytes;    // reference bytes per row
-    uint8_t* d_data;     // device bytes, repacked for Q6_K / Q8_0
+    uint8_t* d_data;     // device bytes, repacked at upload per type
     int device;
 };
 
@@ -102,6 +102,17 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     uint16_t hb;
     __builtin_memcpy(&hb, &v, 2);
     return hb;
+}
+
+// Q4_K device row layout (upload repack; the same 144 bytes per block):
+// the row's B block headers (d, dmin, 12 scale bytes; 16 bytes each) first,
+// then its B nibble blocks of 128 bytes, in which AVX2 lane k's 16 bytes
+// (bytes 4k..4k+3 of each of the four 32-byte chunks) sit at 16k.  Eight
+// consecutive blocks' headers are 128 contiguous bytes, so the eight lanes
+// of a row fetch them with one 16-byte load each.
+__host__ __device__ __forceinline__ size_t q4k_hdr_off(int b) { return (size_t)b * 16; }
+__host__ __device__ __forceinline__ size_t q4k_nib_off(int B, int b) {
+    return (size_t)B * 16 + (size_t)b * 128;
 }
 
 // Byte offset, inside one 256-element block of the lane-permuted Q8K

@@ -151,9 +151,9 @@ __device__ __forceinline__ void pf_load(const PfArgs& a, int row0, int tok0, int
     for (int i = 0; i < R::NH; i++) {
         const int u = tid + R::T * i;
         const int row = min(row0 + u % kRows, a.rows - 1);
-        const uint8_t* blk = a.w + (size_t)row * a.rb + (size_t)b * 144;
-        r.h[i] = *(const u4v*)blk;
-        r.w[i] = *(const u4v*)(blk + 16 + 16 * (u / kRows));
+        const uint8_t* rp = a.w + (size_t)row * a.rb;
+        r.h[i] = *(const u4v*)(rp + q4k_hdr_off(b));
+        r.w[i] = *(const u4v*)(rp + q4k_nib_off(a.blocks, b) + 16 * (u / kRows));
     }
 }
 
