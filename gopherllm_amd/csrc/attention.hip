@@ -14,6 +14,7 @@
 // with an online-softmax merge; it agrees with the exact path to float
 // rounding (not bitwise) and is the long-context fast path.
 #include <algorithm>
+#include <cstdlib>
 
 #include "gllm_common.h"
 
@@ -177,6 +178,7 @@ struct AttnRope {
     const float* v;
     uint16_t* kc;          // this layer's caches
     uint16_t* vc;
+    const float* cur;      // optional: the current position's sin row then cos row
 };
 
 __global__ __launch_bounds__(256) void attn_scores128_kernel(
@@ -206,18 +208,22 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
         for (int c = 0; c < kFusedHD / 8; c++) kr[c] = krow[c];
     }
     if (rope.sin_tab) {
+        // the current position's rows: from rope.cur when the caller uploads
+        // them with the position (no wait on the position before the load)
         const int pos = start + tcur, pairs = kFusedHD / 2;
+        const float* srow = rope.cur ? rope.cur : rope.sin_tab + (size_t)pos * pairs;
+        const float* crow = rope.cur ? rope.cur + pairs : rope.cos_tab + (size_t)pos * pairs;
         for (int i = tid; i < kvmul * pairs; i += 256) {
             const int pr = i % pairs;
-            const float sn = rope.sin_tab[(size_t)pos * pairs + pr];
-            const float cs = rope.cos_tab[(size_t)pos * pairs + pr];
+            const float sn = srow[pr];
+            const float cs = crow[pr];
             const float v0 = qg[2 * i], v1 = qg[2 * i + 1];
             qs[2 * i] = v0 * cs - v1 * sn;
             qs[2 * i + 1] = v0 * sn + v1 * cs;
         }
         if (has_cur && tid < pairs) {
-            const float sn = rope.sin_tab[(size_t)pos * pairs + tid];
-            const float cs = rope.cos_tab[(size_t)pos * pairs + tid];
+            const float sn = srow[tid];
+            const float cs = crow[tid];
             const float* e = rope.k + (size_t)g * kFusedHD + 2 * tid;
             const float v0 = e[0], v1 = e[1];
             const uint16_t r0 = f32_to_f16_bits(v0 * cs - v1 * sn);
@@ -340,7 +346,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
         wait_lgkm0();
         lds_barrier();
         const int base = it * kVTile;
-        const int n = min(kVTile, span - base);
+        const int n = max(0, min(kVTile, span - base));
         if (chain) {
             if (n == kVTile) {
                 // the whole tile's operands first (one LDS round trip), then
@@ -374,15 +380,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
             for (; p < n; p++) denom = denom + w[base + p];
         }
     };
+    // whole groups of P tiles, unconditionally (a branch around a tile makes
+    // the compiler's vmcnt waits drain the prefetch): tiles past the span
+    // stage clamped rows nobody reads and run no chain steps
     for (int it0 = 0; it0 < ntiles; it0 += P) {
 #pragma unroll
-        for (int q = 0; q < P; q++)
-            if (it0 + q < ntiles) tile(it0 + q, pre[q]);  // uniform
+        for (int q = 0; q < P; q++) tile(it0 + q, pre[q]);
     }
     if (summer) red[4] = denom > 0.0f ? 1.0f / denom : 1.0f;
     __syncthreads();
     if (chain) out[((size_t)tok * n_heads + h) * kFusedHD + slice * DW + d] = acc * red[4];
 }
+
 
 template <int DS>
 static size_t smax_lds_bytes(int span_max) {
@@ -785,7 +794,8 @@ bool attend_exact_graphable(const gllm_hip_kv* kv, int n_heads, int n_kv, int hd
 int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
                  int start, int end0, int p, float scale, float* d_out, hipStream_t s,
                  float* scratch, const int* d_end, int span_cap, const float* rope_sin,
-                 const float* rope_cos, const float* d_knew, const float* d_vnew) {
+                 const float* rope_cos, const float* d_knew, const float* d_vnew,
+                 const float* rope_cur) {
     const int span0 = end0 - start + 1;
     const int span_max = d_end ? span_cap : span0 + p - 1;
     const int kvmul = n_heads / n_kv;
@@ -797,7 +807,7 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
         return fail(GLLM_EUNSUP, "attend: device-side positions need the head_dim 128 path");
     if (rope_sin && (!d_end || !d_knew || !d_vnew))
         return fail(GLLM_EINVAL, "attend: RoPE folding needs one token and its raw k / v rows");
-    const AttnRope rope{rope_sin, rope_cos, d_knew, d_vnew, kv->k[l], kv->v[l]};
+    const AttnRope rope{rope_sin, rope_cos, d_knew, d_vnew, kv->k[l], kv->v[l], rope_cur};
     if (hd == kFusedHD && kvmul <= 4 && kv->kv_dim_k == kv->kv_dim_v && span_max <= kSmaxSpan) {
         float* sc = scratch ? scratch
                             : (float*)thread_scratch(5, (size_t)p * n_heads * span_max * 4 + 256, s);
@@ -907,7 +917,7 @@ int attend_dev_impl(gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n
     if (mode == GLLM_ATTN_SPLITK)
         return attend_splitk(kv, l, d_q, n_heads, n_kv, hd, start, end, scale, d_out, s);
     return attend_exact(kv, l, d_q, n_heads, n_kv, hd, start, end, 1, scale, d_out, s, nullptr,
-                        nullptr, 0, nullptr, nullptr, nullptr, nullptr);
+                        nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr);
 }
 
 int kv_store_dev_impl(gllm_hip_kv* kv, int l, int pos, const float* d_k, const float* d_v,
@@ -1056,7 +1066,7 @@ int gllm_hip_attend_group(gllm_hip_kv* kv, int l, int kvh, const float* q, int q
     view.layers = 1;
     GLLM_TRY(attend_exact(&view, 0, d, q_heads, 1, hd, start, end, 1, scale,
                           d + (size_t)q_heads * hd, s, nullptr, nullptr, 0, nullptr, nullptr,
-                          nullptr, nullptr));
+                          nullptr, nullptr, nullptr));
     GLLM_HIP(hipMemcpyAsync(out, d + (size_t)q_heads * hd, (size_t)q_heads * vd * 4,
                             hipMemcpyDeviceToHost, s));
     GLLM_HIP(hipStreamSynchronize(s));

@@ -27,7 +27,8 @@ int gemv_silu_f32(gllm_hip_weight* w, const float* gate, const float* up, int p,
 int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
                  int start, int end0, int p, float scale, float* d_out, hipStream_t s,
                  float* scratch, const int* d_end, int span_cap, const float* rope_sin,
-                 const float* rope_cos, const float* d_knew, const float* d_vnew);
+                 const float* rope_cos, const float* d_knew, const float* d_vnew,
+                 const float* rope_cur = nullptr);
 bool attend_exact_graphable(const gllm_hip_kv* kv, int n_heads, int n_kv, int hd, int span_cap);
 int attend_splitk(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
                   int start, int end, float scale, float* d_out, hipStream_t s);
@@ -218,6 +219,29 @@ __global__ void rope_kv_kernel(float* __restrict__ q, float* __restrict__ k,
 
 static inline int grid1(size_t n, int block) { return (int)((n + block - 1) / block); }
 
+// RoPE sin / cos of one position (buildRopeInvFreq model.go:1728-1756,
+// prepareRopeScratch model.go:3020-3049): the reference's float64 pow, sin
+// and cos on the host, rounded to float32.
+static void rope_row(const gllm_hip_model_config& c, int pos, float* sn, float* cs) {
+    const int pairs = c.head_dim / 2;
+    for (int i = 0; i < pairs; i++) {
+        const float fi = (float)(i * 2);
+        const float base = (float)pow((double)c.rope_theta, (double)(fi / (float)c.head_dim));
+        const float inv = 1.0f / (1.0f * base);
+        const double angle = (double)((float)pos * inv);
+        sn[i] = (float)sin(angle) * 1.0f;
+        cs[i] = (float)cos(angle) * 1.0f;
+    }
+}
+
+// Decode-step upload: [position][3 pad][sin row][cos row] (floats after the
+// first 16 bytes), so the captured step reads the current position's RoPE
+// rows without first waiting for the position.
+constexpr int kPosHeader = 4;  // 16 bytes
+static size_t pos_bytes(const gllm_hip_model_config& c) {
+    return ((size_t)kPosHeader + (size_t)c.head_dim) * 4;
+}
+
 constexpr int kMaxRepeatWindow = 4096;  // the reference uses 64 (runtime.go:27)
 
 static void drop_decode_graph(gllm_hip_model* m) {
@@ -288,7 +312,7 @@ static int forward(gllm_hip_model* m, int pos0, int p, const int* d_pos = nullpt
             // attention scores launch
             GLLM_TRY(attend_exact(m->kv, l, m->q, c.n_heads, c.n_kv_heads, hd, 0, pos0, p, scale,
                                   m->attn, s, m->scores, d_pos, c.max_len, m->d_sin, m->d_cos,
-                                  m->k, m->v));
+                                  m->k, m->v, (const float*)d_pos + kPosHeader));
         } else {
             const int pairs = std::max(c.n_heads, c.n_kv_heads) * (hd / 2);
             hipLaunchKernelGGL(rope_kv_kernel, dim3(grid1((size_t)pairs, 256), p), dim3(256), 0, s,
@@ -420,18 +444,9 @@ gllm_hip_model* gllm_hip_model_new(const gllm_hip_model_config* cfg) {
     // model.go:3020-3049), computed on the host with the reference's
     // float64 pow / sin / cos and uploaded once for every position.
     const int pairs = cfg->head_dim / 2;
-    std::vector<float> inv(pairs), sn((size_t)cfg->max_len * pairs), cs((size_t)cfg->max_len * pairs);
-    for (int i = 0; i < pairs; i++) {
-        const float fi = (float)(i * 2);
-        const float base = (float)pow((double)cfg->rope_theta, (double)(fi / (float)cfg->head_dim));
-        inv[i] = 1.0f / (1.0f * base);
-    }
+    std::vector<float> sn((size_t)cfg->max_len * pairs), cs((size_t)cfg->max_len * pairs);
     for (int pos = 0; pos < cfg->max_len; pos++)
-        for (int i = 0; i < pairs; i++) {
-            const double angle = (double)((float)pos * inv[i]);
-            sn[(size_t)pos * pairs + i] = (float)sin(angle) * 1.0f;
-            cs[(size_t)pos * pairs + i] = (float)cos(angle) * 1.0f;
-        }
+        rope_row(*cfg, pos, &sn[(size_t)pos * pairs], &cs[(size_t)pos * pairs]);
     if (hipMalloc(&m->d_sin, sn.size() * 4) != hipSuccess) return bail("rope tables");
     if (hipMalloc(&m->d_cos, cs.size() * 4) != hipSuccess) return bail("rope tables");
     if (hipMemcpy(m->d_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
@@ -444,8 +459,9 @@ gllm_hip_model* gllm_hip_model_new(const gllm_hip_model_config* cfg) {
     if (hipMalloc(&m->logits, (size_t)cfg->vocab * 4) != hipSuccess) return bail("logits");
     if (hipMalloc(&m->argmax_keys, argmax_keys(cfg->vocab) * 8) != hipSuccess)
         return bail("argmax keys");
-    if (hipMalloc(&m->d_pos, 64) != hipSuccess) return bail("position");
-    if (hipHostMalloc(&m->h_pos, 64, hipHostMallocDefault) != hipSuccess) return bail("position");
+    if (hipMalloc(&m->d_pos, pos_bytes(*cfg)) != hipSuccess) return bail("position");
+    if (hipHostMalloc(&m->h_pos, pos_bytes(*cfg), hipHostMallocDefault) != hipSuccess)
+        return bail("position");
     return m;
 }
 
@@ -524,8 +540,12 @@ int gllm_hip_model_decode(gllm_hip_model* m, uint32_t token, int pos, uint32_t* 
     GLLM_TRY(upload_recent(m));
     m->h_tokens[0] = token;
     m->h_pos[0] = pos;
+    {
+        float* rows = (float*)m->h_pos + kPosHeader;
+        rope_row(m->cfg, pos, rows, rows + m->cfg.head_dim / 2);
+    }
     GLLM_HIP(hipMemcpyAsync(m->d_tokens, m->h_tokens, 4, hipMemcpyHostToDevice, s));
-    GLLM_HIP(hipMemcpyAsync(m->d_pos, m->h_pos, 4, hipMemcpyHostToDevice, s));
+    GLLM_HIP(hipMemcpyAsync(m->d_pos, m->h_pos, pos_bytes(m->cfg), hipMemcpyHostToDevice, s));
     if (m->decode_graph) {
         GLLM_HIP(hipGraphLaunch(m->decode_graph, s));
     } else {

@@ -101,6 +101,52 @@ __device__ __forceinline__ float rot_prev(float v) {
     }
 }
 
+// Value of lane GG of this lane's G-lane group (adjacent lanes; G = 2 or 4
+// fits one DPP quad): quad_perm broadcast.
+template <int G, int GG>
+__device__ __forceinline__ float slot_bcast(float v) {
+    if constexpr (G == 1) {
+        return v;
+    } else if constexpr (G == 2) {
+        return __int_as_float(
+            __builtin_amdgcn_mov_dpp(__float_as_int(v), GG == 0 ? 0xA0 : 0xF5, 0xF, 0xF, false));
+    } else {
+        static_assert(G == 4, "G must be 1, 2 or 4");
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), GG * 0x55, 0xF, 0xF, false));
+    }
+}
+
+// One round of G blocks of the two sequential fp32 chains: lane g of a group
+// holds block i*G + g's operands; every lane gathers the G lanes' operands
+// (independent DPP reads, off the dependency chain) and advances its own copy
+// of the chains through them in block order, so all G lanes end the round
+// with the reference's chain values.
+template <int G>
+__device__ __forceinline__ void chain_gather(float iv, float dxs, float dmin, float mx,
+                                             float& accF, float& accM) {
+    if constexpr (G == 1) {
+        accF = fmaf(iv, dxs, accF);
+        accM = fmaf(dmin, mx, accM);
+    } else {
+        float a[G], b[G], c[G], e[G];
+        a[0] = slot_bcast<G, 0>(iv); b[0] = slot_bcast<G, 0>(dxs);
+        c[0] = slot_bcast<G, 0>(dmin); e[0] = slot_bcast<G, 0>(mx);
+        a[1] = slot_bcast<G, 1>(iv); b[1] = slot_bcast<G, 1>(dxs);
+        c[1] = slot_bcast<G, 1>(dmin); e[1] = slot_bcast<G, 1>(mx);
+        if constexpr (G == 4) {
+            a[2] = slot_bcast<G, 2>(iv); b[2] = slot_bcast<G, 2>(dxs);
+            c[2] = slot_bcast<G, 2>(dmin); e[2] = slot_bcast<G, 2>(mx);
+            a[3] = slot_bcast<G, 3>(iv); b[3] = slot_bcast<G, 3>(dxs);
+            c[3] = slot_bcast<G, 3>(dmin); e[3] = slot_bcast<G, 3>(mx);
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            accF = fmaf(a[g], b[g], accF);
+            accM = fmaf(c[g], e[g], accM);
+        }
+    }
+}
+
 // 8-lane tree across k when the k lanes of a row sit G lanes apart.
 template <int G>
 __device__ __forceinline__ float tree8_strided(float v) {
@@ -343,11 +389,7 @@ __device__ __forceinline__ void q4k_block(const uint4 h, const uint4 q, int b, i
             const float iv = (float)acc;
             const float dxs = d * xscb[(size_t)t * B + b];
             const float mx = mkf * xs32b[(size_t)t * (cols / 32) + b * 8 + k];
-#pragma unroll
-            for (int step = 0; step < G; step++) {
-                accF[t] = fmaf(iv, dxs, rot_prev<G>(accF[t]));
-                accM[t] = fmaf(dmin, mx, rot_prev<G>(accM[t]));
-            }
+            chain_gather<G>(iv, dxs, dmin, mx, accF[t], accM[t]);
         }
     }
 }
