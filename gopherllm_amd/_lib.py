@@ -12,7 +12,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgllm_hip.so")
 
-TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 8, 12, 14
+TYPE_F32, TYPE_F16, TYPE_BF16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 30, 8, 12, 14
 TYPE_Q4_0, TYPE_Q4_1, TYPE_Q2_K, TYPE_Q3_K, TYPE_Q5_K, TYPE_MXFP4 = 2, 3, 10, 11, 13, 39
 OK, EINVAL, EDEVICE, ENOMEM, EUNSUP = 0, -1, -2, -3, -4
 ATTN_EXACT, ATTN_SPLITK = 0, 1
@@ -45,6 +45,7 @@ SIGNATURES = {
     "gllm_hip_weight_release": (None, [vp]),
     "gllm_hip_weight_shape": (i32, [vp, vp, vp, vp]),
     "gllm_hip_weight_download_dev": (i32, [vp, vp, vp]),
+    "gllm_hip_weight_rows_dev": (i32, [vp, vp, i32, vp, vp]),
     "gllm_hip_matvec": (i32, [vp, vp, vp]),
     "gllm_hip_matvec2": (i32, [vp, vp, vp, vp, vp]),
     "gllm_hip_matvec3": (i32, [vp, vp, vp, vp, vp, vp, vp]),

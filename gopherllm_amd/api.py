@@ -9,6 +9,7 @@ C ABI (include/gllm_hip.h).  Names follow the Go API they stand in for:
     matvec2_into / matvec3_into   MatvecQ4K2IntoWithXSums simd.go:295,
                              Q4KMatvec3IntoWithXSums    metal.go:14
     matvec_batch             matvecBatchQ8              kernels_amd64.go:470
+    Weight.rows_dev          (Weight).RowInto           model.go:1034
     KVCacheF16.store_kv      (*KVCache).storeKV         model.go:1466
     KVCacheF16.attend_head_group (*KVCache).attendHeadGroup model.go:1516
 
@@ -182,6 +183,14 @@ class Weight:
     def lane_ints_dev(self, x, out, stream=None):
         call("gllm_hip_lane_ints_dev", self.handle, _dev(x, "f32", self.cols, "x"),
              _dev(out, "i32", self.rows * (self.cols // 256) * 8, "out"), _stream(stream))
+        return out
+
+    def rows_dev(self, ids, out, stream=None):
+        """(Weight).RowInto (model.go:1034) for every id in the device
+        tensor ids: out[i] = row ids[i] as f32 (ids must be < rows)."""
+        n = ids.numel()
+        call("gllm_hip_weight_rows_dev", self.handle, _dev(ids, "u32", n, "ids"), n,
+             _dev(out, "f32", n * self.cols, "out"), _stream(stream))
         return out
 
     def download_dev(self, out, stream=None):

@@ -3,7 +3,11 @@
 // (forward_batch.go:336-613) in the reference's amd64 float order, and the
 // host driver that sequences them around the row kernels and attention.
 //
-//   embedding      DequantRowQ4KInto simd.go:1530-1557 (Weight.RowInto model.go:1034)
+//   embedding      Weight.RowInto model.go:1034-1100 (launch_weight_rows, any type)
+//   projections    decode: the fused groups of tryMatvecAttentionInto /
+//                  tryMatvec2Into (model.go:3157-3206: int8 row dots, or the
+//                  float kernels for same-type groups of the other formats);
+//                  prefill: matvecBatchQ8 per matrix (forward_batch.go:108-233)
 //   rmsNormInto    model.go:2986-3011: ss = dotF32AVX2(x, x) (kernels_amd64.s:28-93),
 //                  scale = float32(1/sqrt(float64(ss/n + eps))), out = (x*w)*scale
 //   RoPE           prepareRopeScratch model.go:3020-3049 (host tables, the
@@ -22,6 +26,13 @@
 namespace gllm {
 int gemv_f32(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float* const* outs,
              const int* strides, void* act_buf, hipStream_t s);
+int gemv_group(int n, gllm_hip_weight* const* ws, const float* d_x, float* const* outs,
+               const int* strides, void* act_buf, hipStream_t s);
+int group_routing(int n, gllm_hip_weight* const* ws, int* fl);
+bool row_kernel_type(int t);
+bool rows_type(int t);
+int launch_weight_rows(const gllm_hip_weight* w, const uint32_t* d_ids, int n, float* d_out,
+                       hipStream_t s);
 int gemv_silu_f32(gllm_hip_weight* w, const float* gate, const float* up, int p, float* out,
                   void* act_buf, float* hidden, hipStream_t s);
 int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
@@ -78,40 +89,6 @@ namespace gllm {
 // ---------------------------------------------------------------------------
 // kernels
 // ---------------------------------------------------------------------------
-
-// Token embedding rows from a Q4_K table: out[t][j] = d1*q - min1 per
-// DequantRowQ4KInto.  One workgroup per token, one thread per element.
-__global__ __launch_bounds__(256) void embed_q4k_kernel(const uint8_t* __restrict__ table,
-                                                        size_t rb, int dim,
-                                                        const uint32_t* __restrict__ tokens,
-                                                        float* __restrict__ out) {
-    const int t = blockIdx.x;
-    const uint8_t* row = table + (size_t)tokens[t] * rb;
-    for (int e = threadIdx.x; e < dim; e += blockDim.x) {
-        const int b = e >> 8, i = e & 255;
-        const uint8_t* blk = row + q4k_hdr_off(b);
-        const int j = i >> 5;  // sub-block
-        const uint8_t* sc = blk + 4;
-        int s, m;
-        if (j < 4) {
-            s = sc[j] & 63;
-            m = sc[j + 4] & 63;
-        } else {
-            s = (sc[j + 4] & 0x0f) | ((sc[j - 4] >> 6) << 4);
-            m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
-        }
-        const float d = f16_bits_to_f32(blk[0] | (blk[1] << 8));
-        const float dmin = f16_bits_to_f32(blk[2] | (blk[3] << 8));
-        const int chunk = i >> 6, l = i & 31, hi = (i >> 5) & 1;
-        // the upload repack moved nibble byte 32*chunk + l of block b to
-        // q4k_nib_off(B, b) + 16*(l/4) + 4*chunk + l%4
-        const uint8_t qb = row[q4k_nib_off(dim >> 8, b) + (l >> 2) * 16 + chunk * 4 + (l & 3)];
-        const int qv = hi ? (qb >> 4) : (qb & 0x0f);
-        const float d1 = d * (float)s;
-        const float min1 = dmin * (float)m;
-        out[(size_t)t * dim + e] = d1 * (float)qv - min1;
-    }
-}
 
 // addInPlace (x = fma(proj, 1, x): one rounding of x + proj, model.go:3857)
 // followed by rmsNormInto (model.go:2986-3011); with proj null, the norm
@@ -282,20 +259,30 @@ static int matvec(gllm_hip_model* m, int n, gllm_hip_weight* const* ws, const fl
     return gemv_f32(n, ws, x, p, outs, nullptr, m->act, m->stream);
 }
 
+// A layer's fused projections (Q/K/V, gate/up): a generation step routes
+// them as one group (ForwardBodyInto's tryMatvecAttentionInto /
+// tryMatvec2Into); prompt tokens run each projection on its own
+// (matvecBatch3/2 -> matvecBatchQ8, forward_batch.go:210-233).
+static int project(gllm_hip_model* m, bool decode, int n, gllm_hip_weight* const* ws,
+                   const float* x, int p, float* const* outs) {
+    if (decode) return gemv_group(n, ws, x, outs, nullptr, m->act, m->stream);
+    return matvec(m, n, ws, x, p, outs);
+}
+
 // ForwardBatchInto / ForwardBodyInto for p consecutive tokens already in
 // m->d_tokens, at positions pos0 .. pos0+p-1.  Leaves the output-normed
 // hidden state of every token in m->xn.  With d_pos (p == 1), the position
 // is read on the device instead, so the launches do not depend on it.
-static int forward(gllm_hip_model* m, int pos0, int p, const int* d_pos = nullptr) {
+// decode (p == 1) is a generation step, otherwise the tokens are prompt
+// tokens.
+static int forward(gllm_hip_model* m, int pos0, int p, bool decode, const int* d_pos = nullptr) {
     const auto& c = m->cfg;
     hipStream_t s = m->stream;
     const int hd = c.head_dim, kvd = c.n_kv_heads * hd;
     // config.AttentionScale, else float32(1/sqrt(headDim)) (model.go:2685-2688)
     const float scale = m->attn_scale != 0.0f ? m->attn_scale : (float)(1.0 / sqrt((double)hd));
     const size_t norm_lds = (size_t)c.dim * 4;
-    hipLaunchKernelGGL(embed_q4k_kernel, dim3(p), dim3(256), 0, s, m->tok_embd->d_data,
-                       m->tok_embd->row_bytes, c.dim, m->d_tokens, m->x);
-    GLLM_HIP(hipGetLastError());
+    GLLM_TRY(launch_weight_rows(m->tok_embd, m->d_tokens, p, m->x, s));
     const float* pending = nullptr;  // FFN output still to be added to the residual
     for (int l = 0; l < c.n_layers; l++) {
         gllm_hip_weight** W = &m->w[(size_t)l * 7];
@@ -305,7 +292,7 @@ static int forward(gllm_hip_model* m, int pos0, int p, const int* d_pos = nullpt
         {
             gllm_hip_weight* ws[3] = {W[GLLM_T_WQ], W[GLLM_T_WK], W[GLLM_T_WV]};
             float* outs[3] = {m->q, m->k, m->v};
-            GLLM_TRY(matvec(m, 3, ws, m->xn, p, outs));
+            GLLM_TRY(project(m, decode, 3, ws, m->xn, p, outs));
         }
         if (d_pos) {
             // captured decode step: RoPE and the K/V store run inside the
@@ -335,7 +322,7 @@ static int forward(gllm_hip_model* m, int pos0, int p, const int* d_pos = nullpt
         {
             gllm_hip_weight* ws[2] = {W[GLLM_T_W1], W[GLLM_T_W3]};
             float* outs[2] = {m->gate, m->up};
-            GLLM_TRY(matvec(m, 2, ws, m->xn, p, outs));
+            GLLM_TRY(project(m, decode, 2, ws, m->xn, p, outs));
         }
         GLLM_TRY(gemv_silu_f32(W[GLLM_T_W2], m->gate, m->up, p, m->proj, m->act, m->hidden, s));
         pending = m->proj;
@@ -389,26 +376,40 @@ static int model_argmax(gllm_hip_model* m, uint32_t* d_token) {
 // One greedy decode step on the token in d_tokens[0]: forward, the output
 // projection (full logits), then the (penalised) argmax into d_tokens[1].
 static int decode_step(gllm_hip_model* m, int pos, const int* d_pos) {
-    GLLM_TRY(forward(m, pos, 1, d_pos));
+    GLLM_TRY(forward(m, pos, 1, true, d_pos));
     gllm_hip_weight* ws[1] = {m->output};
     float* outs[1] = {m->logits};
     GLLM_TRY(matvec(m, 1, ws, m->xn, 1, outs));
     return model_argmax(m, m->d_tokens + 1);
 }
 
-static int check_ready(const gllm_hip_model* m) {
+// Every weight set, of a type this path runs: any Weight.RowInto type for
+// the embedding, a row-kernel type for the projections; a generation step
+// (decode) also needs each layer's fused groups to be ones this path
+// restates (group_routing refuses same-type groups of a format whose float
+// kernel is not restated).
+static int check_ready(const gllm_hip_model* m, bool decode) {
     if (!m) return fail(GLLM_EINVAL, "null model");
     if (!m->tok_embd || !m->output) return fail(GLLM_EINVAL, "model: embedding/output not set");
-    if (m->tok_embd->type != GLLM_TYPE_Q4_K) return fail(GLLM_EUNSUP, "model: embedding must be Q4_K");
+    if (!rows_type(m->tok_embd->type))
+        return fail(GLLM_EUNSUP, "model: embedding type %d has no row lookup", m->tok_embd->type);
+    if (!row_kernel_type(m->output->type))
+        return fail(GLLM_EUNSUP, "model: output type %d has no row kernel", m->output->type);
     for (size_t i = 0; i < m->w.size(); i++) {
         if (!m->w[i]) return fail(GLLM_EINVAL, "model: layer %zu slot %zu not set", i / 7, i % 7);
-        // the layer's fused projections (Q/K/V, gate/up) are int8 row dots in
-        // the reference only for these two formats (tryMatvecAttentionInto,
-        // model.go:3156-3190); other formats go through its float kernels
-        const int t = m->w[i]->type;
-        if (t != GLLM_TYPE_Q4_K && t != GLLM_TYPE_Q6_K)
-            return fail(GLLM_EUNSUP, "model: layer %zu slot %zu has type %d (layers must be "
-                                     "Q4_K or Q6_K)", i / 7, i % 7, t);
+        if (!row_kernel_type(m->w[i]->type))
+            return fail(GLLM_EUNSUP, "model: layer %zu slot %zu has type %d (no row kernel)",
+                        i / 7, i % 7, m->w[i]->type);
+    }
+    if (decode) {
+        int fl[3];
+        for (int l = 0; l < m->cfg.n_layers; l++) {
+            gllm_hip_weight* const* W = &m->w[(size_t)l * 7];
+            gllm_hip_weight* qkv[3] = {W[GLLM_T_WQ], W[GLLM_T_WK], W[GLLM_T_WV]};
+            gllm_hip_weight* gu[2] = {W[GLLM_T_W1], W[GLLM_T_W3]};
+            GLLM_TRY(group_routing(3, qkv, fl));
+            GLLM_TRY(group_routing(2, gu, fl));
+        }
     }
     return GLLM_OK;
 }
@@ -531,7 +532,7 @@ int gllm_hip_model_set_norm(gllm_hip_model* m, int layer, int slot, const float*
 }
 
 int gllm_hip_model_decode(gllm_hip_model* m, uint32_t token, int pos, uint32_t* next) {
-    GLLM_TRY(check_ready(m));
+    GLLM_TRY(check_ready(m, true));
     if (!next) return fail(GLLM_EINVAL, "gllm_hip_model_decode: null next");
     if (pos < 0 || pos >= m->cfg.max_len) return fail(GLLM_EINVAL, "position %d out of range", pos);
     if (token >= (uint32_t)m->cfg.vocab) return fail(GLLM_EINVAL, "token %u out of range", token);
@@ -578,7 +579,7 @@ int gllm_hip_model_decode(gllm_hip_model* m, uint32_t token, int pos, uint32_t* 
 
 int gllm_hip_model_prefill(gllm_hip_model* m, const uint32_t* tokens, int n, int start_pos,
                            uint32_t* first, float* logits) {
-    GLLM_TRY(check_ready(m));
+    GLLM_TRY(check_ready(m, false));
     if (!tokens || n <= 0 || !first) return fail(GLLM_EINVAL, "gllm_hip_model_prefill: bad arguments");
     if (start_pos < 0 || start_pos + n > m->cfg.max_len)
         return fail(GLLM_EINVAL, "prefill positions %d..%d exceed max_len", start_pos, start_pos + n - 1);
@@ -597,7 +598,7 @@ int gllm_hip_model_prefill(gllm_hip_model* m, const uint32_t* tokens, int n, int
         const int p = std::min(chunk, n - c0);
         memcpy(m->h_tokens, tokens + c0, (size_t)p * 4);
         GLLM_HIP(hipMemcpyAsync(m->d_tokens, m->h_tokens, (size_t)p * 4, hipMemcpyHostToDevice, s));
-        GLLM_TRY(forward(m, start_pos + c0, p));
+        GLLM_TRY(forward(m, start_pos + c0, p, false));
         // h_tokens is reused by the next chunk's copy
         GLLM_HIP(hipStreamSynchronize(s));
     }

@@ -1,0 +1,234 @@
+// float_dot.hip -- float-activation row dots of the reference's same-type
+// fused projection groups (matvecSameType2/3Into via sameTypeQuantDot,
+// model.go:3213-3283): DotQ8_0F32 (simd.go:646-675), DotQ4_0F32
+// (simd.go:677-715), DotQ4_1F32 (quant_extra.go:42-62), DotQ2KF32
+// (quant_extra.go:271-302), DotQ3KF32 (quant_extra.go:376-410), DotQ5KF32
+// (simd.go:1031-1186) and DotMXFP4F32 (simd.go:1458-1477), on the device
+// layouts of the upload repack (read through repacked_offset) and f32
+// activations.
+//
+// Each of these dots adds one term per unit (a 32-element block, a
+// 16-element sub-block, for Q5_K a 32-element half of a 64-element step,
+// for MXFP4 one element) to a row sum, in unit
+// order, and every term depends only on its own unit.  A workgroup computes
+// the terms of its rows in parallel into LDS (each term in the reference's
+// own operation order, unfused float32 operations as Go evaluates them on
+// amd64), then one thread per row adds them up in unit order.
+#include <algorithm>
+
+#include "gllm_common.h"
+
+namespace gllm {
+
+constexpr int kFdThreads = 256;
+constexpr int kFdLdsTerms = 8192;  // 32 KB of terms per workgroup
+
+__host__ __device__ inline int fd_unit_elems(int type) {
+    return type == GLLM_TYPE_MXFP4 ? 1 : (type == GLLM_TYPE_Q2_K || type == GLLM_TYPE_Q3_K) ? 16 : 32;
+}
+
+__device__ __forceinline__ uint32_t fd_byte(const uint8_t* row, int type, size_t o, int B) {
+    return row[repacked_offset(type, o, B)];
+}
+__device__ __forceinline__ float fd_f16(const uint8_t* row, int type, size_t o, int B) {
+    return f16_bits_to_f32(fd_byte(row, type, o, B) | (fd_byte(row, type, o + 1, B) << 8));
+}
+
+// The e2m1 value of a 4-bit code: 0, 0.5, 1, 1.5, 2, 3, 4, 6 and their
+// negatives (code 8 is -0), exact in float32.
+__device__ __forceinline__ float mxfp4_value(uint32_t code) {
+    const uint32_t c = code & 7;
+    const float mag = c < 4 ? 0.5f * (float)c : (float)(2u << ((c - 4) >> 1)) * ((c & 1) ? 1.5f : 1.0f);
+    return (code & 8) ? -mag : mag;
+}
+
+// The term of unit u of one row (reference offsets o, device row `row`).
+__device__ float fd_term(const uint8_t* row, int type, int B, const float* __restrict__ x, int u) {
+    if (type == GLLM_TYPE_Q8_0) {
+        const size_t base = (size_t)u * 34;
+        const float scale = fd_f16(row, type, base, B);
+        const float* xb = x + (size_t)u * 32;
+        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < 32; i += 8) {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                s[j] = s[j] + (float)(int8_t)fd_byte(row, type, base + 2 + i + j, B) * xb[i + j];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                s[j] = s[j] + (float)(int8_t)fd_byte(row, type, base + 2 + i + 4 + j, B) * xb[i + 4 + j];
+        }
+        return scale * ((s[0] + s[1]) + (s[2] + s[3]));
+    }
+    if (type == GLLM_TYPE_Q4_0) {
+        const size_t base = (size_t)u * 18;
+        const float scale = fd_f16(row, type, base, B);
+        const float* xb = x + (size_t)u * 32;
+        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < 16; i += 4) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t p = fd_byte(row, type, base + 2 + i + j, B);
+                const float lo = (float)((int)(p & 15) - 8), hi = (float)((int)((p >> 4) & 15) - 8);
+                s[j] = s[j] + (lo * xb[i + j] + hi * xb[16 + i + j]);
+            }
+        }
+        return scale * ((s[0] + s[1]) + (s[2] + s[3]));
+    }
+    if (type == GLLM_TYPE_Q4_1) {
+        const size_t base = (size_t)u * 20;
+        const float d = fd_f16(row, type, base, B), m = fd_f16(row, type, base + 2, B);
+        const float* xb = x + (size_t)u * 32;
+        float qdot = 0.0f, xsum = 0.0f;
+        for (int i = 0; i < 16; i++) {
+            const uint32_t p = fd_byte(row, type, base + 4 + i, B);
+            qdot = qdot + ((float)(p & 15) * xb[i] + (float)(p >> 4) * xb[16 + i]);
+            xsum = xsum + (xb[i] + xb[16 + i]);
+        }
+        return d * qdot + m * xsum;
+    }
+    if (type == GLLM_TYPE_Q5_K) {
+        // step st = h / 2 of block b, half hf: lane accumulators j = l % 4
+        const int b = u / 8, h = u % 8, st = h / 2, hf = h & 1;
+        const size_t base = (size_t)b * 176;
+        const int j = 2 * st + hf;
+        int sc, m;
+        if (j < 4) {
+            sc = (int)(fd_byte(row, type, base + 4 + j, B) & 63);
+            m = (int)(fd_byte(row, type, base + 8 + j, B) & 63);
+        } else {
+            const uint32_t a = fd_byte(row, type, base + 8 + j, B);
+            sc = (int)((a & 0x0f) | ((fd_byte(row, type, base + j, B) >> 6) << 4));
+            m = (int)((a >> 4) | ((fd_byte(row, type, base + 4 + j, B) >> 6) << 4));
+        }
+        const float d1 = fd_f16(row, type, base, B) * (float)sc;
+        const float min1 = fd_f16(row, type, base + 2, B) * (float)m;
+        const float* x1 = x + (size_t)b * 256 + 64 * st + 32 * hf;
+        float qd[4] = {0.0f, 0.0f, 0.0f, 0.0f}, xs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int l = 0; l < 32; l += 4) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t qb = fd_byte(row, type, base + 48 + 32 * st + l + k, B);
+                const uint32_t hb = (fd_byte(row, type, base + 16 + l + k, B) >> j) & 1;
+                const uint32_t code = (hf ? qb >> 4 : qb & 15) + 16 * hb;
+                qd[k] = qd[k] + (float)code * x1[l + k];
+                xs[k] = xs[k] + x1[l + k];
+            }
+        }
+        const float qdot = (qd[0] + qd[1]) + (qd[2] + qd[3]);
+        const float xsum = (xs[0] + xs[1]) + (xs[2] + xs[3]);
+        return d1 * qdot - min1 * xsum;
+    }
+    if (type == GLLM_TYPE_Q2_K || type == GLLM_TYPE_Q3_K) {
+        const int b = u / 16, is = u % 16;
+        const float* xs = x + (size_t)b * 256 + is * 16;
+        if (type == GLLM_TYPE_Q2_K) {
+            const size_t base = (size_t)b * 84;
+            const float d = fd_f16(row, type, base + 80, B), dmin = fd_f16(row, type, base + 82, B);
+            const uint32_t sc = fd_byte(row, type, base + is, B);
+            const float dl = d * (float)(sc & 15), ml = dmin * (float)(sc >> 4);
+            float qdot = 0.0f, xsum = 0.0f;
+            for (int l = 0; l < 16; l++) {
+                const int e = is * 16 + l, mq = e / 32;
+                const uint32_t q = (fd_byte(row, type, base + 16 + 32 * (mq / 4) + e % 32, B) >> (2 * (mq % 4))) & 3;
+                qdot = qdot + (float)q * xs[l];
+                xsum = xsum + xs[l];
+            }
+            return dl * qdot - ml * xsum;
+        }
+        const size_t base = (size_t)b * 110;
+        const float d = fd_f16(row, type, base + 108, B);
+        // q3KScales: 6-bit scale of sub-block is from the 12 packed bytes
+        const uint32_t lo = (fd_byte(row, type, base + 96 + is % 8, B) >> (4 * (is / 8))) & 15;
+        const uint32_t hi = (fd_byte(row, type, base + 104 + is % 4, B) >> (2 * (is / 4))) & 3;
+        const float dl = d * (float)((int)(lo | (hi << 4)) - 32);
+        float acc = 0.0f;
+        for (int l = 0; l < 16; l++) {
+            const int e = is * 16 + l, mq = e / 32;
+            int v = (int)((fd_byte(row, type, base + 32 + 32 * (mq / 4) + e % 32, B) >> (2 * (mq % 4))) & 3);
+            if (!((fd_byte(row, type, base + e % 32, B) >> mq) & 1)) v -= 4;
+            acc = acc + (float)v * xs[l];
+        }
+        return dl * acc;
+    }
+    // MXFP4: unit = one element
+    const int b = u / 32, i = u % 32;
+    const size_t base = (size_t)b * 17;
+    const float scale = ldexpf(1.0f, (int)fd_byte(row, type, base + 16, B) - 127);
+    const uint32_t p = fd_byte(row, type, base + i / 2, B);
+    const uint32_t code = (i & 1) ? (p >> 4) : (p & 15);
+    const float lut = mxfp4_value(code);
+    return (lut * scale) * x[(size_t)b * 32 + i];
+}
+
+// rows_per_wg rows of one weight per workgroup (grid.y indexes the
+// weight); the row's units are taken `chunk` at a time: terms into LDS in
+// parallel, then one thread per row adds them to its sum in unit order.
+struct FdJob {
+    const uint8_t* w[3];
+    float* out[3];
+    int rows[3];
+    int type, cols, B, units, rows_per_wg, chunk;
+    size_t rb;
+};
+
+__global__ __launch_bounds__(kFdThreads) void float_dot_kernel(FdJob j, const float* __restrict__ x) {
+    __shared__ float terms[kFdLdsTerms];
+    const int wi = blockIdx.y;
+    const int r0 = blockIdx.x * j.rows_per_wg;
+    const int nr = min(j.rows_per_wg, j.rows[wi] - r0);
+    if (nr <= 0) return;  // uniform
+    const uint8_t* w = j.w[wi] + (size_t)r0 * j.rb;
+    float sum = 0.0f;
+    for (int u0 = 0; u0 < j.units; u0 += j.chunk) {
+        const int cu = min(j.chunk, j.units - u0);
+        for (int t = threadIdx.x; t < nr * cu; t += kFdThreads) {
+            const int rr = t / cu, u = t - rr * cu;
+            terms[t] = fd_term(w + (size_t)rr * j.rb, j.type, j.B, x, u0 + u);
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < nr) {
+            const float* tr = terms + threadIdx.x * cu;
+            for (int u = 0; u < cu; u++) sum = sum + tr[u];
+        }
+        __syncthreads();
+    }
+    if ((int)threadIdx.x < nr) j.out[wi][r0 + threadIdx.x] = sum;
+}
+
+bool float_dot_type(int t) {
+    return t == GLLM_TYPE_Q8_0 || t == GLLM_TYPE_Q4_0 || t == GLLM_TYPE_Q4_1 ||
+           t == GLLM_TYPE_Q2_K || t == GLLM_TYPE_Q3_K || t == GLLM_TYPE_Q5_K ||
+           t == GLLM_TYPE_MXFP4;
+}
+
+// n (1..3) weights of one float-dot type and cols against one f32 vector
+int launch_float_dot(int n, gllm_hip_weight* const* ws, const float* d_x, float* const* outs,
+                     hipStream_t s) {
+    if (n < 1 || n > 3) return fail(GLLM_EINVAL, "float row dot: %d weights (1..3)", n);
+    FdJob j{};
+    j.type = ws[0]->type;
+    j.cols = ws[0]->cols;
+    j.B = ws[0]->blocks;
+    j.rb = ws[0]->row_bytes;
+    j.units = j.cols / fd_unit_elems(j.type);
+    if (!float_dot_type(j.type)) return fail(GLLM_EUNSUP, "float row dot: type %d", j.type);
+    int max_rows = 0, total = 0;
+    for (int i = 0; i < n; i++) total += ws[i]->rows;
+    // about 1024 workgroups over the group, at most 256 rows each
+    j.rows_per_wg = std::max(1, std::min(kFdThreads, (total + 1023) / 1024));
+    j.chunk = std::min(j.units, kFdLdsTerms / j.rows_per_wg);
+    for (int i = 0; i < n; i++) {
+        if (ws[i]->type != j.type || ws[i]->cols != j.cols)
+            return fail(GLLM_EINVAL, "float row dot: mixed types or widths");
+        j.w[i] = ws[i]->d_data;
+        j.out[i] = outs[i];
+        j.rows[i] = ws[i]->rows;
+        max_rows = std::max(max_rows, ws[i]->rows);
+    }
+    const dim3 grid((max_rows + j.rows_per_wg - 1) / j.rows_per_wg, n);
+    hipLaunchKernelGGL(float_dot_kernel, grid, dim3(kFdThreads), 0, s, j, d_x);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+}  // namespace gllm

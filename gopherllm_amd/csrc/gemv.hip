@@ -34,6 +34,10 @@ static int mfma_min_tok() {
     return n;
 }
 
+bool float_dot_type(int t);
+int launch_float_dot(int n, gllm_hip_weight* const* ws, const float* d_x, float* const* outs,
+                     hipStream_t s);
+
 struct GemvJob {
     const uint8_t* w[3];
     float* out[3];
@@ -1026,83 +1030,7 @@ __global__ void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restri
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (size_t)gridDim.x * blockDim.x) {
         const size_t r = i / rb, o = i % rb;  // o: offset in the reference row
-        size_t n;                             // offset in the repacked row
-        if (type == GLLM_TYPE_Q4_K) {
-            // headers to the front of the row (q4k_hdr_off), nibble byte
-            // 32s + 4k + j of block b -> q4k_nib_off(B, b) + 16k + 4s + j
-            const size_t b = o / 144, e = o % 144;
-            if (e < 16) {
-                n = q4k_hdr_off((int)b) + e;
-            } else {
-                const size_t qi = e - 16, s4 = qi / 32, l = qi % 32;
-                n = q4k_nib_off(B, (int)b) + (l / 4) * 16 + s4 * 4 + (l % 4);
-            }
-        } else if (type == GLLM_TYPE_Q6_K) {
-            // ql byte 32q + 4k + j -> 16k + 4q + j, qh byte 128 + 32h + 4k + j
-            // -> 128 + 8k + 4h + j (lane k's bytes together), scales
-            // unchanged, d to the row's tail
-            const size_t b = o / 210, e = o % 210;
-            if (e < 128) {
-                const size_t q = e / 32, l = e % 32;
-                n = b * 208 + (l / 4) * 16 + q * 4 + (l % 4);
-            } else if (e < 192) {
-                const size_t h = (e - 128) / 32, l = (e - 128) % 32;
-                n = b * 208 + 128 + (l / 4) * 8 + h * 4 + (l % 4);
-            } else if (e < 208) {
-                n = b * 208 + e;
-            } else {
-                n = (size_t)B * 208 + b * 2 + (e - 208);
-            }
-        } else if (type == GLLM_TYPE_Q8_0) {
-            // [d][32 int8] x 8 -> [8 d][lane k: its dword of blocks q = 0..7 at
-            // 16 + 32k + 4q]
-            const size_t g = o / 272, e = o % 272, q = e / 34, f = e % 34;
-            n = g * 272 + (f < 2 ? q * 2 + f : 16 + ((f - 2) / 4) * 32 + q * 4 + (f - 2) % 4);
-        } else if (type == GLLM_TYPE_Q5_K) {
-            // [header 16][qh 32][nibbles 128] -> [header][lane k: 4 chunk dwords][lane k: qh dword]
-            const size_t b = o / 176, e = o % 176;
-            if (e < 16) {
-                n = o;
-            } else if (e < 48) {
-                n = b * 176 + 144 + (e - 16);
-            } else {
-                const size_t qi = e - 48, s4 = qi / 32, l = qi % 32;
-                n = b * 176 + 16 + (l / 4) * 16 + s4 * 4 + (l % 4);
-            }
-        } else if (type == GLLM_TYPE_Q2_K) {
-            // [scales 16][qs 64][d][dmin] -> [d][dmin][scales][lane k: qs dwords n = 0, 1]
-            const size_t b = o / 84, e = o % 84;
-            if (e < 16) {
-                n = b * 84 + 4 + e;
-            } else if (e < 80) {
-                const size_t qi = e - 16, h = qi / 32, l = qi % 32;
-                n = b * 84 + 20 + (l / 4) * 8 + h * 4 + (l % 4);
-            } else {
-                n = b * 84 + (e - 80);
-            }
-        } else if (type == GLLM_TYPE_Q3_K) {
-            // [hmask 32][qs 64][scales 12][d] -> [d][scales][lane k: hmask, qs n=0, qs n=1 dwords]
-            const size_t b = o / 110, e = o % 110;
-            if (e < 32) {
-                n = b * 110 + 14 + (e / 4) * 12 + (e % 4);
-            } else if (e < 96) {
-                const size_t qi = e - 32, h = qi / 32, l = qi % 32;
-                n = b * 110 + 14 + (l / 4) * 12 + 4 + h * 4 + (l % 4);
-            } else if (e < 108) {
-                n = b * 110 + 2 + (e - 96);
-            } else {
-                n = b * 110 + (e - 108);
-            }
-        } else if (type == GLLM_TYPE_Q4_0 || type == GLLM_TYPE_Q4_1) {
-            // 8 blocks [d (m) | 16 nibble bytes] -> [8 x d (m)][lane group kk: 8 dwords]
-            const size_t hb = type == GLLM_TYPE_Q4_0 ? 2 : 4, bb = hb + 16, sb = 8 * bb;
-            const size_t S = o / sb, e = o % sb, g = e / bb, f = e % bb;
-            n = S * sb + (f < hb ? g * hb + f : 8 * hb + ((f - hb) / 4) * 32 + g * 4 + (f - hb) % 4);
-        } else {  // MXFP4
-            // 8 blocks [16 code bytes | e] -> [8 x e][lane k: 8 code ushorts]
-            const size_t S = o / 136, e = o % 136, g = e / 17, f = e % 17;
-            n = S * 136 + (f == 16 ? g : 8 + (f / 2) * 16 + g * 2 + (f % 2));
-        }
+        const size_t n = repacked_offset(type, o, B);
         if (inverse) dst[r * rb + o] = src[r * rb + n];
         else dst[r * rb + n] = src[r * rb + o];
     }
@@ -1136,6 +1064,8 @@ size_t ref_row_bytes(int type, int cols) {
     case GLLM_TYPE_Q4_0: return (size_t)(cols / 32) * 18;
     case GLLM_TYPE_Q4_1: return (size_t)(cols / 32) * 20;
     case GLLM_TYPE_MXFP4: return (size_t)(cols / 32) * 17;
+    case GLLM_TYPE_F32: return (size_t)cols * 4;
+    case GLLM_TYPE_F16: case GLLM_TYPE_BF16: return (size_t)cols * 2;
     default: return 0;
     }
 }
@@ -1482,19 +1412,68 @@ int validate_matvec(int n, gllm_hip_weight* const* ws, int p, const int* strides
             return fail(GLLM_EINVAL, "fused matvec needs one cols (%d vs %d)", ws[i]->cols,
                         ws[0]->cols);
     if (p <= 0) return fail(GLLM_EINVAL, "p = %d", p);
-    // batch 1: groups of Q4_K / Q6_K, mixed or not, are int8 row dots in the
-    // reference (MatvecQ4K2/3IntoWithXSums, MatvecQ6K2/3Into,
-    // MatvecQ4K2Q6KIntoWithXSums); groups of the other formats go through its
-    // float kernels (matvecSameType2/3Into, model.go:3213-3254).  Batches
-    // share the int8 activations across any formats (matvecBatchQ8Fused).
-    if (n > 1 && p == 1)
-        for (int i = 0; i < n; i++)
-            if (ws[i]->type != GLLM_TYPE_Q4_K && ws[i]->type != GLLM_TYPE_Q6_K)
-                return fail(GLLM_EUNSUP, "fused batch-1 matvec of type %d: the reference uses "
-                                         "its float kernel here (matvecSameType2/3Into, "
-                                         "model.go:3213-3254)", ws[i]->type);
     for (int i = 0; i < n; i++)
         if (strides && strides[i] < ws[i]->rows) return fail(GLLM_EINVAL, "out stride < rows");
+    return GLLM_OK;
+}
+
+// Fused batch-1 groups (tryMatvec2Into model.go:3186-3206 for two weights,
+// tryMatvecAttentionInto model.go:3157-3184 for three): a same-type pair or
+// triple of Q4_K or Q6_K, or Q4_K/Q4_K/Q6_K, runs the int8 row dots, which
+// give each projection the value its own MatvecInto gives; a same-type pair
+// or triple of another format runs the float kernels (matvecSameType2/3Into);
+// for three weights without a same-type triple the first same-type pair of
+// (0,1), (0,2), (1,2) is the fused one and the third runs on its own.
+// fl[i] = 1 marks the weights that take the float kernels.
+static bool pair_float(int ta, int tb) {
+    return ta == tb && ta != GLLM_TYPE_Q4_K && ta != GLLM_TYPE_Q6_K;
+}
+int group_routing(int n, gllm_hip_weight* const* ws, int* fl) {
+    for (int i = 0; i < n; i++) fl[i] = 0;
+    if (n == 2) {
+        fl[0] = fl[1] = pair_float(ws[0]->type, ws[1]->type);
+    } else if (n == 3) {
+        const int t0 = ws[0]->type, t1 = ws[1]->type, t2 = ws[2]->type;
+        if (t0 == t1 && t0 == t2) {
+            fl[0] = fl[1] = fl[2] = pair_float(t0, t0);
+        } else if (!(t0 == GLLM_TYPE_Q4_K && t1 == GLLM_TYPE_Q4_K && t2 == GLLM_TYPE_Q6_K)) {
+            if (t0 == t1) fl[0] = fl[1] = pair_float(t0, t1);
+            else if (t0 == t2) fl[0] = fl[2] = pair_float(t0, t2);
+            else if (t1 == t2) fl[1] = fl[2] = pair_float(t1, t2);
+        }
+    }
+    for (int i = 0; i < n; i++)
+        if (fl[i] && !float_dot_type(ws[i]->type))
+            return fail(GLLM_EUNSUP, "fused batch-1 group of type %d: the reference's float "
+                                     "kernel for it (sameTypeQuantDot, model.go:3258-3283) "
+                                     "is not restated here", ws[i]->type);
+    return GLLM_OK;
+}
+
+// W.x for a batch-1 fused group: the float-kernel members in one launch,
+// the others through gemv_f32's int8 row kernels.
+int gemv_group(int n, gllm_hip_weight* const* ws, const float* d_x, float* const* outs,
+               const int* strides, void* act_buf, hipStream_t s) {
+    int fl[3];
+    GLLM_TRY(group_routing(n, ws, fl));
+    gllm_hip_weight* fw[3];
+    gllm_hip_weight* iw[3];
+    float* fo[3];
+    float* io[3];
+    int is[3];
+    int nf = 0, ni = 0;
+    for (int i = 0; i < n; i++) {
+        if (fl[i]) {
+            fw[nf] = ws[i];
+            fo[nf++] = outs[i];
+        } else {
+            iw[ni] = ws[i];
+            is[ni] = strides ? strides[i] : ws[i]->rows;
+            io[ni++] = outs[i];
+        }
+    }
+    if (nf) GLLM_TRY(launch_float_dot(nf, fw, d_x, fo, s));
+    if (ni) GLLM_TRY(gemv_f32(ni, iw, d_x, 1, io, is, act_buf, s));
     return GLLM_OK;
 }
 
@@ -1503,6 +1482,7 @@ int matvec_multi(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, fl
     GLLM_TRY(validate_matvec(n, ws, p, strides));
     void* sc = thread_scratch(scratch_slot, act_bytes(ws[0]->cols, p), s);
     if (!sc) return scratch_error();
+    if (n > 1 && p == 1) return gemv_group(n, ws, d_xs, outs, strides, sc, s);
     return gemv_f32(n, ws, d_xs, p, outs, strides, sc, s);
 }
 
@@ -1520,12 +1500,16 @@ static int matvec_host(int n, gllm_hip_weight* const* ws, const float* x, int p,
                        float* const* outs);
 
 
+// F32 / F16 / BF16 weights hold rows for gllm_hip_weight_rows_dev (any
+// cols); the block formats need whole 256-element super-blocks per row.
 static gllm_hip_weight* weight_alloc(int ggml_type, int rows, int cols, size_t len) {
-    if (!row_kernel_type(ggml_type)) {
+    const bool scalar = ggml_type == GLLM_TYPE_F32 || ggml_type == GLLM_TYPE_F16 ||
+                        ggml_type == GLLM_TYPE_BF16;
+    if (!row_kernel_type(ggml_type) && !scalar) {
         fail(GLLM_EUNSUP, "weight type %d not supported", ggml_type);
         return nullptr;
     }
-    if (rows <= 0 || cols <= 0 || cols % 256) {
+    if (rows <= 0 || cols <= 0 || (!scalar && cols % 256)) {
         fail(GLLM_EINVAL, "weight shape %dx%d (cols must be a positive multiple of 256)", rows, cols);
         return nullptr;
     }

@@ -115,6 +115,87 @@ __host__ __device__ __forceinline__ size_t q4k_nib_off(int B, int b) {
     return (size_t)B * 16 + (size_t)b * 128;
 }
 
+// Offset, in the device row, of byte o of a reference (GGUF) row of B
+// blocks: the one-time upload repack of each type (same bytes, block sizes
+// unchanged; gllm_hip_weight_download_dev applies it backwards).
+__host__ __device__ inline size_t repacked_offset(int type, size_t o, int B) {
+    if (type == GLLM_TYPE_Q4_K) {
+        // headers to the front of the row (q4k_hdr_off), nibble byte
+        // 32s + 4k + j of block b -> q4k_nib_off(B, b) + 16k + 4s + j
+        const size_t b = o / 144, e = o % 144;
+        if (e < 16) return q4k_hdr_off((int)b) + e;
+        const size_t qi = e - 16, s4 = qi / 32, l = qi % 32;
+        return q4k_nib_off(B, (int)b) + (l / 4) * 16 + s4 * 4 + (l % 4);
+    }
+    if (type == GLLM_TYPE_Q6_K) {
+        // ql byte 32q + 4k + j -> 16k + 4q + j, qh byte 128 + 32h + 4k + j
+        // -> 128 + 8k + 4h + j (lane k's bytes together), scales unchanged,
+        // d to the row's tail
+        const size_t b = o / 210, e = o % 210;
+        if (e < 128) {
+            const size_t q = e / 32, l = e % 32;
+            return b * 208 + (l / 4) * 16 + q * 4 + (l % 4);
+        }
+        if (e < 192) {
+            const size_t h = (e - 128) / 32, l = (e - 128) % 32;
+            return b * 208 + 128 + (l / 4) * 8 + h * 4 + (l % 4);
+        }
+        if (e < 208) return b * 208 + e;
+        return (size_t)B * 208 + b * 2 + (e - 208);
+    }
+    if (type == GLLM_TYPE_Q8_0) {
+        // [d][32 int8] x 8 -> [8 d][lane k: its dword of blocks q = 0..7 at
+        // 16 + 32k + 4q]
+        const size_t g = o / 272, e = o % 272, q = e / 34, f = e % 34;
+        return g * 272 + (f < 2 ? q * 2 + f : 16 + ((f - 2) / 4) * 32 + q * 4 + (f - 2) % 4);
+    }
+    if (type == GLLM_TYPE_Q5_K) {
+        // [header 16][qh 32][nibbles 128] -> [header][lane k: 4 chunk
+        // dwords][lane k: qh dword]
+        const size_t b = o / 176, e = o % 176;
+        if (e < 16) return o;
+        if (e < 48) return b * 176 + 144 + (e - 16);
+        const size_t qi = e - 48, s4 = qi / 32, l = qi % 32;
+        return b * 176 + 16 + (l / 4) * 16 + s4 * 4 + (l % 4);
+    }
+    if (type == GLLM_TYPE_Q2_K) {
+        // [scales 16][qs 64][d][dmin] -> [d][dmin][scales][lane k: qs dwords
+        // n = 0, 1]
+        const size_t b = o / 84, e = o % 84;
+        if (e < 16) return b * 84 + 4 + e;
+        if (e < 80) {
+            const size_t qi = e - 16, h = qi / 32, l = qi % 32;
+            return b * 84 + 20 + (l / 4) * 8 + h * 4 + (l % 4);
+        }
+        return b * 84 + (e - 80);
+    }
+    if (type == GLLM_TYPE_Q3_K) {
+        // [hmask 32][qs 64][scales 12][d] -> [d][scales][lane k: hmask,
+        // qs n = 0, qs n = 1 dwords]
+        const size_t b = o / 110, e = o % 110;
+        if (e < 32) return b * 110 + 14 + (e / 4) * 12 + (e % 4);
+        if (e < 96) {
+            const size_t qi = e - 32, h = qi / 32, l = qi % 32;
+            return b * 110 + 14 + (l / 4) * 12 + 4 + h * 4 + (l % 4);
+        }
+        if (e < 108) return b * 110 + 2 + (e - 96);
+        return b * 110 + (e - 108);
+    }
+    if (type == GLLM_TYPE_Q4_0 || type == GLLM_TYPE_Q4_1) {
+        // 8 blocks [d (m) | 16 nibble bytes] -> [8 x d (m)][lane group kk:
+        // 8 dwords]
+        const size_t hb = type == GLLM_TYPE_Q4_0 ? 2 : 4, bb = hb + 16, sb = 8 * bb;
+        const size_t S = o / sb, e = o % sb, g = e / bb, f = e % bb;
+        return S * sb + (f < hb ? g * hb + f : 8 * hb + ((f - hb) / 4) * 32 + g * 4 + (f - hb) % 4);
+    }
+    if (type == GLLM_TYPE_MXFP4) {
+        // 8 blocks [16 code bytes | e] -> [8 x e][lane k: 8 code ushorts]
+        const size_t S = o / 136, e = o % 136, g = e / 17, f = e % 17;
+        return S * 136 + (f == 16 ? g : 8 + (f / 2) * 16 + g * 2 + (f % 2));
+    }
+    return o;  // F32 / F16 / BF16 rows are stored as they are
+}
+
 // Byte offset, inside one 256-element block of the lane-permuted Q8K
 // activation layout, of element e = 32*m + 4*k + j: lane k of every row
 // kernel reads its eight dwords (m = 0..7) as two contiguous 16-byte loads.

@@ -48,8 +48,12 @@
 extern "C" {
 #endif
 
-/* GGML tensor types accepted by the row kernels (gguf.go:27-60). */
+/* GGML tensor types (gguf.go:27-60).  Every type below except F32, F16 and
+ * BF16 has row kernels; F32 / F16 / BF16 weights hold rows for
+ * gllm_hip_weight_rows_dev only (token embeddings). */
 #define GLLM_TYPE_F32 0
+#define GLLM_TYPE_F16 1
+#define GLLM_TYPE_BF16 30
 #define GLLM_TYPE_Q4_0 2
 #define GLLM_TYPE_Q4_1 3
 #define GLLM_TYPE_Q8_0 8
@@ -99,6 +103,12 @@ gllm_hip_weight* gllm_hip_weight_from_device(const void* d_data, size_t len, int
 /* replaces gllm_metal_release_weight (internal/metal/metal_darwin.go:1001) */
 void gllm_hip_weight_release(gllm_hip_weight* w);
 int gllm_hip_weight_shape(const gllm_hip_weight* w, int* ggml_type, int* rows, int* cols);
+/* Weight.RowInto (model.go:1034-1100, raw_scalar.go:130-161): out[i][0..cols)
+ * = row d_rows[i] dequantised (DequantRow*Into of the weight's type, or the
+ * F32 / F16 / BF16 values) for i < n, device pointers, enqueued on stream.
+ * Ids must be < rows (an id past the end reads the last row). */
+int gllm_hip_weight_rows_dev(const gllm_hip_weight* w, const uint32_t* d_rows, int n,
+                             float* d_out, void* stream);
 /* Device bytes of the weight in the reference's GGUF layout (undoing the
  * repack); dst is a device buffer of rows*row_bytes. */
 int gllm_hip_weight_download_dev(const gllm_hip_weight* w, void* d_dst, void* stream);
@@ -113,11 +123,17 @@ int gllm_hip_weight_download_dev(const gllm_hip_weight* w, void* d_dst, void* st
  * reference's amd64 row kernels bit for bit.  (gllm_metal_q4k_matvec,
  * internal/metal/metal_darwin.go:740) */
 int gllm_hip_matvec(gllm_hip_weight* w, const float* x, float* out);
-/* Two / three weights sharing one activation vector (MatvecQ4K2IntoWithXSums
- * simd.go:295, Q4KMatvec3IntoWithXSums metal.go:14, MatvecQ4K2Q6KIntoWithXSums
- * simd.go:331, MatvecQ6K2Into / MatvecQ6K3Into simd.go:443/483).  Q4_K and
- * Q6_K only: the reference routes Q8_0 pairs to its float kernel
- * (model.go:3213-3230), which this path does not reproduce. */
+/* Two / three weights sharing one activation vector, routed as the
+ * reference routes a decode step's fused groups (tryMatvec2Into
+ * model.go:3186-3206 for two, tryMatvecAttentionInto model.go:3157-3184 for
+ * three): same-type Q4_K or Q6_K groups and Q4_K/Q4_K/Q6_K run the int8 row
+ * dots (MatvecQ4K2IntoWithXSums simd.go:295, Q4KMatvec3IntoWithXSums
+ * metal.go:14, MatvecQ4K2Q6KIntoWithXSums simd.go:331, MatvecQ6K2Into /
+ * MatvecQ6K3Into simd.go:443/483); a same-type pair or triple of Q8_0, Q4_0,
+ * Q4_1, Q2_K, Q3_K, Q5_K or MXFP4 runs the float kernels
+ * (matvecSameType2/3Into model.go:3213-3256: DotQ8_0F32, DotQ4_0F32,
+ * DotQ4_1F32, DotQ2KF32, DotQ3KF32, DotQ5KF32, DotMXFP4F32); a weight
+ * outside a fused pair runs its own int8 row dot. */
 int gllm_hip_matvec2(gllm_hip_weight* a, gllm_hip_weight* b, const float* x, float* out_a,
                      float* out_b);
 int gllm_hip_matvec3(gllm_hip_weight* a, gllm_hip_weight* b, gllm_hip_weight* c,
@@ -144,13 +160,10 @@ int gllm_hip_argmax_penalized(gllm_hip_weight* w, const float* x, const uint32_t
 int gllm_hip_matvec_dev(gllm_hip_weight* w, const float* d_xs, int p, float* d_outs,
                         int out_stride, void* stream);
 /* n weights (same cols) against the same activations; one quantisation of
- * x is shared by all of them, runs of one type are one launch.  Batches
- * (p > 1) take any mix of the int8 formats (matvecBatchQ8Fused2/3,
- * kernels_portable_tunables.go:292-408); batch 1 with n > 1 takes Q4_K and
- * Q6_K, mixed or not (Q4KMatvec3IntoWithXSums, MatvecQ6K2/3Into,
- * MatvecQ4K2Q6KIntoWithXSums: model.go:3110-3190) and refuses the other
- * formats, whose same-type groups the reference runs as floats
- * (matvecSameType2/3Into, model.go:3213-3254). */
+ * x is shared by the int8 row kernels, runs of one type are one launch.
+ * Batches (p > 1) take any mix of the int8 formats (matvecBatch2/3 ->
+ * matvecBatchQ8 per weight, forward_batch.go:108-233); batch 1 with n > 1
+ * is a fused group, routed as gllm_hip_matvec2 / gllm_hip_matvec3 route it. */
 int gllm_hip_matvec_multi_dev(int n, gllm_hip_weight* const* ws, const float* d_xs, int p,
                               float* const* d_outs, const int* out_strides, void* stream);
 int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token, void* stream);

@@ -201,6 +201,7 @@ long ref_row_bytes(int type, int cols) {
     case REF_Q5_K: return (long)(cols / 256) * 176;
     case REF_F32: return (long)cols * 4;
     case REF_F16: return (long)cols * 2;
+    case REF_BF16: return (long)cols * 2;
     default: return -1;
     }
 }
@@ -1293,7 +1294,215 @@ void ref_dequant_row(int type, const uint8_t* row, int cols, float* out) {
         }
     } else if (type == REF_F32) {
         memcpy(out, row, sizeof(float) * (size_t)cols);
+    } else if (type == REF_F16) {
+        /* raw_scalar.go:145-148: F16ToF32 of each little-endian half */
+        for (int i = 0; i < cols; i++) out[i] = ref_f16_to_f32(le16(row + 2L * i));
+    } else if (type == REF_BF16) {
+        /* raw_scalar.go:149-152: the half's bits as the top of a float32 */
+        for (int i = 0; i < cols; i++) {
+            const uint32_t bits = (uint32_t)le16(row + 2L * i) << 16;
+            memcpy(out + i, &bits, 4);
+        }
     }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Float-activation row dots of the reference's same-type fused groups        */
+/* (matvecSameType2/3Into via sameTypeQuantDot, model.go:3213-3283).  Go does */
+/* not contract float32 expressions on amd64 (GOAMD64=v1), so every product  */
+/* and sum below is rounded on its own, in the Go evaluation order.          */
+/* ------------------------------------------------------------------------- */
+
+/* simd.go:646-675 DotQ8_0F32: per block four accumulators over elements
+ * i, i+4, ... (s_j gets elements j, 4+j, ..., 28+j in order), then
+ * sum += scale * ((s0 + s1) + (s2 + s3)). */
+static float float_dot_q8_0(const uint8_t* row, const float* x, int cols) {
+    float sum = 0.0f;
+    for (int b = 0; b < cols / 32; b++) {
+        const uint8_t* blk = row + (long)b * 34;
+        const float scale = ref_f16_to_f32(le16(blk));
+        const int8_t* r = (const int8_t*)(blk + 2);
+        const float* xb = x + (long)b * 32;
+        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < 32; i += 8) {
+            for (int j = 0; j < 4; j++) s[j] = s[j] + (float)r[i + j] * xb[i + j];
+            for (int j = 0; j < 4; j++) s[j] = s[j] + (float)r[i + 4 + j] * xb[i + 4 + j];
+        }
+        sum = sum + scale * ((s[0] + s[1]) + (s[2] + s[3]));
+    }
+    return sum;
+}
+
+/* simd.go:677-715 DotQ4_0F32: s_j += lo*x[i+j] + hi*x[16+i+j] for
+ * i = 0, 4, 8, 12 (codes q - 8), sum += scale * ((s0 + s1) + (s2 + s3)). */
+static float float_dot_q4_0(const uint8_t* row, const float* x, int cols) {
+    float sum = 0.0f;
+    for (int b = 0; b < cols / 32; b++) {
+        const uint8_t* blk = row + (long)b * 18;
+        const float scale = ref_f16_to_f32(le16(blk));
+        const uint8_t* r = blk + 2;
+        const float* xb = x + (long)b * 32;
+        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < 16; i += 4)
+            for (int j = 0; j < 4; j++) {
+                const float lo = (float)((int)(r[i + j] & 0x0f) - 8);
+                const float hi = (float)((int)((r[i + j] >> 4) & 0x0f) - 8);
+                s[j] = s[j] + (lo * xb[i + j] + hi * xb[16 + i + j]);
+            }
+        sum = sum + scale * ((s[0] + s[1]) + (s[2] + s[3]));
+    }
+    return sum;
+}
+
+/* quant_extra.go:42-62 DotQ4_1F32: qdot += q_lo*x[i] + q_hi*x[16+i],
+ * xsum += x[i] + x[16+i] for i = 0..15, sum += d*qdot + m*xsum. */
+static float float_dot_q4_1(const uint8_t* row, const float* x, int cols) {
+    float sum = 0.0f;
+    for (int b = 0; b < cols / 32; b++) {
+        const uint8_t* blk = row + (long)b * 20;
+        const float d = ref_f16_to_f32(le16(blk)), m = ref_f16_to_f32(le16(blk + 2));
+        const float* xb = x + (long)b * 32;
+        float qdot = 0.0f, xsum = 0.0f;
+        for (int i = 0; i < 16; i++) {
+            const uint8_t pk = blk[4 + i];
+            qdot = qdot + ((float)(pk & 0x0f) * xb[i] + (float)(pk >> 4) * xb[16 + i]);
+            xsum = xsum + (xb[i] + xb[16 + i]);
+        }
+        sum = sum + (d * qdot + m * xsum);
+    }
+    return sum;
+}
+
+/* quant_extra.go:271-302 DotQ2KF32: per 16-element sub-block is (scale byte
+ * is: low nibble scale, high nibble min) qdot += code*x, xsum += x in
+ * element order, sum += dl*qdot - ml*xsum. */
+static float float_dot_q2k(const uint8_t* row, const float* x, int cols) {
+    float sum = 0.0f;
+    for (int b = 0; b < cols / 256; b++) {
+        const uint8_t* blk = row + (long)b * 84;
+        const float d = ref_f16_to_f32(le16(blk + 80)), dmin = ref_f16_to_f32(le16(blk + 82));
+        const float* xb = x + (long)b * 256;
+        for (int is = 0; is < 16; is++) {
+            const float dl = d * (float)(blk[is] & 0x0f), ml = dmin * (float)(blk[is] >> 4);
+            float qdot = 0.0f, xsum = 0.0f;
+            for (int l = 0; l < 16; l++) {
+                const float xv = xb[is * 16 + l];
+                qdot = qdot + (float)q2_code(blk + 16, is * 16 + l) * xv;
+                xsum = xsum + xv;
+            }
+            sum = sum + (dl * qdot - ml * xsum);
+        }
+    }
+    return sum;
+}
+
+/* quant_extra.go:376-410 DotQ3KF32: acc += v*x over each 16-element
+ * sub-block (v = code - 4 where the hmask bit is clear), sum += dl*acc with
+ * dl = d*(scale - 32). */
+static float float_dot_q3k(const uint8_t* row, const float* x, int cols) {
+    float sum = 0.0f;
+    for (int b = 0; b < cols / 256; b++) {
+        const uint8_t* blk = row + (long)b * 110;
+        int sc[16];
+        q3k_scales(blk + 96, sc);
+        const float d = ref_f16_to_f32(le16(blk + 108));
+        const float* xb = x + (long)b * 256;
+        for (int is = 0; is < 16; is++) {
+            const float dl = d * (float)(sc[is] - 32);
+            float acc = 0.0f;
+            for (int l = 0; l < 16; l++)
+                acc = acc + (float)q3_value(blk, is * 16 + l) * xb[is * 16 + l];
+            sum = sum + dl * acc;
+        }
+    }
+    return sum;
+}
+
+/* simd.go:1031-1186 DotQ5KF32: per 64-element step s of a block, lane
+ * accumulators j = l % 4 over l = 0..31 of qd1_j += code1*x1, qd2_j +=
+ * code2*x2, xs1_j += x1, xs2_j += x2 (code = nibble + 16 * qh bit 2s / 2s+1),
+ * then sum += d1*qdot1 - min1*xsum1 and sum += d2*qdot2 - min2*xsum2 with
+ * qdot = (a0 + a1) + (a2 + a3). */
+static float float_dot_q5k(const uint8_t* row, const float* x, int cols) {
+    float sum = 0.0f;
+    for (int b = 0; b < cols / 256; b++) {
+        const uint8_t* blk = row + (long)b * 176;
+        const float d = ref_f16_to_f32(le16(blk)), dmin = ref_f16_to_f32(le16(blk + 2));
+        const uint8_t* qh = blk + 16;
+        const float* xb = x + (long)b * 256;
+        for (int st = 0; st < 4; st++) {
+            int sc1, m1, sc2, m2;
+            scale_min_k4(2 * st, blk + 4, &sc1, &m1);
+            scale_min_k4(2 * st + 1, blk + 4, &sc2, &m2);
+            const float d1 = d * (float)sc1, d2 = d * (float)sc2;
+            const float min1 = dmin * (float)m1, min2 = dmin * (float)m2;
+            const uint8_t* q = blk + 48 + 32 * st;
+            const float* x1 = xb + 64 * st;
+            const float* x2 = x1 + 32;
+            float qd1[4] = {0}, qd2[4] = {0}, xs1[4] = {0}, xs2[4] = {0};
+            for (int l = 0; l < 32; l += 4)
+                for (int j = 0; j < 4; j++) {
+                    const int h1 = (qh[l + j] >> (2 * st)) & 1, h2 = (qh[l + j] >> (2 * st + 1)) & 1;
+                    qd1[j] = qd1[j] + (float)((q[l + j] & 0x0f) + 16 * h1) * x1[l + j];
+                    qd2[j] = qd2[j] + (float)((q[l + j] >> 4) + 16 * h2) * x2[l + j];
+                    xs1[j] = xs1[j] + x1[l + j];
+                    xs2[j] = xs2[j] + x2[l + j];
+                }
+            const float qdot1 = (qd1[0] + qd1[1]) + (qd1[2] + qd1[3]);
+            const float qdot2 = (qd2[0] + qd2[1]) + (qd2[2] + qd2[3]);
+            const float xsum1 = (xs1[0] + xs1[1]) + (xs1[2] + xs1[3]);
+            const float xsum2 = (xs2[0] + xs2[1]) + (xs2[2] + xs2[3]);
+            sum = sum + (d1 * qdot1 - min1 * xsum1);
+            sum = sum + (d2 * qdot2 - min2 * xsum2);
+        }
+    }
+    return sum;
+}
+
+/* simd.go:1458-1477 DotMXFP4F32: sum += (lut[code] * scale) * x for every
+ * element in order, scale = float32(2^(e - 127)). */
+static float float_dot_mxfp4(const uint8_t* row, const float* x, int cols) {
+    static const float lut[16] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f,
+                                  -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+    float sum = 0.0f;
+    for (int b = 0; b < cols / 32; b++) {
+        const uint8_t* blk = row + (long)b * 17;
+        const float scale = (float)ldexp(1.0, (int)blk[16] - 127);
+        const float* xb = x + (long)b * 32;
+        for (int i = 0; i < 16; i++) {
+            sum = sum + (lut[blk[i] & 0x0f] * scale) * xb[2 * i];
+            sum = sum + (lut[blk[i] >> 4] * scale) * xb[2 * i + 1];
+        }
+    }
+    return sum;
+}
+
+int ref_float_dot_supported(int type) {
+    return type == REF_Q8_0 || type == REF_Q4_0 || type == REF_Q4_1 || type == REF_Q2_K ||
+           type == REF_Q3_K || type == REF_Q5_K || type == REF_MXFP4;
+}
+
+float ref_float_dot(int type, const uint8_t* row, const float* x, int cols) {
+    switch (type) {
+    case REF_Q8_0: return float_dot_q8_0(row, x, cols);
+    case REF_Q4_0: return float_dot_q4_0(row, x, cols);
+    case REF_Q4_1: return float_dot_q4_1(row, x, cols);
+    case REF_Q2_K: return float_dot_q2k(row, x, cols);
+    case REF_Q3_K: return float_dot_q3k(row, x, cols);
+    case REF_Q5_K: return float_dot_q5k(row, x, cols);
+    case REF_MXFP4: return float_dot_mxfp4(row, x, cols);
+    default: return NAN;
+    }
+}
+
+/* matvecDotRows over all rows (model.go:3213-3256; rows are independent) */
+int ref_matvec_float(int type, const uint8_t* data, const float* x, int rows, int cols,
+                     float* out, int threads) {
+    if (!ref_float_dot_supported(type)) return -1;
+    const long rb = ref_row_bytes(type, cols);
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : ref_num_threads())
+    for (int r = 0; r < rows; r++) out[r] = ref_float_dot(type, data + (long)r * rb, x, cols);
+    return 0;
 }
 
 /* ------------------------------------------------------------------------- */
@@ -1561,11 +1770,45 @@ static int llama_type(const ref_llama* m, int l, int slot) {
     return m->types ? m->types[l * 7 + slot] : m->layer_type;
 }
 
+/* W.x through the float kernels of a same-type fused group
+ * (matvecSameType2/3Into, model.go:3213-3256) */
+static void llama_matvec_float(ref_llama_state* s, int type, const uint8_t* w, const float* x,
+                               int rows, int cols, float* out) {
+    ref_matvec_float(type, w, x, rows, cols, out, s->threads);
+}
+
+/* The fused-group routing of one decode step.  tryMatvec2Into
+ * (model.go:3186-3206): a same-type pair of Q4_K or Q6_K runs the int8 row
+ * dots (which give each projection the same values as its own MatvecInto),
+ * any other same-type pair the float kernels; different types are no pair. */
+static int pair_float(int ta, int tb) { return ta == tb && ta != REF_Q4_K && ta != REF_Q6_K; }
+
+/* tryMatvecAttentionInto (model.go:3157-3184) for Q, K, V of layer l: all
+ * three of one type -> tryMatvec3Into (int8 for Q4_K / Q6_K, float kernels
+ * otherwise); Q4_K/Q4_K/Q6_K -> int8; else the first same-type pair of
+ * (q,k), (q,v), (k,v) fused and the third on its own; else each on its own
+ * (MatvecInto, int8).  fl[i] = 1 marks the projections that run the float
+ * kernels. */
+static void qkv_routing(const ref_llama* m, int l, int fl[3]) {
+    const int tq = llama_type(m, l, 0), tk = llama_type(m, l, 1), tv = llama_type(m, l, 2);
+    fl[0] = fl[1] = fl[2] = 0;
+    if (tq == tk && tq == tv) {
+        if (pair_float(tq, tq)) fl[0] = fl[1] = fl[2] = 1;
+        return;
+    }
+    if (tq == REF_Q4_K && tk == REF_Q4_K && tv == REF_Q6_K) return;
+    if (tq == tk) fl[0] = fl[1] = pair_float(tq, tk);
+    else if (tq == tv) fl[0] = fl[2] = pair_float(tq, tv);
+    else if (tk == tv) fl[1] = fl[2] = pair_float(tk, tv);
+}
+
 /* ForwardBodyInto (model.go:2622-2820) for the plain llama graph; leaves the
- * output-normed hidden state in s->xn.  Every projection is its own int8
- * matvec, which is also what the reference's mixed Q4_K / Q6_K groups compute
- * (tryMatvecAttentionInto, model.go:3156-3190). */
-static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
+ * output-normed hidden state in s->xn.  decode != 0 is the generation step
+ * (fused-group routing, qkv_routing / tryMatvec2Into for gate and up);
+ * decode == 0 is a prompt token of the batched prefill, where every
+ * projection runs matvecBatchQ8's int8 row dots on its own
+ * (forward_batch.go:108-204, matvecBatch3/2 forward_batch.go:210-233). */
+static void llama_body(ref_llama_state* s, uint32_t token, int pos, int decode) {
     const ref_llama* m = &s->m;
     int dim = m->dim, hd = m->head_dim, kvd = m->n_kv_heads * hd;
     int kvmul = m->n_heads / m->n_kv_heads;
@@ -1575,9 +1818,14 @@ static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
     float scale = m->attn_scale != 0.0f ? m->attn_scale : (float)(1.0 / sqrt((double)hd));
     for (int l = 0; l < m->n_layers; l++) {
         ref_rmsnorm(s->x, m->attn_norm[l], m->rms_eps, dim, s->xn);
-        llama_matvec(s, llama_type(m, l, 0), m->wq[l], s->xn, m->n_heads * hd, dim, s->q);
-        llama_matvec(s, llama_type(m, l, 1), m->wk[l], s->xn, kvd, dim, s->k);
-        llama_matvec(s, llama_type(m, l, 2), m->wv[l], s->xn, kvd, dim, s->v);
+        int fl[3] = {0, 0, 0};
+        if (decode) qkv_routing(m, l, fl);
+        (fl[0] ? llama_matvec_float : llama_matvec)(s, llama_type(m, l, 0), m->wq[l], s->xn,
+                                                    m->n_heads * hd, dim, s->q);
+        (fl[1] ? llama_matvec_float : llama_matvec)(s, llama_type(m, l, 1), m->wk[l], s->xn, kvd,
+                                                    dim, s->k);
+        (fl[2] ? llama_matvec_float : llama_matvec)(s, llama_type(m, l, 2), m->wv[l], s->xn, kvd,
+                                                    dim, s->v);
         ref_rope_apply(s->q, hd, m->n_heads, hd / 2, s->sinv, s->cosv);
         ref_rope_apply(s->k, hd, m->n_kv_heads, hd / 2, s->sinv, s->cosv);
         ref_f32_to_f16_row(s->k, s->kc[l] + (long)pos * kvd, kvd);
@@ -1591,8 +1839,11 @@ static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
         llama_matvec(s, llama_type(m, l, 3), m->wo[l], s->attn, dim, m->n_heads * hd, s->proj);
         for (int i = 0; i < dim; i++) s->x[i] = fmaf(s->proj[i], 1.0f, s->x[i]);
         ref_rmsnorm(s->x, m->ffn_norm[l], m->rms_eps, dim, s->xn);
-        llama_matvec(s, llama_type(m, l, 4), m->w1[l], s->xn, m->hidden, dim, s->gate);
-        llama_matvec(s, llama_type(m, l, 6), m->w3[l], s->xn, m->hidden, dim, s->up);
+        const int gu_float = decode && pair_float(llama_type(m, l, 4), llama_type(m, l, 6));
+        (gu_float ? llama_matvec_float : llama_matvec)(s, llama_type(m, l, 4), m->w1[l], s->xn,
+                                                       m->hidden, dim, s->gate);
+        (gu_float ? llama_matvec_float : llama_matvec)(s, llama_type(m, l, 6), m->w3[l], s->xn,
+                                                       m->hidden, dim, s->up);
         ref_silu_mul(s->gate, s->up, s->hidden, m->hidden);
         llama_matvec(s, llama_type(m, l, 5), m->w2[l], s->hidden, dim, m->hidden, s->proj);
         for (int i = 0; i < dim; i++) s->x[i] = fmaf(s->proj[i], 1.0f, s->x[i]);
@@ -1602,7 +1853,7 @@ static void llama_body(ref_llama_state* s, uint32_t token, int pos) {
 
 /* ForwardBodyInto + ArgmaxMatvec (runtime.go:1607-1656, model.go:2574-2610) */
 uint32_t ref_llama_decode(ref_llama_state* s, uint32_t token, int pos, float* hidden_out) {
-    llama_body(s, token, pos);
+    llama_body(s, token, pos, 1);
     if (hidden_out) memcpy(hidden_out, s->xn, sizeof(float) * s->m.dim);
     llama_push_recent(s, token);  /* emitToken appends before the next choice */
     if (s->penalty != 1.0f) {
@@ -1631,7 +1882,7 @@ uint32_t ref_llama_prefill(ref_llama_state* s, const uint32_t* tokens, int n, in
                            int chunk, float* logits_out) {
     (void)chunk;
     for (int t = 0; t < n; t++) {
-        llama_body(s, tokens[t], start_pos + t);
+        llama_body(s, tokens[t], start_pos + t, 0);
         llama_push_recent(s, tokens[t]);
     }
     llama_matvec(s, s->m.out_type, s->m.output, s->xn, s->m.vocab, s->m.dim, s->logits);

@@ -28,7 +28,7 @@ extern "C" {
 /* GGML type ids (gguf.go:27-60). */
 enum {
     REF_F32 = 0, REF_F16 = 1, REF_Q4_0 = 2, REF_Q4_1 = 3, REF_Q8_0 = 8, REF_Q2_K = 10,
-    REF_Q3_K = 11, REF_Q4_K = 12, REF_Q5_K = 13, REF_Q6_K = 14, REF_MXFP4 = 39
+    REF_Q3_K = 11, REF_Q4_K = 12, REF_Q5_K = 13, REF_Q6_K = 14, REF_BF16 = 30, REF_MXFP4 = 39
 };
 enum { REF_ORDER_GENERIC = 0, REF_ORDER_AMD64 = 1 };
 
@@ -64,6 +64,16 @@ float ref_row_dot_any(int type, const uint8_t* row, const int8_t* q8, const floa
 int ref_type_supported(int type);
 void ref_lane_ints(int type, const uint8_t* row, const int8_t* q8, int blocks,
                    int32_t* out);
+
+/* ---- float-activation row dots of same-type fused groups ----
+ * (sameTypeQuantDot model.go:3258-3283: DotQ8_0F32 simd.go:646, DotQ4_0F32
+ * simd.go:677, DotQ4_1F32 quant_extra.go:42, DotQ2KF32 quant_extra.go:271,
+ * DotQ3KF32 quant_extra.go:376, DotMXFP4F32 simd.go:1458) on GGUF rows and
+ * f32 x; cols % 256 == 0 for the K formats, % 32 otherwise. */
+int ref_float_dot_supported(int type);
+float ref_float_dot(int type, const uint8_t* row, const float* x, int cols);
+int ref_matvec_float(int type, const uint8_t* data, const float* x, int rows, int cols,
+                     float* out, int threads);
 
 /* bytes per row for a GGML type */
 long ref_row_bytes(int type, int cols);

@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
 Q4_0, Q4_1, Q2_K, Q3_K, Q5_K, MXFP4 = 2, 3, 10, 11, 13, 39
+BF16 = 30
 EXTRA_TYPES = (Q5_K, Q4_0, Q4_1, MXFP4, Q2_K, Q3_K)
 GENERIC, AMD64 = 0, 1
 
@@ -63,6 +64,9 @@ def lib():
             "ref_row_bytes": (l, [i, i]),
             "ref_matvec": (i, [i, vp, vp, i, i, vp, i, i]),
             "ref_matvec_batch": (i, [i, vp, vp, i, i, i, vp, i, i]),
+            "ref_float_dot_supported": (i, [i]),
+            "ref_float_dot": (f, [i, vp, vp, i]),
+            "ref_matvec_float": (i, [i, vp, vp, i, i, vp, i]),
             "ref_matvec_batch_fast": (i, [i, vp, vp, i, i, i, vp, i]),
             "ref_argmax_matvec": (C.c_uint32, [i, vp, vp, i, i, i, i]),
             "ref_argmax_finite": (C.c_uint32, [vp, l]),
@@ -243,6 +247,26 @@ def quantize_rows(qtype, w, threads=0):
     rows, cols = w.shape
     out = np.empty(rows * row_bytes(qtype, cols), np.uint8)
     lib().ref_quantize_rows(qtype, _p(w), rows, cols, _p(out), threads)
+    return out
+
+
+def float_dot_supported(qtype):
+    return bool(lib().ref_float_dot_supported(qtype))
+
+
+def float_dot(qtype, row, x, cols):
+    """One row's float-activation dot of a same-type fused group
+    (DotQ8_0F32 / DotQ4_0F32 / DotQ4_1F32 / DotQ2KF32 / DotQ3KF32 /
+    DotMXFP4F32)."""
+    row, x = _u8(row), _f32(x)
+    return float(lib().ref_float_dot(qtype, _p(row), _p(x), cols))
+
+
+def matvec_float(qtype, data, x, rows, cols, threads=0):
+    data, x = _u8(data), _f32(x)
+    out = np.empty(rows, np.float32)
+    if lib().ref_matvec_float(qtype, _p(data), _p(x), rows, cols, _p(out), threads) != 0:
+        raise ValueError(f"no float row dot for type {qtype}")
     return out
 
 

@@ -30,7 +30,19 @@ def normal(seed, shape, std=1.0):
 
 
 def quant_matrix(qtype, rows, cols, seed, std=0.02):
+    """GGUF-layout bytes of a rows x cols matrix of type qtype: N(0, std)
+    values quantised by the oracle (Q4_K, Q6_K, Q8_0), stored as they are
+    (F32, F16, BF16 truncated), or random codes with sane scales for the
+    other block formats (random_rows)."""
     w = normal(seed, (rows, cols), std)
+    if qtype == ref.F32:
+        return w.view(np.uint8).reshape(-1), w
+    if qtype == ref.F16:
+        return w.astype(np.float16).view(np.uint8).reshape(-1), w
+    if qtype == ref.BF16:
+        return (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(-1), w
+    if qtype in BLOCK:
+        return random_rows(qtype, rows, cols, seed), w
     return ref.quantize_rows(qtype, w), w
 
 
@@ -38,18 +50,19 @@ MATRICES = ("wq", "wk", "wv", "wo", "w1", "w2", "w3")
 
 
 def tiny_llama(seed=1, n_layers=2, dim=512, hidden=1024, n_heads=8, n_kv_heads=2, head_dim=64,
-               vocab=1000, layer_type=ref.Q4_K, out_type=ref.Q6_K, type_of=None):
+               vocab=1000, layer_type=ref.Q4_K, out_type=ref.Q6_K, type_of=None,
+               emb_type=ref.Q4_K):
     """A small llama-shaped model with the reference's tensor roles
     (model.go:2027 loadLayer) and RMSNorm weights of 1.0.  type_of(layer,
     name), if given, picks each matrix's type (mixed files such as Q4_K_M)
     and the model then carries "types" [n_layers][7] in MATRICES order."""
     cfg = dict(n_layers=n_layers, dim=dim, hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv_heads,
                head_dim=head_dim, vocab=vocab, rms_eps=1e-5, rope_theta=500000.0,
-               emb_type=ref.Q4_K, out_type=out_type, layer_type=layer_type)
+               emb_type=emb_type, out_type=out_type, layer_type=layer_type)
     qd, kvd = n_heads * head_dim, n_kv_heads * head_dim
     s = seed * 1000
     m = {"config": cfg}
-    m["tok_embd"], _ = quant_matrix(ref.Q4_K, vocab, dim, s + 1)
+    m["tok_embd"], _ = quant_matrix(emb_type, vocab, dim, s + 1)
     m["output"], _ = quant_matrix(out_type, vocab, dim, s + 2)
     m["out_norm"] = np.ones(dim, np.float32)
     shapes = {"wq": (qd, dim), "wk": (kvd, dim), "wv": (kvd, dim), "wo": (dim, qd),

@@ -81,14 +81,16 @@ def test_download_roundtrip_and_argmax(hip, qtype):
     assert w.argmax_matvec(x) == ref.argmax_finite(ref.matvec(qtype, data, x, rows, cols))
 
 
-def test_fused_matvec_of_other_types_rejected(hip):
-    """matvecSameType2/3Into (model.go:3213-3254) run the float kernels for
-    these formats, so the int8 fused call refuses them instead of returning
-    different numbers."""
+def test_fused_pair_of_other_types_runs_float_kernel(hip):
+    """matvecSameType2Into (model.go:3213-3230) runs DotQ5KF32 for a Q5_K
+    pair: both outputs are the float kernel's, not the int8 row dot's."""
     data = random_rows(ref.Q5_K, 64, 256, 1)
     a = hip.Weight.from_host(data, ref.Q5_K, 64, 256)
-    with pytest.raises(hip.GllmError):
-        hip.matvec2_into(a, a, normal(2, 256))
+    x = normal(2, 256)
+    oa, ob = hip.matvec2_into(a, a, x)
+    want = ref.matvec_float(ref.Q5_K, data, x, 64, 256)
+    assert_bits(oa, want, "pair a")
+    assert_bits(ob, want, "pair b")
 
 
 @pytest.mark.parametrize("qtype", [ref.Q6_K, ref.Q8_0] + FORMATS,

@@ -149,11 +149,16 @@ def test_fused_equals_separate(hip, qtype):
         assert np.array_equal(bits(a), bits(b))
 
 
-def test_fused_q8_0_rejected(hip):
+def test_fused_q8_0_pair_runs_float_kernel(hip):
+    """A Q8_0 pair is DotQ8_0F32 per row (matvecSameType2Into,
+    model.go:3213-3230)."""
     d, _ = quant_matrix(ref.Q8_0, 64, 256, 1)
     a = hip.Weight.from_host(d, ref.Q8_0, 64, 256)
-    with pytest.raises(hip.GllmError):
-        hip.matvec2_into(a, a, normal(2, 256))
+    x = normal(2, 256)
+    oa, ob = hip.matvec2_into(a, a, x)
+    want = ref.matvec_float(ref.Q8_0, d, x, 64, 256)
+    assert np.array_equal(bits(oa), bits(want))
+    assert np.array_equal(bits(ob), bits(want))
 
 
 @pytest.mark.parametrize("qtype", [ref.Q6_K, ref.Q4_K])
@@ -296,8 +301,11 @@ def test_mixed_type_groups_share_activations(hip):
             for (t, r), d, o in zip(mix, datas, outs):
                 want = ref.matvec_batch(t, d, xs, r, cols)
                 assert np.array_equal(bits(o.cpu().numpy()), bits(want)), (t, p)
-    # batch 1 with a format whose fused group the reference runs as floats
-    with pytest.raises(hip.GllmError):
-        hip.matvec_multi_dev(ws, torch.from_numpy(normal(1, (1, cols))).cuda(),
-                             [torch.empty((1, r), dtype=torch.float32, device="cuda")
-                              for _, r in others])
+    # batch 1, three formats and no same-type pair: three MatvecInto
+    # (tryMatvecAttentionInto's last case, model.go:3181-3183)
+    x1 = normal(1, (1, cols))
+    outs = [torch.empty((1, r), dtype=torch.float32, device="cuda") for _, r in others]
+    hip.matvec_multi_dev(ws, torch.from_numpy(x1).cuda(), outs)
+    torch.cuda.synchronize()
+    for (t, r), d, o in zip(others, datas, outs):
+        assert np.array_equal(bits(o.cpu().numpy()[0]), bits(ref.matvec(t, d, x1[0], r, cols)))

@@ -180,14 +180,20 @@ def test_mixed_q4k_q6k_layers_match_oracle(hip):
         tok = want
 
 
-def test_layers_of_float_kernel_formats_rejected(hip):
-    """The reference runs fused Q/K/V and gate/up groups of formats other
-    than Q4_K / Q6_K through float kernels (matvecSameType2/3Into), so the
-    resident decoder refuses such layers instead of returning other numbers."""
+def test_q4k_pair_with_a_q8_0_projection_matches_oracle(hip):
+    """Q/K/V = Q4_K, Q8_0, Q4_K: the Q4_K pair (0, 2) is the fused group and
+    runs the int8 row dots, the Q8_0 K its own MatvecInto
+    (tryMatvecAttentionInto, model.go:3157-3184)."""
     from gopherllm_amd.decoder import LlamaDecoder
     m = tiny_llama(seed=14, n_layers=1, dim=256, hidden=512, n_heads=4, n_kv_heads=1,
                    head_dim=64, vocab=300,
                    type_of=lambda l, k: ref.Q8_0 if k == "wk" else ref.Q4_K)
     gpu = LlamaDecoder.from_host_model(m, 32)
-    with pytest.raises(hip.GllmError):
-        gpu.decode(1, 0)
+    cpu = ref.Llama(m, 32)
+    tok = 1
+    for pos in range(6):
+        want, hid = cpu.decode(tok, pos)
+        got = gpu.decode(tok, pos)
+        assert np.array_equal(bits(gpu.hidden()), bits(hid)), pos
+        assert got == want, pos
+        tok = want

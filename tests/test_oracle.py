@@ -583,3 +583,21 @@ def test_tiny_llama_fast_port_identical_to_lane_restatement(oracle_lib):
         a, ha = s2.decode(ts, len(prompt))
         b, hb = f2.decode(tf, len(prompt))
         assert a == b and np.array_equal(ha.view(np.uint32), hb.view(np.uint32))
+
+
+def test_scalar_row_dequant(oracle_lib):
+    """rawScalarRowInto (raw_scalar.go:130-161): F16 rows widen exactly
+    (numpy's float16 -> float32, subnormals, infinities and NaN payloads
+    kept), BF16 rows are the 16 bits as the top of a float32, F32 rows are
+    copied."""
+    rng = np.random.default_rng(77)
+    bits16 = rng.integers(0, 1 << 16, 512, dtype=np.uint16)
+    bits16[:4] = [0x0001, 0x7c00, 0xfc00, 0x8000]
+    raw = bits16.view(np.uint8)
+    f16 = ref.dequant_row(ref.F16, raw, 512)
+    assert np.array_equal(f16.view(np.uint32), bits16.view(np.float16).astype(np.float32).view(np.uint32))
+    bf = ref.dequant_row(ref.BF16, raw, 512)
+    assert np.array_equal(bf.view(np.uint32), bits16.astype(np.uint32) << 16)
+    f32 = rng.standard_normal(300).astype(np.float32)
+    assert np.array_equal(ref.dequant_row(ref.F32, f32.view(np.uint8), 300), f32)
+    assert ref.row_bytes(ref.BF16, 300) == 600 and ref.row_bytes(ref.F16, 300) == 600
