@@ -536,6 +536,153 @@ def launch_floor(args):
               flush=True)
 
 
+def kernel_bench(args):
+    """llm-kernel-bench.v1 (kernel_bench.go:26-203) for layer 0 of the
+    synthetic Llama-3-8B-shape model of configs[4] (Q4_K layers and
+    embeddings, Q6_K output): the embedding row lookup, every layer matvec
+    alone, the fused paths a generation step runs (attn_qkv_path =
+    tryMatvecAttentionInto, ffn_gate_up_path = tryMatvec2Into,
+    ffn_swiglu_down_path = gate/up + siluMulF32 + down, output_argmax_path
+    and its repeat-penalty form) on deterministicBenchVector inputs
+    ((i % 251) - 125) / 125.  Each row's `runs` calls are one HIP graph of
+    back-to-back launches, replayed and timed with HIP events on the replay
+    stream, so avg_ms is the device time per call without host launch cost.
+    With the CPU leg, cpu_avg_ms is the oracle's AVX2 port of
+    kernels_amd64.s (all host cores) on the same weights for the matvec
+    rows."""
+    import numpy as np
+    import torch
+
+    import gopherllm_amd as g
+    from gopherllm_amd import synth
+
+    g.load()
+    cfg = dict(synth.LLAMA3_8B)
+    dim, hid, vocab = cfg["dim"], cfg["hidden"], cfg["vocab"]
+    qd = cfg["n_heads"] * cfg["head_dim"]
+    shapes = synth.layer_shapes(cfg)
+    sc = synth._Scratch(torch, vocab * dim, vocab * g.row_bytes(cfg["out_type"], dim))
+    W = {k: sc.weight(cfg["layer_type"], r, c, synth.tensor_seed(1, 0, k))
+         for k, (r, c) in shapes.items()}
+    emb = sc.weight(cfg["emb_type"], vocab, dim, synth.tensor_seed(1, -1, "tok_embd"))
+    out_w = sc.weight(cfg["out_type"], vocab, dim, synth.tensor_seed(1, -1, "output"))
+    torch.cuda.synchronize()
+    del sc
+
+    def bench_vec(n):
+        i = np.arange(n)
+        return torch.from_numpy((((i % 251) - 125) / 125).astype(np.float32)).cuda().view(1, -1)
+
+    x_dim, x_attn, x_hid = bench_vec(dim), bench_vec(qd), bench_vec(hid)
+    bufs = {n: torch.empty((1, n), dtype=torch.float32, device="cuda") for n in (dim, hid, vocab)}
+    o2 = torch.empty((1, hid), dtype=torch.float32, device="cuda")
+    o3 = torch.empty((1, shapes["wv"][0]), dtype=torch.float32, device="cuda")
+    ok = torch.empty((1, shapes["wk"][0]), dtype=torch.float32, device="cuda")
+    ids = torch.zeros(1, dtype=torch.int32, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    recent = torch.tensor([0, 1, 1, vocab - 1], dtype=torch.int32, device="cuda")
+    names = {g.TYPE_Q4_K: "Q4_K", g.TYPE_Q6_K: "Q6_K", g.TYPE_Q8_0: "Q8_0"}
+    T = {k: names[w.type] for k, w in W.items()}
+    ot = names[out_w.type]
+
+    rows = [
+        ("token_embd.row", names[emb.type], vocab, dim, lambda: emb.rows_dev(ids, bufs[dim]),
+         (dim // 256) * 144 + 4 * dim, None),
+        ("attn_q", T["wq"], qd, dim, lambda: W["wq"].matvec_dev(x_dim, bufs[dim]), None, ["wq"]),
+        ("attn_k", T["wk"], shapes["wk"][0], dim, lambda: W["wk"].matvec_dev(x_dim, ok), None, ["wk"]),
+        ("attn_v", T["wv"], shapes["wv"][0], dim, lambda: W["wv"].matvec_dev(x_dim, o3), None, ["wv"]),
+        ("attn_qkv_path", "/".join(T[k] for k in ("wq", "wk", "wv")),
+         qd + 2 * shapes["wk"][0], dim,
+         lambda: g.matvec_multi_dev([W["wq"], W["wk"], W["wv"]], x_dim, [bufs[dim], ok, o3]),
+         None, ["wq", "wk", "wv"]),
+        ("attn_output", T["wo"], dim, qd, lambda: W["wo"].matvec_dev(x_attn, bufs[dim]), None, ["wo"]),
+        ("ffn_gate", T["w1"], hid, dim, lambda: W["w1"].matvec_dev(x_dim, bufs[hid]), None, ["w1"]),
+        ("ffn_up", T["w3"], hid, dim, lambda: W["w3"].matvec_dev(x_dim, o2), None, ["w3"]),
+        ("ffn_gate_up_path", f"{T['w1']}/{T['w3']}", 2 * hid, dim,
+         lambda: g.matvec_multi_dev([W["w1"], W["w3"]], x_dim, [bufs[hid], o2]), None, ["w1", "w3"]),
+        ("ffn_down", T["w2"], dim, hid, lambda: W["w2"].matvec_dev(x_hid, bufs[dim]), None, ["w2"]),
+        ("ffn_swiglu_down_path", f"{T['w1']}/{T['w3']}/SiLU/{T['w2']}", 2 * hid + dim, dim,
+         lambda: g.swiglu_down_dev(W["w1"], W["w3"], W["w2"], x_dim, bufs[dim]), None,
+         ["w1", "w3", "w2"]),
+        ("output", ot, vocab, dim, lambda: out_w.matvec_dev(x_dim, bufs[vocab]), None, ["output"]),
+        ("output_argmax_path", f"{ot}/argmax", vocab, dim, lambda: out_w.argmax_dev(x_dim, tok),
+         None, ["output"]),
+        ("output_argmax_penalized_path", f"{ot}/argmax/repeat-penalty", vocab, dim,
+         lambda: out_w.argmax_dev(x_dim, tok, recent=recent, penalty=1.1), None, ["output"]),
+    ]
+    wmap = dict(W, output=out_w)
+
+    def wbytes(keys):
+        tot = 0
+        for k in keys:
+            w = wmap[k]
+            tot += w.rows * g.row_bytes(w.type, w.cols) + 4 * w.rows
+        return tot + 4 * wmap[keys[0]].cols
+
+    host = {}
+    cores = len(os.sched_getaffinity(0))
+    if not args.no_cpu_baseline:
+        from oracle import oracle as ref
+        for k, w in wmap.items():
+            buf = torch.empty(w.rows * g.row_bytes(w.type, w.cols), dtype=torch.uint8, device="cuda")
+            w.download_dev(buf)
+            torch.cuda.synchronize()
+            host[k] = buf.cpu().numpy()
+    runs = args.kernel_bench_runs
+    kernels = []
+    for name, dtype, r, c, fn, nbytes, keys in rows:
+        def body(fn=fn):
+            for _ in range(runs):
+                fn()
+        graph = timed_graph(torch, body)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 5
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        avg_ms = e0.elapsed_time(e1) / (reps * runs)
+        nbytes = nbytes if nbytes is not None else wbytes(keys)
+        row = {"name": name, "dtype": dtype, "rows": r, "cols": c, "runs": runs,
+               "avg_ms": round(avg_ms, 6), "total_ms": round(avg_ms * runs, 4),
+               "alg_bytes": int(nbytes), "gb_s": round(nbytes / (avg_ms * 1e-3) / 1e9, 1),
+               "frac_hbm": round(nbytes / (avg_ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}
+        if host and keys and name.startswith(("attn_", "ffn_gate", "ffn_up", "ffn_down", "output")) \
+                and "argmax" not in name and "swiglu" not in name:
+            xin = bench_vec(wmap[keys[0]].cols).cpu().numpy()[0]
+            n, t0 = 0, time.perf_counter()
+            while n < 3 or (time.perf_counter() - t0 < 1.0 and n < 200):
+                for k in keys:
+                    w = wmap[k]
+                    ref.matvec_batch_fast(w.type, host[k], xin, w.rows, w.cols, threads=cores)
+                n += 1
+            row["cpu_avg_ms"] = round((time.perf_counter() - t0) / n * 1e3, 4)
+        kernels.append(row)
+        print(json.dumps(row), file=sys.stderr, flush=True)
+    doc = {"type": "gopherllm.kernel_benchmark", "format": "llm-kernel-bench.v1",
+           "runtime": "gopherllm_amd (HIP, MI355X)",
+           "command": " ".join(["python", "bench.py"] + sys.argv[1:]),
+           "model": {"path": None, "name": "synthetic Llama-3-8B shape (configs[4])",
+                     "arch": "llama", "dim": dim, "hidden_dim": hid, "layers": cfg["n_layers"]},
+           "layer": 0, "runs": runs, "kernels": kernels,
+           "timing": "device time per call: each row's runs calls captured as one HIP graph, "
+                     "5 replays timed with HIP events on the replay stream",
+           "alg_bytes": "weight bytes + 4*(rows + cols) per matvec; token_embd.row: one Q4_K "
+                        "row + the f32 output"}
+    if host:
+        doc["cpu"] = dict(cpu_identity(), cores=cores, kind="port",
+                          note="cpu_avg_ms: oracle AVX2 port of kernels_amd64.s (int8 row "
+                               "dots, bit-identical results) per call, all listed cores")
+    text = json.dumps(doc, indent=2)
+    print(text, flush=True)
+    if args.kernel_bench_json:
+        with open(args.kernel_bench_json, "w") as f:
+            f.write(text + "\n")
+
+
 def profile_run():
     """Eager launches for rocprofv3 counter passes (no graphs, no timing):
     20 row-kernel launches over the rotating copies, then 5 plain device
@@ -576,6 +723,10 @@ def main():
                     help="eager launches for rocprofv3 counter collection")
     ap.add_argument("--launch-floor", action="store_true",
                     help="per-node cost of short launches replayed from one HIP graph")
+    ap.add_argument("--kernel-bench", action="store_true",
+                    help="llm-kernel-bench.v1 per-path report for layer 0 of the 8B-shape model")
+    ap.add_argument("--kernel-bench-runs", type=int, default=100)
+    ap.add_argument("--kernel-bench-json", default="", help="also write the report to this file")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
@@ -590,6 +741,9 @@ def main():
         return
     if args.launch_floor:
         launch_floor(args)
+        return
+    if args.kernel_bench:
+        kernel_bench(args)
         return
     if args.suite:
         suite(args)

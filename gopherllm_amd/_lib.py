@@ -56,6 +56,7 @@ SIGNATURES = {
     "gllm_hip_matvec_dev": (i32, [vp, vp, i32, vp, i32, vp]),
     "gllm_hip_matvec_dev_noalloc": (i32, [vp, vp, i32, vp, i32, vp]),
     "gllm_hip_matvec_multi_dev": (i32, [i32, vp, vp, i32, vp, vp, vp]),
+    "gllm_hip_swiglu_down_dev": (i32, [vp, vp, vp, vp, vp, vp]),
     "gllm_hip_argmax_dev": (i32, [vp, vp, vp, vp]),
     "gllm_hip_act_bytes": (sz, [i32, i32]),
     "gllm_hip_q8k_prepare_dev": (i32, [vp, i32, i32, vp, vp]),

@@ -212,6 +212,16 @@ def matvec_multi_dev(weights, xs, outs, stream=None):
          strides, _stream(stream))
 
 
+def swiglu_down_dev(gate: Weight, up: Weight, down: Weight, x, out, stream=None):
+    """down . siluMulF32(gate . x, up . x) for one token (ForwardBodyInto's
+    FFN, model.go:2780-2800), gate/up routed as tryMatvec2Into routes them."""
+    if gate.cols != up.cols or gate.rows != up.rows or down.cols != gate.rows:
+        raise ValueError("swiglu_down_dev: gate / up / down shapes do not chain")
+    call("gllm_hip_swiglu_down_dev", gate.handle, up.handle, down.handle,
+         _dev(x, "f32", gate.cols, "x"), _dev(out, "f32", down.rows, "out"), _stream(stream))
+    return out
+
+
 def _matvec_into(qtype, data, x, rows, cols, out):
     w = Weight.from_host(data, qtype, rows, cols)
     try:

@@ -1632,6 +1632,25 @@ int gllm_hip_matvec_multi_dev(int n, gllm_hip_weight* const* ws, const float* d_
     return matvec_multi(n, ws, d_xs, p, d_outs, out_strides, (hipStream_t)stream, 0);
 }
 
+int gllm_hip_swiglu_down_dev(gllm_hip_weight* gate, gllm_hip_weight* up, gllm_hip_weight* down,
+                             const float* d_x, float* d_out, void* stream) {
+    if (!d_x || !d_out) return fail(GLLM_EINVAL, "gllm_hip_swiglu_down_dev: null pointer");
+    gllm_hip_weight* ws[2] = {gate, up};
+    GLLM_TRY(validate_matvec(2, ws, 1, nullptr));
+    GLLM_TRY(validate_weight(down));
+    if (gate->rows != up->rows || down->cols != gate->rows)
+        return fail(GLLM_EINVAL, "gllm_hip_swiglu_down_dev: gate/up rows %d/%d, down cols %d",
+                    gate->rows, up->rows, down->cols);
+    hipStream_t s = (hipStream_t)stream;
+    const int hidden = gate->rows;
+    float* buf = (float*)thread_scratch(9, (size_t)hidden * 3 * 4, s);
+    void* act = thread_scratch(0, act_bytes(std::max(gate->cols, hidden), 1), s);
+    if (!buf || !act) return scratch_error();
+    float* outs[2] = {buf, buf + hidden};
+    GLLM_TRY(gemv_group(2, ws, d_x, outs, nullptr, act, s));
+    return gemv_silu_f32(down, buf, buf + hidden, 1, d_out, act, buf + 2 * (size_t)hidden, s);
+}
+
 size_t gllm_hip_act_bytes(int cols, int p) {
     if (cols <= 0 || cols % 256 || p <= 0) return 0;
     return act_bytes(cols, p);

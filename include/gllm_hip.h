@@ -166,6 +166,14 @@ int gllm_hip_matvec_dev(gllm_hip_weight* w, const float* d_xs, int p, float* d_o
  * is a fused group, routed as gllm_hip_matvec2 / gllm_hip_matvec3 route it. */
 int gllm_hip_matvec_multi_dev(int n, gllm_hip_weight* const* ws, const float* d_xs, int p,
                               float* const* d_outs, const int* out_strides, void* stream);
+/* A generation step's SwiGLU FFN (ForwardBodyInto model.go:2780-2800, the
+ * path matvecMetalSwiGLUInto metal_darwin.go:161 fuses on Apple GPUs):
+ * gate, up = the fused group of tryMatvec2Into (routed as gllm_hip_matvec2),
+ * hidden = siluMulF32(gate, up) (kernels_amd64.go:711), d_out =
+ * down.MatvecInto(hidden).  Batch 1, device pointers, enqueued on stream;
+ * gate / up / hidden live in library scratch of the calling thread. */
+int gllm_hip_swiglu_down_dev(gllm_hip_weight* gate, gllm_hip_weight* up, gllm_hip_weight* down,
+                             const float* d_x, float* d_out, void* stream);
 int gllm_hip_argmax_dev(gllm_hip_weight* w, const float* d_x, uint32_t* d_token, void* stream);
 /* d_recent: n_recent device token ids. */
 int gllm_hip_argmax_penalized_dev(gllm_hip_weight* w, const float* d_x, const uint32_t* d_recent,

@@ -195,3 +195,21 @@ def test_output_without_row_kernel_rejected(hip):
     gpu = LlamaDecoder.from_host_model(m, 32)
     with pytest.raises(hip.GllmError):
         gpu.decode(1, 0)
+
+
+@pytest.mark.parametrize("qtype", [ref.Q4_K, ref.Q8_0, ref.Q5_K], ids=["q4k", "q8_0", "q5k"])
+@pytest.mark.parametrize("dim,hidden", [(256, 512), (4096, 14336)])
+def test_swiglu_down_path(hip, qtype, dim, hidden):
+    """gllm_hip_swiglu_down_dev == down.MatvecInto(siluMulF32(gate, up)) with
+    gate / up from the fused pair (int8 for Q4_K, the float kernels for the
+    other formats) and down's own int8 row dot."""
+    import torch
+    (dg, wg), (du, wu) = (weight(hip, qtype, hidden, dim, 100 + i) for i in range(2))
+    dd, wd = weight(hip, qtype, dim, hidden, 102)
+    x = normal(103, dim)
+    out = torch.empty(dim, dtype=torch.float32, device="cuda")
+    hip.swiglu_down_dev(wg, wu, wd, torch.from_numpy(x).cuda(), out)
+    torch.cuda.synchronize()
+    mv = ref.matvec if qtype == ref.Q4_K else ref.matvec_float
+    h = ref.silu_mul(mv(qtype, dg, x, hidden, dim), mv(qtype, du, x, hidden, dim))
+    assert_bits(out.cpu().numpy(), ref.matvec(qtype, dd, h, dim, hidden), "swiglu down")
