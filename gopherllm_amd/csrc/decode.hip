@@ -29,6 +29,9 @@ int gemv_f32(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float*
 int gemv_group(int n, gllm_hip_weight* const* ws, const float* d_x, float* const* outs,
                const int* strides, void* act_buf, hipStream_t s);
 int group_routing(int n, gllm_hip_weight* const* ws, int* fl);
+bool norm_fusable(int n, gllm_hip_weight* const* ws);
+int gemv_norm_f32(int n, gllm_hip_weight* const* ws, const float* x, const float* res,
+                  const float* nw, float eps, float* xout, float* const* outs, hipStream_t s);
 bool row_kernel_type(int t);
 bool rows_type(int t);
 int launch_weight_rows(const gllm_hip_weight* w, const uint32_t* d_ids, int n, float* d_out,
@@ -63,6 +66,7 @@ struct gllm_hip_model {
     hipStream_t stream = nullptr;
     int max_p = 0;  // capacity of the activation buffers below (tokens)
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
+    float* x2 = nullptr;  // second residual-stream buffer (norm-fused launches alternate x / x2)
     float *proj = nullptr, *gate = nullptr, *up = nullptr, *hidden = nullptr, *logits = nullptr;
     uint32_t* d_tokens = nullptr;
     uint32_t* h_tokens = nullptr;  // pinned
@@ -230,11 +234,11 @@ static int ensure_buffers(gllm_hip_model* m, int p) {
     if (p <= m->max_p) return GLLM_OK;
     const auto& c = m->cfg;
     float** bufs[] = {&m->x, &m->xn, &m->q, &m->k, &m->v, &m->attn, &m->proj, &m->gate, &m->up,
-                      &m->hidden};
+                      &m->hidden, &m->x2};
     const size_t qd = (size_t)c.n_heads * c.head_dim, kvd = (size_t)c.n_kv_heads * c.head_dim;
     const size_t sizes[] = {(size_t)c.dim, (size_t)c.dim, qd, kvd, kvd, qd, (size_t)c.dim,
-                            (size_t)c.hidden, (size_t)c.hidden, (size_t)c.hidden};
-    for (int i = 0; i < 10; i++) {
+                            (size_t)c.hidden, (size_t)c.hidden, (size_t)c.hidden, (size_t)c.dim};
+    for (int i = 0; i < 11; i++) {
         if (*bufs[i]) (void)hipFree(*bufs[i]);
         *bufs[i] = nullptr;
         GLLM_HIP(hipMalloc(bufs[i], sizes[i] * p * 4));
@@ -283,16 +287,34 @@ static int forward(gllm_hip_model* m, int pos0, int p, bool decode, const int* d
     const float scale = m->attn_scale != 0.0f ? m->attn_scale : (float)(1.0 / sqrt((double)hd));
     const size_t norm_lds = (size_t)c.dim * 4;
     GLLM_TRY(launch_weight_rows(m->tok_embd, m->d_tokens, p, m->x, s));
+    // the residual stream: a norm-fused launch reads X[xi] and writes the
+    // updated stream to X[xi ^ 1] (its workgroups all read X[xi] first)
+    float* X[2] = {m->x, m->x2};
+    int xi = 0;
+    const bool fuse = decode && p == 1;
+    // addInPlace(x, res) + rmsNormInto(x, norm) + the fused projections:
+    // inside the projections' launch when their row kernels take the norm
+    // prologue, else the add_rmsnorm kernel first
+    auto norm_project = [&](int n, gllm_hip_weight* const* ws, const float* res,
+                            const float* norm, float* const* outs) -> int {
+        if (fuse && norm_fusable(n, ws)) {
+            GLLM_TRY(gemv_norm_f32(n, ws, X[xi], res, norm, c.rms_eps, res ? X[xi ^ 1] : nullptr,
+                                   outs, s));
+            if (res) xi ^= 1;
+            return GLLM_OK;
+        }
+        hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(p), dim3(256), norm_lds, s, X[xi], res, norm,
+                           c.dim, c.rms_eps, m->xn);
+        GLLM_HIP(hipGetLastError());
+        return project(m, decode, n, ws, m->xn, p, outs);
+    };
     const float* pending = nullptr;  // FFN output still to be added to the residual
     for (int l = 0; l < c.n_layers; l++) {
         gllm_hip_weight** W = &m->w[(size_t)l * 7];
-        hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(p), dim3(256), norm_lds, s, m->x, pending,
-                           m->d_norms + (size_t)(2 * l) * c.dim, c.dim, c.rms_eps, m->xn);
-        GLLM_HIP(hipGetLastError());
         {
             gllm_hip_weight* ws[3] = {W[GLLM_T_WQ], W[GLLM_T_WK], W[GLLM_T_WV]};
             float* outs[3] = {m->q, m->k, m->v};
-            GLLM_TRY(project(m, decode, 3, ws, m->xn, p, outs));
+            GLLM_TRY(norm_project(3, ws, pending, m->d_norms + (size_t)(2 * l) * c.dim, outs));
         }
         if (d_pos) {
             // captured decode step: RoPE and the K/V store run inside the
@@ -316,18 +338,15 @@ static int forward(gllm_hip_model* m, int pos0, int p, bool decode, const int* d
             float* outs[1] = {m->proj};
             GLLM_TRY(matvec(m, 1, ws, m->attn, p, outs));
         }
-        hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(p), dim3(256), norm_lds, s, m->x, m->proj,
-                           m->d_norms + (size_t)(2 * l + 1) * c.dim, c.dim, c.rms_eps, m->xn);
-        GLLM_HIP(hipGetLastError());
         {
             gllm_hip_weight* ws[2] = {W[GLLM_T_W1], W[GLLM_T_W3]};
             float* outs[2] = {m->gate, m->up};
-            GLLM_TRY(project(m, decode, 2, ws, m->xn, p, outs));
+            GLLM_TRY(norm_project(2, ws, m->proj, m->d_norms + (size_t)(2 * l + 1) * c.dim, outs));
         }
         GLLM_TRY(gemv_silu_f32(W[GLLM_T_W2], m->gate, m->up, p, m->proj, m->act, m->hidden, s));
         pending = m->proj;
     }
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(p), dim3(256), norm_lds, s, m->x, pending,
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(p), dim3(256), norm_lds, s, X[xi], pending,
                        m->d_norms + (size_t)(2 * c.n_layers) * c.dim, c.dim, c.rms_eps, m->xn);
     GLLM_HIP(hipGetLastError());
     (void)kvd;
@@ -470,7 +489,7 @@ void gllm_hip_model_release(gllm_hip_model* m) {
     if (!m) return;
     if (m->stream) (void)hipStreamSynchronize(m->stream);
     float* bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->proj, m->gate, m->up, m->hidden,
-                     m->logits, m->d_norms, m->d_sin, m->d_cos};
+                     m->logits, m->d_norms, m->d_sin, m->d_cos, m->x2};
     for (float* b : bufs)
         if (b) (void)hipFree(b);
     if (m->d_tokens) (void)hipFree(m->d_tokens);

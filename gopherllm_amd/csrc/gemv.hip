@@ -53,6 +53,13 @@ struct GemvJob {
     int rows_per_wg;  // rows per workgroup: blockDim.x / (8 * G)
     int tok0;         // first activation row of this launch
     int ntok;         // activation rows in this launch (<= NT)
+    // RMSNorm prologue (batch-1 Q4_K with xf): x = rmsNormInto(fma(res, 1,
+    // xf), nw) computed in the kernel; res may be null; workgroup 0 writes
+    // fma(res, 1, xf) to xout when xout is set
+    const float* nw;
+    const float* res;
+    float* xout;
+    float eps;
 };
 
 __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
@@ -360,6 +367,76 @@ __device__ __forceinline__ void fused_act_store(const XRegs<kFuseQB>& xr, int B,
     lds_barrier();
 }
 
+// rmsNormInto (model.go:2986-3011) of x' = fma(res, 1, x) (addInPlace,
+// model.go:3857) on an activation held in the xq_load layout (lane (m, kk)
+// of the wave owning block b has x[256b + 32m + kk + 8e] in v[e]): x' is
+// staged in LDS (xs: cols floats, then 48 floats of scratch), threads 0..31
+// run the dotF32AVX2 accumulator chains (kernels_amd64.s:28-93: chain
+// 8r + k over elements 32c + 8r + k, c in order), 0..7 join them as
+// (y0 + y1) + (y2 + y3), thread 0 runs the 8 -> 1 tree and
+// float32(1 / sqrt(float64(ss / n + eps))); then v = (x' * w) * scale.
+// Barriers are LDS-only, so the caller's weight prefetch stays in flight.
+// xout (workgroup 0 only) receives x'.
+template <int QB, bool RES>
+__device__ __forceinline__ void norm_regs(XRegs<QB>& xr, const XRegs<QB>& wr,
+                                          const XRegs<QB>& rr, int B, float eps, float* xout,
+                                          float* xs) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int m = lane >> 3, kk = lane & 7;
+    const int n = B * 256;
+#pragma unroll
+    for (int i = 0; i < QB; i++) {
+        const int b = wave + nw * i;
+        if (b >= B) break;  // wave-uniform
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float v = xr.v[i][e];
+            if constexpr (RES) v = fmaf(rr.v[i][e], 1.0f, v);
+            xr.v[i][e] = v;
+            const int idx = b * 256 + 32 * m + kk + 8 * e;
+            xs[idx] = v;
+            if (xout) xout[idx] = v;
+        }
+    }
+    float* part = xs + n;
+    wait_lgkm0();
+    lds_barrier();
+    if (tid < 32) {
+        float y = 0.0f;
+        for (int c = 0; c < n; c += 16 * 32) {
+            float xb[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) xb[u] = xs[c + 32 * u + tid];
+#pragma unroll
+            for (int u = 0; u < 16; u++) y = fmaf(xb[u], xb[u], y);
+        }
+        part[tid] = y;
+    }
+    wait_lgkm0();
+    lds_barrier();
+    if (tid < 8) part[32 + tid] = (part[tid] + part[8 + tid]) + (part[16 + tid] + part[24 + tid]);
+    wait_lgkm0();
+    lds_barrier();
+    if (tid == 0) {
+        const float a0 = part[32] + part[36], a1 = part[33] + part[37];
+        const float a2 = part[34] + part[38], a3 = part[35] + part[39];
+        const float ss = (a0 + a1) + (a2 + a3);
+        part[40] = (float)(1.0 / sqrt((double)(ss / (float)n + eps)));
+    }
+    wait_lgkm0();
+    lds_barrier();
+    const float scale = part[40];
+#pragma unroll
+    for (int i = 0; i < QB; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) xr.v[i][e] = (xr.v[i][e] * wr.v[i][e]) * scale;
+}
+constexpr size_t kNormLds = 48 * 4;  // norm scratch after the cols floats
+// LDS offset of the norm's x' (after the quantised activation, 16-aligned)
+__host__ __device__ constexpr size_t q4k_norm_off(int cols) {
+    return ((size_t)cols + (size_t)(cols / 32) * 4 + (size_t)(cols / 256) * 4 + 15) & ~(size_t)15;
+}
+
 #include "gemv_formats.h"
 
 // One Q4_K block of one AVX2 lane for NT tokens: exact int32 lane sum
@@ -445,11 +522,14 @@ __device__ __forceinline__ uint4 hdr_of(uint4 v, int j) {  // j: compile-time af
 // the compiler's in-order vmcnt waits hand the x registers to the quantiser
 // while the weights are still streaming.  Otherwise the pre-quantised
 // activations are copied to LDS with direct global->LDS loads issued before
-// the prefetch.
-template <int NT, int G, int NL, int D, bool FUSE>
+// the prefetch.  FUSE = 2 (3 with a residual) puts the RMSNorm in front of
+// the quantiser (norm_regs): the norm weights (and residual) are loaded with
+// x, the LDS for x' follows the quantised activation.
+template <int NT, int G, int NL, int D, int FUSE>
 __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(GemvJob j) {
     static_assert(NL % D == 0, "prefetch depth must divide the blocks per lane");
     static_assert(!FUSE || NT == 1, "fused quantisation is batch 1 only");
+    constexpr bool NORM = FUSE >= 2;
     constexpr int B = NL * G;
     constexpr int NH = (NL + 7) / 8;  // header loads per lane
     constexpr int QB = FUSE ? (B + 3) / 4 : 1;
@@ -468,8 +548,11 @@ __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(
     float* xs32b = (float*)(smem + (size_t)NT * cols);
     float* xscb = xs32b + (size_t)NT * (cols / 32);
     XRegs<QB> xr;
+    XRegs<NORM ? QB : 1> wr, resr;
     if constexpr (FUSE) {
         xq_load<QB>(j.xf + (size_t)j.tok0 * cols, B, xr);
+        if constexpr (NORM) xq_load<QB>(j.nw, B, wr);
+        if constexpr (FUSE == 3) xq_load<QB>(j.res, B, resr);
     } else {
         stage_act_asm<NT>(j, smem);
     }
@@ -490,6 +573,9 @@ __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (FUSE) {
+        if constexpr (NORM)
+            norm_regs<QB, FUSE == 3>(xr, wr, resr, B, j.eps, blockIdx.x == 0 ? j.xout : nullptr,
+                                     (float*)(smem + q4k_norm_off(cols)));
         xq_store<QB, false>(xr, B, q8b, xs32b, nullptr, xscb);
         wait_lgkm0();
     } else {
@@ -1083,12 +1169,18 @@ constexpr size_t kMaxStage = 48 << 10;
 template <int NT, int G, int NL, int D>
 static void launch_q4k_nl(const GemvJob& j, dim3 grid, dim3 block, size_t stage, hipStream_t s) {
     if constexpr (NT == 1 && NL * G * 256 <= kFuseCols) {
+        if (j.xf && j.nw) {
+            const size_t lds = q4k_norm_off(j.cols) + (size_t)j.cols * 4 + kNormLds;
+            if (j.res) hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, 3>), grid, block, lds, s, j);
+            else hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, 2>), grid, block, lds, s, j);
+            return;
+        }
         if (j.xf) {
-            hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, true>), grid, block, stage, s, j);
+            hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, 1>), grid, block, stage, s, j);
             return;
         }
     }
-    hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, NL, D, false>), grid, block, stage, s, j);
+    hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, NL, D, 0>), grid, block, stage, s, j);
 }
 
 // Blocks per lane with a compiled row kernel (and its prefetch depth).
@@ -1294,13 +1386,29 @@ int validate_weight(const gllm_hip_weight* w) {
 
 // Row kernels for n weights against p activation rows already quantised
 // into `act` (activation rows tok0 .. tok0+p-1 of act).
+// RMSNorm prologue arguments (GemvJob::nw .. eps)
+struct NormIn {
+    const float* w;
+    const float* res;
+    float* xout;
+    float eps;
+};
+
 int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* const* outs,
-             const int* strides, hipStream_t s, const float* xf) {
+             const int* strides, hipStream_t s, const float* xf, const NormIn* ni = nullptr) {
     if (n < 1 || n > 3) return fail(GLLM_EINVAL, "gemv: %d weights (1..3 supported)", n);
     if (xf && p != 1) return fail(GLLM_EINVAL, "gemv: fused quantisation is batch 1 only");
     GemvJob j{};
     j.n = n;
     j.xf = xf;
+    if (ni) {
+        if (!xf || ws[0]->type != GLLM_TYPE_Q4_K)
+            return fail(GLLM_EINVAL, "gemv: the RMSNorm prologue needs a fused Q4_K launch");
+        j.nw = ni->w;
+        j.res = ni->res;
+        j.xout = ni->xout;
+        j.eps = ni->eps;
+    }
     const gllm_hip_weight* w0 = ws[0];
     j.blocks = w0->blocks;
     j.cols = w0->cols;
@@ -1381,6 +1489,26 @@ int gemv_f32(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float*
         i = e;
     }
     return GLLM_OK;
+}
+
+// True when a batch-1 group can take the RMSNorm prologue: Q4_K row kernels
+// of one cols that quantise x themselves.
+bool norm_fusable(int n, gllm_hip_weight* const* ws) {
+    for (int i = 0; i < n; i++)
+        if (ws[i]->type != GLLM_TYPE_Q4_K || ws[i]->cols != ws[0]->cols) return false;
+    return fused_quant(n, ws);
+}
+
+// W.rmsNormInto(fma(res, 1, x), nw) for a batch-1 Q4_K group in one launch:
+// ForwardBodyInto's addInPlace + rmsNormInto in front of the layer's fused
+// projections (model.go:2686-2790); res may be null; xout (optional)
+// receives fma(res, 1, x), the updated residual stream.
+int gemv_norm_f32(int n, gllm_hip_weight* const* ws, const float* x, const float* res,
+                  const float* nw, float eps, float* xout, float* const* outs, hipStream_t s) {
+    if (!norm_fusable(n, ws)) return fail(GLLM_EUNSUP, "gemv: no RMSNorm prologue for this group");
+    const NormIn ni{nw, res, xout, eps};
+    ActQ8 none{};
+    return run_gemv(n, ws, none, 1, outs, nullptr, s, x, &ni);
 }
 
 // W.siluMulF32(gate, up) for p rows (the FFN down projection): the SwiGLU is
