@@ -683,6 +683,64 @@ def kernel_bench(args):
             f.write(text + "\n")
 
 
+def bandwidth(args):
+    """HBM calibration with library-independent kernels (torch's device copy and
+    sum), graph replays timed with HIP events: what one launch of the
+    headline's size (33 MB) and a large one (512 MiB) reach on this part."""
+    import torch
+
+    for mb in (33.1, 512.0):
+        n = int(mb * 1e6 / 4) if mb < 100 else int(mb * (1 << 20) / 4)
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        out = torch.empty(1, dtype=torch.float32, device="cuda")
+        reps = 200 if mb < 100 else 20
+        for name, fn, bytes_moved in (("copy (read + write)", lambda: dst.copy_(src), 2 * n * 4),
+                                      ("sum (read)", lambda: torch.sum(src.view(1, -1), dim=1, out=out),
+                                       n * 4)):
+            def body(fn=fn):
+                for _ in range(reps):
+                    fn()
+            graph = timed_graph(torch, body)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(3):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / (3 * reps) * 1e3
+            print(json.dumps({"bandwidth": name, "bytes_per_launch": bytes_moved,
+                              "us_per_launch": round(us, 3),
+                              "tb_s": round(bytes_moved / (us * 1e-6) / 1e12, 3)}), flush=True)
+        del src, dst
+
+
+def summarize_decode_trace(path):
+    """Per-token kernel breakdown of the last 40 decode steps in a rocprofv3
+    kernel-trace CSV of a bench run (each step ends with argmax_final_kernel)."""
+    import collections
+    import csv
+
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    ends = [i for i, r in enumerate(rows) if "argmax_final" in r["Kernel_Name"]][-41:]
+    seg = rows[ends[0] + 1: ends[-1] + 1]
+    steps = len(ends) - 1
+    agg = collections.defaultdict(lambda: [0, 0.0])
+    for r in seg:
+        name = r["Kernel_Name"].replace("gllm::", "").split("(")[0][:60]
+        if "gemv" in name:
+            name += f" grid {r['Grid_Size_X']} wg {r['Workgroup_Size_X']}"
+        agg[name][0] += 1
+        agg[name][1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    wall = (int(seg[-1]["End_Timestamp"]) - int(seg[0]["Start_Timestamp"])) / 1e3 / steps
+    busy = sum(v[1] for v in agg.values()) / steps
+    print(f"steps {steps}: wall per step {wall:.1f} us, kernel-busy {busy:.1f} us")
+    print("| us per token | calls per token | us per call | kernel |")
+    print("|---|---|---|---|")
+    for name, (c, t) in sorted(agg.items(), key=lambda x: -x[1][1]):
+        print(f"| {t / steps:.1f} | {c / steps:.1f} | {t / c:.2f} | `{name}` |")
+
+
 def profile_run():
     """Eager launches for rocprofv3 counter passes (no graphs, no timing):
     20 row-kernel launches over the rotating copies, then 5 plain device
@@ -723,6 +781,10 @@ def main():
                     help="eager launches for rocprofv3 counter collection")
     ap.add_argument("--launch-floor", action="store_true",
                     help="per-node cost of short launches replayed from one HIP graph")
+    ap.add_argument("--summarize-decode-trace", default="",
+                    help="print the per-token kernel breakdown of a rocprofv3 kernel-trace CSV")
+    ap.add_argument("--bandwidth", action="store_true",
+                    help="HBM calibration: torch copy / sum of 33 MB and 512 MiB, graph replays")
     ap.add_argument("--kernel-bench", action="store_true",
                     help="llm-kernel-bench.v1 per-path report for layer 0 of the 8B-shape model")
     ap.add_argument("--kernel-bench-runs", type=int, default=100)
@@ -744,6 +806,12 @@ def main():
         return
     if args.kernel_bench:
         kernel_bench(args)
+        return
+    if args.bandwidth:
+        bandwidth(args)
+        return
+    if args.summarize_decode_trace:
+        summarize_decode_trace(args.summarize_decode_trace)
         return
     if args.suite:
         suite(args)

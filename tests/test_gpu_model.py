@@ -197,3 +197,35 @@ def test_q4k_pair_with_a_q8_0_projection_matches_oracle(hip):
         assert np.array_equal(bits(gpu.hidden()), bits(hid)), pos
         assert got == want, pos
         tok = want
+
+
+@pytest.mark.parametrize("n_heads,n_kv", [(8, 2), (4, 4), (8, 1)])
+def test_decode_attention_head_dim_128_matches_oracle(hip, n_heads, n_kv):
+    """head_dim 128 generation steps (captured decode step: RoPE and the
+    K / V store folded into the scores launch, the value chains over V tiles
+    staged through LDS): hidden states, tokens and the cache rows equal the
+    oracle's, for spans that cross the 64-position tiles, with 1, 4 and 8
+    query heads per KV head."""
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = tiny_llama(seed=31, n_layers=2, dim=512, hidden=1024, n_heads=n_heads, n_kv_heads=n_kv,
+                   head_dim=128, vocab=700)
+    max_len = 200
+    prompt = np.random.default_rng(32).integers(0, 700, 60)
+    gpu = LlamaDecoder.from_host_model(m, max_len)
+    cpu = ref.Llama(m, max_len)
+    gt = gpu.prefill(prompt)
+    ct, _ = cpu.prefill(prompt)
+    assert gt == ct
+    tok = ct
+    for pos in range(len(prompt), len(prompt) + 75):
+        want, hid = cpu.decode(tok, pos)
+        got = gpu.decode(tok, pos)
+        assert np.array_equal(bits(gpu.hidden()), bits(hid)), pos
+        assert got == want, pos
+        tok = want
+    kv = gpu.kv_cache()
+    used = len(prompt) + 75
+    for l in range(2):
+        k, v = kv.read(l, 0, used)
+        assert np.array_equal(k, cpu.kcache(l, max_len)[:used])
+        assert np.array_equal(v, cpu.vcache(l, max_len)[:used])
