@@ -30,6 +30,10 @@ int gemv_group(int n, gllm_hip_weight* const* ws, const float* d_x, float* const
                const int* strides, void* act_buf, hipStream_t s);
 int group_routing(int n, gllm_hip_weight* const* ws, int* fl);
 bool norm_fusable(int n, gllm_hip_weight* const* ws);
+bool swiglu_epi_ok(gllm_hip_weight* const* gu, const gllm_hip_weight* down);
+int gemv_norm_swiglu_f32(gllm_hip_weight* const* gu, gllm_hip_weight* down, const float* x,
+                         const float* res, const float* nw, float eps, float* xout, float* gate,
+                         float* up, float* out, void* act_buf, int* cnt, hipStream_t s);
 int gemv_norm_f32(int n, gllm_hip_weight* const* ws, const float* x, const float* res,
                   const float* nw, float eps, float* xout, float* const* outs, hipStream_t s);
 bool row_kernel_type(int t);
@@ -67,6 +71,7 @@ struct gllm_hip_model {
     int max_p = 0;  // capacity of the activation buffers below (tokens)
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
     float* x2 = nullptr;  // second residual-stream buffer (norm-fused launches alternate x / x2)
+    int* sq_cnt = nullptr;  // [hidden / 256] block counters of the SwiGLU epilogue (zero at rest)
     float *proj = nullptr, *gate = nullptr, *up = nullptr, *hidden = nullptr, *logits = nullptr;
     uint32_t* d_tokens = nullptr;
     uint32_t* h_tokens = nullptr;  // pinned
@@ -340,10 +345,19 @@ static int forward(gllm_hip_model* m, int pos0, int p, bool decode, const int* d
         }
         {
             gllm_hip_weight* ws[2] = {W[GLLM_T_W1], W[GLLM_T_W3]};
-            float* outs[2] = {m->gate, m->up};
-            GLLM_TRY(norm_project(2, ws, m->proj, m->d_norms + (size_t)(2 * l + 1) * c.dim, outs));
+            const float* ffn_norm = m->d_norms + (size_t)(2 * l + 1) * c.dim;
+            if (fuse && swiglu_epi_ok(ws, W[GLLM_T_W2])) {
+                // norm in the gate/up launch, SwiGLU + Q8K in its epilogue
+                GLLM_TRY(gemv_norm_swiglu_f32(ws, W[GLLM_T_W2], X[xi], m->proj, ffn_norm, c.rms_eps,
+                                              X[xi ^ 1], m->gate, m->up, m->proj, m->act,
+                                              m->sq_cnt, s));
+                xi ^= 1;
+            } else {
+                float* outs[2] = {m->gate, m->up};
+                GLLM_TRY(norm_project(2, ws, m->proj, ffn_norm, outs));
+                GLLM_TRY(gemv_silu_f32(W[GLLM_T_W2], m->gate, m->up, p, m->proj, m->act, m->hidden, s));
+            }
         }
-        GLLM_TRY(gemv_silu_f32(W[GLLM_T_W2], m->gate, m->up, p, m->proj, m->act, m->hidden, s));
         pending = m->proj;
     }
     hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(p), dim3(256), norm_lds, s, X[xi], pending,
@@ -477,6 +491,9 @@ gllm_hip_model* gllm_hip_model_new(const gllm_hip_model_config* cfg) {
     if (!m->kv) return bail("kv cache");
     if (ensure_buffers(m, 1) != GLLM_OK) return bail("activation buffers");
     if (hipMalloc(&m->logits, (size_t)cfg->vocab * 4) != hipSuccess) return bail("logits");
+    if (hipMalloc(&m->sq_cnt, (size_t)(cfg->hidden / 256) * 4) != hipSuccess ||
+        hipMemset(m->sq_cnt, 0, (size_t)(cfg->hidden / 256) * 4) != hipSuccess)
+        return bail("SwiGLU counters");
     if (hipMalloc(&m->argmax_keys, argmax_keys(cfg->vocab) * 8) != hipSuccess)
         return bail("argmax keys");
     if (hipMalloc(&m->d_pos, pos_bytes(*cfg)) != hipSuccess) return bail("position");
@@ -499,6 +516,7 @@ void gllm_hip_model_release(gllm_hip_model* m) {
     drop_decode_graph(m);
     if (m->scores) (void)hipFree(m->scores);
     if (m->d_pos) (void)hipFree(m->d_pos);
+    if (m->sq_cnt) (void)hipFree(m->sq_cnt);
     if (m->h_pos) (void)hipHostFree(m->h_pos);
     if (m->kv) gllm_hip_kv_release(m->kv);
     if (m->d_recent) (void)hipFree(m->d_recent);

@@ -60,6 +60,11 @@ struct GemvJob {
     const float* res;
     float* xout;
     float eps;
+    // SwiGLU epilogue (gate/up group, batch 1): workgroups count finished
+    // 256-row blocks in sq_cnt; the last of a block's 2 * 256 / rows_per_wg
+    // workgroups quantises siluMulF32(out[0], out[1]) of the block into sq_act
+    int* sq_cnt;
+    ActQ8 sq_act;
 };
 
 __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
@@ -525,7 +530,7 @@ __device__ __forceinline__ uint4 hdr_of(uint4 v, int j) {  // j: compile-time af
 // the prefetch.  FUSE = 2 (3 with a residual) puts the RMSNorm in front of
 // the quantiser (norm_regs): the norm weights (and residual) are loaded with
 // x, the LDS for x' follows the quantised activation.
-template <int NT, int G, int NL, int D, int FUSE>
+template <int NT, int G, int NL, int D, int FUSE, bool SQ = false>
 __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(GemvJob j) {
     static_assert(NL % D == 0, "prefetch depth must divide the blocks per lane");
     static_assert(!FUSE || NT == 1, "fused quantisation is batch 1 only");
@@ -601,8 +606,38 @@ __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const float v = tree8_strided<G>(accF[t] - accM[t]);  // VSUBPS + tree
-        if (live && k == 0 && gi == G - 1 && t < j.ntok)
-            j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
+        if (live && k == 0 && gi == G - 1 && t < j.ntok) {
+            float* o = &j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r];
+            if constexpr (SQ) __hip_atomic_store(o, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            else *o = v;
+        }
+    }
+    if constexpr (SQ) {
+        // the FFN's SwiGLU + Q8K for the down projection (q8k_prep_kernel's
+        // work) by the last workgroup to finish each 256-row block: stores
+        // made visible device-wide, then one counter increment per workgroup
+        __shared__ int s_last;
+        __shared__ float sq_x[256];
+        __shared__ float sq_max[4];
+        // The outputs above are system-scope stores (written through past
+        // the XCD's L2); every thread waits for its stores to complete before
+        // the barrier, then one system-scope counter increment per
+        // workgroup; the last workgroup reads the block with system-scope
+        // loads.  No cache-wide writeback or invalidate is needed.
+        const int blk = (((int)blockIdx.x - j.wg_begin[wi]) * j.rows_per_wg) / 256;
+        wait_vmem_le<0>();  // this thread's output stores have completed
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int total = 2 * (256 / j.rows_per_wg);
+            s_last = __hip_atomic_fetch_add(&j.sq_cnt[blk], 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_SYSTEM) == total - 1;
+        }
+        __syncthreads();
+        if (s_last) {
+            silu_q8_block<true>(j.out[0], j.out[1], blk, j.sq_act, sq_x, sq_max);
+            if (threadIdx.x == 0)  // ready for the next step
+                __hip_atomic_store(&j.sq_cnt[blk], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
 }
 
@@ -1171,7 +1206,9 @@ static void launch_q4k_nl(const GemvJob& j, dim3 grid, dim3 block, size_t stage,
     if constexpr (NT == 1 && NL * G * 256 <= kFuseCols) {
         if (j.xf && j.nw) {
             const size_t lds = q4k_norm_off(j.cols) + (size_t)j.cols * 4 + kNormLds;
-            if (j.res) hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, 3>), grid, block, lds, s, j);
+            if (j.res && j.sq_cnt)
+                hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, 3, true>), grid, block, lds, s, j);
+            else if (j.res) hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, 3>), grid, block, lds, s, j);
             else hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, 2>), grid, block, lds, s, j);
             return;
         }
@@ -1386,12 +1423,15 @@ int validate_weight(const gllm_hip_weight* w) {
 
 // Row kernels for n weights against p activation rows already quantised
 // into `act` (activation rows tok0 .. tok0+p-1 of act).
-// RMSNorm prologue arguments (GemvJob::nw .. eps)
+// RMSNorm prologue arguments (GemvJob::nw .. eps) and the optional SwiGLU
+// epilogue (GemvJob::sq_cnt, sq_act)
 struct NormIn {
     const float* w;
     const float* res;
     float* xout;
     float eps;
+    int* sq_cnt;
+    ActQ8 sq_act;
 };
 
 int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* const* outs,
@@ -1408,6 +1448,10 @@ int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* 
         j.res = ni->res;
         j.xout = ni->xout;
         j.eps = ni->eps;
+        j.sq_cnt = ni->sq_cnt;
+        j.sq_act = ni->sq_act;
+        if (j.sq_cnt && (n != 2 || !j.res))
+            return fail(GLLM_EINVAL, "gemv: the SwiGLU epilogue needs the gate/up pair and a residual");
     }
     const gllm_hip_weight* w0 = ws[0];
     j.blocks = w0->blocks;
@@ -1506,9 +1550,42 @@ bool norm_fusable(int n, gllm_hip_weight* const* ws) {
 int gemv_norm_f32(int n, gllm_hip_weight* const* ws, const float* x, const float* res,
                   const float* nw, float eps, float* xout, float* const* outs, hipStream_t s) {
     if (!norm_fusable(n, ws)) return fail(GLLM_EUNSUP, "gemv: no RMSNorm prologue for this group");
-    const NormIn ni{nw, res, xout, eps};
+    const NormIn ni{nw, res, xout, eps, nullptr, ActQ8{}};
     ActQ8 none{};
     return run_gemv(n, ws, none, 1, outs, nullptr, s, x, &ni);
+}
+
+// The decode step's FFN with the SwiGLU in the gate/up launch: gate/up =
+// W1/W3 . rmsNormInto(fma(res, 1, x), nw) (one launch, norm prologue), whose
+// last workgroup per 256-row block evaluates siluMulF32 for the block and
+// quantises it into act_buf (the work of q8k_prep_silu); then down . act in
+// the row kernel that reads pre-quantised activations.  Needs the gate/up
+// shape to cover each 256-row block with whole workgroups and a down
+// projection that does not quantise x itself (swiglu_epi_ok); cnt: hidden /
+// 256 ints, zero between calls (each block's last workgroup resets its own).
+bool swiglu_epi_ok(gllm_hip_weight* const* gu, const gllm_hip_weight* down) {
+    if (!norm_fusable(2, gu) || gu[0]->rows != gu[1]->rows || gu[0]->rows % 256 ||
+        down->cols != gu[0]->rows || !row_kernel_type(down->type))
+        return false;
+    gllm_hip_weight* dw[1] = {const_cast<gllm_hip_weight*>(down)};
+    if (fused_quant(1, dw)) return false;
+    const Q4KShape sh = q4k_shape(2 * gu[0]->rows, gu[0]->blocks);
+    return sh.rows_per_wg > 0 && 256 % sh.rows_per_wg == 0;
+}
+
+int gemv_norm_swiglu_f32(gllm_hip_weight* const* gu, gllm_hip_weight* down, const float* x,
+                         const float* res, const float* nw, float eps, float* xout, float* gate,
+                         float* up, float* out, void* act_buf, int* cnt, hipStream_t s) {
+    if (!swiglu_epi_ok(gu, down)) return fail(GLLM_EUNSUP, "gemv: no SwiGLU epilogue for this FFN");
+    ActQ8 act;
+    act_carve(act_buf, down->cols, 1, &act);
+    const NormIn ni{nw, res, xout, eps, cnt, act};
+    float* outs[2] = {gate, up};
+    ActQ8 none{};
+    GLLM_TRY(run_gemv(2, gu, none, 1, outs, nullptr, s, x, &ni));
+    gllm_hip_weight* dw[1] = {down};
+    float* dout[1] = {out};
+    return run_gemv(1, dw, act, 1, dout, nullptr, s, nullptr);
 }
 
 // W.siluMulF32(gate, up) for p rows (the FFN down projection): the SwiGLU is

@@ -290,6 +290,68 @@ __device__ __forceinline__ float silu_mul(float g, float up) {
     return (g * s) * up;
 }
 
+// siluMulF32(gate, up) of 256-element block b of one activation row,
+// quantised into a (q8kQuantizePortable, quant_q8k_portable.go:36-62, with
+// sumF32Groups32 / sumF32Groups16, kernels_amd64.s:208-254): the work of
+// q8k_prep_kernel's workgroup for that block, run by threads 0..255 of the
+// calling workgroup (every thread of it calls this; sx: 256 floats and
+// wmax: 4 floats of LDS).  SYS: read gate / up with system-scope loads
+// (written by other workgroups of the same launch).
+template <bool SYS = false>
+__device__ inline void silu_q8_block(const float* gate, const float* up, int b, const ActQ8& a,
+                                     float* sx, float* wmax) {
+    const int e = threadIdx.x;
+    const bool on = e < 256;
+    const int nb = a.cols / 256;
+    float v = 0.0f;
+    if (on) {
+        const size_t idx = (size_t)b * 256 + e;
+        float gv, uv;
+        if constexpr (SYS) {
+            gv = __hip_atomic_load(gate + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            uv = __hip_atomic_load(up + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        } else {
+            gv = gate[idx];
+            uv = up[idx];
+        }
+        v = silu_mul(gv, uv);
+        sx[e] = v;
+        float m = fabsf(v);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if ((e & 63) == 0) wmax[e >> 6] = m;
+    }
+    __syncthreads();
+    if (!on) return;  // no barrier follows
+    const float amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    float scale = 0.0f;
+    int q = 0;
+    if (amax != 0.0f && amax == amax) {
+        scale = amax / 127.0f;
+        const float inv = 127.0f / amax;
+        q = (int)rintf(v * inv);
+    }
+    a.q8perm[(size_t)b * 256 + q8perm_offset(e)] = (int8_t)q;
+    if (e == 0) a.xscale[b] = scale;
+    if (e < 8) {
+        const float* g = sx + 32 * e;
+        float s8[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) s8[k] = ((g[k] + g[8 + k]) + g[16 + k]) + g[24 + k];
+        const float a0 = s8[0] + s8[4], a1 = s8[1] + s8[5], a2 = s8[2] + s8[6], a3 = s8[3] + s8[7];
+        a.xs32[(size_t)b * 8 + e] = (a0 + a1) + (a2 + a3);
+    } else if (e >= 64 && e < 80) {
+        const int gi = e - 64;
+        const float* g = sx + 16 * gi;
+        float s8[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) s8[k] = g[k] + g[8 + k];
+        const float a0 = s8[0] + s8[4], a1 = s8[1] + s8[5], a2 = s8[2] + s8[6], a3 = s8[3] + s8[7];
+        a.xs16[(size_t)b * 16 + gi] = (a0 + a1) + (a2 + a3);
+    }
+    (void)nb;
+}
+
 // Direct global->LDS copies issued from inline assembly.  The compiler does
 // not see them as outstanding vector-memory operations, which is the point:
 // they are issued before the weight prefetch and retire first (in order), so
