@@ -30,6 +30,8 @@
 // stages the 32 tokens' q8 (as f16), xsums and xscales and the 64 rows'
 // decoded scales/mins and nibble bytes in LDS (double-buffered, loaded one
 // block ahead).
+#include <cstdlib>
+
 #include "gllm_common.h"
 
 namespace gllm {
@@ -314,18 +316,205 @@ static void launch_pf(const PfArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((prefill_q4k_mfma_kernel<RW, TW>), grid, dim3(64 * RW * TW), 0, s, a);
 }
 
+// --- at most 16 activation rows (decode batches) ---------------------------
+// One workgroup of four waves per 16 weight rows; wave w computes the
+// products of blocks b = w, w + 4, ... (MFMA tiles of 16 rows x 16 tokens,
+// one per AVX2 lane k, straight from registers: lane (g, c) loads row c's
+// nibble dword g of every lane k and token c's q8 bytes 32k + 8g .. + 7),
+// and per group of four blocks the waves exchange the products through LDS
+// and run the float chains in block order, wave w the chains of lanes
+// k = 2w, 2w + 1 for the 16 x 16 (row, token) pairs.  The chains therefore
+// see the same operands in the same order as the row kernel's; only the
+// exact integer products are computed block-parallel.
+struct SbParams {  // one block's factors: rows 0..15 and tokens 0..15 of the tile
+    float d[16], dmin[16], m[8][16];
+    float xs[16], xsum[8][16];
+};
+struct SbOps {     // one block's operands in a lane's registers
+    uint32_t wd[8];
+    u4v hdr;
+    uint2 q8[8];
+    float xs;
+    f4v xsa, xsb;
+};
+
+__device__ __forceinline__ void sb_load(const PfArgs& a, const uint8_t* wrow, int tok, int g, int b,
+                                        SbOps& o) {
+    const int cols = a.blocks * 256;
+    b = min(b, a.blocks - 1);  // past the end: re-read the last block (not used)
+    const uint8_t* nib = wrow + q4k_nib_off(a.blocks, b) + 4 * g;
+#pragma unroll
+    for (int k = 0; k < 8; k++) o.wd[k] = *(const uint32_t*)(nib + 16 * k);
+    o.hdr = *(const u4v*)(wrow + q4k_hdr_off(b));
+    const int8_t* q = a.act.q8perm + (size_t)tok * cols + (size_t)b * 256 + 8 * g;
+#pragma unroll
+    for (int k = 0; k < 8; k++) o.q8[k] = *(const uint2*)(q + 32 * k);
+    o.xs = a.act.xscale[(size_t)tok * a.blocks + b];
+    o.xsa = *(const f4v*)(a.act.xs32 + (size_t)tok * (cols / 32) + b * 8);
+    o.xsb = *(const f4v*)(a.act.xs32 + (size_t)tok * (cols / 32) + b * 8 + 4);
+}
+
+// getScaleMinK4 (simd.go:1672-1677): 6-bit scale and min of sub-block j
+__device__ __forceinline__ void sb_scale_min(const u4v h, int j, uint32_t& sc, uint32_t& mn) {
+    const uint32_t s03 = h.y, s47 = h.z, s811 = h.w;
+    if (j < 4) {
+        sc = (s03 >> (8 * j)) & 63u;
+        mn = (s47 >> (8 * j)) & 63u;
+    } else {
+        const int jj = j - 4;
+        const uint32_t b8 = (s811 >> (8 * jj)) & 0xffu;
+        sc = (b8 & 15u) | (((s03 >> (8 * jj + 6)) & 3u) << 4);
+        mn = (b8 >> 4) | (((s47 >> (8 * jj + 6)) & 3u) << 4);
+    }
+}
+
+constexpr int kSbDepth = 1;  // blocks in flight per wave (register ring; deeper measured slower)
+
+__global__ __launch_bounds__(256) void prefill_q4k_b16_kernel(PfArgs a) {
+    __shared__ __align__(16) f4v sdI[4][8][64];  // [wave][lane k][MFMA lane] products
+    __shared__ __align__(16) SbParams sp[4];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int row0 = blockIdx.x * 16;
+    const uint8_t* wrow = a.w + (size_t)min(row0 + c, a.rows - 1) * a.rb;  // A row of this lane
+    const int tok = min(c, a.p - 1);                                         // B token of this lane
+    const int nb = a.blocks;
+    float accF[2][4], accM[2][4];
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) accF[kk][i] = accM[kk][i] = 0.0f;
+    // wave w's blocks w, w + 4, ...: kSbDepth of them in flight, each
+    // refilled as soon as it is used (loads unconditional, clamped)
+    SbOps ring[kSbDepth];
+#pragma unroll
+    for (int d = 0; d < kSbDepth; d++) sb_load(a, wrow, tok, g, w + 4 * d, ring[d]);
+    auto group = [&](int q0, SbOps& cur) __attribute__((always_inline)) {
+        const int b = q0 + w;
+        if (b < nb) {  // wave-uniform
+            uint32_t sc_lo, sc_hi, mn;
+            sb_scale_min(cur.hdr, 2 * g, sc_lo, mn);
+            sb_scale_min(cur.hdr, 2 * g + 1, sc_hi, mn);
+            const _Float16 hl = (_Float16)(float)sc_lo, nl = (_Float16)(-1024.0f * (float)sc_lo);
+            const _Float16 hh = (_Float16)(float)sc_hi, nh = (_Float16)(-1024.0f * (float)sc_hi);
+            const uint32_t bl = __builtin_bit_cast(uint16_t, hl), bnl = __builtin_bit_cast(uint16_t, nl);
+            const uint32_t bh = __builtin_bit_cast(uint16_t, hh), bnh = __builtin_bit_cast(uint16_t, nh);
+            const uint32_t sh_lo = bl | (bl << 16), sn_lo = bnl | (bnl << 16);
+            const uint32_t sh_hi = bh | (bh << 16), sn_hi = bnh | (bnh << 16);
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const h8v av = dequant_a(cur.wd[k], sh_lo, sn_lo, sh_hi, sn_hi);
+                uint32_t v[4];
+                i8x4_to_h(cur.q8[k].x, v[0], v[1]);
+                i8x4_to_h(cur.q8[k].y, v[2], v[3]);
+                const h8v bv = __builtin_bit_cast(h8v, u4v{v[0], v[1], v[2], v[3]});
+                const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+                sdI[w][k][lane] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, z, 0, 0, 0);
+            }
+            if (g == 0) {
+                sp[w].d[c] = f16_bits_to_f32(cur.hdr.x & 0xffffu);
+                sp[w].dmin[c] = f16_bits_to_f32(cur.hdr.x >> 16);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    uint32_t scj, mnj;
+                    sb_scale_min(cur.hdr, j, scj, mnj);
+                    sp[w].m[j][c] = (float)mnj;
+                }
+            } else if (g == 1) {
+                sp[w].xs[c] = cur.xs;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    sp[w].xsum[k][c] = cur.xsa[k];
+                    sp[w].xsum[4 + k][c] = cur.xsb[k];
+                }
+            }
+        }
+        sb_load(a, wrow, tok, g, b + 4 * kSbDepth, cur);
+        wait_lgkm0();
+        lds_barrier();
+        // the group's blocks in order: chains of lanes k = 2w, 2w + 1 for
+        // rows 4g + i and token c (the MFMA D layout of this lane)
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (q0 + u >= nb) break;  // uniform
+            const SbParams& P = sp[u];
+            const f4v d4 = *(const f4v*)&P.d[4 * g];
+            const f4v dm4 = *(const f4v*)&P.dmin[4 * g];
+            const float xs = P.xs[c];
+            float dxs[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) dxs[i] = d4[i] * xs;
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+                const int k = 2 * w + kk;
+                const f4v dI = sdI[u][k][lane];
+                const f4v m4 = *(const f4v*)&P.m[k][4 * g];
+                const float xk = P.xsum[k][c];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    accF[kk][i] = fmaf(dI[i], dxs[i], accF[kk][i]);
+                    const float mx = m4[i] * xk;
+                    accM[kk][i] = fmaf(dm4[i], mx, accM[kk][i]);
+                }
+            }
+        }
+        wait_lgkm0();
+        lds_barrier();
+    };
+#pragma unroll 1
+    for (int q0 = 0; q0 < nb; q0 += 4 * kSbDepth) {
+#pragma unroll
+        for (int d = 0; d < kSbDepth; d++) group(q0 + 4 * d, ring[d]);
+    }
+    // tree8 over the lanes k (held by the four waves) through LDS
+    float* vb = (float*)&sdI[0][0][0];  // [k][MFMA lane][row i]
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) vb[((2 * w + kk) * 64 + lane) * 4 + i] = accF[kk][i] - accM[kk][i];
+    __syncthreads();
+    if (w == 0 && c < a.p) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = row0 + 4 * g + i;
+            if (r >= a.rows) continue;
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = vb[(k * 64 + lane) * 4 + i];
+            const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+            a.out[(size_t)c * a.out_stride + r] = (s0 + s1) + (s2 + s3);
+        }
+    }
+}
+
 // Workgroup shape: 64 rows x 32 tokens for real prefill batches, 64 rows x 16
 // tokens for at most 16 activation rows (a decode batch).  The per-block
 // staging (q8 to f16, scale decoding) is a fixed cost per workgroup, so 64
 // rows per workgroup beat smaller tiles that would fill more CUs (measured
 // at batch 8: 22.8 vs 28.4 us for 14336 x 4096, 58.8 vs 72.3 us for
 // 4096 x 14336).
+// Batches of at most 16 rows take prefill_q4k_b16_kernel unless
+// GLLM_Q4K_B16=0 (the 64-row tile kernel, for measurement; same bits).
+static bool q4k_b16_on() {
+    static const bool on = [] {
+        const char* e = getenv("GLLM_Q4K_B16");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
                     float* out, int out_stride, hipStream_t s) {
     if (rows <= 0 || blocks <= 0 || p <= 0) return GLLM_OK;
     PfArgs a{d_w, rb, rows, blocks, act, p, out, out_stride};
-    if (p > 16) launch_pf<4, 2>(a, s);
-    else launch_pf<4, 1>(a, s);
+    if (p > 16) {
+        launch_pf<4, 2>(a, s);
+    } else if (q4k_b16_on() && (rows + 63) / 64 < 2 * device_cus() / 3) {
+        // the 64-row tile leaves CUs idle: 16-row tiles, block-parallel waves
+        hipLaunchKernelGGL(prefill_q4k_b16_kernel, dim3((rows + 15) / 16), dim3(256), 0, s, a);
+    } else {
+        launch_pf<4, 1>(a, s);
+    }
     GLLM_HIP(hipGetLastError());
     return GLLM_OK;
 }
