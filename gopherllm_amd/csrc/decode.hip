@@ -622,7 +622,11 @@ int gllm_hip_model_prefill(gllm_hip_model* m, const uint32_t* tokens, int n, int
         return fail(GLLM_EINVAL, "prefill positions %d..%d exceed max_len", start_pos, start_pos + n - 1);
     for (int i = 0; i < n; i++)
         if (tokens[i] >= (uint32_t)m->cfg.vocab) return fail(GLLM_EINVAL, "token %u out of range", tokens[i]);
-    const int chunk = 64;
+    // up to 512 prompt tokens per forward: the batched matrix-core products
+    // need many token tiles to fill the GPU; the score buffer
+    // (tokens x heads x max_len floats) is kept under 1 GiB
+    const size_t per_tok = (size_t)m->cfg.n_heads * m->cfg.max_len * 4;
+    const int chunk = (int)std::max<size_t>(64, std::min<size_t>(512, ((size_t)1 << 30) / per_tok));
     GLLM_TRY(ensure_buffers(m, std::min(n, chunk)));
     hipStream_t s = m->stream;
     // a prefill from position 0 starts a request: its window is the tail of

@@ -54,8 +54,17 @@ struct ActQ8 {
     float* xscale;   // [p][cols/256]
     float* xs32;     // [p][cols/32]   per-32 sums (amd64 order)
     float* xs16;     // [p][cols/16]   per-16 sums (amd64 order; Q6_K scales them by 32)
+    // Batches of more than kTiledMinP rows also get the q8 values as f16 in
+    // the matrix-core operand layout of the batched Q4_K kernel:
+    // [block][16-token tile][lane k][group g][token c][8 halves], the eight
+    // halves being q8perm's bytes 32 k + 8 g .. + 7 of token 16 tile + c.
+    // Tokens p .. 16 tiles - 1 hold zeros.  Null for smaller batches.
+    uint16_t* b16t;
+    float* xs32t;    // xs32 of the same batches as [block][tile][lane k][token c]
+    int tiles;       // ceil(p / 16) when b16t is set
     int cols, p;
 };
+constexpr int kTiledMinP = 16;
 size_t act_bytes(int cols, int p);
 void act_carve(void* base, int cols, int p, ActQ8* a);
 int launch_q8k_prep(const float* d_x, int cols, int p, const ActQ8& a, hipStream_t s);

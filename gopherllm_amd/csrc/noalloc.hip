@@ -30,7 +30,8 @@ int gemv_f32(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float*
              const int* strides, void* act_buf, hipStream_t s);
 }  // namespace gllm
 
-// 4 MiB: batch 1 to about 700 rows at 4096 columns, about 200 at 14336.
+// 4 MiB: up to about 280 activation rows at 4096 columns, about 80 at 14336
+// (batches of more than 16 rows also carry the f16 operand tiles).
 constexpr size_t kNoAllocScratchBytes = 4u << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 

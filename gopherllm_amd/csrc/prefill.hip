@@ -487,6 +487,282 @@ __global__ __launch_bounds__(256) void prefill_q4k_b16_kernel(PfArgs a) {
     }
 }
 
+// --- more than 16 activation rows: operands staged once per workgroup -----
+// A workgroup of eight waves covers 64 weight rows x 64 tokens.  Per block it
+// stages in LDS, double-buffered:
+//   * the 64 rows' A operands, sc_j * q4 as f16, dequantised once for the
+//     whole workgroup: wave w copies the nibbles of AVX2 lanes 4 (w % 2) ..
+//     + 3 of rows 16 (w / 2) .. + 15, and those rows' headers, into LDS two
+//     blocks ahead and dequantises them itself, lane (row, k) the 16 nibble
+//     bytes of AVX2 lane k (16 rows per wave keep its LDS writes on distinct
+//     banks);
+//   * the four 16-token tiles' B operands, q8 as f16 written by the quantiser
+//     in this operand layout, copied global -> LDS one block ahead;
+//   * the rows' d, dmin and mins and the tokens' xscale and xsums.
+// Every global read is a direct global -> LDS copy, so the waits are exact
+// vmcnt counts of this wave's own copies.  Both operand tiles are laid out
+// [tile][lane k][group g][row or token c][8 halves], so each MFMA operand
+// read of a wave is 1 KB of consecutive LDS.  Wave w owns rows 16 (w % 4) ..
+// + 15 and the two token tiles 2 (w / 4), 2 (w / 4) + 1, sharing its A
+// operand between them; per lane k and tile it runs q4kDotQ8KRow's two chains
+// on the exact MFMA lane sums, in block order:
+//   accF = fma(I, d * xscale, accF); accM = fma(dmin, m * xsum, accM).
+constexpr int kTlRows = 64, kTlTok = 64;
+
+constexpr int kTlMStride = 80;     // floats per sub-block row of m: writes on distinct banks
+struct TlStage {
+    uint8_t a16[4 * 8 * 4 * 256];  // [row group][lane k][group g][row c][8 halves]
+    uint8_t b16[4 * 8 * 4 * 256];  // [token tile][lane k][group g][token c][8 halves]
+    float m[8][kTlMStride];        // [sub-block k][row] 6-bit min
+    float xsum[4][8][16];          // [token tile][lane k][token c]
+    float d[kTlRows], dmin[kTlRows], xs[kTlTok];
+};
+struct TlRaw {                     // one block of the 64 rows as stored, per wave
+    uint8_t nib[8][64][16];        // [wave][lane: row 16 (w / 2) + lane / 4, lane k 4 (w % 2) + lane % 4]
+    uint8_t hdr[8][16][16];        // [wave][row 16 (w / 2) + r]: d, dmin, 12 scale bytes
+};
+
+// Direct global -> LDS copies addressed by a wave-uniform base and a 32-bit
+// per-lane byte offset (the saddr form), so a copy costs one VGPR.
+__device__ __forceinline__ void lds_copy16_s(const void* sbase, uint32_t voff, uint32_t lds_dst) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_dst)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4_s(const void* sbase, uint32_t voff, uint32_t lds_dst) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_dst)
+                 : "memory", "m0");
+}
+
+// Block b's token operands into S: 32 one-KB pieces of B (four per wave),
+// the four tiles' xsums (waves 0, 1) and the 64 xscales (wave 2).  Issues 5
+// copies on waves 0-2 and 4 on the others.
+__device__ __forceinline__ void tl_copy_tokens(const PfArgs& a, int w, int lane, int tile0, int tok0,
+                                               int b, TlStage& S) {
+    const int cols = a.blocks * 256;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int ch = 4 * w + i, tt = ch >> 3, piece = ch & 7;
+        const int gt = min(tile0 + tt, a.act.tiles - 1);
+        const uint8_t* base = (const uint8_t*)a.act.b16t + ((size_t)b * a.act.tiles + gt) * 8192 + piece * 1024;
+        lds_copy16_s(base, 16 * lane, lds_addr(S.b16 + tt * 8192 + piece * 1024));
+    }
+    if (w < 2) {
+        const int gt = min(tile0 + 2 * w + (lane >> 5), a.act.tiles - 1);
+        lds_copy16_s(a.act.xs32t, (uint32_t)(((size_t)b * a.act.tiles + gt) * 512 + 16 * (lane & 31)),
+                     lds_addr(&S.xsum[2 * w][0][0]));
+    } else if (w == 2) {
+        lds_copy4_s(a.act.xscale + b, (uint32_t)min(tok0 + lane, a.p - 1) * a.blocks * 4,
+                    lds_addr(&S.xs[0]));
+    }
+}
+
+// Block b of this wave's rows into R: lane (row 16 (w / 2) + lane / 4, lane
+// k = 4 (w % 2) + lane % 4) copies 16 nibble bytes, lanes 0-15 the rows'
+// headers.  Two copies.  noff / hoff: this lane's 32-bit offsets of its
+// nibble chunk and header row (the launcher checks that rows * rb < 2^32).
+__device__ __forceinline__ void tl_copy_raw(const PfArgs& a, int w, int lane, uint32_t noff,
+                                            uint32_t hoff, int b, TlRaw& R) {
+    lds_copy16_s(a.w + q4k_nib_off(a.blocks, b), noff, lds_addr(&R.nib[w][0][0]));
+    if (lane < 16) lds_copy16_s(a.w + q4k_hdr_off(b), hoff, lds_addr(&R.hdr[w][0][0]));
+}
+
+// Dequantisation of this wave's part of one block from R into S, in parts
+// that the kernel interleaves with the MFMA chains: A operands sc_j * q4
+// (f16), the rows' mins (lane k: sub-block k), d and dmin.
+struct TlDq {
+    u4v nib;
+    uint32_t sc03, sc47, mn03, mn47, dd;
+};
+
+__device__ __forceinline__ void tl_dq_begin(int w, int lane, const TlRaw& R, TlDq& q) {
+    q.nib = *(const u4v*)&R.nib[w][lane][0];
+    const u4v h = *(const u4v*)&R.hdr[w][lane >> 2][0];
+    // getScaleMinK4 (simd.go:1672-1677) for all eight sub-blocks at once, one
+    // byte each: j < 4 from s03 / s47, j >= 4 from s811 and their top bits
+    q.sc03 = h.y & 0x3f3f3f3fu;
+    q.sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+    q.mn03 = h.z & 0x3f3f3f3fu;
+    q.mn47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+    q.dd = h.x;
+}
+
+// nibble dword sg: sub-blocks 2 sg (low nibbles) and 2 sg + 1 (high nibbles)
+__device__ __forceinline__ void tl_dq_part(int w, int lane, int sg, const TlDq& q, TlStage& S) {
+    const int c = lane >> 2, k = 4 * (w & 1) + (lane & 3), rg = w >> 1;
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    const h2v m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    // scale bytes 2 (sg & 1) and 2 (sg & 1) + 1 of sc03 / sc47 as (1024 + sc)
+    const uint32_t src = sg < 2 ? q.sc03 : q.sc47;
+    const uint32_t sel_lo = (sg & 1) ? 0x04020402u : 0x04000400u;
+    const uint32_t sel_hi = (sg & 1) ? 0x04030403u : 0x04010401u;
+    const h2v pl = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, src, sel_lo));
+    const h2v ph = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, src, sel_hi));
+    const h2v sl = pl + m1024, sh = ph + m1024;  // exact small integers
+    const h2v nl = sl * m1024, nh = sh * m1024;  // exact: at most 64512
+    const h8v av = dequant_a(q.nib[sg], __builtin_bit_cast(uint32_t, sl), __builtin_bit_cast(uint32_t, nl),
+                             __builtin_bit_cast(uint32_t, sh), __builtin_bit_cast(uint32_t, nh));
+    *(h8v*)(S.a16 + ((rg * 8 + k) * 4 + sg) * 256 + c * 16) = av;
+}
+
+__device__ __forceinline__ void tl_dq_end(int w, int lane, const TlDq& q, TlStage& S) {
+    const int c = lane >> 2, k = 4 * (w & 1) + (lane & 3), lr = 16 * (w >> 1) + c;
+    const uint32_t msrc = k < 4 ? q.mn03 : q.mn47;
+    S.m[k][lr] = (float)((msrc >> (8 * (k & 3))) & 63u);
+    if (k == 0) S.d[lr] = f16_bits_to_f32(q.dd & 0xffffu);
+    if (k == 1) S.dmin[lr] = f16_bits_to_f32(q.dd >> 16);
+}
+
+__device__ __forceinline__ void tl_dequant(int w, int lane, const TlRaw& R, TlStage& S) {
+    TlDq q;
+    tl_dq_begin(w, lane, R, q);
+#pragma unroll
+    for (int sg = 0; sg < 4; sg++) tl_dq_part(w, lane, sg, q, S);
+    tl_dq_end(w, lane, q, S);
+}
+
+__global__ __launch_bounds__(512) void prefill_q4k_tiled_kernel(PfArgs a, int row_tiles, int tok_tiles) {
+    __shared__ __align__(16) TlStage st[2];
+    __shared__ __align__(16) TlRaw raw[2];
+    // XCD-aware order: workgroups i, i + 8, ... share an XCD (and its L2);
+    // the token tiles of one row tile run there back to back.
+    const int id = blockIdx.x, xcd = id & 7, k8 = id >> 3;
+    const int rtile = (k8 / tok_tiles) * 8 + xcd, ttile = k8 % tok_tiles;
+    if (rtile >= row_tiles) return;  // whole workgroup
+    const int row0 = rtile * kTlRows, tok0 = ttile * kTlTok, tile0 = tok0 / 16;
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, c = lane & 15;
+    const int rg = w & 3, tg = w >> 2;
+    const int nb = a.blocks;
+    const uint32_t noff = (uint32_t)min(row0 + 16 * (w >> 1) + (lane >> 2), a.rows - 1) * (uint32_t)a.rb +
+                          16 * (4 * (w & 1) + (lane & 3));
+    const uint32_t hoff = (uint32_t)min(row0 + 16 * (w >> 1) + (lane & 15), a.rows - 1) * (uint32_t)a.rb;
+
+    float accF[2][8][4], accM[2][8][4];
+#pragma unroll
+    for (int n = 0; n < 2; n++)
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) accF[n][k][i] = accM[n][k][i] = 0.0f;
+
+    // prologue: raw blocks 0 and 1, token operands of block 0
+    tl_copy_raw(a, w, lane, noff, hoff, 0, raw[0]);
+    tl_copy_raw(a, w, lane, noff, hoff, min(1, nb - 1), raw[1]);
+    tl_copy_tokens(a, w, lane, tile0, tok0, 0, st[0]);
+    wait_vmem_le<0>();
+    tl_dequant(w, lane, raw[0], st[0]);
+    wait_lgkm0();
+    lds_barrier();
+#pragma unroll 1
+    for (int b = 0; b < nb; b++) {
+        // copies stay unconditional (clamped to the last block; the buffers
+        // they fill are not read this iteration) so the vmcnt counts below
+        // are constants: tokens of b + 1 (5 / 4 copies), raw of b + 2 (2)
+        tl_copy_tokens(a, w, lane, tile0, tok0, min(b + 1, nb - 1), st[(b + 1) & 1]);
+        tl_copy_raw(a, w, lane, noff, hoff, min(b + 2, nb - 1), raw[b & 1]);
+        const TlStage& S = st[b & 1];
+        const f4v dv = *(const f4v*)&S.d[16 * rg + 4 * g];
+        const f4v dm = *(const f4v*)&S.dmin[16 * rg + 4 * g];
+        float dxs[2][4];
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            const float xc = S.xs[32 * tg + 16 * n + c];
+#pragma unroll
+            for (int i = 0; i < 4; i++) dxs[n][i] = dv[i] * xc;
+        }
+        // raw block b + 1 (copied last iteration) has landed once at most this
+        // iteration's copies are outstanding; its dequantisation into the
+        // other stage runs in parts between the chain steps below
+        if (w < 3) wait_vmem_le<7>();
+        else wait_vmem_le<6>();
+        asm volatile("" ::: "memory");
+        TlDq dq;
+        tl_dq_begin(w, lane, raw[(b + 1) & 1], dq);
+        // Operands of lane k + 2 are read while lane k's chains run.  The
+        // empty asm statements pin that order: lane k's accumulators are
+        // final and lane k + 1's operands have arrived when step k ends, so
+        // three lanes' operands and one lane's products are live (more would
+        // not fit the register budget of two waves per SIMD).
+        struct Ops {
+            h8v av, bv[2];
+            f4v mk;
+            float xk[2];
+        };
+        auto ops = [&](int k, Ops& o) __attribute__((always_inline)) {
+            o.av = *(const h8v*)(S.a16 + ((rg * 8 + k) * 4 + g) * 256 + c * 16);
+            o.mk = *(const f4v*)&S.m[k][16 * rg + 4 * g];
+#pragma unroll
+            for (int n = 0; n < 2; n++) {
+                o.bv[n] = *(const h8v*)(S.b16 + (((2 * tg + n) * 8 + k) * 4 + g) * 256 + c * 16);
+                o.xk[n] = S.xsum[2 * tg + n][k][c];
+            }
+        };
+        Ops o[3];
+        ops(0, o[0]);
+        ops(1, o[1]);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            if (k < 6) ops(k + 2, o[(k + 2) % 3]);
+            const Ops& cur = o[k % 3];
+#pragma unroll
+            for (int n = 0; n < 2; n++) {
+                const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+                const f4v dI = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.av, cur.bv[n], z, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    accF[n][k][i] = fmaf(dI[i], dxs[n][i], accF[n][k][i]);
+                    const float mx = cur.mk[i] * cur.xk[n];
+                    accM[n][k][i] = fmaf(dm[i], mx, accM[n][k][i]);
+                }
+            }
+            if (k & 1) tl_dq_part(w, lane, k >> 1, dq, st[(b + 1) & 1]);
+#pragma unroll
+            for (int n = 0; n < 2; n++)
+                asm volatile("" : "+v"(accF[n][k][0]), "+v"(accF[n][k][1]), "+v"(accF[n][k][2]),
+                             "+v"(accF[n][k][3]), "+v"(accM[n][k][0]), "+v"(accM[n][k][1]),
+                             "+v"(accM[n][k][2]), "+v"(accM[n][k][3]));
+            if (k < 7) {
+                Ops& nx = o[(k + 1) % 3];
+                asm volatile("" : "+v"(nx.av), "+v"(nx.bv[0]), "+v"(nx.bv[1]), "+v"(nx.mk),
+                             "+v"(nx.xk[0]), "+v"(nx.xk[1]));
+            }
+        }
+        tl_dq_end(w, lane, dq, st[(b + 1) & 1]);
+        wait_vmem_le<2>();  // token operands of b + 1
+        wait_lgkm0();
+        lds_barrier();
+    }
+    wait_vmem_le<0>();  // the clamped copies of the last iterations
+    // tree8 of the reference's horizontal sum, then the (row, token) stores
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+        const int t = tok0 + 32 * tg + 16 * n + c;
+        if (t >= a.p) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int rr = row0 + 16 * rg + 4 * g + i;
+            if (rr >= a.rows) continue;
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = accF[n][k][i] - accM[n][k][i];
+            const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+            a.out[(size_t)t * a.out_stride + rr] = (s0 + s1) + (s2 + s3);
+        }
+    }
+}
+
+static bool q4k_tiled_on() {
+    static const bool on = [] {
+        const char* e = getenv("GLLM_Q4K_TILED");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 // Workgroup shape: 64 rows x 32 tokens for real prefill batches, 64 rows x 16
 // tokens for at most 16 activation rows (a decode batch).  The per-block
 // staging (q8 to f16, scale decoding) is a fixed cost per workgroup, so 64
@@ -507,7 +783,11 @@ int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const A
                     float* out, int out_stride, hipStream_t s) {
     if (rows <= 0 || blocks <= 0 || p <= 0) return GLLM_OK;
     PfArgs a{d_w, rb, rows, blocks, act, p, out, out_stride};
-    if (p > 16) {
+    if (p > kTiledMinP && act.b16t && q4k_tiled_on() && (size_t)rows * rb < ((size_t)1 << 32)) {
+        const int rt = (rows + kTlRows - 1) / kTlRows, tt = (p + kTlTok - 1) / kTlTok;
+        const int grid = (rt + 7) / 8 * 8 * tt;
+        hipLaunchKernelGGL(prefill_q4k_tiled_kernel, dim3(grid), dim3(512), 0, s, a, rt, tt);
+    } else if (p > 16) {
         launch_pf<4, 2>(a, s);
     } else if (q4k_b16_on() && (rows + 63) / 64 < 2 * device_cus() / 3) {
         // the 64-row tile leaves CUs idle: 16-row tiles, block-parallel waves

@@ -17,6 +17,11 @@ size_t act_bytes(int cols, int p) {
     n = (n + 255) & ~(size_t)255;
     n += (size_t)(cols / 32) * p * 4;              // xs32
     n += (size_t)(cols / 16) * p * 4;              // xs16
+    if (p > kTiledMinP) {
+        n = (n + 255) & ~(size_t)255;
+        n += (size_t)(p + 15) / 16 * 16 * cols * 2;  // b16t
+        n += (size_t)(p + 15) / 16 * 16 * (cols / 32) * 4;  // xs32t
+    }
     return n + 256;
 }
 
@@ -30,6 +35,17 @@ void act_carve(void* base, int cols, int p, ActQ8* a) {
     a->xs32 = (float*)c;
     c += (size_t)(cols / 32) * p * 4;
     a->xs16 = (float*)c;
+    c += (size_t)(cols / 16) * p * 4;
+    a->b16t = nullptr;
+    a->xs32t = nullptr;
+    a->tiles = 0;
+    if (p > kTiledMinP) {
+        c = (uint8_t*)(((uintptr_t)c + 255) & ~(uintptr_t)255);
+        a->tiles = (p + 15) / 16;
+        a->b16t = (uint16_t*)c;
+        c += (size_t)a->tiles * 16 * cols * 2;
+        a->xs32t = (float*)c;
+    }
     a->cols = cols;
     a->p = p;
 }
@@ -44,6 +60,13 @@ __global__ __launch_bounds__(256) void q8k_prep_kernel(const float* __restrict__
                                                        const float* __restrict__ up) {
     const int b = blockIdx.x, t = blockIdx.y, e = threadIdx.x;
     const int nb = cols / 256;
+    if (a.b16t && t >= a.p) {  // padding tokens of the last f16 tile (uniform per workgroup)
+        const int kappa = q8perm_offset(e);
+        a.b16t[((size_t)b * a.tiles + (t >> 4)) * 4096 + ((kappa >> 3) * 16 + (t & 15)) * 8 +
+               (kappa & 7)] = 0;
+        if (e < 8) a.xs32t[(((size_t)b * a.tiles + (t >> 4)) * 8 + e) * 16 + (t & 15)] = 0.0f;
+        return;
+    }
     __shared__ float sx[256];
     __shared__ float wmax[4];
     const size_t idx = (size_t)t * cols + (size_t)b * 256 + e;
@@ -69,7 +92,13 @@ __global__ __launch_bounds__(256) void q8k_prep_kernel(const float* __restrict__
         if (e == 0) plain_scale[(size_t)t * nb + b] = scale;
         return;
     }
-    a.q8perm[(size_t)t * cols + (size_t)b * 256 + q8perm_offset(e)] = (int8_t)q;
+    const int kappa = q8perm_offset(e);
+    a.q8perm[(size_t)t * cols + (size_t)b * 256 + kappa] = (int8_t)q;
+    if (a.b16t) {
+        // kappa = 32 k + 8 g + i -> ((k 4 + g) 16 + c) 8 + i of the tile block
+        a.b16t[((size_t)b * a.tiles + (t >> 4)) * 4096 + ((kappa >> 3) * 16 + (t & 15)) * 8 +
+               (kappa & 7)] = __builtin_bit_cast(uint16_t, (_Float16)(float)q);
+    }
     if (e == 0) a.xscale[(size_t)t * nb + b] = scale;
     if (e < 8) {
         // sumF32Groups32: v_k = ((x[k] + x[8+k]) + x[16+k]) + x[24+k]
@@ -78,7 +107,9 @@ __global__ __launch_bounds__(256) void q8k_prep_kernel(const float* __restrict__
 #pragma unroll
         for (int k = 0; k < 8; k++) s[k] = ((g[k] + g[8 + k]) + g[16 + k]) + g[24 + k];
         const float a0 = s[0] + s[4], a1 = s[1] + s[5], a2 = s[2] + s[6], a3 = s[3] + s[7];
-        a.xs32[(size_t)t * (cols / 32) + b * 8 + e] = (a0 + a1) + (a2 + a3);
+        const float xs = (a0 + a1) + (a2 + a3);
+        a.xs32[(size_t)t * (cols / 32) + b * 8 + e] = xs;
+        if (a.xs32t) a.xs32t[(((size_t)b * a.tiles + (t >> 4)) * 8 + e) * 16 + (t & 15)] = xs;
     } else if (e >= 64 && e < 80) {
         // sumF32Groups16: v_k = x[k] + x[8+k], then the same tree, then x32
         const int gi = e - 64;
@@ -93,7 +124,7 @@ __global__ __launch_bounds__(256) void q8k_prep_kernel(const float* __restrict__
 
 int launch_q8k_prep(const float* d_x, int cols, int p, const ActQ8& a, hipStream_t s) {
     if (cols <= 0 || cols % 256 || p <= 0) return fail(GLLM_EINVAL, "q8k: cols %d p %d", cols, p);
-    dim3 grid(cols / 256, p);
+    dim3 grid(cols / 256, a.b16t ? 16 * a.tiles : p);
     hipLaunchKernelGGL(q8k_prep_kernel, grid, dim3(256), 0, s, d_x, cols, a, (int8_t*)nullptr,
                        (float*)nullptr, (const float*)nullptr);
     GLLM_HIP(hipGetLastError());
@@ -103,7 +134,7 @@ int launch_q8k_prep(const float* d_x, int cols, int p, const ActQ8& a, hipStream
 int launch_q8k_prep_silu(const float* d_gate, const float* d_up, int cols, int p, const ActQ8& a,
                          hipStream_t s) {
     if (cols <= 0 || cols % 256 || p <= 0) return fail(GLLM_EINVAL, "q8k: cols %d p %d", cols, p);
-    dim3 grid(cols / 256, p);
+    dim3 grid(cols / 256, a.b16t ? 16 * a.tiles : p);
     hipLaunchKernelGGL(q8k_prep_kernel, grid, dim3(256), 0, s, d_gate, cols, a, (int8_t*)nullptr,
                        (float*)nullptr, d_up);
     GLLM_HIP(hipGetLastError());
