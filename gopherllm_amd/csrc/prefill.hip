@@ -575,7 +575,7 @@ __device__ __forceinline__ void tl_copy_raw(const PfArgs& a, int w, int lane, ui
 // (f16), the rows' mins (lane k: sub-block k), d and dmin.
 struct TlDq {
     u4v nib;
-    uint32_t sc03, sc47, mn03, mn47, dd;
+    uint32_t sc03, sc47;
 };
 
 __device__ __forceinline__ void tl_dq_begin(int w, int lane, const TlRaw& R, TlDq& q) {
@@ -585,9 +585,6 @@ __device__ __forceinline__ void tl_dq_begin(int w, int lane, const TlRaw& R, TlD
     // byte each: j < 4 from s03 / s47, j >= 4 from s811 and their top bits
     q.sc03 = h.y & 0x3f3f3f3fu;
     q.sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
-    q.mn03 = h.z & 0x3f3f3f3fu;
-    q.mn47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
-    q.dd = h.x;
 }
 
 // nibble dword sg: sub-blocks 2 sg (low nibbles) and 2 sg + 1 (high nibbles)
@@ -608,12 +605,16 @@ __device__ __forceinline__ void tl_dq_part(int w, int lane, int sg, const TlDq& 
     *(h8v*)(S.a16 + ((rg * 8 + k) * 4 + sg) * 256 + c * 16) = av;
 }
 
-__device__ __forceinline__ void tl_dq_end(int w, int lane, const TlDq& q, TlStage& S) {
+// the rows' mins (lane k: sub-block k, same packing as the scales), d, dmin;
+// the header is read again from R, which the next copies overwrite only
+// after the workgroup barrier
+__device__ __forceinline__ void tl_dq_end(int w, int lane, const TlRaw& R, TlStage& S) {
     const int c = lane >> 2, k = 4 * (w & 1) + (lane & 3), lr = 16 * (w >> 1) + c;
-    const uint32_t msrc = k < 4 ? q.mn03 : q.mn47;
+    const u4v h = *(const u4v*)&R.hdr[w][c][0];
+    const uint32_t msrc = k < 4 ? h.z & 0x3f3f3f3fu : ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
     S.m[k][lr] = (float)((msrc >> (8 * (k & 3))) & 63u);
-    if (k == 0) S.d[lr] = f16_bits_to_f32(q.dd & 0xffffu);
-    if (k == 1) S.dmin[lr] = f16_bits_to_f32(q.dd >> 16);
+    if (k == 0) S.d[lr] = f16_bits_to_f32(h.x & 0xffffu);
+    if (k == 1) S.dmin[lr] = f16_bits_to_f32(h.x >> 16);
 }
 
 __device__ __forceinline__ void tl_dequant(int w, int lane, const TlRaw& R, TlStage& S) {
@@ -621,17 +622,40 @@ __device__ __forceinline__ void tl_dequant(int w, int lane, const TlRaw& R, TlSt
     tl_dq_begin(w, lane, R, q);
 #pragma unroll
     for (int sg = 0; sg < 4; sg++) tl_dq_part(w, lane, sg, q, S);
-    tl_dq_end(w, lane, q, S);
+    tl_dq_end(w, lane, R, S);
 }
 
-__global__ __launch_bounds__(512) void prefill_q4k_tiled_kernel(PfArgs a, int row_tiles, int tok_tiles) {
+// Workgroup -> tile map.  Workgroup i runs on XCD i % 8 (round robin); the
+// eight XCDs form an h x v grid, XCD x taking token-tile group x % h and
+// row-tile group x / h, so each XCD reads its share of the weights once and
+// its (at most four 64-token tiles' worth of) activations stay in its L2
+// while the weight rows stream past.  Within an XCD the token tiles of one
+// row tile are consecutive, so they read its weights at about the same time.
+struct TlMap {
+    int row_tiles, tok_tiles;  // whole problem
+    int h, v;                  // XCD grid: h token groups x v row groups
+    int tg_size, rg_size;      // token / row tiles per group
+};
+
+static TlMap tl_map(int rows, int p) {
+    TlMap m;
+    m.row_tiles = (rows + kTlRows - 1) / kTlRows;
+    m.tok_tiles = (p + kTlTok - 1) / kTlTok;
+    m.h = 1;
+    while (m.h < 8 && (m.tok_tiles + m.h - 1) / m.h > 4) m.h *= 2;
+    m.v = 8 / m.h;
+    m.tg_size = (m.tok_tiles + m.h - 1) / m.h;
+    m.rg_size = (m.row_tiles + m.v - 1) / m.v;
+    return m;
+}
+
+__global__ __launch_bounds__(512) void prefill_q4k_tiled_kernel(PfArgs a, TlMap mp) {
     __shared__ __align__(16) TlStage st[2];
     __shared__ __align__(16) TlRaw raw[2];
-    // XCD-aware order: workgroups i, i + 8, ... share an XCD (and its L2);
-    // the token tiles of one row tile run there back to back.
-    const int id = blockIdx.x, xcd = id & 7, k8 = id >> 3;
-    const int rtile = (k8 / tok_tiles) * 8 + xcd, ttile = k8 % tok_tiles;
-    if (rtile >= row_tiles) return;  // whole workgroup
+    const int id = blockIdx.x, xcd = id & 7, local = id >> 3;
+    const int lt = local % mp.tg_size, lrow = local / mp.tg_size;
+    const int ttile = (xcd % mp.h) * mp.tg_size + lt, rtile = (xcd / mp.h) * mp.rg_size + lrow;
+    if (lrow >= mp.rg_size || ttile >= mp.tok_tiles || rtile >= mp.row_tiles) return;  // whole workgroup
     const int row0 = rtile * kTlRows, tok0 = ttile * kTlTok, tile0 = tok0 / 16;
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, c = lane & 15;
@@ -682,11 +706,13 @@ __global__ __launch_bounds__(512) void prefill_q4k_tiled_kernel(PfArgs a, int ro
         asm volatile("" ::: "memory");
         TlDq dq;
         tl_dq_begin(w, lane, raw[(b + 1) & 1], dq);
-        // Operands of lane k + 2 are read while lane k's chains run.  The
-        // empty asm statements pin that order: lane k's accumulators are
-        // final and lane k + 1's operands have arrived when step k ends, so
-        // three lanes' operands and one lane's products are live (more would
-        // not fit the register budget of two waves per SIMD).
+        // Software pipeline over the lanes k: step k reads lane k + 2's
+        // operands, issues lane k + 1's MFMAs and runs lane k's chains on the
+        // products issued one step earlier, so neither the LDS latency nor the
+        // MFMA latency sits in front of the chains.  The empty asm statements
+        // pin that order (lane k's accumulators final and lane k + 2's
+        // operands arrived when step k ends); without them the compiler
+        // hoists more lanes' operands than two waves per SIMD have registers for.
         struct Ops {
             h8v av, bv[2];
             f4v mk;
@@ -701,20 +727,31 @@ __global__ __launch_bounds__(512) void prefill_q4k_tiled_kernel(PfArgs a, int ro
                 o.xk[n] = S.xsum[2 * tg + n][k][c];
             }
         };
+        const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
         Ops o[3];
+        f4v dI[2][2];  // [lane k parity][token tile]
         ops(0, o[0]);
         ops(1, o[1]);
+        asm volatile("" : "+v"(o[0].av), "+v"(o[0].bv[0]), "+v"(o[0].bv[1]));
+#pragma unroll
+        for (int n = 0; n < 2; n++) dI[0][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o[0].av, o[0].bv[n], z, 0, 0, 0);
+        asm volatile("" : "+v"(o[1].av), "+v"(o[1].bv[0]), "+v"(o[1].bv[1]), "+v"(o[1].mk), "+v"(o[1].xk[0]),
+                     "+v"(o[1].xk[1]));
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             if (k < 6) ops(k + 2, o[(k + 2) % 3]);
+            if (k < 7) {
+                const Ops& nx = o[(k + 1) % 3];
+#pragma unroll
+                for (int n = 0; n < 2; n++)
+                    dI[(k + 1) & 1][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(nx.av, nx.bv[n], z, 0, 0, 0);
+            }
             const Ops& cur = o[k % 3];
 #pragma unroll
             for (int n = 0; n < 2; n++) {
-                const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
-                const f4v dI = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.av, cur.bv[n], z, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    accF[n][k][i] = fmaf(dI[i], dxs[n][i], accF[n][k][i]);
+                    accF[n][k][i] = fmaf(dI[k & 1][n][i], dxs[n][i], accF[n][k][i]);
                     const float mx = cur.mk[i] * cur.xk[n];
                     accM[n][k][i] = fmaf(dm[i], mx, accM[n][k][i]);
                 }
@@ -725,13 +762,13 @@ __global__ __launch_bounds__(512) void prefill_q4k_tiled_kernel(PfArgs a, int ro
                 asm volatile("" : "+v"(accF[n][k][0]), "+v"(accF[n][k][1]), "+v"(accF[n][k][2]),
                              "+v"(accF[n][k][3]), "+v"(accM[n][k][0]), "+v"(accM[n][k][1]),
                              "+v"(accM[n][k][2]), "+v"(accM[n][k][3]));
-            if (k < 7) {
-                Ops& nx = o[(k + 1) % 3];
+            if (k < 6) {
+                Ops& nx = o[(k + 2) % 3];
                 asm volatile("" : "+v"(nx.av), "+v"(nx.bv[0]), "+v"(nx.bv[1]), "+v"(nx.mk),
                              "+v"(nx.xk[0]), "+v"(nx.xk[1]));
             }
         }
-        tl_dq_end(w, lane, dq, st[(b + 1) & 1]);
+        tl_dq_end(w, lane, raw[(b + 1) & 1], st[(b + 1) & 1]);
         wait_vmem_le<2>();  // token operands of b + 1
         wait_lgkm0();
         lds_barrier();
@@ -763,14 +800,15 @@ static bool q4k_tiled_on() {
     return on;
 }
 
-// Workgroup shape: 64 rows x 32 tokens for real prefill batches, 64 rows x 16
-// tokens for at most 16 activation rows (a decode batch).  The per-block
-// staging (q8 to f16, scale decoding) is a fixed cost per workgroup, so 64
-// rows per workgroup beat smaller tiles that would fill more CUs (measured
-// at batch 8: 22.8 vs 28.4 us for 14336 x 4096, 58.8 vs 72.3 us for
-// 4096 x 14336).
-// Batches of at most 16 rows take prefill_q4k_b16_kernel unless
-// GLLM_Q4K_B16=0 (the 64-row tile kernel, for measurement; same bits).
+// Kernel choice.  More than 16 activation rows: the 64 x 64 staged tile
+// (prefill_q4k_tiled_kernel; GLLM_Q4K_TILED=0 selects the older 64 rows x 32
+// tokens kernel, for measurement, same bits).  At most 16 rows (a decode
+// batch): 64 rows x 16 tokens; the per-block staging (q8 to f16, scale
+// decoding) is a fixed cost per workgroup, so 64 rows per workgroup beat
+// smaller tiles that would fill more CUs (measured at batch 8: 22.8 vs 28.4
+// us for 14336 x 4096), except where 64-row tiles leave a third of the CUs
+// idle: there prefill_q4k_b16_kernel (16-row tiles) runs unless
+// GLLM_Q4K_B16=0.
 static bool q4k_b16_on() {
     static const bool on = [] {
         const char* e = getenv("GLLM_Q4K_B16");
@@ -784,9 +822,9 @@ int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const A
     if (rows <= 0 || blocks <= 0 || p <= 0) return GLLM_OK;
     PfArgs a{d_w, rb, rows, blocks, act, p, out, out_stride};
     if (p > kTiledMinP && act.b16t && q4k_tiled_on() && (size_t)rows * rb < ((size_t)1 << 32)) {
-        const int rt = (rows + kTlRows - 1) / kTlRows, tt = (p + kTlTok - 1) / kTlTok;
-        const int grid = (rt + 7) / 8 * 8 * tt;
-        hipLaunchKernelGGL(prefill_q4k_tiled_kernel, dim3(grid), dim3(512), 0, s, a, rt, tt);
+        const TlMap mp = tl_map(rows, p);
+        const int grid = 8 * mp.tg_size * mp.rg_size;
+        hipLaunchKernelGGL(prefill_q4k_tiled_kernel, dim3(grid), dim3(512), 0, s, a, mp);
     } else if (p > 16) {
         launch_pf<4, 2>(a, s);
     } else if (q4k_b16_on() && (rows + 63) / 64 < 2 * device_cus() / 3) {
