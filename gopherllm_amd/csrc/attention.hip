@@ -163,7 +163,10 @@ constexpr int kFusedHD = 128;
 constexpr int kScoreChunk = 64;   // positions per scores workgroup
 constexpr int kVTile = 64;        // positions per staged V tile (16 KB)
 constexpr int kVPrefetch = 4;     // tiles in flight per thread (registers)
-constexpr int kSmaxSpan = 6144;   // longest span the softmax/values kernel keeps in LDS (< 64 KB)
+constexpr int kSmaxSpan = 6144;   // longest span the softmax/values kernel keeps in LDS, several tokens
+// One token (four workgroups per head, 32-element slices): the score row and
+// two V tiles fit the 160 KB of LDS a gfx950 workgroup may use up to here.
+constexpr int kSmaxSpan1 = 36864;
 
 // RoPE for one decode token folded into the scores launch (rope != null,
 // one token, position `end` read from d_end): applyPreparedRope on q
@@ -784,7 +787,7 @@ __global__ __launch_bounds__(256) void attn_merge2_kernel(const float* __restric
 // start .. end0 + t.  d_q / d_out: [p][n_heads][hd].
 bool attend_exact_graphable(const gllm_hip_kv* kv, int n_heads, int n_kv, int hd, int span_cap) {
     return hd == kFusedHD && n_heads / n_kv <= 4 && kv->kv_dim_k == kv->kv_dim_v &&
-           span_cap <= kSmaxSpan;
+           span_cap <= kSmaxSpan1;
 }
 
 // scratch: p * n_heads * span_max floats of device memory, or null for the
@@ -808,7 +811,8 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
     if (rope_sin && (!d_end || !d_knew || !d_vnew))
         return fail(GLLM_EINVAL, "attend: RoPE folding needs one token and its raw k / v rows");
     const AttnRope rope{rope_sin, rope_cos, d_knew, d_vnew, kv->k[l], kv->v[l], rope_cur};
-    if (hd == kFusedHD && kvmul <= 4 && kv->kv_dim_k == kv->kv_dim_v && span_max <= kSmaxSpan) {
+    if (hd == kFusedHD && kvmul <= 4 && kv->kv_dim_k == kv->kv_dim_v &&
+        span_max <= (p == 1 ? kSmaxSpan1 : kSmaxSpan)) {
         float* sc = scratch ? scratch
                             : (float*)thread_scratch(5, (size_t)p * n_heads * span_max * 4 + 256, s);
         if (!sc) return scratch_error();
@@ -820,6 +824,18 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
         // one token: four workgroups per head (a quarter of each V row apiece);
         // prefill tokens already give n_heads * p workgroups
         if (p == 1) {
+            static const bool lds_ok = [] {
+                // dynamic LDS beyond 64 KB for long rows
+                return hipFuncSetAttribute((const void*)attn_softmax_values_kernel<4>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)smax_lds_bytes<4>(kSmaxSpan1)) == hipSuccess;
+            }();
+            if (!lds_ok) {
+                (void)hipGetLastError();
+                if (smax_lds_bytes<4>(span_max) > 65536)
+                    return fail(GLLM_EDEVICE, "attend: %zu bytes of LDS not available",
+                                smax_lds_bytes<4>(span_max));
+            }
             hipLaunchKernelGGL(attn_softmax_values_kernel<4>, dim3(n_heads * 4, p), dim3(256),
                                smax_lds_bytes<4>(span_max), s, sc, kv->v[l], kv->kv_dim_v, kvmul,
                                start, span0, span_max, d_out, d_end);
