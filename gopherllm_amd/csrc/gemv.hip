@@ -53,6 +53,7 @@ struct GemvJob {
     int rows_per_wg;  // rows per workgroup: blockDim.x / (8 * G)
     int tok0;         // first activation row of this launch
     int ntok;         // activation rows in this launch (<= NT)
+    int sa;           // batch Q6_K / Q8_0: the launch's activations are staged in dynamic LDS
     // RMSNorm prologue (batch-1 Q4_K with xf): x = rmsNormInto(fma(res, 1,
     // xf), nw) computed in the kernel; res may be null; workgroup 0 writes
     // fma(res, 1, xf) to xout when xout is set
@@ -673,6 +674,37 @@ __global__ __launch_bounds__(256) void gemv_q4k_any_kernel(GemvJob j) {
             j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
     }
 }
+// Batch launches of the Q6_K / Q8_0 row kernels (j.sa): the launch's ntok
+// activation rows (q8, xscale and, for Q6_K, xs16) are copied into dynamic
+// LDS once per workgroup, so the per-token operands of every block come from
+// LDS instead of ntok rounds of global loads per block.  Layout: q8 [ntok][cols],
+// then xscale [ntok][B], then xs16 [ntok][cols / 16], each 16-byte aligned.
+struct StagedAct {
+    const int8_t* q8;
+    const float* xsc;
+    const float* xs16;
+};
+
+__host__ __device__ inline size_t staged_act_bytes(int ntok, int cols, bool xs16) {
+    const size_t q = (size_t)ntok * cols, x = ((size_t)ntok * (cols / 256) * 4 + 15) & ~(size_t)15;
+    return q + x + (xs16 ? (size_t)ntok * (cols / 16) * 4 : 0);
+}
+
+__device__ __forceinline__ StagedAct stage_act(const GemvJob& j, uint8_t* lds, bool xs16) {
+    const int B = j.blocks, nt = j.ntok, tid = threadIdx.x;
+    const size_t nq = (size_t)nt * j.cols, nx = ((size_t)nt * B * 4 + 15) & ~(size_t)15;
+    const uint4* q = (const uint4*)(j.act.q8perm + (size_t)j.tok0 * j.cols);
+    for (size_t i = tid; i < nq / 16; i += 256) ((uint4*)lds)[i] = q[i];
+    const float* xsc = j.act.xscale + (size_t)j.tok0 * B;
+    for (int i = tid; i < nt * B; i += 256) ((float*)(lds + nq))[i] = xsc[i];
+    if (xs16) {
+        const uint4* x = (const uint4*)(j.act.xs16 + (size_t)j.tok0 * (j.cols / 16));
+        for (int i = tid; i < nt * j.cols / 64; i += 256) ((uint4*)(lds + nq + nx))[i] = x[i];
+    }
+    __syncthreads();
+    return StagedAct{(const int8_t*)lds, (const float*)(lds + nq), (const float*)(lds + nq + nx)};
+}
+
 // ---------------------------------------------------------------------------
 // Q6_K, repacked at upload: per row, B blocks of 208 bytes
 // [ql 128][qh 64][int8 scales 16] followed by B f16 d values.  AVX2 lane k
@@ -697,11 +729,15 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
     constexpr int D = kQ6Depth<NT>;
     __shared__ __attribute__((aligned(16))) uint8_t fa_raw[FUSE ? sizeof(FusedAct) : 16];
     FusedAct& fa = *(FusedAct*)fa_raw;
+    extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
     int wi;
     const int tid = threadIdx.x;
     const int gi = tid % G, k = (tid / G) & 7;
     const int r = locate(j, blockIdx.x, &wi) + tid / (8 * G);
-    if (!FUSE && r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    const bool sa = NT > 1 && j.sa;  // uniform
+    if (!FUSE && !sa && r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    StagedAct st{};
+    if (sa) st = stage_act(j, dyn_lds, true);  // every thread, then lanes past the last row idle
     const bool live = r < j.rows[wi];
     const int B = j.blocks, NB = B / G;
     const uint8_t* row = j.w[wi] + (size_t)(live ? r : j.rows[wi] - 1) * j.rb;
@@ -785,9 +821,10 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
             if (NT == 1 || t < j.ntok) {
-                const int4 qa = NT == 1 ? o.qa : *(const int4*)(q8 + (size_t)t * j.cols + b * 256);
-                const int4 qb =
-                    NT == 1 ? o.qb : *(const int4*)(q8 + (size_t)t * j.cols + b * 256 + 16);
+                const int8_t* q8t = sa ? st.q8 + (size_t)t * j.cols + b * 256 + k * 32
+                                       : q8 + (size_t)t * j.cols + b * 256;
+                const int4 qa = NT == 1 ? o.qa : *(const int4*)q8t;
+                const int4 qb = NT == 1 ? o.qb : *(const int4*)(q8t + 16);
                 int acc = scl[0] * sdot4(code[0], qa.x, 0);
                 acc += scl[1] * sdot4(code[1], qa.y, 0);
                 acc += scl[2] * sdot4(code[2], qa.z, 0);
@@ -796,10 +833,12 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
                 acc += scl[5] * sdot4(code[5], qb.y, 0);
                 acc += scl[6] * sdot4(code[6], qb.z, 0);
                 acc += scl[7] * sdot4(code[7], qb.w, 0);
-                const float* xs = xs16 + (size_t)t * (j.cols / 16) + b * 16;
+                const float* xs = sa ? st.xs16 + (size_t)t * (j.cols / 16) + b * 16 + k
+                                     : xs16 + (size_t)t * (j.cols / 16) + b * 16;
                 float o2 = sk * (NT == 1 ? o.x0 : xs[0] * 32.0f);       // VMULPS
                 o2 = fmaf(sk8, NT == 1 ? o.x8 : xs[8] * 32.0f, o2);     // VFMADD231PS
-                const float dxs = d * (NT == 1 ? o.xs : xsc[(size_t)t * B + b]);  // VMULSS
+                const float xv = sa ? st.xsc[t * B + b] : xsc[(size_t)t * B + b];
+                const float dxs = d * (NT == 1 ? o.xs : xv);  // VMULSS
                 const float iv = (float)acc;
 #pragma unroll
                 for (int step = 0; step < G; step++) {
@@ -865,11 +904,15 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(GemvJob j) {
     constexpr int D = kQ8Depth<NT>;
     __shared__ __attribute__((aligned(16))) uint8_t fa_raw[FUSE ? sizeof(FusedAct) : 16];
     FusedAct& fa = *(FusedAct*)fa_raw;
+    extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
     int wi;
     const int tid = threadIdx.x;
     const int gi = tid % G, k = (tid / G) & 7;
     const int r = locate(j, blockIdx.x, &wi) + tid / (8 * G);
-    if (!FUSE && r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    const bool sa = NT > 1 && j.sa;  // uniform
+    if (!FUSE && !sa && r >= j.rows[wi]) return;  // whole rows: the rotation and tree stay inside one row
+    StagedAct st{};
+    if (sa) st = stage_act(j, dyn_lds, false);  // every thread, then lanes past the last row idle
     const bool live = r < j.rows[wi];
     const int B = j.blocks, NB = B / G;
     const uint8_t* row = j.w[wi] + (size_t)(live ? r : j.rows[wi] - 1) * j.rb;
@@ -925,14 +968,15 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(GemvJob j) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
             if (NT == 1 || t < j.ntok) {
-                const int4 qa = NT == 1 ? o.qa : *(const int4*)(q8 + (size_t)t * j.cols + b * 256);
-                const int4 qb =
-                    NT == 1 ? o.qb : *(const int4*)(q8 + (size_t)t * j.cols + b * 256 + 16);
+                const int8_t* q8t = sa ? st.q8 + (size_t)t * j.cols + b * 256 + k * 32
+                                       : q8 + (size_t)t * j.cols + b * 256;
+                const int4 qa = NT == 1 ? o.qa : *(const int4*)q8t;
+                const int4 qb = NT == 1 ? o.qb : *(const int4*)(q8t + 16);
                 const int xq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
                 float acc12 = 0.0f;
 #pragma unroll
                 for (int q = 0; q < 8; q++) acc12 = fmaf((float)sdot4(o.wv[q], xq[q], 0), dj[q], acc12);
-                const float xs = NT == 1 ? o.xs : xsc[(size_t)t * B + b];
+                const float xs = NT == 1 ? o.xs : sa ? st.xsc[t * B + b] : xsc[(size_t)t * B + b];
 #pragma unroll
                 for (int step = 0; step < G; step++) acc11[t] = fmaf(acc12, xs, rot_prev<G>(acc11[t]));
             }
@@ -1362,6 +1406,24 @@ static void (*fmt_kernel(int g))(GemvJob) {
                       gemv_fmt_kernel<F, NT, 4, FUSE>);
 }
 
+// Dynamic LDS of the staged batch activations: up to the 160 KB a gfx950
+// workgroup may use, after a one-time opt-in per kernel.
+constexpr size_t kStagedActMax = 160 * 1024 - 64;
+static bool lds_opt_in(const void* kern) {
+    static std::mutex mu;
+    static std::vector<const void*> done;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const void* d : done)
+        if (d == kern) return true;
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStagedActMax) !=
+        hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    done.push_back(kern);
+    return true;
+}
+
 // The Q6_K, Q8_0 and other-format row kernel for this type, batch tile NT
 // and G; FUSE selects the variant that quantises x itself.
 template <int NT, bool FUSE>
@@ -1409,7 +1471,17 @@ int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t 
     if constexpr (NT == 1) {
         if (j.xf) kern = row_kernel<1, true>(type, g);
     }
-    hipLaunchKernelGGL(kern, dim3(wg), dim3(256), 0, s, j);
+    size_t lds = 0;
+    j.sa = 0;
+    if (NT > 1 && (type == GLLM_TYPE_Q6_K || type == GLLM_TYPE_Q8_0)) {
+        lds = staged_act_bytes(j.ntok, j.cols, type == GLLM_TYPE_Q6_K);
+        if (lds <= kStagedActMax && lds_opt_in((const void*)kern)) {
+            j.sa = 1;
+        } else {
+            lds = 0;
+        }
+    }
+    hipLaunchKernelGGL(kern, dim3(wg), dim3(256), lds, s, j);
     GLLM_HIP(hipGetLastError());
     return GLLM_OK;
 }
