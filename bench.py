@@ -350,7 +350,8 @@ def suite(args):
 
     g.load()
     qnames = {g.TYPE_Q4_K: "Q4_K", g.TYPE_Q6_K: "Q6_K", g.TYPE_Q8_0: "Q8_0"}
-    only = set(args.only.split(",")) if args.only else {"gemv", "formats", "prefill", "attention"}
+    only = set(args.only.split(",")) if args.only else {"gemv", "formats", "groups", "prefill",
+                                                        "attention"}
 
     def graph_time(body, reps):
         graph = timed_graph(torch, body, 1)
@@ -439,6 +440,32 @@ def suite(args):
                               "batch": p, "us": round(us, 3), "GB_s": round(nbytes / us / 1e3, 1),
                               "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
         del ws
+
+    # same-type fused groups of the float-kernel formats (matvecSameType2/3Into):
+    # the gate/up pair and the Q/K/V triple of the 8B shape, batch 1
+    for qtype, name in ((g.TYPE_Q8_0, "Q8_0"),) if "groups" in only else ():
+        for shapes in (((14336, 4096), (14336, 4096)), ((4096, 4096), (1024, 4096), (1024, 4096))):
+            copies = []
+            nbytes = 0
+            for rows, cols in shapes:
+                ws, wb = weights_for(qtype, rows, cols, min_bytes=100e6)
+                copies.append(ws)
+                nbytes += wb
+            x = torch.empty((1, 4096), dtype=torch.float32, device="cuda")
+            g.fill_normal_dev(x, 7, 1.0)
+            outs = [torch.empty((1, r), dtype=torch.float32, device="cuda") for r, _ in shapes]
+            nc = min(len(c) for c in copies)
+
+            def body():
+                for i in range(nc):
+                    g.matvec_multi_dev([c[i] for c in copies], x, outs)
+
+            us = graph_time(body, 20) / nc
+            print(json.dumps({"suite": "same-type group (float kernels)", "type": name,
+                              "rows": [r for r, _ in shapes], "cols": 4096, "us": round(us, 2),
+                              "GB_s": round(nbytes / us / 1e3, 1),
+                              "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
+            del copies
 
     for rows, cols in ((4096, 4096), (14336, 4096)) if "prefill" in only else ():
         ws, wb = weights_for(g.TYPE_Q4_K, rows, cols, min_bytes=0)
@@ -777,7 +804,7 @@ def main():
     ap.add_argument("--suite", action="store_true",
                     help="measure the other configs (GEMV types/shapes/batch 8, prefill, attention)")
     ap.add_argument("--only", default="",
-                    help="suite parts to run: comma list of gemv, formats, prefill, attention")
+                    help="suite parts to run: comma list of gemv, formats, groups, prefill, attention")
     ap.add_argument("--ctx", type=int, default=0, help="suite attention: only this context")
     ap.add_argument("--profile-run", action="store_true",
                     help="eager launches for rocprofv3 counter collection")

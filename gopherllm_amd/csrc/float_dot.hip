@@ -42,38 +42,70 @@ __device__ __forceinline__ float mxfp4_value(uint32_t code) {
     return (code & 8) ? -mag : mag;
 }
 
+// Q8_0 and Q4_0 terms read their bytes as dwords of the device layout:
+// Q8_0 groups of 8 blocks are [8 x f16 d][lane k: the dword of elements
+// 4k .. 4k + 3 of blocks q = 0..7 at 16 + 32k + 4q], Q4_0 groups [8 x f16 d]
+// [dword kk of blocks g = 0..7 at 16 + 32kk + 4g].  DotQ8_0F32: four lane
+// sums over i = 0, 8, 16, 24 of q[i + j] x[i + j] then q[i + 4 + j] x[i + 4 +
+// j]; DotQ4_0F32: four lane sums of (lo x[i + j] + hi x[16 + i + j]) over
+// i = 0, 4, 8, 12; then scale * ((s0 + s1) + (s2 + s3)), unfused.
+struct XSlice {  // the 32 activations of one 32-element unit
+    float4 v[8];
+};
+__device__ __forceinline__ XSlice fd_xslice(const float* __restrict__ x, int u) {
+    XSlice r;
+    const float4* xb = (const float4*)(x + (size_t)u * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.v[i] = xb[i];
+    return r;
+}
+
+__device__ __forceinline__ float fd_term_q8_0(const uint8_t* row, const XSlice& xsl, int u) {
+    const uint8_t* grp = row + (size_t)(u >> 3) * 272;
+    const int q = u & 7;
+    const float scale = f16_bits_to_f32(*(const uint16_t*)(grp + 2 * q));
+    uint32_t dw[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) dw[k] = *(const uint32_t*)(grp + 16 + 32 * k + 4 * q);
+    const float4* xb = xsl.v;
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const float4 xa = xb[2 * m], xc = xb[2 * m + 1];
+        const float va[4] = {xa.x, xa.y, xa.z, xa.w}, vc[4] = {xc.x, xc.y, xc.z, xc.w};
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) s[jj] = s[jj] + (float)(int8_t)(dw[2 * m] >> (8 * jj)) * va[jj];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) s[jj] = s[jj] + (float)(int8_t)(dw[2 * m + 1] >> (8 * jj)) * vc[jj];
+    }
+    return scale * ((s[0] + s[1]) + (s[2] + s[3]));
+}
+
+__device__ __forceinline__ float fd_term_q4_0(const uint8_t* row, const XSlice& xsl, int u) {
+    const uint8_t* grp = row + (size_t)(u >> 3) * 144;
+    const int gb = u & 7;
+    const float scale = f16_bits_to_f32(*(const uint16_t*)(grp + 2 * gb));
+    const float4* xb = xsl.v;
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+        const uint32_t p4 = *(const uint32_t*)(grp + 16 + 32 * kk + 4 * gb);
+        const float4 xl = xb[kk], xh = xb[4 + kk];
+        const float vl[4] = {xl.x, xl.y, xl.z, xl.w}, vh[4] = {xh.x, xh.y, xh.z, xh.w};
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            const uint32_t p = p4 >> (8 * jj);
+            const float lo = (float)((int)(p & 15) - 8), hi = (float)((int)((p >> 4) & 15) - 8);
+            s[jj] = s[jj] + (lo * vl[jj] + hi * vh[jj]);
+        }
+    }
+    return scale * ((s[0] + s[1]) + (s[2] + s[3]));
+}
+
 // The term of unit u of one row (reference offsets o, device row `row`).
 __device__ float fd_term(const uint8_t* row, int type, int B, const float* __restrict__ x, int u) {
-    if (type == GLLM_TYPE_Q8_0) {
-        const size_t base = (size_t)u * 34;
-        const float scale = fd_f16(row, type, base, B);
-        const float* xb = x + (size_t)u * 32;
-        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int i = 0; i < 32; i += 8) {
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                s[j] = s[j] + (float)(int8_t)fd_byte(row, type, base + 2 + i + j, B) * xb[i + j];
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                s[j] = s[j] + (float)(int8_t)fd_byte(row, type, base + 2 + i + 4 + j, B) * xb[i + 4 + j];
-        }
-        return scale * ((s[0] + s[1]) + (s[2] + s[3]));
-    }
-    if (type == GLLM_TYPE_Q4_0) {
-        const size_t base = (size_t)u * 18;
-        const float scale = fd_f16(row, type, base, B);
-        const float* xb = x + (size_t)u * 32;
-        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int i = 0; i < 16; i += 4) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t p = fd_byte(row, type, base + 2 + i + j, B);
-                const float lo = (float)((int)(p & 15) - 8), hi = (float)((int)((p >> 4) & 15) - 8);
-                s[j] = s[j] + (lo * xb[i + j] + hi * xb[16 + i + j]);
-            }
-        }
-        return scale * ((s[0] + s[1]) + (s[2] + s[3]));
-    }
+    if (type == GLLM_TYPE_Q8_0) return fd_term_q8_0(row, fd_xslice(x, u), u);
+    if (type == GLLM_TYPE_Q4_0) return fd_term_q4_0(row, fd_xslice(x, u), u);
     if (type == GLLM_TYPE_Q4_1) {
         const size_t base = (size_t)u * 20;
         const float d = fd_f16(row, type, base, B), m = fd_f16(row, type, base + 2, B);
@@ -195,6 +227,43 @@ __global__ __launch_bounds__(kFdThreads) void float_dot_kernel(FdJob j, const fl
     if ((int)threadIdx.x < nr) j.out[wi][r0 + threadIdx.x] = sum;
 }
 
+// Q8_0 / Q4_0 (32-element units): thread (unit u, row subgroup) loads its
+// unit's activations once and computes that unit's term for every
+// rows-per-workgroup / subgroups-th row; the terms of a row sit kFdPad floats
+// apart so the serial per-row sums (thread per row) read distinct banks.
+constexpr int kFdPad = 1;
+
+template <int TYPE>
+__global__ __launch_bounds__(kFdThreads) void float_dot_u32_kernel(FdJob j, const float* __restrict__ x) {
+    __shared__ float terms[kFdLdsTerms];
+    const int wi = blockIdx.y, tid = threadIdx.x;
+    const int r0 = blockIdx.x * j.rows_per_wg;
+    const int nr = min(j.rows_per_wg, j.rows[wi] - r0);
+    if (nr <= 0) return;  // uniform
+    const uint8_t* w = j.w[wi] + (size_t)r0 * j.rb;
+    const int U = j.chunk, ld = U + kFdPad, RG = kFdThreads / U;
+    const int u = tid % U, rs = tid / U;
+    float sum = 0.0f;
+    for (int u0 = 0; u0 < j.units; u0 += U) {
+        const int cu = min(U, j.units - u0);
+        if (rs < RG && u < cu) {
+            const XSlice xsl = fd_xslice(x, u0 + u);
+            for (int rr = rs; rr < nr; rr += RG) {
+                const uint8_t* row = w + (size_t)rr * j.rb;
+                terms[rr * ld + u] = TYPE == GLLM_TYPE_Q8_0 ? fd_term_q8_0(row, xsl, u0 + u)
+                                                            : fd_term_q4_0(row, xsl, u0 + u);
+            }
+        }
+        __syncthreads();
+        if (tid < nr) {
+            const float* tr = terms + tid * ld;
+            for (int uu = 0; uu < cu; uu++) sum = sum + tr[uu];
+        }
+        __syncthreads();
+    }
+    if (tid < nr) j.out[wi][r0 + tid] = sum;
+}
+
 bool float_dot_type(int t) {
     return t == GLLM_TYPE_Q8_0 || t == GLLM_TYPE_Q4_0 || t == GLLM_TYPE_Q4_1 ||
            t == GLLM_TYPE_Q2_K || t == GLLM_TYPE_Q3_K || t == GLLM_TYPE_Q5_K ||
@@ -224,6 +293,19 @@ int launch_float_dot(int n, gllm_hip_weight* const* ws, const float* d_x, float*
         j.out[i] = outs[i];
         j.rows[i] = ws[i]->rows;
         max_rows = std::max(max_rows, ws[i]->rows);
+    }
+    if (j.type == GLLM_TYPE_Q8_0 || j.type == GLLM_TYPE_Q4_0) {
+        // one unit per thread (at most 256 at a time), rows by subgroups
+        j.chunk = std::min(j.units, kFdThreads);
+        j.rows_per_wg = std::max(1, std::min(kFdLdsTerms / (j.chunk + kFdPad),
+                                             (total + 1023) / 1024 * (kFdThreads / j.chunk)));
+        const dim3 grid((max_rows + j.rows_per_wg - 1) / j.rows_per_wg, n);
+        if (j.type == GLLM_TYPE_Q8_0)
+            hipLaunchKernelGGL(float_dot_u32_kernel<GLLM_TYPE_Q8_0>, grid, dim3(kFdThreads), 0, s, j, d_x);
+        else
+            hipLaunchKernelGGL(float_dot_u32_kernel<GLLM_TYPE_Q4_0>, grid, dim3(kFdThreads), 0, s, j, d_x);
+        GLLM_HIP(hipGetLastError());
+        return GLLM_OK;
     }
     const dim3 grid((max_rows + j.rows_per_wg - 1) / j.rows_per_wg, n);
     hipLaunchKernelGGL(float_dot_kernel, grid, dim3(kFdThreads), 0, s, j, d_x);
