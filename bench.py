@@ -441,14 +441,34 @@ def suite(args):
                               "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
         del ws
 
+    def random_weights(qtype, rows, cols, min_bytes):
+        """Copies of one weight of a format without a device encoder: random
+        code bytes, f16 scales in 0.002..0.02 (and MXFP4 exponents near 1)."""
+        import numpy as np
+        name, bb, be, halfs, ebyte = fmt_layout[qtype]
+        rng = np.random.default_rng(qtype + rows)
+        nb = rows * cols // be
+        blk = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
+        for lo, hi in halfs:
+            blk[:, lo:hi] = rng.uniform(0.002, 0.02, nb).astype(np.float16).view(np.uint8).reshape(nb, 2)
+        if ebyte is not None:
+            blk[:, ebyte] = rng.integers(118, 130, nb)
+        raw = blk.reshape(-1)
+        return [g.Weight.from_host(raw, qtype, rows, cols)
+                for _ in range(max(2, math.ceil(min_bytes / raw.size)))], raw.size
+
     # same-type fused groups of the float-kernel formats (matvecSameType2/3Into):
     # the gate/up pair and the Q/K/V triple of the 8B shape, batch 1
-    for qtype, name in ((g.TYPE_Q8_0, "Q8_0"),) if "groups" in only else ():
+    groups = ((g.TYPE_Q8_0, "Q8_0"), (g.TYPE_Q4_0, "Q4_0"), (g.TYPE_Q5_K, "Q5_K"))
+    for qtype, name in groups if "groups" in only else ():
         for shapes in (((14336, 4096), (14336, 4096)), ((4096, 4096), (1024, 4096), (1024, 4096))):
             copies = []
             nbytes = 0
             for rows, cols in shapes:
-                ws, wb = weights_for(qtype, rows, cols, min_bytes=100e6)
+                if qtype == g.TYPE_Q8_0:
+                    ws, wb = weights_for(qtype, rows, cols, min_bytes=100e6)
+                else:
+                    ws, wb = random_weights(qtype, rows, cols, 100e6)
                 copies.append(ws)
                 nbytes += wb
             x = torch.empty((1, 4096), dtype=torch.float32, device="cuda")

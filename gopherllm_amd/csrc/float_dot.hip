@@ -102,10 +102,64 @@ __device__ __forceinline__ float fd_term_q4_0(const uint8_t* row, const XSlice& 
     return scale * ((s[0] + s[1]) + (s[2] + s[3]));
 }
 
+// Q5_K unit u = half hf of step st of block b (DotQ5KF32): d1 * qdot -
+// min1 * xsum with four lane sums over l = 0, 4, .., 28, k = 0..3.  Device
+// block: [16-byte header][lane m: nibble dwords of steps 0..3 at 16 + 16m +
+// 4 st][qh bytes at 144 ..].  xsum depends only on x, so the caller passes it.
+__device__ __forceinline__ float fd_q5k_xsum(const XSlice& xsl) {
+    float xs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const float4 xv = xsl.v[m];
+        xs[0] = xs[0] + xv.x;
+        xs[1] = xs[1] + xv.y;
+        xs[2] = xs[2] + xv.z;
+        xs[3] = xs[3] + xv.w;
+    }
+    return (xs[0] + xs[1]) + (xs[2] + xs[3]);
+}
+
+__device__ __forceinline__ float fd_term_q5k(const uint8_t* row, const XSlice& xsl, float xsum, int u) {
+    const int b = u >> 3, h = u & 7, st = h >> 1, hf = h & 1, j = h;  // j = 2 st + hf
+    const uint8_t* blk = row + (size_t)b * 176;
+    const uint4 hd = *(const uint4*)blk;
+    const uint32_t hw[4] = {hd.x, hd.y, hd.z, hd.w};
+    auto hbyte = [&](int i) { return (hw[i >> 2] >> (8 * (i & 3))) & 0xffu; };
+    int sc, mn;
+    if (j < 4) {
+        sc = (int)(hbyte(4 + j) & 63);
+        mn = (int)(hbyte(8 + j) & 63);
+    } else {
+        const uint32_t a = hbyte(8 + j);
+        sc = (int)((a & 0x0f) | ((hbyte(j) >> 6) << 4));
+        mn = (int)((a >> 4) | ((hbyte(4 + j) >> 6) << 4));
+    }
+    const float d1 = f16_bits_to_f32(hd.x & 0xffffu) * (float)sc;
+    const float min1 = f16_bits_to_f32(hd.x >> 16) * (float)mn;
+    float qd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const uint32_t nb = *(const uint32_t*)(blk + 16 + 16 * m + 4 * st);
+        const uint32_t qh = *(const uint32_t*)(blk + 144 + 4 * m);
+        const float4 xv = xsl.v[m];
+        const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+        // the four 5-bit codes of elements l .. l + 3, one per byte
+        const uint32_t code4 = ((hf ? nb >> 4 : nb) & 0x0f0f0f0fu) | (((qh >> j) & 0x01010101u) << 4);
+#pragma unroll
+        for (int k = 0; k < 4; k++) qd[k] = qd[k] + (float)((code4 >> (8 * k)) & 0xffu) * xa[k];
+    }
+    const float qdot = (qd[0] + qd[1]) + (qd[2] + qd[3]);
+    return d1 * qdot - min1 * xsum;
+}
+
 // The term of unit u of one row (reference offsets o, device row `row`).
 __device__ float fd_term(const uint8_t* row, int type, int B, const float* __restrict__ x, int u) {
     if (type == GLLM_TYPE_Q8_0) return fd_term_q8_0(row, fd_xslice(x, u), u);
     if (type == GLLM_TYPE_Q4_0) return fd_term_q4_0(row, fd_xslice(x, u), u);
+    if (type == GLLM_TYPE_Q5_K) {
+        const XSlice xsl = fd_xslice(x, u);
+        return fd_term_q5k(row, xsl, fd_q5k_xsum(xsl), u);
+    }
     if (type == GLLM_TYPE_Q4_1) {
         const size_t base = (size_t)u * 20;
         const float d = fd_f16(row, type, base, B), m = fd_f16(row, type, base + 2, B);
@@ -117,38 +171,6 @@ __device__ float fd_term(const uint8_t* row, int type, int B, const float* __res
             xsum = xsum + (xb[i] + xb[16 + i]);
         }
         return d * qdot + m * xsum;
-    }
-    if (type == GLLM_TYPE_Q5_K) {
-        // step st = h / 2 of block b, half hf: lane accumulators j = l % 4
-        const int b = u / 8, h = u % 8, st = h / 2, hf = h & 1;
-        const size_t base = (size_t)b * 176;
-        const int j = 2 * st + hf;
-        int sc, m;
-        if (j < 4) {
-            sc = (int)(fd_byte(row, type, base + 4 + j, B) & 63);
-            m = (int)(fd_byte(row, type, base + 8 + j, B) & 63);
-        } else {
-            const uint32_t a = fd_byte(row, type, base + 8 + j, B);
-            sc = (int)((a & 0x0f) | ((fd_byte(row, type, base + j, B) >> 6) << 4));
-            m = (int)((a >> 4) | ((fd_byte(row, type, base + 4 + j, B) >> 6) << 4));
-        }
-        const float d1 = fd_f16(row, type, base, B) * (float)sc;
-        const float min1 = fd_f16(row, type, base + 2, B) * (float)m;
-        const float* x1 = x + (size_t)b * 256 + 64 * st + 32 * hf;
-        float qd[4] = {0.0f, 0.0f, 0.0f, 0.0f}, xs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int l = 0; l < 32; l += 4) {
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t qb = fd_byte(row, type, base + 48 + 32 * st + l + k, B);
-                const uint32_t hb = (fd_byte(row, type, base + 16 + l + k, B) >> j) & 1;
-                const uint32_t code = (hf ? qb >> 4 : qb & 15) + 16 * hb;
-                qd[k] = qd[k] + (float)code * x1[l + k];
-                xs[k] = xs[k] + x1[l + k];
-            }
-        }
-        const float qdot = (qd[0] + qd[1]) + (qd[2] + qd[3]);
-        const float xsum = (xs[0] + xs[1]) + (xs[2] + xs[3]);
-        return d1 * qdot - min1 * xsum;
     }
     if (type == GLLM_TYPE_Q2_K || type == GLLM_TYPE_Q3_K) {
         const int b = u / 16, is = u % 16;
@@ -227,7 +249,7 @@ __global__ __launch_bounds__(kFdThreads) void float_dot_kernel(FdJob j, const fl
     if ((int)threadIdx.x < nr) j.out[wi][r0 + threadIdx.x] = sum;
 }
 
-// Q8_0 / Q4_0 (32-element units): thread (unit u, row subgroup) loads its
+// Q8_0 / Q4_0 / Q5_K (32-element units): thread (unit u, row subgroup) loads its
 // unit's activations once and computes that unit's term for every
 // rows-per-workgroup / subgroups-th row; the terms of a row sit kFdPad floats
 // apart so the serial per-row sums (thread per row) read distinct banks.
@@ -248,10 +270,12 @@ __global__ __launch_bounds__(kFdThreads) void float_dot_u32_kernel(FdJob j, cons
         const int cu = min(U, j.units - u0);
         if (rs < RG && u < cu) {
             const XSlice xsl = fd_xslice(x, u0 + u);
+            const float xsum = TYPE == GLLM_TYPE_Q5_K ? fd_q5k_xsum(xsl) : 0.0f;
             for (int rr = rs; rr < nr; rr += RG) {
                 const uint8_t* row = w + (size_t)rr * j.rb;
                 terms[rr * ld + u] = TYPE == GLLM_TYPE_Q8_0 ? fd_term_q8_0(row, xsl, u0 + u)
-                                                            : fd_term_q4_0(row, xsl, u0 + u);
+                                   : TYPE == GLLM_TYPE_Q4_0 ? fd_term_q4_0(row, xsl, u0 + u)
+                                                            : fd_term_q5k(row, xsl, xsum, u0 + u);
             }
         }
         __syncthreads();
@@ -294,7 +318,7 @@ int launch_float_dot(int n, gllm_hip_weight* const* ws, const float* d_x, float*
         j.rows[i] = ws[i]->rows;
         max_rows = std::max(max_rows, ws[i]->rows);
     }
-    if (j.type == GLLM_TYPE_Q8_0 || j.type == GLLM_TYPE_Q4_0) {
+    if (j.type == GLLM_TYPE_Q8_0 || j.type == GLLM_TYPE_Q4_0 || j.type == GLLM_TYPE_Q5_K) {
         // one unit per thread (at most 256 at a time), rows by subgroups
         j.chunk = std::min(j.units, kFdThreads);
         j.rows_per_wg = std::max(1, std::min(kFdLdsTerms / (j.chunk + kFdPad),
@@ -302,8 +326,10 @@ int launch_float_dot(int n, gllm_hip_weight* const* ws, const float* d_x, float*
         const dim3 grid((max_rows + j.rows_per_wg - 1) / j.rows_per_wg, n);
         if (j.type == GLLM_TYPE_Q8_0)
             hipLaunchKernelGGL(float_dot_u32_kernel<GLLM_TYPE_Q8_0>, grid, dim3(kFdThreads), 0, s, j, d_x);
-        else
+        else if (j.type == GLLM_TYPE_Q4_0)
             hipLaunchKernelGGL(float_dot_u32_kernel<GLLM_TYPE_Q4_0>, grid, dim3(kFdThreads), 0, s, j, d_x);
+        else
+            hipLaunchKernelGGL(float_dot_u32_kernel<GLLM_TYPE_Q5_K>, grid, dim3(kFdThreads), 0, s, j, d_x);
         GLLM_HIP(hipGetLastError());
         return GLLM_OK;
     }
