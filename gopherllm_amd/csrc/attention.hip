@@ -401,6 +401,212 @@ static size_t smax_lds_bytes(int span_max) {
     return ((size_t)((span_max + 3) & ~3) + 8) * 4 + 2 * (size_t)kVTile * (kFusedHD / DS) * 2;
 }
 
+// Softmax + values for one decode token, head_dim 128, KVMUL query heads per
+// kv head (the arithmetic of attn_softmax_values_kernel, so the same bits).
+// Workgroup = (kv head g, slice c of DW = 64 / KVMUL elements), 256 threads:
+//   * every thread stages part of the slice's V rows into LDS transposed,
+//     vt[e][t] (element-major, two positions per 32-bit store), and part of
+//     the KVMUL score rows into w[hh][t];
+//   * wave hh (< KVMUL) takes row hh's max (order-free) and replaces the row
+//     by fastExpF32(s - max);
+//   * wave 0 runs the KVMUL * DW value chains, lane (hh, e):
+//     out = fma(w_t, v_t, out) in position order, eight positions per
+//     ds_read_b128 of vt and two of w; lanes 64 + hh (wave 1) sum row hh's
+//     denominator in position order meanwhile; then out *= 1 / denom.
+// One workgroup holds the whole span: vt and w take (2 * DW + 4 * KVMUL)
+// bytes per position (vdec_lds_bytes).  The kv head's V rows are read by
+// 2 * KVMUL workgroups, each its own slice, once.
+constexpr int kVDecThreads = 256;
+constexpr int kVDecCh = 3;  // V items (two 16-byte loads each) per thread per chunk
+constexpr int kVDecSc = 3;  // score positions per thread and head per chunk
+__host__ __device__ constexpr int vdec_pad(int span_max) {
+    // rows of vt / w: at least span_max + 64 positions (the value chains read
+    // up to 56 past the span), 8 mod 128 so the 16 lanes' ds_read_b128 of
+    // one step fall on distinct banks
+    return (span_max + 56 + 127) / 128 * 128 + 8;
+}
+static size_t vdec_lds_bytes(int kvmul, int span_max) {
+    const size_t pad = (size_t)vdec_pad(span_max);
+    return pad * (size_t)(2 * (64 / kvmul) + 4 * kvmul) + 64;
+}
+template <int KVMUL>
+__global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
+    const float* __restrict__ scores, const uint16_t* __restrict__ V, int kv_dim, int start,
+    int span0, int span_max, float* __restrict__ out, const int* __restrict__ d_end) {
+    static_assert(KVMUL == 1 || KVMUL == 2 || KVMUL == 4, "1, 2 or 4 query heads per kv head");
+    constexpr int DW = 64 / KVMUL;    // elements per workgroup
+    constexpr int NP = DW / 8;        // 16-byte pieces per V row slice
+    constexpr int NS = kFusedHD / DW;  // slices per kv head
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int g = blockIdx.x / NS, c = blockIdx.x % NS;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pad = vdec_pad(span_max);
+    uint16_t* vt = (uint16_t*)lds;                  // [DW][pad] f16
+    float* w = lds + (size_t)DW * pad / 2;          // [KVMUL][pad]
+    float* red = w + (size_t)KVMUL * pad;           // [KVMUL] 1 / denom
+    // V slice, two positions per item: rows 2tp and 2tp + 1 of piece pc.
+    // Loads go out in unrolled chunks of kVDecCh items per thread, every
+    // address clamped to a cache row, so a chunk's loads are all in flight
+    // before the first one is used; the first chunk (and the score rows) is
+    // issued before the device-side position is read, clamped to span_max.
+    const uint16_t* Vg = V + (size_t)start * kv_dim + (size_t)g * kFusedHD + c * DW;
+    constexpr int CH = kVDecCh;
+    uint4 va[CH], vb[CH];
+    auto vload = [&](int base, int last) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < CH; k++) {
+            const int i = base + tid + k * kVDecThreads;
+            const int tp = i / NP, pc = i % NP;
+            const int t0 = min(2 * tp, last), t1 = min(2 * tp + 1, last);
+            va[k] = *(const uint4*)(Vg + (size_t)t0 * kv_dim + 8 * pc);
+            vb[k] = *(const uint4*)(Vg + (size_t)t1 * kv_dim + 8 * pc);
+        }
+    };
+    auto vstore = [&](int base, int nitems) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < CH; k++) {
+            const int i = base + tid + k * kVDecThreads;
+            if (i < nitems) {
+                const int tp = i / NP, pc = i % NP;
+                const uint32_t av[4] = {va[k].x, va[k].y, va[k].z, va[k].w};
+                const uint32_t bv[4] = {vb[k].x, vb[k].y, vb[k].z, vb[k].w};
+                uint32_t* col = (uint32_t*)(vt + (size_t)(8 * pc) * pad + 2 * tp);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const uint32_t lo = (av[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+                    const uint32_t hi = (bv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+                    col[(size_t)j * pad / 2] = lo | (hi << 16);
+                }
+            }
+        }
+    };
+    // score rows: kVDecSc positions per thread and head per chunk
+    constexpr int SC = kVDecSc;
+    const float* srow = scores + (size_t)g * KVMUL * span_max;
+    float sv[KVMUL][SC];
+    auto sload = [&](int base) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hh = 0; hh < KVMUL; hh++)
+#pragma unroll
+            for (int k = 0; k < SC; k++)
+                sv[hh][k] = srow[(size_t)hh * span_max +
+                                 min(base + tid + k * kVDecThreads, span_max - 1)];
+    };
+    auto sstore = [&](int base, int n) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hh = 0; hh < KVMUL; hh++)
+#pragma unroll
+            for (int k = 0; k < SC; k++) {
+                const int t = base + tid + k * kVDecThreads;
+                if (t < n) w[(size_t)hh * pad + t] = sv[hh][k];
+            }
+    };
+    vload(0, span_max - 1);
+    sload(0);
+    // (clamped to the rows the LDS image was sized for)
+    const int span = min(d_end ? *d_end - start + 1 : span0, span_max);
+    const int nitems = ((span + 1) >> 1) * NP;
+    vstore(0, nitems);
+    sstore(0, span);
+    for (int base = CH * kVDecThreads; base < nitems; base += CH * kVDecThreads) {
+        vload(base, span - 1);
+        vstore(base, nitems);
+    }
+    for (int base = SC * kVDecThreads; base < span; base += SC * kVDecThreads) {
+        sload(base);
+        sstore(base, span);
+    }
+    __syncthreads();
+    if (wave < KVMUL) {
+        float* wr = w + (size_t)wave * pad;
+        float m = -__int_as_float(0x7f800000);
+        for (int t = lane; t < span; t += 64) m = fmaxf(m, wr[t]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        for (int t = lane; t < span; t += 64) wr[t] = fast_exp(wr[t] - m);
+    }
+    __syncthreads();
+    const int hh = lane / DW, e = lane % DW;
+    float acc = 0.0f;
+    if (wave == 0) {
+        const uint16_t* vrow = vt + (size_t)e * pad;
+        const float* wrow = w + (size_t)hh * pad;
+        // groups of eight positions in a ring of four, three groups ahead
+        // (reads past the span stay inside the row: pad >= span_max + 64)
+        struct Grp {
+            uint4 v;
+            float4 a, b;
+        };
+        auto ld = [&](Grp& r, int t) __attribute__((always_inline)) {
+            r.v = *(const uint4*)(vrow + t);
+            r.a = *(const float4*)(wrow + t);
+            r.b = *(const float4*)(wrow + t + 4);
+        };
+        auto run = [&](const Grp& r) __attribute__((always_inline)) {
+            acc = fmaf(r.a.x, f16_bits_to_f32(r.v.x & 0xffffu), acc);
+            acc = fmaf(r.a.y, f16_bits_to_f32(r.v.x >> 16), acc);
+            acc = fmaf(r.a.z, f16_bits_to_f32(r.v.y & 0xffffu), acc);
+            acc = fmaf(r.a.w, f16_bits_to_f32(r.v.y >> 16), acc);
+            acc = fmaf(r.b.x, f16_bits_to_f32(r.v.z & 0xffffu), acc);
+            acc = fmaf(r.b.y, f16_bits_to_f32(r.v.z >> 16), acc);
+            acc = fmaf(r.b.z, f16_bits_to_f32(r.v.w & 0xffffu), acc);
+            acc = fmaf(r.b.w, f16_bits_to_f32(r.v.w >> 16), acc);
+        };
+        Grp r0, r1, r2, r3;
+        int t0 = 0;
+        ld(r0, 0);
+        ld(r1, 8);
+        ld(r2, 16);
+        for (; t0 + 32 <= span; t0 += 32) {
+            ld(r3, t0 + 24);
+            __builtin_amdgcn_sched_barrier(0);
+            run(r0);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(r0, t0 + 32);
+            __builtin_amdgcn_sched_barrier(0);
+            run(r1);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(r1, t0 + 40);
+            __builtin_amdgcn_sched_barrier(0);
+            run(r2);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(r2, t0 + 48);
+            __builtin_amdgcn_sched_barrier(0);
+            run(r3);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // r0, r1, r2 hold groups t0, t0 + 8, t0 + 16
+        if (t0 + 8 <= span) {
+            run(r0);
+            t0 += 8;
+            if (t0 + 8 <= span) {
+                run(r1);
+                t0 += 8;
+                if (t0 + 8 <= span) {
+                    run(r2);
+                    t0 += 8;
+                }
+            }
+        }
+        for (int t = t0; t < span; t++) acc = fmaf(wrow[t], f16_bits_to_f32(vrow[t]), acc);
+    } else if (wave == 1 && lane < KVMUL) {
+        const float* wr = w + (size_t)lane * pad;
+        float denom = 0.0f;
+        int t = 0;
+        for (; t + 4 <= span; t += 4) {
+            const float4 q = *(const float4*)(wr + t);
+            denom = denom + q.x;
+            denom = denom + q.y;
+            denom = denom + q.z;
+            denom = denom + q.w;
+        }
+        for (; t < span; t++) denom = denom + wr[t];
+        red[lane] = denom > 0.0f ? 1.0f / denom : 1.0f;
+    }
+    __syncthreads();
+    if (wave == 0) out[(size_t)(g * KVMUL + hh) * kFusedHD + c * DW + e] = acc * red[hh];
+}
+
 // --- split-K path ------------------------------------------------------------
 
 constexpr int kSplitTile = 64;  // positions per tile
@@ -783,6 +989,30 @@ __global__ __launch_bounds__(256) void attn_merge2_kernel(const float* __restric
     }
 }
 
+// The one-token values kernel applies when its LDS image of the whole span
+// fits a workgroup (GLLM_ATTN_VDEC=0 keeps attn_softmax_values_kernel, for
+// measurement; both give the same bits).
+static bool vdec_usable(int kvmul, int span_max) {
+    static const bool on = [] {
+        const char* e = getenv("GLLM_ATTN_VDEC");
+        return !(e && atoi(e) == 0);
+    }();
+    if (!on || (kvmul != 1 && kvmul != 2 && kvmul != 4)) return false;
+    const size_t bytes = vdec_lds_bytes(kvmul, span_max);
+    if (bytes <= 65536) return true;
+    static const bool big_ok = [] {
+        const int cap = 160 * 1024;
+        return hipFuncSetAttribute((const void*)attn_values_dec_kernel<4>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, cap) == hipSuccess &&
+               hipFuncSetAttribute((const void*)attn_values_dec_kernel<2>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, cap) == hipSuccess &&
+               hipFuncSetAttribute((const void*)attn_values_dec_kernel<1>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, cap) == hipSuccess;
+    }();
+    if (!big_ok) (void)hipGetLastError();
+    return big_ok && bytes <= 160 * 1024;
+}
+
 // Exact attention for p consecutive query tokens: token t attends
 // start .. end0 + t.  d_q / d_out: [p][n_heads][hd].
 bool attend_exact_graphable(const gllm_hip_kv* kv, int n_heads, int n_kv, int hd, int span_cap) {
@@ -823,7 +1053,19 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
         GLLM_HIP(hipGetLastError());
         // one token: four workgroups per head (a quarter of each V row apiece);
         // prefill tokens already give n_heads * p workgroups
-        if (p == 1) {
+        if (p == 1 && vdec_usable(kvmul, span_max)) {
+            const dim3 grid(n_kv * (kFusedHD / (64 / kvmul)));
+            const size_t lds = vdec_lds_bytes(kvmul, span_max);
+            if (kvmul == 4)
+                hipLaunchKernelGGL(attn_values_dec_kernel<4>, grid, dim3(kVDecThreads), lds, s, sc,
+                                   kv->v[l], kv->kv_dim_v, start, span0, span_max, d_out, d_end);
+            else if (kvmul == 2)
+                hipLaunchKernelGGL(attn_values_dec_kernel<2>, grid, dim3(kVDecThreads), lds, s, sc,
+                                   kv->v[l], kv->kv_dim_v, start, span0, span_max, d_out, d_end);
+            else
+                hipLaunchKernelGGL(attn_values_dec_kernel<1>, grid, dim3(kVDecThreads), lds, s, sc,
+                                   kv->v[l], kv->kv_dim_v, start, span0, span_max, d_out, d_end);
+        } else if (p == 1) {
             static const bool lds_ok = [] {
                 // dynamic LDS beyond 64 KB for long rows
                 return hipFuncSetAttribute((const void*)attn_softmax_values_kernel<4>,
