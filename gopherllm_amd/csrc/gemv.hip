@@ -66,9 +66,6 @@ struct GemvJob {
     // workgroups quantises siluMulF32(out[0], out[1]) of the block into sq_act
     int* sq_cnt;
     ActQ8 sq_act;
-    // batch-1 fused quantiser: 1 = the weight prefetch is issued only after
-    // the activation loads have returned (GLLM_Q4K_XWAIT, measurement)
-    int xwait;
 };
 
 __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
@@ -411,13 +408,36 @@ __device__ __forceinline__ void norm_regs(XRegs<QB>& xr, const XRegs<QB>& wr,
     wait_lgkm0();
     lds_barrier();
     if (tid < 32) {
+        // chain 8r + k over elements 32c + 8r + k in c order, sixteen
+        // elements per batch, the next batch's reads in flight meanwhile
         float y = 0.0f;
-        for (int c = 0; c < n; c += 16 * 32) {
-            float xb[16];
+        float xa[16], xb[16];
+        if (n % 512) {  // other sizes: the same chain, one element at a time
+            for (int e = tid; e < n; e += 32) y = fmaf(xs[e], xs[e], y);
+        } else {
 #pragma unroll
-            for (int u = 0; u < 16; u++) xb[u] = xs[c + 32 * u + tid];
+            for (int u = 0; u < 16; u++) xa[u] = xs[32 * u + tid];
+            int c = 0;
+            for (; c + 1024 <= n; c += 1024) {
 #pragma unroll
-            for (int u = 0; u < 16; u++) y = fmaf(xb[u], xb[u], y);
+                for (int u = 0; u < 16; u++) xb[u] = xs[c + 512 + 32 * u + tid];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int u = 0; u < 16; u++) y = fmaf(xa[u], xa[u], y);
+                __builtin_amdgcn_sched_barrier(0);
+                if (c + 1024 < n) {
+#pragma unroll
+                    for (int u = 0; u < 16; u++) xa[u] = xs[c + 1024 + 32 * u + tid];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int u = 0; u < 16; u++) y = fmaf(xb[u], xb[u], y);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (c < n) {  // an odd number of 512-element batches: xa holds the last
+#pragma unroll
+                for (int u = 0; u < 16; u++) y = fmaf(xa[u], xa[u], y);
+            }
         }
         part[tid] = y;
     }
@@ -534,7 +554,7 @@ __device__ __forceinline__ uint4 hdr_of(uint4 v, int j) {  // j: compile-time af
 // the prefetch.  FUSE = 2 (3 with a residual) puts the RMSNorm in front of
 // the quantiser (norm_regs): the norm weights (and residual) are loaded with
 // x, the LDS for x' follows the quantised activation.
-template <int NT, int G, int NL, int D, int FUSE, bool SQ = false, bool HV = false>
+template <int NT, int G, int NL, int D, int FUSE, bool SQ = false>
 __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(GemvJob j) {
     static_assert(NL % D == 0, "prefetch depth must divide the blocks per lane");
     static_assert(!FUSE || NT == 1, "fused quantisation is batch 1 only");
@@ -562,29 +582,22 @@ __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(
         xq_load<QB>(j.xf + (size_t)j.tok0 * cols, B, xr);
         if constexpr (NORM) xq_load<QB>(j.nw, B, wr);
         if constexpr (FUSE == 3) xq_load<QB>(j.res, B, resr);
-        __builtin_amdgcn_sched_barrier(0);
-        if (j.xwait) wait_vmem_le<0>();
     } else {
         stage_act_asm<NT>(j, smem);
     }
     __builtin_amdgcn_sched_barrier(0);
-    uint4 HG[HV ? 1 : NH];
-    if constexpr (!HV) {
+    uint4 HG[NH];
 #pragma unroll
-        for (int h = 0; h < NH; h++) {
-            const int i = 8 * h + k < NL ? 8 * h + k : NL - 1;  // clamped lanes are never read
-            HG[h] = *(const uint4*)(row + q4k_hdr_off(i * G + gi));
-        }
+    for (int h = 0; h < NH; h++) {
+        const int i = 8 * h + k < NL ? 8 * h + k : NL - 1;  // clamped lanes are never read
+        HG[h] = *(const uint4*)(row + q4k_hdr_off(i * G + gi));
     }
     __builtin_amdgcn_sched_barrier(0);
     // nibble loads pinned in block order: vmcnt retires in issue order, so
-    // block i is usable as soon as its own data is in.  HV: each block's
-    // header is loaded with its nibbles (every k-lane of a row loads the same
-    // 16 bytes) instead of being broadcast from the header plane.
-    uint4 Q[D], H[HV ? D : 1];
+    // block i is usable as soon as its own data is in
+    uint4 Q[D];
 #pragma unroll
     for (int i = 0; i < D; i++) {
-        if constexpr (HV) H[i] = *(const uint4*)(row + q4k_hdr_off(i * G + gi));
         Q[i] = *(const uint4*)(lane_nib + (size_t)i * G * 128);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -595,7 +608,7 @@ __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(
         xq_store<QB, false>(xr, B, q8b, xs32b, nullptr, xscb);
         wait_lgkm0();
     } else {
-        wait_vmem_le<HV ? 2 * D : NH + D>();
+        wait_vmem_le<NH + D>();
     }
     lds_barrier();
     const MinSel ms(k);
@@ -608,13 +621,7 @@ __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(
         for (int ii = 0; ii < D; ii++) {
             const int i = i0 + ii;
             const uint4 q = Q[ii];
-            uint4 h;
-            if constexpr (HV) {
-                h = H[ii];
-                if (i0 + D < NL) H[ii] = *(const uint4*)(row + q4k_hdr_off((i + D) * G + gi));
-            } else {
-                h = hdr_of<G>(HG[i / 8], i);
-            }
+            const uint4 h = hdr_of<G>(HG[i / 8], i);
             if (i0 + D < NL) Q[ii] = *(const uint4*)(lane_nib + (size_t)(i + D) * G * 128);
             q4k_block<NT, G>(h, q, i * G + gi, k, ms, j.ntok, q8b, xs32b, xscb, cols, B, accF,
                              accM);
@@ -1261,16 +1268,6 @@ static size_t q4k_stage_bytes(int nt, int cols) {
 }
 constexpr size_t kMaxStage = 48 << 10;
 
-// GLLM_Q4K_HDR=1: per-block header loads instead of the header-plane
-// broadcast (measurement; same bits).
-static int q4k_hdr_vmem() {
-    static const int n = [] {
-        const char* e = getenv("GLLM_Q4K_HDR");
-        return e ? atoi(e) : 0;
-    }();
-    return n;
-}
-
 template <int NT, int G, int NL, int D>
 static void launch_q4k_nl(const GemvJob& j, dim3 grid, dim3 block, size_t stage, hipStream_t s) {
     if constexpr (NT == 1 && NL * G * 256 <= kFuseCols) {
@@ -1283,35 +1280,11 @@ static void launch_q4k_nl(const GemvJob& j, dim3 grid, dim3 block, size_t stage,
             return;
         }
         if (j.xf) {
-            if (NL == 16 && D == 4 && q4k_hdr_vmem())
-                hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, 1, false, true>), grid, block, stage, s, j);
-            else
-                hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, 1>), grid, block, stage, s, j);
+            hipLaunchKernelGGL((gemv_q4k_kernel<1, G, NL, D, 1>), grid, block, stage, s, j);
             return;
         }
     }
     hipLaunchKernelGGL((gemv_q4k_kernel<NT, G, NL, D, 0>), grid, block, stage, s, j);
-}
-
-// Prefetch depth of the batch-1 kernel at 16 blocks per lane (4, 8 or 16;
-// GLLM_Q4K_D overrides, for measurement; every depth gives the same bits).
-static int q4k_depth16() {
-    static const int n = [] {
-        const char* e = getenv("GLLM_Q4K_D");
-        const int v = e ? atoi(e) : 0;
-        return v == 4 || v == 8 || v == 16 ? v : 4;
-    }();
-    return n;
-}
-
-// GLLM_Q4K_XWAIT=1: fused quantiser waits for x before the weight prefetch
-// (measurement; same bits).
-static int q4k_xwait() {
-    static const int n = [] {
-        const char* e = getenv("GLLM_Q4K_XWAIT");
-        return e ? atoi(e) : 0;
-    }();
-    return n;
 }
 
 // Blocks per lane with a compiled row kernel (and its prefetch depth).
@@ -1388,7 +1361,6 @@ int launch_q4k(GemvJob& j, const int* rows, int n, const Q4KShape& sh, hipStream
         return fail(GLLM_EINVAL, "gemv: fused quantisation needs batch 1 and a compiled shape");
     // the generic kernel keeps 256-thread workgroups of 32 / G rows
     j.rows_per_wg = compiled ? sh.rows_per_wg : 32 / G;
-    j.xwait = q4k_xwait();
     int wg = 0;
     for (int i = 0; i < n; i++) {
         j.wg_begin[i] = wg;
@@ -1405,14 +1377,7 @@ int launch_q4k(GemvJob& j, const int* rows, int n, const Q4KShape& sh, hipStream
     } else if (nl == 14) {
         launch_q4k_nl<NT, G, 14, 7>(j, grid, block, stage, s);
     } else if (nl == 16) {
-        if constexpr (NT == 1) {
-            const int d = q4k_depth16();
-            if (d == 16) launch_q4k_nl<NT, G, 16, 16>(j, grid, block, stage, s);
-            else if (d == 8) launch_q4k_nl<NT, G, 16, 8>(j, grid, block, stage, s);
-            else launch_q4k_nl<NT, G, 16, 4>(j, grid, block, stage, s);
-        } else {
-            launch_q4k_nl<NT, G, 16, 4>(j, grid, block, stage, s);
-        }
+        launch_q4k_nl<NT, G, 16, 4>(j, grid, block, stage, s);
     } else {
         launch_q4k_nl<NT, G, 28, 7>(j, grid, block, stage, s);
     }
