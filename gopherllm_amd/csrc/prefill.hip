@@ -368,30 +368,37 @@ __device__ __forceinline__ void sb_scale_min(const u4v h, int j, uint32_t& sc, u
     }
 }
 
-constexpr int kSbDepth = 1;  // blocks in flight per wave (register ring; deeper measured slower)
-
-__global__ __launch_bounds__(256) void prefill_q4k_b16_kernel(PfArgs a) {
-    __shared__ __align__(16) f4v sdI[4][8][64];  // [wave][lane k][MFMA lane] products
-    __shared__ __align__(16) SbParams sp[4];
+// NW waves per workgroup (4 or 8): wave w computes the products of blocks
+// w, w + NW, ... and runs the chains of AVX2 lanes KK w .. KK w + KK - 1
+// (KK = 8 / NW); DEPTH blocks in flight per wave (register ring).
+template <int NW, int DEPTH>
+__global__ __launch_bounds__(64 * NW) void prefill_q4k_b16_kernel(PfArgs a) {
+    constexpr int KK = 8 / NW;
+    constexpr int kSbDepth = DEPTH;
+    __shared__ __align__(16) f4v sdI[NW][8][64];  // [wave][lane k][MFMA lane] products
+    __shared__ __align__(16) SbParams sp[NW];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int row0 = blockIdx.x * 16;
     const uint8_t* wrow = a.w + (size_t)min(row0 + c, a.rows - 1) * a.rb;  // A row of this lane
     const int tok = min(c, a.p - 1);                                         // B token of this lane
     const int nb = a.blocks;
-    float accF[2][4], accM[2][4];
+    float accF[KK][4], accM[KK][4];
 #pragma unroll
-    for (int kk = 0; kk < 2; kk++)
+    for (int kk = 0; kk < KK; kk++)
 #pragma unroll
         for (int i = 0; i < 4; i++) accF[kk][i] = accM[kk][i] = 0.0f;
-    // wave w's blocks w, w + 4, ...: kSbDepth of them in flight, each
+    // wave w's blocks w, w + NW, ...: kSbDepth of them in flight, each
     // refilled as soon as it is used (loads unconditional, clamped)
     SbOps ring[kSbDepth];
 #pragma unroll
-    for (int d = 0; d < kSbDepth; d++) sb_load(a, wrow, tok, g, w + 4 * d, ring[d]);
+    for (int d = 0; d < kSbDepth; d++) sb_load(a, wrow, tok, g, w + NW * d, ring[d]);
     auto group = [&](int q0, SbOps& cur) __attribute__((always_inline)) {
         const int b = q0 + w;
-        if (b < nb) {  // wave-uniform
+        // straight-line for every wave (a block past the end re-reads the
+        // last block and its products are never read), so the compiler's
+        // vmcnt waits count exactly and the ring's later blocks stay in flight
+        {
             uint32_t sc_lo, sc_hi, mn;
             sb_scale_min(cur.hdr, 2 * g, sc_lo, mn);
             sb_scale_min(cur.hdr, 2 * g + 1, sc_hi, mn);
@@ -429,13 +436,13 @@ __global__ __launch_bounds__(256) void prefill_q4k_b16_kernel(PfArgs a) {
                 }
             }
         }
-        sb_load(a, wrow, tok, g, b + 4 * kSbDepth, cur);
+        sb_load(a, wrow, tok, g, b + NW * kSbDepth, cur);
         wait_lgkm0();
         lds_barrier();
-        // the group's blocks in order: chains of lanes k = 2w, 2w + 1 for
+        // the group's blocks in order: chains of lanes k = KK w .. for
         // rows 4g + i and token c (the MFMA D layout of this lane)
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < NW; u++) {
             if (q0 + u >= nb) break;  // uniform
             const SbParams& P = sp[u];
             const f4v d4 = *(const f4v*)&P.d[4 * g];
@@ -445,8 +452,8 @@ __global__ __launch_bounds__(256) void prefill_q4k_b16_kernel(PfArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; i++) dxs[i] = d4[i] * xs;
 #pragma unroll
-            for (int kk = 0; kk < 2; kk++) {
-                const int k = 2 * w + kk;
+            for (int kk = 0; kk < KK; kk++) {
+                const int k = KK * w + kk;
                 const f4v dI = sdI[u][k][lane];
                 const f4v m4 = *(const f4v*)&P.m[k][4 * g];
                 const float xk = P.xsum[k][c];
@@ -462,16 +469,16 @@ __global__ __launch_bounds__(256) void prefill_q4k_b16_kernel(PfArgs a) {
         lds_barrier();
     };
 #pragma unroll 1
-    for (int q0 = 0; q0 < nb; q0 += 4 * kSbDepth) {
+    for (int q0 = 0; q0 < nb; q0 += NW * kSbDepth) {
 #pragma unroll
-        for (int d = 0; d < kSbDepth; d++) group(q0 + 4 * d, ring[d]);
+        for (int d = 0; d < kSbDepth; d++) group(q0 + NW * d, ring[d]);
     }
     // tree8 over the lanes k (held by the four waves) through LDS
     float* vb = (float*)&sdI[0][0][0];  // [k][MFMA lane][row i]
 #pragma unroll
-    for (int kk = 0; kk < 2; kk++)
+    for (int kk = 0; kk < KK; kk++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) vb[((2 * w + kk) * 64 + lane) * 4 + i] = accF[kk][i] - accM[kk][i];
+        for (int i = 0; i < 4; i++) vb[((KK * w + kk) * 64 + lane) * 4 + i] = accF[kk][i] - accM[kk][i];
     __syncthreads();
     if (w == 0 && c < a.p) {
 #pragma unroll
@@ -800,6 +807,208 @@ static bool q4k_tiled_on() {
     return on;
 }
 
+// --- at most 16 activation rows, operands through a per-wave LDS ring -----
+// prefill_q4k_b16_kernel's arithmetic (MFMA products of a block per wave,
+// exchanged through LDS, chains in block order), with each wave's operands
+// copied global -> LDS by the wave itself, DEPTH blocks ahead, in layouts
+// that make every MFMA operand read of a wave conflict-free:
+//   nib [lane k][row c][16 bytes]   (lane (g, c) reads dword g: consecutive)
+//   q8  [lane k][token t][32 bytes] (lane (g, c) reads 8 bytes at 8 g)
+// The copies are inline-asm global_load_lds, so their vmcnt waits are
+// explicit counts: NC copies per block, DEPTH blocks in flight.
+template <int PT>  // tokens staged per block (8 or 16)
+struct SsSlot {
+    uint8_t nib[8][16][16];
+    uint8_t hdr[16][16];
+    uint8_t q8[8][PT][32];
+    float xs32[PT][8];
+    float xs[64];  // [token]; copy lanes past the tokens land in the tail
+};
+template <int PT>
+constexpr int ss_copies() { return 2 + 1 + PT / 4 + PT / 8 + 1; }
+
+template <int PT>
+__device__ __forceinline__ void ss_copy(const PfArgs& a, int b, uint32_t slot, int lane) {
+    typedef SsSlot<PT> S;
+    b = min(b, a.blocks - 1);  // past the end: the last block again (never read)
+    const int cols = a.blocks * 256;
+    const int row0 = blockIdx.x * 16;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {  // piece 64 i + lane = (k, c)
+        const int idx = 64 * i + lane, k = idx >> 4, c = idx & 15;
+        const size_t r = (size_t)min(row0 + c, a.rows - 1);
+        lds_copy16_s(a.w, (uint32_t)(r * a.rb + q4k_nib_off(a.blocks, b) + 16 * k),
+                     slot + offsetof(S, nib) + 1024 * i);
+    }
+    {
+        const size_t r = (size_t)min(row0 + (lane >> 2), a.rows - 1);
+        lds_copy4_s(a.w, (uint32_t)(r * a.rb + q4k_hdr_off(b) + 4 * (lane & 3)), slot + offsetof(S, hdr));
+    }
+#pragma unroll
+    for (int i = 0; i < PT / 4; i++) {  // piece 64 i + lane = ((k, t), half)
+        const int idx = 64 * i + lane, h = idx & 1, t = (idx >> 1) % PT, k = (idx >> 1) / PT;
+        const size_t tok = (size_t)min(t, a.p - 1);
+        lds_copy16_s(a.act.q8perm, (uint32_t)(tok * cols + (size_t)b * 256 + 32 * k + 16 * h),
+                     slot + offsetof(S, q8) + 1024 * i);
+    }
+#pragma unroll
+    for (int i = 0; i < PT / 8; i++) {  // dword 64 i + lane = (t, k)
+        const int idx = 64 * i + lane;
+        const size_t t = (size_t)min(idx >> 3, a.p - 1);
+        lds_copy4_s(a.act.xs32, (uint32_t)((t * (cols / 32) + (size_t)b * 8 + (idx & 7)) * 4),
+                    slot + offsetof(S, xs32) + 256 * i);
+    }
+    {
+        const size_t t = (size_t)min(lane, a.p - 1);
+        lds_copy4_s(a.act.xscale, (uint32_t)((t * a.blocks + b) * 4), slot + offsetof(S, xs));
+    }
+}
+
+template <int NW, int DEPTH, int PT>
+constexpr size_t ss_lds_bytes() {
+    return sizeof(f4v) * NW * 8 * 64 + sizeof(SbParams) * NW + sizeof(SsSlot<PT>) * NW * DEPTH;
+}
+
+template <int NW, int DEPTH, int PT>
+__global__ __launch_bounds__(64 * NW) void prefill_q4k_b16s_kernel(PfArgs a) {
+    constexpr int KK = 8 / NW;
+    constexpr int NC = ss_copies<PT>();
+    typedef SsSlot<PT> S;
+    extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
+    f4v (*sdI)[8][64] = (f4v (*)[8][64])dyn;                         // [wave][lane k][MFMA lane]
+    SbParams* sp = (SbParams*)(dyn + sizeof(f4v) * NW * 8 * 64);      // [wave]
+    uint8_t* ring = dyn + sizeof(f4v) * NW * 8 * 64 + sizeof(SbParams) * NW;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, c = lane & 15;
+    const int row0 = blockIdx.x * 16;
+    const int tc = min(c, a.p - 1);  // B token of this lane
+    const int nb = a.blocks;
+    const uint32_t ring_w = lds_addr(ring + sizeof(S) * DEPTH * w);
+    float accF[KK][4], accM[KK][4];
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) accF[kk][i] = accM[kk][i] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < DEPTH; d++) ss_copy<PT>(a, w + NW * d, ring_w + sizeof(S) * d, lane);
+    int slot = 0;
+#pragma unroll 1
+    for (int q0 = 0; q0 < nb; q0 += NW) {
+        // this wave's block q0 + w is in `slot` once the later copies alone
+        // are outstanding
+        wait_vmem_le<(DEPTH - 1) * NC>();
+        const S& sl = *(const S*)(ring + sizeof(S) * (DEPTH * w + slot));
+        {
+            const u4v hdr = *(const u4v*)&sl.hdr[c][0];
+            uint32_t sc_lo, sc_hi, mn;
+            sb_scale_min(hdr, 2 * g, sc_lo, mn);
+            sb_scale_min(hdr, 2 * g + 1, sc_hi, mn);
+            const _Float16 hl = (_Float16)(float)sc_lo, nl = (_Float16)(-1024.0f * (float)sc_lo);
+            const _Float16 hh = (_Float16)(float)sc_hi, nh = (_Float16)(-1024.0f * (float)sc_hi);
+            const uint32_t bl = __builtin_bit_cast(uint16_t, hl), bnl = __builtin_bit_cast(uint16_t, nl);
+            const uint32_t bh = __builtin_bit_cast(uint16_t, hh), bnh = __builtin_bit_cast(uint16_t, nh);
+            const uint32_t sh_lo = bl | (bl << 16), sn_lo = bnl | (bnl << 16);
+            const uint32_t sh_hi = bh | (bh << 16), sn_hi = bnh | (bnh << 16);
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t wd = *(const uint32_t*)&sl.nib[k][c][4 * g];
+                const uint2 q8 = *(const uint2*)&sl.q8[k][tc][8 * g];
+                const h8v av = dequant_a(wd, sh_lo, sn_lo, sh_hi, sn_hi);
+                uint32_t v[4];
+                i8x4_to_h(q8.x, v[0], v[1]);
+                i8x4_to_h(q8.y, v[2], v[3]);
+                const h8v bv = __builtin_bit_cast(h8v, u4v{v[0], v[1], v[2], v[3]});
+                const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+                sdI[w][k][lane] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, z, 0, 0, 0);
+            }
+            if (g == 0) {
+                sp[w].d[c] = f16_bits_to_f32(hdr.x & 0xffffu);
+                sp[w].dmin[c] = f16_bits_to_f32(hdr.x >> 16);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    uint32_t scj, mnj;
+                    sb_scale_min(hdr, j, scj, mnj);
+                    sp[w].m[j][c] = (float)mnj;
+                }
+            } else if (g == 1) {
+                sp[w].xs[c] = sl.xs[tc];
+#pragma unroll
+                for (int k = 0; k < 8; k++) sp[w].xsum[k][c] = sl.xs32[tc][k];
+            }
+        }
+        // the slot's reads are done: refill it DEPTH groups ahead
+        wait_lgkm0();
+        ss_copy<PT>(a, q0 + w + NW * DEPTH, ring_w + sizeof(S) * slot, lane);
+        slot = slot + 1 == DEPTH ? 0 : slot + 1;
+        lds_barrier();
+        // the group's blocks in order: chains of lanes k = KK w .. for rows
+        // 4g + i and token c (the MFMA D layout of this lane)
+#pragma unroll
+        for (int u = 0; u < NW; u++) {
+            if (q0 + u >= nb) break;  // uniform
+            const SbParams& P = sp[u];
+            const f4v d4 = *(const f4v*)&P.d[4 * g];
+            const f4v dm4 = *(const f4v*)&P.dmin[4 * g];
+            const float xs = P.xs[c];
+            float dxs[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) dxs[i] = d4[i] * xs;
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) {
+                const int k = KK * w + kk;
+                const f4v dI = sdI[u][k][lane];
+                const f4v m4 = *(const f4v*)&P.m[k][4 * g];
+                const float xk = P.xsum[k][c];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    accF[kk][i] = fmaf(dI[i], dxs[i], accF[kk][i]);
+                    const float mx = m4[i] * xk;
+                    accM[kk][i] = fmaf(dm4[i], mx, accM[kk][i]);
+                }
+            }
+        }
+        wait_lgkm0();
+        lds_barrier();
+    }
+    wait_vmem_le<0>();  // the last refills (never read) have landed
+    // tree8 over the lanes k (held by the waves) through LDS
+    float* vb = (float*)dyn;  // [k][MFMA lane][row i]
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) vb[((KK * w + kk) * 64 + lane) * 4 + i] = accF[kk][i] - accM[kk][i];
+    __syncthreads();
+    if (w == 0 && c < a.p) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = row0 + 4 * g + i;
+            if (r >= a.rows) continue;
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = vb[(k * 64 + lane) * 4 + i];
+            const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+            a.out[(size_t)c * a.out_stride + r] = (s0 + s1) + (s2 + s3);
+        }
+    }
+}
+
+template <int NW, int DEPTH, int PT>
+static bool launch_b16s(const PfArgs& a, hipStream_t s) {
+    constexpr size_t lds = ss_lds_bytes<NW, DEPTH, PT>();
+    static_assert(lds <= 160 * 1024, "LDS");
+    static const bool ok = hipFuncSetAttribute((const void*)prefill_q4k_b16s_kernel<NW, DEPTH, PT>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)lds) == hipSuccess;
+    if (!ok) {
+        (void)hipGetLastError();
+        return false;
+    }
+    hipLaunchKernelGGL((prefill_q4k_b16s_kernel<NW, DEPTH, PT>), dim3((a.rows + 15) / 16),
+                       dim3(64 * NW), lds, s, a);
+    return true;
+}
+
 // Kernel choice.  More than 16 activation rows: the 64 x 64 staged tile
 // (prefill_q4k_tiled_kernel; GLLM_Q4K_TILED=0 selects the older 64 rows x 32
 // tokens kernel, for measurement, same bits).  At most 16 rows (a decode
@@ -817,6 +1026,16 @@ static bool q4k_b16_on() {
     return on;
 }
 
+// GLLM_Q4K_B16S=0 keeps the register-ring 16-row kernel (measurement; same
+// bits).
+static bool q4k_b16s_on() {
+    static const bool on = [] {
+        const char* e = getenv("GLLM_Q4K_B16S");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
                     float* out, int out_stride, hipStream_t s) {
     if (rows <= 0 || blocks <= 0 || p <= 0) return GLLM_OK;
@@ -828,8 +1047,16 @@ int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const A
     } else if (p > 16) {
         launch_pf<4, 2>(a, s);
     } else if (q4k_b16_on() && (rows + 63) / 64 < 2 * device_cus() / 3) {
-        // the 64-row tile leaves CUs idle: 16-row tiles, block-parallel waves
-        hipLaunchKernelGGL(prefill_q4k_b16_kernel, dim3((rows + 15) / 16), dim3(256), 0, s, a);
+        // the 64-row tile leaves CUs idle: 16-row tiles, block-parallel
+        // waves, operands through per-wave LDS
+        // rings (eight waves at up to 8 tokens, four at 9-16, as the LDS
+        // allows); the register-ring kernel where the ring kernel cannot run
+        const bool fits = (size_t)rows * rb < ((size_t)1 << 32);
+        const bool done = fits && q4k_b16s_on() &&
+                          (p <= 8 ? launch_b16s<8, 2, 8>(a, s) : launch_b16s<4, 3, 16>(a, s));
+        if (!done)
+            hipLaunchKernelGGL((prefill_q4k_b16_kernel<4, 1>), dim3((rows + 15) / 16), dim3(256), 0,
+                               s, a);
     } else {
         launch_pf<4, 1>(a, s);
     }
