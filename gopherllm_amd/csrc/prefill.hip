@@ -993,6 +993,153 @@ __global__ __launch_bounds__(64 * NW) void prefill_q4k_b16s_kernel(PfArgs a) {
     }
 }
 
+// At most 8 tokens: lane pairs.  Tile m of a block holds AVX2 lanes 2m
+// (MFMA columns 0-7, tokens 0-7) and 2m + 1 (columns 8-15): two MFMAs
+// accumulate into it, each with the other lane's B columns zero, so every
+// column is a real (lane, token) product (the exact integer I, below 2^24,
+// whatever the accumulation order).  Eight waves, wave w: the block w of each
+// group for the MFMA phase, then the chains of pair w / 2 for rows
+// 4g + 2 (w % 2) .. + 1 of each D lane.  Half the products in LDS, half the
+// chain steps and B conversions of prefill_q4k_b16s_kernel, and room for a
+// ring three blocks deep.
+template <int DEPTH>
+constexpr size_t sp_lds_bytes() {
+    return sizeof(f4v) * 8 * 4 * 64 + sizeof(SbParams) * 8 + sizeof(SsSlot<8>) * 8 * DEPTH;
+}
+template <int DEPTH>
+__global__ __launch_bounds__(512) void prefill_q4k_b16p_kernel(PfArgs a) {
+    constexpr int NW = 8;
+    constexpr int NC = ss_copies<8>();
+    typedef SsSlot<8> S;
+    extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
+    f4v (*sdI)[4][64] = (f4v (*)[4][64])dyn;                          // [block][pair][MFMA lane]
+    SbParams* sp = (SbParams*)(dyn + sizeof(f4v) * NW * 4 * 64);       // [block]
+    uint8_t* ring = dyn + sizeof(f4v) * NW * 4 * 64 + sizeof(SbParams) * NW;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, c = lane & 15;
+    const int row0 = blockIdx.x * 16;
+    const int odd = c >> 3, t = c & 7;    // this lane's B column: lane parity, token
+    const int tb = min(t, a.p - 1);      // token whose q8 this lane supplies
+    const int tc = min(c, a.p - 1);      // token of the per-token factors (columns < 8 used)
+    const int nb = a.blocks;
+    const int pm = w >> 1, ih = w & 1;   // chain phase: pair, row half
+    const uint32_t ring_w = lds_addr(ring + sizeof(S) * DEPTH * w);
+    float accF[2], accM[2];
+    accF[0] = accF[1] = accM[0] = accM[1] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < DEPTH; d++) ss_copy<8>(a, w + NW * d, ring_w + sizeof(S) * d, lane);
+    int slot = 0;
+#pragma unroll 1
+    for (int q0 = 0; q0 < nb; q0 += NW) {
+        wait_vmem_le<(DEPTH - 1) * NC>();
+        const S& sl = *(const S*)(ring + sizeof(S) * (DEPTH * w + slot));
+        {
+            const u4v hdr = *(const u4v*)&sl.hdr[c][0];
+            uint32_t sc_lo, sc_hi, mn;
+            sb_scale_min(hdr, 2 * g, sc_lo, mn);
+            sb_scale_min(hdr, 2 * g + 1, sc_hi, mn);
+            const _Float16 hl = (_Float16)(float)sc_lo, nl = (_Float16)(-1024.0f * (float)sc_lo);
+            const _Float16 hh = (_Float16)(float)sc_hi, nh = (_Float16)(-1024.0f * (float)sc_hi);
+            const uint32_t bl = __builtin_bit_cast(uint16_t, hl), bnl = __builtin_bit_cast(uint16_t, nl);
+            const uint32_t bh = __builtin_bit_cast(uint16_t, hh), bnh = __builtin_bit_cast(uint16_t, nh);
+            const uint32_t sh_lo = bl | (bl << 16), sn_lo = bnl | (bnl << 16);
+            const uint32_t sh_hi = bh | (bh << 16), sn_hi = bnh | (bnh << 16);
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const uint32_t w0 = *(const uint32_t*)&sl.nib[2 * m][c][4 * g];
+                const uint32_t w1 = *(const uint32_t*)&sl.nib[2 * m + 1][c][4 * g];
+                const uint2 q8 = *(const uint2*)&sl.q8[2 * m + odd][tb][8 * g];
+                const h8v a0 = dequant_a(w0, sh_lo, sn_lo, sh_hi, sn_hi);
+                const h8v a1 = dequant_a(w1, sh_lo, sn_lo, sh_hi, sn_hi);
+                uint32_t v[4];
+                i8x4_to_h(q8.x, v[0], v[1]);
+                i8x4_to_h(q8.y, v[2], v[3]);
+                const u4v zero = {0u, 0u, 0u, 0u};
+                const u4v bu = {v[0], v[1], v[2], v[3]};
+                const h8v b0 = __builtin_bit_cast(h8v, odd ? zero : bu);
+                const h8v b1 = __builtin_bit_cast(h8v, odd ? bu : zero);
+                const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+                f4v dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, z, 0, 0, 0);
+                dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, dd, 0, 0, 0);
+                sdI[w][m][lane] = dd;
+            }
+            if (g == 0) {
+                sp[w].d[c] = f16_bits_to_f32(hdr.x & 0xffffu);
+                sp[w].dmin[c] = f16_bits_to_f32(hdr.x >> 16);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    uint32_t scj, mnj;
+                    sb_scale_min(hdr, j, scj, mnj);
+                    sp[w].m[j][c] = (float)mnj;
+                }
+            } else if (g == 1) {
+                sp[w].xs[c] = sl.xs[tc];
+#pragma unroll
+                for (int k = 0; k < 8; k++) sp[w].xsum[k][c] = sl.xs32[tc][k];
+            }
+        }
+        wait_lgkm0();
+        ss_copy<8>(a, q0 + w + NW * DEPTH, ring_w + sizeof(S) * slot, lane);
+        slot = slot + 1 == DEPTH ? 0 : slot + 1;
+        lds_barrier();
+        // chains of pair pm, rows 4g + 2 ih + ii, lane k = 2 pm + odd, token t
+        const int k = 2 * pm + odd;
+#pragma unroll
+        for (int u = 0; u < NW; u++) {
+            if (q0 + u >= nb) break;  // uniform
+            const SbParams& P = sp[u];
+            const f4v dI = sdI[u][pm][lane];
+            const float xs = P.xs[t];
+            const float xk = P.xsum[k][t];
+#pragma unroll
+            for (int ii = 0; ii < 2; ii++) {
+                const int i = 2 * ih + ii;
+                const float dxs = P.d[4 * g + i] * xs;
+                accF[ii] = fmaf(dI[i], dxs, accF[ii]);
+                const float mx = P.m[k][4 * g + i] * xk;
+                accM[ii] = fmaf(P.dmin[4 * g + i], mx, accM[ii]);
+            }
+        }
+        wait_lgkm0();
+        lds_barrier();
+    }
+    wait_vmem_le<0>();
+    // tree8 over the lanes k through LDS: vb[k][row][token]
+    float* vb = (float*)dyn;
+#pragma unroll
+    for (int ii = 0; ii < 2; ii++)
+        vb[((2 * pm + odd) * 16 + 4 * g + 2 * ih + ii) * 8 + t] = accF[ii] - accM[ii];
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < 128) {
+        const int r = tid >> 3, tt = tid & 7;
+        if (tt < a.p && row0 + r < a.rows) {
+            float v[8];
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) v[kk] = vb[(kk * 16 + r) * 8 + tt];
+            const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+            a.out[(size_t)tt * a.out_stride + row0 + r] = (s0 + s1) + (s2 + s3);
+        }
+    }
+}
+
+template <int DEPTH>
+static bool launch_b16p(const PfArgs& a, hipStream_t s) {
+    constexpr size_t lds = sp_lds_bytes<DEPTH>();
+    static_assert(lds <= 160 * 1024, "LDS");
+    static const bool ok = hipFuncSetAttribute((const void*)prefill_q4k_b16p_kernel<DEPTH>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)lds) == hipSuccess;
+    if (!ok) {
+        (void)hipGetLastError();
+        return false;
+    }
+    hipLaunchKernelGGL((prefill_q4k_b16p_kernel<DEPTH>), dim3((a.rows + 15) / 16), dim3(512), lds,
+                       s, a);
+    return true;
+}
+
 template <int NW, int DEPTH, int PT>
 static bool launch_b16s(const PfArgs& a, hipStream_t s) {
     constexpr size_t lds = ss_lds_bytes<NW, DEPTH, PT>();
@@ -1026,6 +1173,18 @@ static bool q4k_b16_on() {
     return on;
 }
 
+// Lane-pair kernel at up to 8 tokens (GLLM_B16P=0 runs the per-lane ring
+// kernel instead, for measurement; same bits).  Batch 8, one sweep: 4096 x
+// 14336 26.2 / 25.5 / 26.9 us (per-lane ring / pairs, ring of 2 / pairs,
+// ring of 3), 4096 x 4096 11.8 / 11.3 / 12.0 us.
+static bool q4k_b16p_on() {
+    static const bool on = [] {
+        const char* e = getenv("GLLM_B16P");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 // GLLM_Q4K_B16S=0 keeps the register-ring 16-row kernel (measurement; same
 // bits).
 static bool q4k_b16s_on() {
@@ -1053,7 +1212,9 @@ int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const A
         // allows); the register-ring kernel where the ring kernel cannot run
         const bool fits = (size_t)rows * rb < ((size_t)1 << 32);
         const bool done = fits && q4k_b16s_on() &&
-                          (p <= 8 ? launch_b16s<8, 2, 8>(a, s) : launch_b16s<4, 3, 16>(a, s));
+                          (p > 8 ? launch_b16s<4, 3, 16>(a, s)
+                           : q4k_b16p_on() ? launch_b16p<2>(a, s)
+                                           : launch_b16s<8, 2, 8>(a, s));
         if (!done)
             hipLaunchKernelGGL((prefill_q4k_b16_kernel<4, 1>), dim3((rows + 15) / 16), dim3(256), 0,
                                s, a);
