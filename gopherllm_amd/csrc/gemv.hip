@@ -276,14 +276,21 @@ struct XRegs {
     float v[QB][4];
 };
 
-template <int QB>
+template <int QB, bool SKIP = false>
 __device__ __forceinline__ void xq_load(const float* __restrict__ x, int B, XRegs<QB>& xr) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int m = lane >> 3, kk = lane & 7;
 #pragma unroll
     for (int i = 0; i < QB; i++) {
         const int b = wave + nw * i;
-        const int bb = b < B ? b : B - 1;  // clamped; results of b >= B are not stored
+        // QB assumes four waves; wider workgroups own fewer blocks per wave.
+        // SKIP: blocks past the end are not loaded (a wave-uniform branch
+        // ahead of the weight prefetch, so the vmcnt waits stay exact; taken
+        // by the norm prologue, which loads three rows: decode 473 -> 480
+        // tok/s in a same-box A/B); otherwise they re-read the last block
+        // (the plain fused quantiser measured 1.5 % faster that way)
+        if (SKIP && b >= B) break;
+        const int bb = b < B ? b : B - 1;  // results of b >= B are not stored
         const float* g = x + (size_t)bb * 256 + 32 * m + kk;
 #pragma unroll
         for (int e = 0; e < 4; e++) xr.v[i][e] = g[8 * e];
@@ -579,9 +586,9 @@ __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(
     XRegs<QB> xr;
     XRegs<NORM ? QB : 1> wr, resr;
     if constexpr (FUSE) {
-        xq_load<QB>(j.xf + (size_t)j.tok0 * cols, B, xr);
-        if constexpr (NORM) xq_load<QB>(j.nw, B, wr);
-        if constexpr (FUSE == 3) xq_load<QB>(j.res, B, resr);
+        xq_load<QB, NORM>(j.xf + (size_t)j.tok0 * cols, B, xr);
+        if constexpr (NORM) xq_load<QB, true>(j.nw, B, wr);
+        if constexpr (FUSE == 3) xq_load<QB, true>(j.res, B, resr);
     } else {
         stage_act_asm<NT>(j, smem);
     }
