@@ -287,8 +287,10 @@ __device__ __forceinline__ void xq_load(const float* __restrict__ x, int B, XReg
         // SKIP: blocks past the end are not loaded (a wave-uniform branch
         // ahead of the weight prefetch, so the vmcnt waits stay exact; taken
         // by the norm prologue, which loads three rows: decode 473 -> 480
-        // tok/s in a same-box A/B); otherwise they re-read the last block
-        // (the plain fused quantiser measured 1.5 % faster that way)
+        // tok/s in a same-box A/B, and by eight-wave G = 4 launches such as
+        // the attention output projection: 482 -> 487 tok/s); otherwise they
+        // re-read the last block (the seven-wave batch-1 kernel of 14336 x
+        // 4096 measured 1.5 % faster that way)
         if (SKIP && b >= B) break;
         const int bb = b < B ? b : B - 1;  // results of b >= B are not stored
         const float* g = x + (size_t)bb * 256 + 32 * m + kk;
@@ -586,7 +588,7 @@ __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(
     XRegs<QB> xr;
     XRegs<NORM ? QB : 1> wr, resr;
     if constexpr (FUSE) {
-        xq_load<QB, NORM>(j.xf + (size_t)j.tok0 * cols, B, xr);
+        xq_load<QB, NORM || G == 4>(j.xf + (size_t)j.tok0 * cols, B, xr);
         if constexpr (NORM) xq_load<QB, true>(j.nw, B, wr);
         if constexpr (FUSE == 3) xq_load<QB, true>(j.res, B, resr);
     } else {
