@@ -190,6 +190,9 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
     const int* __restrict__ d_end, AttnRope rope) {
     __shared__ float qs[4 * kFusedHD];
     __shared__ __align__(16) uint16_t kcur[kFusedHD];
+    // the chunk's K rows, [16-byte piece][row]: copied once per workgroup
+    // (four 1 KB copies per wave), read by every head's thread of a row
+    __shared__ __align__(16) uint8_t kst[kFusedHD / 8][kScoreChunk][16];
     const int g = blockIdx.x, chunk = blockIdx.y, tok = blockIdx.z;
     const int tid = threadIdx.x;
     if (d_end) span0 = *d_end - start + 1;  // position read on the device (graph replay)
@@ -205,10 +208,14 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
     const int h = tid / kScoreChunk, t = chunk * kScoreChunk + tid % kScoreChunk;
     uint4 kr[kFusedHD / 8];
     {
-        const uint4* krow = (const uint4*)(K + (size_t)(start + min(t, span_max - 1)) * kv_dim +
-                                           (size_t)g * kFusedHD);
+        // wave wv copies pieces 4 wv .. 4 wv + 3 of the chunk's 64 rows; lane
+        // l the row chunk * 64 + l (clamped to span_max - 1, inside the cache)
+        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
+        const uint16_t* krow = K + (size_t)(start + min(chunk * kScoreChunk + l, span_max - 1)) * kv_dim +
+                               (size_t)g * kFusedHD;
 #pragma unroll
-        for (int c = 0; c < kFusedHD / 8; c++) kr[c] = krow[c];
+        for (int pc = 0; pc < 4; pc++)
+            lds_copy16(krow + 8 * (4 * wv + pc), lds_addr(&kst[4 * wv + pc][0][0]));
     }
     if (rope.sin_tab) {
         // the current position's rows: from rope.cur when the caller uploads
@@ -246,11 +253,15 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
     } else {
         for (int i = tid; i < kvmul * kFusedHD; i += 256) qs[i] = qg[i];
     }
+    wait_vmem_le<0>();  // this wave's K copies have landed
     __syncthreads();
     if (h >= kvmul || t >= span) return;
     if (has_cur && t == tcur) {
 #pragma unroll
         for (int c = 0; c < kFusedHD / 8; c++) kr[c] = *(const uint4*)&kcur[8 * c];
+    } else {
+#pragma unroll
+        for (int c = 0; c < kFusedHD / 8; c++) kr[c] = *(const uint4*)&kst[c][tid & 63][0];
     }
     const float* qh = qs + h * kFusedHD;
     float acc[8];
