@@ -223,7 +223,7 @@ static void rope_row(const gllm_hip_model_config& c, int pos, float* sn, float* 
 // Decode-step upload: [position][3 pad][sin row][cos row] (floats after the
 // first 16 bytes), so the captured step reads the current position's RoPE
 // rows without first waiting for the position.
-constexpr int kPosHeader = 4;  // 16 bytes
+constexpr int kPosHeader = 4;  // 16 bytes: the decode position, the decode token, padding
 static size_t pos_bytes(const gllm_hip_model_config& c) {
     return ((size_t)kPosHeader + (size_t)c.head_dim) * 4;
 }
@@ -284,14 +284,15 @@ static int project(gllm_hip_model* m, bool decode, int n, gllm_hip_weight* const
 // is read on the device instead, so the launches do not depend on it.
 // decode (p == 1) is a generation step, otherwise the tokens are prompt
 // tokens.
-static int forward(gllm_hip_model* m, int pos0, int p, bool decode, const int* d_pos = nullptr) {
+static int forward(gllm_hip_model* m, int pos0, int p, bool decode, const int* d_pos = nullptr,
+                   const uint32_t* d_tok = nullptr) {
     const auto& c = m->cfg;
     hipStream_t s = m->stream;
     const int hd = c.head_dim, kvd = c.n_kv_heads * hd;
     // config.AttentionScale, else float32(1/sqrt(headDim)) (model.go:2685-2688)
     const float scale = m->attn_scale != 0.0f ? m->attn_scale : (float)(1.0 / sqrt((double)hd));
     const size_t norm_lds = (size_t)c.dim * 4;
-    GLLM_TRY(launch_weight_rows(m->tok_embd, m->d_tokens, p, m->x, s));
+    GLLM_TRY(launch_weight_rows(m->tok_embd, d_tok ? d_tok : m->d_tokens, p, m->x, s));
     // the residual stream: a norm-fused launch reads X[xi] and writes the
     // updated stream to X[xi ^ 1] (its workgroups all read X[xi] first)
     float* X[2] = {m->x, m->x2};
@@ -409,7 +410,8 @@ static int model_argmax(gllm_hip_model* m, uint32_t* d_token) {
 // One greedy decode step on the token in d_tokens[0]: forward, the output
 // projection (full logits), then the (penalised) argmax into d_tokens[1].
 static int decode_step(gllm_hip_model* m, int pos, const int* d_pos) {
-    GLLM_TRY(forward(m, pos, 1, true, d_pos));
+    // the token rides in the position buffer's header (word 1): one upload
+    GLLM_TRY(forward(m, pos, 1, true, d_pos, (const uint32_t*)m->d_pos + 1));
     gllm_hip_weight* ws[1] = {m->output};
     float* outs[1] = {m->logits};
     GLLM_TRY(matvec(m, 1, ws, m->xn, 1, outs));
@@ -576,13 +578,13 @@ int gllm_hip_model_decode(gllm_hip_model* m, uint32_t token, int pos, uint32_t* 
     hipStream_t s = m->stream;
     push_recent(m, token);
     GLLM_TRY(upload_recent(m));
-    m->h_tokens[0] = token;
+    // header: position, token; then the position's RoPE rows
     m->h_pos[0] = pos;
+    m->h_pos[1] = (int)token;
     {
         float* rows = (float*)m->h_pos + kPosHeader;
         rope_row(m->cfg, pos, rows, rows + m->cfg.head_dim / 2);
     }
-    GLLM_HIP(hipMemcpyAsync(m->d_tokens, m->h_tokens, 4, hipMemcpyHostToDevice, s));
     GLLM_HIP(hipMemcpyAsync(m->d_pos, m->h_pos, pos_bytes(m->cfg), hipMemcpyHostToDevice, s));
     if (m->decode_graph) {
         GLLM_HIP(hipGraphLaunch(m->decode_graph, s));
