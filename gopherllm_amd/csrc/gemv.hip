@@ -1120,7 +1120,7 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int r) {
 // key, then one workgroup reduces the keys.  Keys compare larger for a
 // larger finite value, or the same value at a lower row, so the result is
 // the lowest-index maximum regardless of the reduction order.
-constexpr int kArgmaxChunk = 4096;
+constexpr int kArgmaxChunk = 1024;  // four logits per thread, all loads in flight together
 
 __device__ __forceinline__ unsigned long long wg_max_key(unsigned long long best) {
 #pragma unroll
@@ -1172,9 +1172,19 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
         }
         __syncthreads();
     }
+    constexpr int PER = kArgmaxChunk / 256;
+    float lv[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int i = lo + threadIdx.x + k * 256;
+        lv[k] = i < hi ? logits[i] : 0.0f;
+    }
     unsigned long long best = 0;
-    for (int i = lo + threadIdx.x; i < hi; i += 256) {
-        float v = logits[i];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int i = lo + threadIdx.x + k * 256;
+        if (i >= hi) break;
+        float v = lv[k];
         if (pen) v = repeat_penalty(v, hits[i - lo], penalty);
         if (finite_logit(v)) {
             const unsigned long long key = argmax_key(v, i);
