@@ -29,20 +29,19 @@ __device__ __forceinline__ float rw_f16_soft(uint32_t h) {
     return __uint_as_float(sign | ((e + 112) << 23) | (m << 13));
 }
 
-// scaleMinK4 (simd.go:1524-1528): 6-bit scale and min of sub-block j
+// scaleMinK4 (simd.go:1524-1528): 6-bit scale and min of sub-block j.  The
+// bytes j % 4, j % 4 + 4 and j % 4 + 8 of the 12 scale bytes hold both
+// cases, so all three are read and the case is a select, not a branch.
 __device__ __forceinline__ void rw_scale_min(const uint8_t* row, int type, size_t q, int B, int j,
                                              int* sc, int* m) {
-    if (j < 4) {
-        *sc = (int)(rw_byte(row, type, q + j, B) & 63);
-        *m = (int)(rw_byte(row, type, q + j + 4, B) & 63);
-    } else {
-        const uint32_t a = rw_byte(row, type, q + j + 4, B);
-        *sc = (int)((a & 0x0f) | ((rw_byte(row, type, q + j - 4, B) >> 6) << 4));
-        *m = (int)((a >> 4) | ((rw_byte(row, type, q + j, B) >> 6) << 4));
-    }
+    const int jl = j & 3;
+    const uint32_t b0 = rw_byte(row, type, q + jl, B), b4 = rw_byte(row, type, q + jl + 4, B);
+    const uint32_t b8 = rw_byte(row, type, q + jl + 8, B);
+    *sc = j < 4 ? (int)(b0 & 63) : (int)((b8 & 0x0f) | ((b0 >> 6) << 4));
+    *m = j < 4 ? (int)(b4 & 63) : (int)((b8 >> 4) | ((b4 >> 6) << 4));
 }
 
-__device__ float rw_element(const uint8_t* row, int type, int B, int e) {
+__device__ __forceinline__ float rw_element(const uint8_t* row, int type, int B, int e) {
     switch (type) {
     case GLLM_TYPE_F32: {
         const uint32_t bits = rw_u16(row, type, 4 * (size_t)e, B) |
@@ -123,7 +122,9 @@ __device__ float rw_element(const uint8_t* row, int type, int B, int e) {
 }
 
 // out[t][0..cols) = row ids[t] (clamped to the last row); grid (ceil(cols /
-// 256), n), one element per thread
+// 256), n), one element per thread.  T >= 0 fixes the type at compile time
+// (the element's loads are then straight-line code); T < 0 reads it at run time.
+template <int T>
 __global__ __launch_bounds__(256) void weight_rows_kernel(const uint8_t* __restrict__ w, size_t rb,
                                                           int type, int B, int rows, int cols,
                                                           const uint32_t* __restrict__ ids,
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(256) void weight_rows_kernel(const uint8_t* __restr
     const int t = blockIdx.y, e = blockIdx.x * 256 + threadIdx.x;
     if (e >= cols) return;
     const uint32_t id = min(ids[t], (uint32_t)(rows - 1));
-    out[(size_t)t * cols + e] = rw_element(w + (size_t)id * rb, type, B, e);
+    out[(size_t)t * cols + e] = rw_element(w + (size_t)id * rb, T >= 0 ? T : type, B, e);
 }
 
 bool rows_type(int t) {
@@ -146,8 +147,13 @@ int launch_weight_rows(const gllm_hip_weight* w, const uint32_t* d_ids, int n, f
     if (!rows_type(w->type)) return fail(GLLM_EUNSUP, "weight rows: type %d", w->type);
     if (n <= 0) return n == 0 ? GLLM_OK : fail(GLLM_EINVAL, "weight rows: n = %d", n);
     const dim3 grid((unsigned)((w->cols + 255) / 256), (unsigned)n);
-    hipLaunchKernelGGL(weight_rows_kernel, grid, dim3(256), 0, s, w->d_data, w->row_bytes, w->type,
-                       w->blocks, w->rows, w->cols, d_ids, d_out);
+#define GLLM_ROWS(T)                                                                        \
+    hipLaunchKernelGGL(weight_rows_kernel<T>, grid, dim3(256), 0, s, w->d_data, w->row_bytes,    \
+                       w->type, w->blocks, w->rows, w->cols, d_ids, d_out)
+    if (w->type == GLLM_TYPE_Q4_K) GLLM_ROWS(GLLM_TYPE_Q4_K);
+    else if (w->type == GLLM_TYPE_Q6_K) GLLM_ROWS(GLLM_TYPE_Q6_K);
+    else GLLM_ROWS(-1);
+#undef GLLM_ROWS
     GLLM_HIP(hipGetLastError());
     return GLLM_OK;
 }
