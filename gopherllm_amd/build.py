@@ -9,6 +9,11 @@ built library travels with the repository snapshot.  Flags:
 * ``-fhip-fp32-correctly-rounded-divide-sqrt``: IEEE division (the Q8K scale
   amax/127 and the softmax 1/denom must round exactly like the CPU).
 * ``-Xclang -target-feature -Xclang -packed-fp32-ops``: no packed fp32 math.
+* ``-mllvm -amdgpu-kernarg-preload-count=8``: the leading eight dwords of a
+  kernel's plain (non-aggregate) arguments are preloaded into SGPRs by the
+  command processor, so such a kernel issues its first loads without waiting
+  for scalar loads of its arguments (the code keeps the loads as a fallback
+  prologue for firmware without preloading).
 """
 from __future__ import annotations
 
@@ -32,6 +37,7 @@ FLAGS = [
     "-ffp-contract=off",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=8",
     "-Wall",
     "-Wno-unused-function",
 ]

@@ -734,11 +734,6 @@ __global__ __launch_bounds__(256) void attn_splitk_kernel(const float* __restric
 constexpr int kSkTile = 16;
 constexpr int kSkWaves = 4;
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
 __device__ __forceinline__ void f16x8_to_f32(const uint4 r, float* f) {
     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
@@ -1001,14 +996,10 @@ __global__ __launch_bounds__(256) void attn_merge2_kernel(const float* __restric
 }
 
 // The one-token values kernel applies when its LDS image of the whole span
-// fits a workgroup (GLLM_ATTN_VDEC=0 keeps attn_softmax_values_kernel, for
-// measurement; both give the same bits).
+// fits a workgroup (attn_softmax_values_kernel otherwise; both give the
+// same bits).
 static bool vdec_usable(int kvmul, int span_max) {
-    static const bool on = [] {
-        const char* e = getenv("GLLM_ATTN_VDEC");
-        return !(e && atoi(e) == 0);
-    }();
-    if (!on || (kvmul != 1 && kvmul != 2 && kvmul != 4)) return false;
+    if (kvmul != 1 && kvmul != 2 && kvmul != 4) return false;
     const size_t bytes = vdec_lds_bytes(kvmul, span_max);
     if (bytes <= 65536) return true;
     static const bool big_ok = [] {

@@ -23,16 +23,9 @@ namespace gllm {
 
 constexpr int kRowsPerWG = 32;  // 256 threads / 8 lanes per row
 constexpr int kMaxTok = 8;      // activation rows per launch
-// Q4_K batches from this many activation rows run on the matrix cores
-// (GLLM_MFMA_MIN_TOK overrides, for measurement; both paths give the same bits)
-static int mfma_min_tok() {
-    static const int n = [] {
-        const char* e = getenv("GLLM_MFMA_MIN_TOK");
-        const int v = e ? atoi(e) : 0;
-        return v > 0 ? v : 8;
-    }();
-    return n;
-}
+// Q4_K batches from this many activation rows run on the matrix cores (both
+// paths give the same bits)
+constexpr int kMfmaMinTok = 8;
 
 bool float_dot_type(int t);
 int launch_float_dot(int n, gllm_hip_weight* const* ws, const float* d_x, float* const* outs,
@@ -167,18 +160,34 @@ __device__ __forceinline__ void chain_gather(float iv, float dxs, float dmin, fl
 // 8-lane tree across k when the k lanes of a row sit G lanes apart.
 template <int G>
 __device__ __forceinline__ float tree8_strided(float v) {
-    v = v + __shfl_xor(v, 4 * G, 8 * G);
-    v = v + __shfl_xor(v, 1 * G, 8 * G);
-    v = v + __shfl_xor(v, 2 * G, 8 * G);
-    return v;
+    if constexpr (G == 1) {
+        return tree8(v);
+    } else if constexpr (G == 2) {
+        // lane (k, gi) = 2 k + gi of a 16-lane row; lane gi = 1 (k = 0) ends
+        // with the sum: k reads k + 4 (row_shl:8), k ^ 1 (quad xor 2), k ^ 2
+        // (row_shl:4); every operand lane lies inside the row
+        v = v + dpp_f<kRowShl8>(v);
+        v = v + dpp_f<kQuadXor2>(v);
+        v = v + dpp_f<kRowShl4>(v);
+        return v;
+    } else {
+        v = v + __shfl_xor(v, 4 * G, 8 * G);
+        v = v + __shfl_xor(v, 1 * G, 8 * G);
+        v = v + __shfl_xor(v, 2 * G, 8 * G);
+        return v;
+    }
 }
 
 __device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
 
-// Exact int8 dot of four byte pairs (v_dot4c_i32_i8).  Every VALU operation
-// here is left to the compiler: hand-written VALU instructions in inline
-// assembly bypass its hazard tracking.
-__device__ __forceinline__ int dot4z(int a, int b) { return __builtin_amdgcn_sdot4(a, b, 0, false); }
+// Exact int8 dot of four byte pairs with a zero accumulator.  With clamp the
+// compiler selects the VOP3P v_dot4_i32_i8 with an inline 0 (without it, the
+// accumulating v_dot4c_i32_i8 behind a v_mov of the zero: one more VALU
+// instruction per dot); the clamp never acts, as |dot| <= 4 * 15 * 127 or
+// 4 * 127 * 127 at most.  VALU instructions are left to the compiler, which
+// tracks the wait states a dot result needs before another VALU reads it;
+// hand-written ones in inline assembly would bypass that.
+__device__ __forceinline__ int dot4z(int a, int b) { return __builtin_amdgcn_sdot4(a, b, 0, true); }
 
 // a * (byte N of s): a is a 14-bit signed dot and s holds 6-bit scales, so
 // the 24-bit multiply (v_mul_i32_i24, full rate) is exact.
@@ -203,8 +212,10 @@ __device__ __forceinline__ s16x2 sc_pair(uint32_t s) {
 }
 __device__ __forceinline__ int q4k_lane_sum(int t0, int t1, int t2, int t3, int t4, int t5, int t6,
                                             int t7, uint32_t sc03, uint32_t sc47) {
-    // one accumulator chain (the integer sum is exact in any order)
-    int acc = __builtin_amdgcn_sdot2(pack16(t0, t1), sc_pair<0>(sc03), 0, false);
+    // one accumulator chain (the integer sum is exact in any order; the first
+    // step clamps only to take the VOP3P form with an inline zero, and
+    // |sum| <= 8 * 7620 * 63 never saturates)
+    int acc = __builtin_amdgcn_sdot2(pack16(t0, t1), sc_pair<0>(sc03), 0, true);
     acc = __builtin_amdgcn_sdot2(pack16(t2, t3), sc_pair<1>(sc03), acc, false);
     acc = __builtin_amdgcn_sdot2(pack16(t4, t5), sc_pair<0>(sc47), acc, false);
     return __builtin_amdgcn_sdot2(pack16(t6, t7), sc_pair<1>(sc47), acc, false);
@@ -277,8 +288,10 @@ struct XRegs {
 };
 
 template <int QB, bool SKIP = false>
-__device__ __forceinline__ void xq_load(const float* __restrict__ x, int B, XRegs<QB>& xr) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+__device__ __forceinline__ void xq_load(const float* __restrict__ x, int B, XRegs<QB>& xr,
+                                        int nw = -1) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (nw < 0) nw = blockDim.x >> 6;
     const int m = lane >> 3, kk = lane & 7;
 #pragma unroll
     for (int i = 0; i < QB; i++) {
@@ -308,38 +321,34 @@ __device__ __forceinline__ void xq_block(const float* xv, int b, int8_t* q8, flo
     const int lane = threadIdx.x & 63;
     const int m = lane >> 3, kk = lane & 7;
     const float x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
-    // amax, NaN skipped: v_max_f32 is IEEE maxNum
-    float a = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
-    float scale = 0.0f, inv = 0.0f;
-    const bool nz = a != 0.0f && a == a;
-    if (nz) {
-        scale = a / 127.0f;
-        inv = 127.0f / a;
-    }
+    // amax, NaN skipped like the reference's `a > amax` scan: v_max_f32 is
+    // IEEE maxNum, so the lane's max over |x| and 0 drops NaNs and is a
+    // non-negative float, whose bits order like its value; the cross-lane
+    // maximum then runs on the bits (integer max, no NaN canonicalisation).
+    // A block of NaNs and zeros ends at 0, as the reference's amax does.
+    const float a = fmaxf(fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3))), 0.0f);
+    const float amax = __uint_as_float(wave_max_u32(__float_as_uint(a)));
+    const bool nz = amax != 0.0f;
+    // scale = amax / 127 and inv = 127 / amax, both IEEE-rounded, in one
+    // division: even lanes divide amax by 127, odd lanes 127 by amax
+    const bool odd = lane & 1;
+    const float quo = (odd ? 127.0f : amax) / (odd ? amax : 127.0f);
+    const float scale = nz ? readlane_f(quo, 0) : 0.0f;
+    const float inv = nz ? readlane_f(quo, 1) : 0.0f;
+    // inv = 0 makes every q 0 (x * 0 is +-0, or NaN, which converts to 0)
     int8_t* qb = q8 + (size_t)b * 256 + 4 * m + (kk & 3) + 32 * (kk >> 2);
-    qb[0] = (int8_t)(nz ? (int)rintf(x0 * inv) : 0);
-    qb[64] = (int8_t)(nz ? (int)rintf(x1 * inv) : 0);
-    qb[128] = (int8_t)(nz ? (int)rintf(x2 * inv) : 0);
-    qb[192] = (int8_t)(nz ? (int)rintf(x3 * inv) : 0);
+    qb[0] = (int8_t)(int)rintf(x0 * inv);
+    qb[64] = (int8_t)(int)rintf(x1 * inv);
+    qb[128] = (int8_t)(int)rintf(x2 * inv);
+    qb[192] = (int8_t)(int)rintf(x3 * inv);
     if (lane == 0) xsc[b] = scale;
     // v_kk = ((x[kk] + x[8+kk]) + x[16+kk]) + x[24+kk]; a_k = v_k + v_{k+4};
-    // r = (a0 + a1) + (a2 + a3)
-    float v = ((x0 + x1) + x2) + x3;
-    v = v + __shfl_xor(v, 4);
-    v = v + __shfl_xor(v, 1);
-    v = v + __shfl_xor(v, 2);
+    // r = (a0 + a1) + (a2 + a3): the 8 lanes kk of group m are lanes 8m..8m+7
+    const float v = tree8(((x0 + x1) + x2) + x3);
     if (kk == 0) xs32[b * 8 + m] = v;
     if constexpr (XS16) {
         // 16-groups 2m (x0, x1) and 2m+1 (x2, x3): v_k = x[k] + x[8+k]
-        float u = x0 + x1, w = x2 + x3;
-        u = u + __shfl_xor(u, 4);
-        w = w + __shfl_xor(w, 4);
-        u = u + __shfl_xor(u, 1);
-        w = w + __shfl_xor(w, 1);
-        u = u + __shfl_xor(u, 2);
-        w = w + __shfl_xor(w, 2);
+        const float u = tree8(x0 + x1), w = tree8(x2 + x3);
         if (kk == 0) {
             xs16[b * 16 + 2 * m] = u;
             xs16[b * 16 + 2 * m + 1] = w;
@@ -350,8 +359,9 @@ __device__ __forceinline__ void xq_block(const float* xv, int b, int8_t* q8, flo
 // Quantise the blocks held in xr (wave w holds blocks w, w + nw, ...).
 template <int QB, bool XS16>
 __device__ __forceinline__ void xq_store(const XRegs<QB>& xr, int B, int8_t* q8, float* xs32,
-                                         float* xs16, float* xsc) {
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+                                         float* xs16, float* xsc, int nw = -1) {
+    const int wave = threadIdx.x >> 6;
+    if (nw < 0) nw = blockDim.x >> 6;
 #pragma unroll
     for (int i = 0; i < QB; i++) {
         const int b = wave + nw * i;
@@ -482,6 +492,34 @@ __host__ __device__ constexpr size_t q4k_norm_off(int cols) {
 // then the fp32 chain steps (G-lane rotation when G > 1):
 //   accF = fma(float(accI), d*xs, accF)          VMULSS + VFMADD231PS
 //   accM = fma(dmin, m_k*xsum_k, accM)           VMULPS + VFMADD231PS
+// Lane k's 32 nibbles of a block as eight dwords of four 4-bit values:
+// n[2c] the low and n[2c + 1] the high nibbles of its chunk-c dword.
+struct Nib8 {
+    int n[8];
+    __device__ __forceinline__ explicit Nib8(const uint4 q) {
+        n[0] = (int)(q.x & 0x0f0f0f0fu); n[1] = (int)((q.x >> 4) & 0x0f0f0f0fu);
+        n[2] = (int)(q.y & 0x0f0f0f0fu); n[3] = (int)((q.y >> 4) & 0x0f0f0f0fu);
+        n[4] = (int)(q.z & 0x0f0f0f0fu); n[5] = (int)((q.z >> 4) & 0x0f0f0f0fu);
+        n[6] = (int)(q.w & 0x0f0f0f0fu); n[7] = (int)((q.w >> 4) & 0x0f0f0f0fu);
+    }
+};
+
+// The exact int32 lane sum of lane k's nibbles against its 32 q8 bytes at qp
+// (two 16-byte LDS reads), with the block's 6-bit scales sc03 / sc47.
+__device__ __forceinline__ int q4k_lane_int(const Nib8& w, const int8_t* qp, uint32_t sc03,
+                                            uint32_t sc47) {
+    const int4 qa = *(const int4*)qp;
+    const int4 qb = *(const int4*)(qp + 16);
+    return q4k_lane_sum(dot4z(w.n[0], qa.x), dot4z(w.n[1], qa.y), dot4z(w.n[2], qa.z),
+                        dot4z(w.n[3], qa.w), dot4z(w.n[4], qb.x), dot4z(w.n[5], qb.y),
+                        dot4z(w.n[6], qb.z), dot4z(w.n[7], qb.w), sc03, sc47);
+}
+
+__device__ __forceinline__ uint32_t q4k_sc03(const uint4 h) { return h.y & 0x3f3f3f3fu; }
+__device__ __forceinline__ uint32_t q4k_sc47(const uint4 h) {
+    return (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+}
+
 template <int NT, int G>
 __device__ __forceinline__ void q4k_block(const uint4 h, const uint4 q, int b, int k,
                                           const MinSel& ms, int ntok, const int8_t* q8b,
@@ -489,22 +527,13 @@ __device__ __forceinline__ void q4k_block(const uint4 h, const uint4 q, int b, i
                                           float* accF, float* accM) {
     const float d = f16_bits_to_f32(h.x & 0xffffu);
     const float dmin = f16_bits_to_f32(h.x >> 16);
-    const uint32_t sc03 = h.y & 0x3f3f3f3fu;
-    const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t sc03 = q4k_sc03(h), sc47 = q4k_sc47(h);
     const float mkf = (float)ms.get(h.z, h.w);
-    const int l0 = (int)(q.x & 0x0f0f0f0fu), h0 = (int)((q.x >> 4) & 0x0f0f0f0fu);
-    const int l1 = (int)(q.y & 0x0f0f0f0fu), h1 = (int)((q.y >> 4) & 0x0f0f0f0fu);
-    const int l2 = (int)(q.z & 0x0f0f0f0fu), h2 = (int)((q.z >> 4) & 0x0f0f0f0fu);
-    const int l3 = (int)(q.w & 0x0f0f0f0fu), h3 = (int)((q.w >> 4) & 0x0f0f0f0fu);
+    const Nib8 w(q);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         if (NT == 1 || t < ntok) {
-            const int8_t* qp = q8b + (size_t)t * cols + b * 256 + k * 32;
-            const int4 qa = *(const int4*)qp;
-            const int4 qb = *(const int4*)(qp + 16);
-            const int acc = q4k_lane_sum(dot4z(l0, qa.x), dot4z(h0, qa.y), dot4z(l1, qa.z),
-                                         dot4z(h1, qa.w), dot4z(l2, qb.x), dot4z(h2, qb.y),
-                                         dot4z(l3, qb.z), dot4z(h3, qb.w), sc03, sc47);
+            const int acc = q4k_lane_int(w, q8b + (size_t)t * cols + b * 256 + k * 32, sc03, sc47);
             const float iv = (float)acc;
             const float dxs = d * xscb[(size_t)t * B + b];
             const float mx = mkf * xs32b[(size_t)t * (cols / 32) + b * 8 + k];
@@ -706,6 +735,393 @@ __global__ __launch_bounds__(256) void gemv_q4k_any_kernel(GemvJob j) {
             j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
     }
 }
+// ---------------------------------------------------------------------------
+// Block-parallel batch-1 Q4_K row kernel.  Of a row dot, only the two fp32
+// chains per AVX2 lane k (accF, accM: one step per block, in block order)
+// and the final 8->4->2->1 tree are sequential; the four chain operands of a
+// block -- float(exact int32 lane sum), d * xscale, dmin and m_k * xs32 --
+// depend on that block alone.  NS slices of eight lanes therefore share a
+// row: slice s forms the operands of blocks s, s + NS, s + 2 NS, ... (its NB
+// = B / NS nibble loads all issued at entry, headers broadcast from the
+// 16-byte header plane as in gemv_q4k_kernel) and stores them to LDS at
+// X[row][block][k]; after one barrier thread (row, k) runs the two chains
+// over the row's B blocks in block order and the tree.  The operands, the
+// chains and the tree are the row kernel's, so the bits are the same; the
+// slices give a compute unit NS times the waves over the same rows, with the
+// whole weight slice in flight from the start.
+//
+// FUSE = 1: the workgroup quantises x itself (xq_load issued before the
+// weight loads, as in gemv_q4k_kernel); FUSE = 0: pre-quantised activations
+// copied to LDS with direct global->LDS loads.
+// ---------------------------------------------------------------------------
+// Rows per workgroup of a launch shape: NTH / (8 NS) row groups, RP rows
+// per lane.
+__host__ __device__ constexpr int q4k_bp_rows(int ns, int nth, int rp) { return nth / (8 * ns) * rp; }
+// float4 stride of one row of the exchange: B blocks x 8 lanes, padded by 8
+// so the chain pass's reads (two rows per 16 lanes) fall in distinct banks
+__host__ __device__ constexpr int q4k_bp_xstride(int B) { return B * 8 + 8; }
+// LDS: the activation image, then the exchange X[rows][xstride] of float4
+__host__ __device__ constexpr size_t q4k_bp_lds(int B, int ns, int nth, int rp) {
+    return q4k_norm_off(B * 256) + (size_t)q4k_bp_rows(ns, nth, rp) * q4k_bp_xstride(B) * 16;
+}
+
+// Decoded header of one Q4_K block for AVX2 lane k: d, dmin, the eight
+// 6-bit scales as two byte-packed dwords and m_k (getScaleMinK4).
+struct Q4KHdr {
+    float d, dmin, mk;
+    uint32_t sc03, sc47;
+    __device__ __forceinline__ Q4KHdr() = default;
+    __device__ __forceinline__ Q4KHdr(const uint4 h, const MinSel& ms)
+        : d(f16_bits_to_f32(h.x & 0xffffu)),
+          dmin(f16_bits_to_f32(h.x >> 16)),
+          mk((float)ms.get(h.z, h.w)),
+          sc03(q4k_sc03(h)),
+          sc47(q4k_sc47(h)) {}
+};
+
+// Lane (row group g, slice s, k) owns rows r0 + g + R p (p < RP) and, of
+// each, blocks s, s + NS, ..., s + NS (NB - 1).  Load order: the headers,
+// then x (or the staged activations), then P blocks per row; the wave then
+// waits for its own x and issues the rest of its weights before quantising.
+// Every wave's x request thus enters the memory system ahead of any weight
+// flood but the P blocks (an x read queued behind a full flood arrives
+// microseconds late), and the weight stream starts as soon as x is in,
+// not after the workgroup's quantiser barrier.
+template <int B, int NS, int NTH, int RP, int FUSE, int P>
+__global__ __launch_bounds__(NTH) void gemv_q4k_bp_kernel(GemvJob j) {
+    constexpr int NB = B / NS;
+    static_assert(B % NS == 0 && NTH % (8 * NS) == 0 && NTH % 64 == 0, "launch shape");
+    static_assert(NB <= 8, "one header load per lane and row");
+    static_assert(P >= 0 && P <= NB, "blocks before the quantiser");
+    constexpr int R = NTH / (8 * NS);
+    constexpr int RW = R * RP;
+    constexpr int NW = NTH / 64;
+    constexpr int QB = FUSE ? (B + NW - 1) / NW : 1;
+    constexpr int cols = B * 256;
+    constexpr int XS = q4k_bp_xstride(B);
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x;
+    const int k = tid & 7, u = tid >> 3, s = u % NS, g = u / NS;
+    int wi = 0;
+    while (wi + 1 < j.n && (int)blockIdx.x >= j.wg_begin[wi + 1]) wi++;
+    const int r0 = ((int)blockIdx.x - j.wg_begin[wi]) * RW;
+    const int nrows = j.rows[wi];
+    const uint8_t* rowp[RP];
+#pragma unroll
+    for (int p = 0; p < RP; p++) {
+        const int r = r0 + g + R * p;
+        rowp[p] = j.w[wi] + (size_t)(r < nrows ? r : nrows - 1) * j.rb;  // dead rows read a valid row
+    }
+    int8_t* q8b = (int8_t*)smem;
+    float* xs32b = (float*)(smem + cols);
+    float* xscb = xs32b + cols / 32;
+    float4* X = (float4*)(smem + q4k_norm_off(cols));
+    uint4 H[RP];
+#pragma unroll
+    for (int p = 0; p < RP; p++)
+        H[p] = *(const uint4*)(rowp[p] + q4k_hdr_off(NS * (k < NB ? k : NB - 1) + s));
+    __builtin_amdgcn_sched_barrier(0);
+    XRegs<QB> xr;
+    if constexpr (FUSE) {
+        xq_load<QB, true>(j.xf, B, xr);
+    } else {
+        stage_act_asm<1>(j, smem);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 Q[NB][RP];
+    const size_t nib0 = q4k_nib_off(B, s) + 16 * k;  // block NS i + s at + NS i 128
+#pragma unroll
+    for (int i = 0; i < P; i++)
+#pragma unroll
+        for (int p = 0; p < RP; p++) {
+            Q[i][p] = *(const uint4*)(rowp[p] + nib0 + (size_t)i * NS * 128);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    wait_vmem_le<P * RP>();  // this wave's headers and x (or staged activations)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = P; i < NB; i++)
+#pragma unroll
+        for (int p = 0; p < RP; p++) {
+            Q[i][p] = *(const uint4*)(rowp[p] + nib0 + (size_t)i * NS * 128);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    const MinSel ms(k);
+    Q4KHdr hd[NB][RP];
+#pragma unroll
+    for (int i = 0; i < NB; i++)
+#pragma unroll
+        for (int p = 0; p < RP; p++) hd[i][p] = Q4KHdr(hdr_of<1>(H[p], i), ms);
+    if constexpr (FUSE) xq_store<QB, false>(xr, B, q8b, xs32b, nullptr, xscb);
+    wait_lgkm0();
+    lds_barrier();
+    // this lane's operands: block NS i + s at a compile-time offset from here
+    const int8_t* q8s = q8b + s * 256 + k * 32;
+    const float* x32s = xs32b + s * 8 + k;
+    const float* xscs = xscb + s;
+    float4* xo = X + (size_t)g * XS + s * 8 + k;
+#pragma unroll
+    for (int i = 0; i < NB; i++)
+#pragma unroll
+        for (int p = 0; p < RP; p++) {
+            const Nib8 w(Q[i][p]);
+            const Q4KHdr& h = hd[i][p];
+            const int acc = q4k_lane_int(w, q8s + i * NS * 256, h.sc03, h.sc47);
+            xo[(size_t)R * p * XS + i * NS * 8] =
+                make_float4((float)acc, h.d * xscs[i * NS], h.dmin, h.mk * x32s[i * NS * 8]);
+        }
+    __syncthreads();
+#pragma unroll
+    for (int t0 = 0; t0 < 8 * RW; t0 += NTH) {
+        const int t = t0 + tid;
+        if (t0 + NTH <= 8 * RW || t < 8 * RW) {
+            const int cr = t >> 3;
+            const float4* xp = X + (size_t)cr * XS + k;
+            float accF = 0.0f, accM = 0.0f;
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const float4 v = xp[b * 8];
+                accF = fmaf(v.x, v.y, accF);  // VMULSS + VFMADD231PS
+                accM = fmaf(v.z, v.w, accM);  // VMULPS + VFMADD231PS
+            }
+            const float v = tree8(accF - accM);  // VSUBPS + tree
+            if (k == 0 && r0 + cr < nrows) j.out[wi][r0 + cr] = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Wave-specialised batch-1 Q4_K row kernel.  A workgroup owns R rows (one
+// workgroup per compute unit at the configs' shapes).  Its last NLD waves
+// are loaders: they copy the rows' header planes and nibble blocks straight
+// from HBM into LDS (global_load_lds_dwordx4, no registers held) and set a
+// per-block flag in LDS once a block's copies have landed (an exact vmcnt
+// wait: copies retire in issue order).  The other waves compute, eight lanes
+// per row as in gemv_q4k_kernel (AVX2 lane k, chains in block order, the
+// 8->4->2->1 tree), so the bits are that kernel's: they quantise x, then
+// walk the blocks as they land, reading nibbles, headers and activations
+// from LDS.  With NS = 2 a row's lanes come in two slices: slice 1 forms
+// the chain operands of the second half of the blocks while slice 0 runs
+// the chains over the first half, then continues them from slice 0's values
+// (handed over through LDS), so the chains still see every block in order.
+//
+// Only the loaders ever wait on HBM: a wave issuing a compute unit's whole
+// weight slice stalls on issue once the memory queues fill, which here
+// never holds up the arithmetic.  The compute waves' x reads are issued at
+// entry, ahead of the copies in the compute unit's queue.
+//
+// LDS: activations (q8 | xs32 | xscale), headers [R][B + 1][16 B] (one
+// padding slot per row keeps two rows' broadcast reads in distinct banks),
+// nibbles [B][R][k][16 B], B block flags, the compute barrier's counter and
+// the chain handover [R][k][2] floats.
+// ---------------------------------------------------------------------------
+template <int B, int R>
+struct Q4KWsLayout {
+    static constexpr int cols = B * 256;
+    static constexpr int hslots = R * (B + 1);  // header slots, 16 B each
+    static constexpr size_t hdr = q4k_norm_off(cols);
+    static constexpr size_t nib = hdr + ((size_t)hslots * 16 + 1023) / 1024 * 1024;
+    static constexpr size_t flags = nib + (size_t)B * R * 128;
+    static constexpr size_t count = flags + (size_t)B * 4;
+    static constexpr size_t hand = count + 64;
+    static constexpr size_t bytes = hand + (size_t)R * 8 * 8;
+};
+
+// Copy order of the blocks: with two slices the halves interleave (0,
+// B/2, 1, B/2 + 1, ...) so both slices are fed from the start (slice 0's
+// blocks first measured 9.03 against 8.80 us at 14336 x 4096).
+template <int B, int NS>
+__device__ __forceinline__ constexpr int ws_block(int pos) {
+    return NS == 1 ? pos : (pos & 1) ? B / 2 + pos / 2 : pos / 2;
+}
+
+// Loader LW copies the header slots n = LW, LW + NLD, ... (1 KB each), then
+// the blocks at copy positions LW, LW + NLD, ... (R / 8 copies each), and
+// sets a block's flag once its copies have completed, keeping up to D
+// blocks in flight before it waits.
+template <int B, int R, int NS, int NLD, int D, int LW, int I>
+__device__ __forceinline__ void ws_loader_blocks(const uint8_t* __restrict__ w, size_t rb, int r0,
+                                                 int nrows, uint8_t* smem) {
+    using L = Q4KWsLayout<B, R>;
+    constexpr int PER = R / 8;
+    constexpr int NBW = (B - LW + NLD - 1) / NLD;
+    if constexpr (I < NBW + D) {
+        const int lane = threadIdx.x & 63, rl = lane >> 3, k = lane & 7;
+        if constexpr (I < NBW) {
+            constexpr int b = ws_block<B, NS>(LW + NLD * I);
+#pragma unroll
+            for (int c = 0; c < PER; c++) {
+                const int r = r0 + 8 * c + rl;
+                const uint8_t* g =
+                    w + (size_t)(r < nrows ? r : nrows - 1) * rb + q4k_nib_off(B, b) + 16 * k;
+                lds_copy16(g, lds_addr(smem + L::nib + ((size_t)b * R + 8 * c) * 128));
+            }
+        }
+        if constexpr (I >= D) {
+            // block I - D is complete once at most the copies issued after it remain
+            constexpr int after = (I < NBW ? I : NBW - 1) - (I - D);
+            wait_vmem_le<after * PER>();
+            asm volatile("" ::: "memory");
+            if (lane == 0) {
+                int* flag = (int*)(smem + L::flags) + ws_block<B, NS>(LW + NLD * (I - D));
+                __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
+        ws_loader_blocks<B, R, NS, NLD, D, LW, I + 1>(w, rb, r0, nrows, smem);
+    }
+}
+
+template <int B, int R, int NS, int NLD, int D, int LW>
+__device__ __forceinline__ void q4k_ws_loader(const uint8_t* __restrict__ w, size_t rb, int r0,
+                                              int nrows, uint8_t* smem) {
+    using L = Q4KWsLayout<B, R>;
+    constexpr int HI = (L::hslots + 63) / 64;
+    const int lane = threadIdx.x & 63;
+    // header slot t = r (B + 1) + b: row r's header b (b == B: padding)
+#pragma unroll
+    for (int n = LW; n < HI; n += NLD) {
+        const int t = n * 64 + lane;
+        const int r = t / (B + 1), b = t % (B + 1);
+        const int rr = r0 + r < nrows ? r0 + r : nrows - 1;
+        const uint8_t* g = w + (size_t)rr * rb + q4k_hdr_off(b < B ? b : 0);
+        if (t < L::hslots) lds_copy16(g, lds_addr(smem + L::hdr + (size_t)n * 1024));
+    }
+    // copies retire in issue order: the flag of this loader's first block
+    // also covers its header copies
+    ws_loader_blocks<B, R, NS, NLD, D, LW, 0>(w, rb, r0, nrows, smem);
+}
+
+// One weight, plain arguments (the command processor can preload them into
+// SGPRs, where a GemvJob by value is read with scalar loads first): the
+// rows' weights w (row bytes rb), f32 x, out[nrows].
+template <int B, int R, int NS, int NLD, int D>
+__global__ __launch_bounds__(R * 8 * NS + NLD * 64) void gemv_q4k_ws_kernel(
+    const uint8_t* __restrict__ w, const float* __restrict__ xf, float* __restrict__ out, int nrows,
+    int rb) {
+    using L = Q4KWsLayout<B, R>;
+    constexpr int NCW = R * NS / 8;  // compute waves
+    constexpr int QB = (B + NCW - 1) / NCW;
+    constexpr int cols = B * 256;
+    constexpr int BS = B / NS;  // blocks per slice
+    static_assert(R % 8 == 0 && B % NS == 0 && (NS == 1 || NS == 2), "workgroup shape");
+    static_assert(L::bytes <= 160 * 1024 - 64, "LDS");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r0 = (int)blockIdx.x * R;
+    int* flags = (int*)(smem + L::flags);
+    int* count = (int*)(smem + L::count);  // [0]: compute barrier, [1 + w]: handover of wave w
+    XRegs<QB> xr;
+    if (wave < NCW) xq_load<QB, true>(xf, B, xr, NCW);  // x first, ahead of every copy
+    // LDS holds whatever an earlier workgroup left: clear the flags and the
+    // counters before anyone sets or reads them
+    if (tid < B) __hip_atomic_store(flags + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (tid < 16) __hip_atomic_store(count + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    wait_lgkm0();
+    lds_barrier();
+    if (wave >= NCW) {
+        if constexpr (NLD > 0) if (wave == NCW + 0) q4k_ws_loader<B, R, NS, NLD, D, 0>(w, rb, r0, nrows, smem);
+        if constexpr (NLD > 1) if (wave == NCW + 1) q4k_ws_loader<B, R, NS, NLD, D, 1>(w, rb, r0, nrows, smem);
+        if constexpr (NLD > 2) if (wave == NCW + 2) q4k_ws_loader<B, R, NS, NLD, D, 2>(w, rb, r0, nrows, smem);
+        if constexpr (NLD > 3) if (wave == NCW + 3) q4k_ws_loader<B, R, NS, NLD, D, 3>(w, rb, r0, nrows, smem);
+        return;
+    }
+    int8_t* q8b = (int8_t*)smem;
+    float* xs32b = (float*)(smem + cols);
+    float* xscb = xs32b + cols / 32;
+    xq_store<QB, false>(xr, B, q8b, xs32b, nullptr, xscb, NCW);
+    // barrier of the compute waves only (the loaders never wait for them)
+    wait_lgkm0();
+    if ((tid & 63) == 0) __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (__hip_atomic_load(count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < NCW)
+        __builtin_amdgcn_s_sleep(1);
+    const int sl = NS == 1 ? 0 : tid / (R * 8);  // slice
+    const int rl = (tid >> 3) % R, k = tid & 7;
+    const MinSel ms(k);
+    const uint8_t* hrow = smem + L::hdr + (size_t)rl * (B + 1) * 16;
+    const uint8_t* nrow = smem + L::nib + (size_t)rl * 128 + 16 * k;
+    auto ready = [&](int b) {
+        while (__hip_atomic_load(flags + b, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+            __builtin_amdgcn_s_sleep(1);
+    };
+    // every loader's headers: the first block each of them flags
+#pragma unroll
+    for (int l = 0; l < NLD; l++) ready(ws_block<B, NS>(l));
+    const int b0 = sl * BS;
+    float accF = 0.0f, accM = 0.0f;
+    // chain operands of slice 1's blocks, held until slice 0's chains arrive
+    float oI[NS == 2 ? BS : 1], oD[NS == 2 ? BS : 1], oN[NS == 2 ? BS : 1], oX[NS == 2 ? BS : 1];
+    // the LDS operands of one block, read a block ahead of their use
+    struct Ops {
+        uint4 h, q;
+        int4 qa, qb;
+        float xsc, x32;
+    };
+    auto fetch = [&](int b) {
+        Ops o;
+        o.h = *(const uint4*)(hrow + b * 16);
+        o.q = *(const uint4*)(nrow + (size_t)b * R * 128);
+        const int8_t* qp = q8b + b * 256 + k * 32;
+        o.qa = *(const int4*)qp;
+        o.qb = *(const int4*)(qp + 16);
+        o.xsc = xscb[b];
+        o.x32 = xs32b[b * 8 + k];
+        return o;
+    };
+    ready(b0);
+    Ops cur = fetch(b0);
+#pragma unroll
+    for (int i = 0; i < BS; i++) {
+        const int b = b0 + i;
+        Ops nxt = cur;
+        if (i + 1 < BS) {
+            ready(b + 1);
+            nxt = fetch(b + 1);
+        }
+        const Q4KHdr hd(cur.h, ms);
+        const Nib8 wn(cur.q);
+        const int acc = q4k_lane_sum(dot4z(wn.n[0], cur.qa.x), dot4z(wn.n[1], cur.qa.y),
+                                     dot4z(wn.n[2], cur.qa.z), dot4z(wn.n[3], cur.qa.w),
+                                     dot4z(wn.n[4], cur.qb.x), dot4z(wn.n[5], cur.qb.y),
+                                     dot4z(wn.n[6], cur.qb.z), dot4z(wn.n[7], cur.qb.w), hd.sc03,
+                                     hd.sc47);
+        const float iv = (float)acc, dxs = hd.d * cur.xsc, mx = hd.mk * cur.x32;
+        if (NS == 1 || sl == 0) {
+            accF = fmaf(iv, dxs, accF);      // VMULSS + VFMADD231PS
+            accM = fmaf(hd.dmin, mx, accM);  // VMULPS + VFMADD231PS
+        } else {
+            oI[NS == 2 ? i : 0] = iv;
+            oD[NS == 2 ? i : 0] = dxs;
+            oN[NS == 2 ? i : 0] = hd.dmin;
+            oX[NS == 2 ? i : 0] = mx;
+        }
+        cur = nxt;
+    }
+    if constexpr (NS == 2) {
+        float2* hand = (float2*)(smem + L::hand) + rl * 8 + k;
+        const int hw = 1 + (wave % (NCW / 2));  // the slice-0 wave over the same rows
+        if (sl == 0) {
+            *hand = make_float2(accF, accM);
+            wait_lgkm0();
+            if ((tid & 63) == 0)
+                __hip_atomic_store(count + hw, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            return;
+        }
+        while (__hip_atomic_load(count + hw, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+            __builtin_amdgcn_s_sleep(1);
+        const float2 a = *hand;
+        accF = a.x;
+        accM = a.y;
+#pragma unroll
+        for (int i = 0; i < BS; i++) {
+            accF = fmaf(oI[i], oD[i], accF);  // VMULSS + VFMADD231PS
+            accM = fmaf(oN[i], oX[i], accM);  // VMULPS + VFMADD231PS
+        }
+    }
+    const float v = tree8(accF - accM);  // VSUBPS + tree
+    if (k == 0 && r0 + rl < nrows) out[r0 + rl] = v;
+}
+
 // Batch launches of the Q6_K / Q8_0 row kernels (j.sa): the launch's ntok
 // activation rows (q8, xscale and, for Q6_K, xs16) are copied into dynamic
 // LDS once per workgroup, so the per-token operands of every block come from
@@ -1318,41 +1734,17 @@ struct Q4KShape {
     int g, rows_per_wg, threads;
 };
 // Smallest workgroup the shape search accepts before trying a larger G
-// (GLLM_Q4K_MIN_THREADS overrides, for measurement; every G gives the same
-// bits; at 14336x4096, 896 threads measured 11.8 us against 9.7 us).
-static int q4k_min_threads() {
-    static const int n = [] {
-        const char* e = getenv("GLLM_Q4K_MIN_THREADS");
-        const int v = e ? atoi(e) : 0;
-        return v > 0 ? v : 448;
-    }();
-    return n;
-}
+// (every G gives the same bits; at 14336x4096, 896 threads measured 11.8 us
+// against 9.7 us).
+constexpr int kQ4KMinThreads = 448;
 // Largest workgroup in rows at G = 1, and in lanes (rows x 8 x G) at any G:
 // 64 rows, 512 threads.  Matrices with more rows than that per compute unit
 // (the decode step's fused gate/up, 28672 rows) take several workgroups per
 // CU instead of one large one; measured on the 8B decode step, 438 tok/s at
 // 64 rows against 434 at 128 (1024 threads), 425 at 72, 414 at 80 and 56,
-// 404 at 96.  GLLM_Q4K_MAX_ROWS overrides, for measurement (8..128); every
-// shape gives the same bits.
-static int q4k_max_rows() {
-    static const int n = [] {
-        const char* e = getenv("GLLM_Q4K_MAX_ROWS");
-        const int v = e ? atoi(e) : 0;
-        return v >= 8 && v <= 128 ? v / 8 * 8 : 64;
-    }();
-    return n;
-}
-// Largest workgroup in lanes (GLLM_Q4K_MAX_THREADS overrides, for
-// measurement, up to 1024: every shape gives the same bits).
-static int q4k_max_threads() {
-    static const int n = [] {
-        const char* e = getenv("GLLM_Q4K_MAX_THREADS");
-        const int v = e ? atoi(e) : 0;
-        return v >= 64 && v <= 1024 ? v : 512;
-    }();
-    return n;
-}
+// 404 at 96; every shape gives the same bits.
+constexpr int kQ4KMaxRows = 64;
+constexpr int kQ4KMaxThreads = 512;
 static Q4KShape q4k_shape(int total_rows, int blocks) {
     const int ncu = device_cus();
     Q4KShape best{0, 0, 0};
@@ -1361,12 +1753,12 @@ static Q4KShape q4k_shape(int total_rows, int blocks) {
         const int unit = 8 / g;  // rows per wave
         int rpw = (total_rows + ncu - 1) / ncu;
         rpw = (rpw + unit - 1) / unit * unit;
-        rpw = std::min(rpw, std::max(unit, q4k_max_rows() / g));
-        rpw = std::min(rpw, std::max(unit, q4k_max_threads() / (8 * g) / unit * unit));
+        rpw = std::min(rpw, std::max(unit, kQ4KMaxRows / g));
+        rpw = std::min(rpw, std::max(unit, kQ4KMaxThreads / (8 * g) / unit * unit));
         const Q4KShape sh{g, rpw, rpw * 8 * g};
         if (!q4k_has_nl(blocks / g) && best.g) continue;
         best = sh;
-        if (sh.threads >= q4k_min_threads() && q4k_has_nl(blocks / g)) break;
+        if (sh.threads >= kQ4KMinThreads && q4k_has_nl(blocks / g)) break;
     }
     return best;
 }
@@ -1416,14 +1808,8 @@ int launch_q4k(GemvJob& j, const int* rows, int n, const Q4KShape& sh, hipStream
 // there (Q5_K 16.4 / 18.7 us, Q3_K 18.8 / 20.7 us at G = 2 / 4).  Batches (per-token
 // activation reads make each block several times longer) take the largest G
 // that keeps the launch at one workgroup per compute unit or fewer.
-// GLLM_ROW_G overrides, for measurement; every G gives the same bits.
+// Every G gives the same bits.
 static int row_lanes_g(int total_rows, int blocks, int ntok, int type) {
-    static const int forced = [] {
-        const char* e = getenv("GLLM_ROW_G");
-        const int v = e ? atoi(e) : 0;
-        return v == 1 || v == 2 || v == 4 ? v : 0;
-    }();
-    if (forced && blocks % forced == 0) return forced;
     const int ncu = device_cus();
     auto wgs = [&](int g) { return (total_rows * g + kRowsPerWG - 1) / kRowsPerWG; };
     int g = 1;
@@ -1488,8 +1874,114 @@ static void (*row_kernel(int type, int g))(GemvJob) {
     }
 }
 
+// Launch shape of the block-parallel batch-1 Q4_K kernel: NS slices per row,
+// NTH threads per workgroup, RP rows per lane, P blocks per lane issued
+// before the wave waits for its x.  ns == 0: not taken.  Measured on one
+// box against gemv_q4k_kernel (three alternations): 4096 x 4096, 4.59
+// against 4.98 us per step; 4096 x 14336 (pre-quantised
+// activations), 11.88 against 12.75 us.  Other shapes keep the row kernels.
+struct Q4KBpShape {
+    int ns, nth, rp, p;
+};
+static Q4KBpShape q4k_bp_pick(int total_rows, int B) {
+    const bool rows4k = total_rows >= 3584 && total_rows <= 4608;
+    if (B == 16 && rows4k) return {8, 1024, 1, 1};
+    if (B == 56 && rows4k) return {14, 896, 1, 2};
+    return {0, 0, 0, 0};
+}
+
+template <int B, int NS, int NTH, int RP, int P>
+static int launch_q4k_bp_inst(GemvJob& j, const int* rows, hipStream_t s) {
+    constexpr int RW = q4k_bp_rows(NS, NTH, RP);
+    j.rows_per_wg = RW;
+    int wg = 0;
+    for (int i = 0; i < j.n; i++) {
+        j.wg_begin[i] = wg;
+        wg += (rows[i] + RW - 1) / RW;
+    }
+    j.wg_begin[j.n] = wg;
+    constexpr size_t lds = q4k_bp_lds(B, NS, NTH, RP);
+    static_assert(lds <= kStagedActMax, "block-parallel LDS");
+    void (*kern)(GemvJob) = gemv_q4k_bp_kernel<B, NS, NTH, RP, 0, P>;
+    if constexpr (B * 256 <= kFuseCols) {
+        if (j.xf) kern = gemv_q4k_bp_kernel<B, NS, NTH, RP, 1, P>;
+    }
+    if (lds > 64 * 1024 && !lds_opt_in((const void*)kern))
+        return fail(GLLM_EDEVICE, "gemv: %zu B of LDS refused", lds);
+    hipLaunchKernelGGL(kern, dim3(wg), dim3(NTH), lds, s, j);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+// Batch-1 Q4_K through the block-parallel kernel when this row length has an
+// instance; *done = false otherwise (the row kernels take it).
+static int launch_q4k_bp(GemvJob& j, const int* rows, hipStream_t s, bool* done) {
+    int total = 0;
+    for (int i = 0; i < j.n; i++) total += rows[i];
+    const Q4KBpShape sh = q4k_bp_pick(total, j.blocks);
+    *done = sh.ns != 0 && (!j.xf || j.cols <= kFuseCols) && !j.nw;
+    if (!*done) return GLLM_OK;
+#define GLLM_BP_INST(b_, ns_, nth_, rp_, p_)                                               \
+    if (j.blocks == b_ && sh.ns == ns_ && sh.nth == nth_ && sh.rp == rp_ && sh.p == p_) \
+        return launch_q4k_bp_inst<b_, ns_, nth_, rp_, p_>(j, rows, s);
+    GLLM_BP_INST(16, 8, 1024, 1, 1)
+    GLLM_BP_INST(56, 14, 896, 1, 2)
+#undef GLLM_BP_INST
+    return fail(GLLM_EINVAL, "gemv: no block-parallel instance (%d, %d, %d, %d, %d)", j.blocks, sh.ns,
+                sh.nth, sh.rp, sh.p);
+}
+
+// Wave-specialised launch: R rows per workgroup, NS slices, NLD loader
+// waves, D blocks in flight per loader before it waits.  r == 0: not taken.
+// One weight with at least 230 workgroups of 56 rows (14336 x 4096, one
+// workgroup per CU): 8.61 against 8.91 us per step for gemv_q4k_kernel
+// (same box, three alternations); the block-parallel kernel took 8.85 there.
+// Measured alternatives: D = 2 / 4, 8.93 / 9.58 us; 16-row workgroups 10.4.
+struct Q4KWsShape {
+    int r, ns, nld, d;
+};
+static Q4KWsShape q4k_ws_pick(int total_rows, int B) {
+    if (B == 16 && total_rows >= 230 * 56) return {56, 2, 2, 1};
+    return {0, 0, 0, 0};
+}
+
+template <int B, int R, int NS, int NLD, int D>
+static int launch_q4k_ws_inst(GemvJob& j, const int* rows, hipStream_t s) {
+    constexpr size_t lds = Q4KWsLayout<B, R>::bytes;
+    auto kern = gemv_q4k_ws_kernel<B, R, NS, NLD, D>;
+    if (lds > 64 * 1024 && !lds_opt_in((const void*)kern))
+        return fail(GLLM_EDEVICE, "gemv: %zu B of LDS refused", lds);
+    hipLaunchKernelGGL(kern, dim3((rows[0] + R - 1) / R), dim3(R * 8 * NS + NLD * 64), lds, s,
+                       j.w[0], j.xf, j.out[0], rows[0], (int)j.rb);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
+// Batch-1 Q4_K of one weight that quantises x itself through the
+// wave-specialised kernel when the shape has an instance; *done = false
+// otherwise.
+static int launch_q4k_ws(GemvJob& j, const int* rows, hipStream_t s, bool* done) {
+    const Q4KWsShape sh = q4k_ws_pick(rows[0], j.blocks);
+    *done = sh.r != 0 && j.n == 1 && j.xf && j.cols <= kFuseCols && !j.nw && j.tok0 == 0;
+    if (!*done) return GLLM_OK;
+#define GLLM_WS_INST(b_, r_, ns_, nld_, d_)                                                \
+    if (j.blocks == b_ && sh.r == r_ && sh.ns == ns_ && sh.nld == nld_ && sh.d == d_) \
+        return launch_q4k_ws_inst<b_, r_, ns_, nld_, d_>(j, rows, s);
+    GLLM_WS_INST(16, 56, 2, 2, 1)
+#undef GLLM_WS_INST
+    return fail(GLLM_EINVAL, "gemv: no wave-specialised instance (%d, %d, %d, %d, %d)", j.blocks, sh.r,
+                sh.ns, sh.nld, sh.d);
+}
+
 template <int NT>
 int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t s) {
+    if (NT == 1 && type == GLLM_TYPE_Q4_K && j.ntok == 1) {
+        bool done = false;
+        GLLM_TRY(launch_q4k_ws(j, rows, s, &done));
+        if (done) return GLLM_OK;
+        GLLM_TRY(launch_q4k_bp(j, rows, s, &done));
+        if (done) return GLLM_OK;
+    }
     if (type == GLLM_TYPE_Q4_K) {
         int total = 0;
         for (int i = 0; i < j.n; i++) total += rows[i];
@@ -1585,7 +2077,7 @@ int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* 
     }
     j.wg_begin[n] = wg;
     if (wg == 0) return GLLM_OK;
-    if (w0->type == GLLM_TYPE_Q4_K && p >= mfma_min_tok()) {
+    if (w0->type == GLLM_TYPE_Q4_K && p >= kMfmaMinTok) {
         // batched prefill: matrix-core products, same bits as the row kernel
         for (int i = 0; i < n; i++)
             GLLM_TRY(launch_q4k_mfma(ws[i]->d_data, ws[i]->row_bytes, ws[i]->rows, ws[i]->blocks,

@@ -217,13 +217,67 @@ __device__ __forceinline__ int sdot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
+// DPP lane moves: a VALU operand modifier, no LDS round trip (a shuffle
+// through ds_bpermute waits out an LDS access per step).  CTRL: quad_perm
+// 0x00-0xFF, row_shl:n 0x100 + n (lane i of a 16-lane row reads lane i + n;
+// lanes past the row end read 0), row_mirror 0x140 (lane i reads 15 - i),
+// row_half_mirror 0x141 (lane i reads 7 - i of its 8-lane half).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+constexpr int kQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int kQuadXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+constexpr int kRowShl4 = 0x104;
+constexpr int kRowShl8 = 0x108;
+constexpr int kRowMirror = 0x140;
+constexpr int kRowHalfMirror = 0x141;
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+
+// Maximum of unsigned values over the 64 lanes of a wave (every lane
+// active), returned as a wave-uniform value.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t a) {
+    a = max(a, dpp_u<0xB1>(a));   // quad_perm [1, 0, 3, 2]
+    a = max(a, dpp_u<0x4E>(a));   // quad_perm [2, 3, 0, 1]
+    a = max(a, dpp_u<0x141>(a));  // row_half_mirror: 8-lane halves
+    a = max(a, dpp_u<0x140>(a));  // row_mirror: 16-lane rows
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)a, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)a, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)a, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)a, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Maximum over the 64 lanes of a wave (every lane active), in every lane.
+// v_max_f32 is IEEE maxNum: a NaN operand is skipped, and the result does
+// not depend on the order of the comparisons.
+__device__ __forceinline__ float wave_max(float a) {
+    a = fmaxf(a, dpp_f<kQuadXor1>(a));
+    a = fmaxf(a, dpp_f<kQuadXor2>(a));
+    a = fmaxf(a, dpp_f<kRowHalfMirror>(a));  // 8-lane halves
+    a = fmaxf(a, dpp_f<kRowMirror>(a));      // 16-lane rows
+    return fmaxf(fmaxf(readlane_f(a, 0), readlane_f(a, 16)),
+                 fmaxf(readlane_f(a, 32), readlane_f(a, 48)));
+}
+
 // 8-lane horizontal tree of the reference's VEXTRACTF128 / VADDPS /
 // VHADDPS / VHADDPS sequence: a_k = v_k + v_{k+4}; (a0 + a1) + (a2 + a3).
-// Lanes k = 0..7 must be 8 consecutive lanes; lane k == 0 ends with the sum.
+// Lanes k = 0..7 must be 8 consecutive lanes starting at a multiple of 8;
+// lane k == 0 ends with the sum (lanes k = 1..3 hold partial sums, k >= 4
+// garbage).  DPP: k reads k + 4 (row_shl:4), then k ^ 1 and k ^ 2 (quad
+// permutes); the operands meet in exactly the reference's order.
 __device__ __forceinline__ float tree8(float v) {
-    v = v + __shfl_xor(v, 4, 8);
-    v = v + __shfl_xor(v, 1, 8);
-    v = v + __shfl_xor(v, 2, 8);
+    v = v + dpp_f<kRowShl4>(v);
+    v = v + dpp_f<kQuadXor1>(v);
+    v = v + dpp_f<kQuadXor2>(v);
     return v;
 }
 
@@ -325,9 +379,7 @@ __device__ inline void silu_q8_block(const float* gate, const float* up, int b, 
         }
         v = silu_mul(gv, uv);
         sx[e] = v;
-        float m = fabsf(v);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float m = wave_max(fabsf(v));
         if ((e & 63) == 0) wmax[e >> 6] = m;
     }
     __syncthreads();

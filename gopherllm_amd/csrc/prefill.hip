@@ -316,44 +316,12 @@ static void launch_pf(const PfArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((prefill_q4k_mfma_kernel<RW, TW>), grid, dim3(64 * RW * TW), 0, s, a);
 }
 
-// --- at most 16 activation rows (decode batches) ---------------------------
-// One workgroup of four waves per 16 weight rows; wave w computes the
-// products of blocks b = w, w + 4, ... (MFMA tiles of 16 rows x 16 tokens,
-// one per AVX2 lane k, straight from registers: lane (g, c) loads row c's
-// nibble dword g of every lane k and token c's q8 bytes 32k + 8g .. + 7),
-// and per group of four blocks the waves exchange the products through LDS
-// and run the float chains in block order, wave w the chains of lanes
-// k = 2w, 2w + 1 for the 16 x 16 (row, token) pairs.  The chains therefore
-// see the same operands in the same order as the row kernel's; only the
-// exact integer products are computed block-parallel.
+// One block's per-row and per-token factors of a 16 x 16 tile (rows 0..15,
+// tokens 0..15), shared by the waves of the 16-row kernels below.
 struct SbParams {  // one block's factors: rows 0..15 and tokens 0..15 of the tile
     float d[16], dmin[16], m[8][16];
     float xs[16], xsum[8][16];
 };
-struct SbOps {     // one block's operands in a lane's registers
-    uint32_t wd[8];
-    u4v hdr;
-    uint2 q8[8];
-    float xs;
-    f4v xsa, xsb;
-};
-
-__device__ __forceinline__ void sb_load(const PfArgs& a, const uint8_t* wrow, int tok, int g, int b,
-                                        SbOps& o) {
-    const int cols = a.blocks * 256;
-    b = min(b, a.blocks - 1);  // past the end: re-read the last block (not used)
-    const uint8_t* nib = wrow + q4k_nib_off(a.blocks, b) + 4 * g;
-#pragma unroll
-    for (int k = 0; k < 8; k++) o.wd[k] = *(const uint32_t*)(nib + 16 * k);
-    o.hdr = *(const u4v*)(wrow + q4k_hdr_off(b));
-    const int8_t* q = a.act.q8perm + (size_t)tok * cols + (size_t)b * 256 + 8 * g;
-#pragma unroll
-    for (int k = 0; k < 8; k++) o.q8[k] = *(const uint2*)(q + 32 * k);
-    o.xs = a.act.xscale[(size_t)tok * a.blocks + b];
-    o.xsa = *(const f4v*)(a.act.xs32 + (size_t)tok * (cols / 32) + b * 8);
-    o.xsb = *(const f4v*)(a.act.xs32 + (size_t)tok * (cols / 32) + b * 8 + 4);
-}
-
 // getScaleMinK4 (simd.go:1672-1677): 6-bit scale and min of sub-block j
 __device__ __forceinline__ void sb_scale_min(const u4v h, int j, uint32_t& sc, uint32_t& mn) {
     const uint32_t s03 = h.y, s47 = h.z, s811 = h.w;
@@ -365,132 +333,6 @@ __device__ __forceinline__ void sb_scale_min(const u4v h, int j, uint32_t& sc, u
         const uint32_t b8 = (s811 >> (8 * jj)) & 0xffu;
         sc = (b8 & 15u) | (((s03 >> (8 * jj + 6)) & 3u) << 4);
         mn = (b8 >> 4) | (((s47 >> (8 * jj + 6)) & 3u) << 4);
-    }
-}
-
-// NW waves per workgroup (4 or 8): wave w computes the products of blocks
-// w, w + NW, ... and runs the chains of AVX2 lanes KK w .. KK w + KK - 1
-// (KK = 8 / NW); DEPTH blocks in flight per wave (register ring).
-template <int NW, int DEPTH>
-__global__ __launch_bounds__(64 * NW) void prefill_q4k_b16_kernel(PfArgs a) {
-    constexpr int KK = 8 / NW;
-    constexpr int kSbDepth = DEPTH;
-    __shared__ __align__(16) f4v sdI[NW][8][64];  // [wave][lane k][MFMA lane] products
-    __shared__ __align__(16) SbParams sp[NW];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int g = lane >> 4, c = lane & 15;
-    const int row0 = blockIdx.x * 16;
-    const uint8_t* wrow = a.w + (size_t)min(row0 + c, a.rows - 1) * a.rb;  // A row of this lane
-    const int tok = min(c, a.p - 1);                                         // B token of this lane
-    const int nb = a.blocks;
-    float accF[KK][4], accM[KK][4];
-#pragma unroll
-    for (int kk = 0; kk < KK; kk++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) accF[kk][i] = accM[kk][i] = 0.0f;
-    // wave w's blocks w, w + NW, ...: kSbDepth of them in flight, each
-    // refilled as soon as it is used (loads unconditional, clamped)
-    SbOps ring[kSbDepth];
-#pragma unroll
-    for (int d = 0; d < kSbDepth; d++) sb_load(a, wrow, tok, g, w + NW * d, ring[d]);
-    auto group = [&](int q0, SbOps& cur) __attribute__((always_inline)) {
-        const int b = q0 + w;
-        // straight-line for every wave (a block past the end re-reads the
-        // last block and its products are never read), so the compiler's
-        // vmcnt waits count exactly and the ring's later blocks stay in flight
-        {
-            uint32_t sc_lo, sc_hi, mn;
-            sb_scale_min(cur.hdr, 2 * g, sc_lo, mn);
-            sb_scale_min(cur.hdr, 2 * g + 1, sc_hi, mn);
-            const _Float16 hl = (_Float16)(float)sc_lo, nl = (_Float16)(-1024.0f * (float)sc_lo);
-            const _Float16 hh = (_Float16)(float)sc_hi, nh = (_Float16)(-1024.0f * (float)sc_hi);
-            const uint32_t bl = __builtin_bit_cast(uint16_t, hl), bnl = __builtin_bit_cast(uint16_t, nl);
-            const uint32_t bh = __builtin_bit_cast(uint16_t, hh), bnh = __builtin_bit_cast(uint16_t, nh);
-            const uint32_t sh_lo = bl | (bl << 16), sn_lo = bnl | (bnl << 16);
-            const uint32_t sh_hi = bh | (bh << 16), sn_hi = bnh | (bnh << 16);
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const h8v av = dequant_a(cur.wd[k], sh_lo, sn_lo, sh_hi, sn_hi);
-                uint32_t v[4];
-                i8x4_to_h(cur.q8[k].x, v[0], v[1]);
-                i8x4_to_h(cur.q8[k].y, v[2], v[3]);
-                const h8v bv = __builtin_bit_cast(h8v, u4v{v[0], v[1], v[2], v[3]});
-                const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
-                sdI[w][k][lane] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, z, 0, 0, 0);
-            }
-            if (g == 0) {
-                sp[w].d[c] = f16_bits_to_f32(cur.hdr.x & 0xffffu);
-                sp[w].dmin[c] = f16_bits_to_f32(cur.hdr.x >> 16);
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    uint32_t scj, mnj;
-                    sb_scale_min(cur.hdr, j, scj, mnj);
-                    sp[w].m[j][c] = (float)mnj;
-                }
-            } else if (g == 1) {
-                sp[w].xs[c] = cur.xs;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    sp[w].xsum[k][c] = cur.xsa[k];
-                    sp[w].xsum[4 + k][c] = cur.xsb[k];
-                }
-            }
-        }
-        sb_load(a, wrow, tok, g, b + NW * kSbDepth, cur);
-        wait_lgkm0();
-        lds_barrier();
-        // the group's blocks in order: chains of lanes k = KK w .. for
-        // rows 4g + i and token c (the MFMA D layout of this lane)
-#pragma unroll
-        for (int u = 0; u < NW; u++) {
-            if (q0 + u >= nb) break;  // uniform
-            const SbParams& P = sp[u];
-            const f4v d4 = *(const f4v*)&P.d[4 * g];
-            const f4v dm4 = *(const f4v*)&P.dmin[4 * g];
-            const float xs = P.xs[c];
-            float dxs[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) dxs[i] = d4[i] * xs;
-#pragma unroll
-            for (int kk = 0; kk < KK; kk++) {
-                const int k = KK * w + kk;
-                const f4v dI = sdI[u][k][lane];
-                const f4v m4 = *(const f4v*)&P.m[k][4 * g];
-                const float xk = P.xsum[k][c];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    accF[kk][i] = fmaf(dI[i], dxs[i], accF[kk][i]);
-                    const float mx = m4[i] * xk;
-                    accM[kk][i] = fmaf(dm4[i], mx, accM[kk][i]);
-                }
-            }
-        }
-        wait_lgkm0();
-        lds_barrier();
-    };
-#pragma unroll 1
-    for (int q0 = 0; q0 < nb; q0 += NW * kSbDepth) {
-#pragma unroll
-        for (int d = 0; d < kSbDepth; d++) group(q0 + NW * d, ring[d]);
-    }
-    // tree8 over the lanes k (held by the four waves) through LDS
-    float* vb = (float*)&sdI[0][0][0];  // [k][MFMA lane][row i]
-#pragma unroll
-    for (int kk = 0; kk < KK; kk++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) vb[((KK * w + kk) * 64 + lane) * 4 + i] = accF[kk][i] - accM[kk][i];
-    __syncthreads();
-    if (w == 0 && c < a.p) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = row0 + 4 * g + i;
-            if (r >= a.rows) continue;
-            float v[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) v[k] = vb[(k * 64 + lane) * 4 + i];
-            const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
-            a.out[(size_t)c * a.out_stride + r] = (s0 + s1) + (s2 + s3);
-        }
     }
 }
 
@@ -799,19 +641,14 @@ __global__ __launch_bounds__(512) void prefill_q4k_tiled_kernel(PfArgs a, TlMap 
     }
 }
 
-static bool q4k_tiled_on() {
-    static const bool on = [] {
-        const char* e = getenv("GLLM_Q4K_TILED");
-        return !(e && e[0] == '0');
-    }();
-    return on;
-}
-
 // --- at most 16 activation rows, operands through a per-wave LDS ring -----
-// prefill_q4k_b16_kernel's arithmetic (MFMA products of a block per wave,
-// exchanged through LDS, chains in block order), with each wave's operands
-// copied global -> LDS by the wave itself, DEPTH blocks ahead, in layouts
-// that make every MFMA operand read of a wave conflict-free:
+// One workgroup per 16 weight rows; wave w computes the MFMA products of
+// blocks b = w, w + NW, ... (16-row x 16-token tiles, one per AVX2 lane k),
+// the waves exchange the exact products through LDS per group of blocks and
+// run the float chains in block order (only the integer products are
+// block-parallel, so the bits are the row kernel's).  Each wave copies its
+// own operands global -> LDS, DEPTH blocks ahead, in layouts that make every
+// MFMA operand read of a wave conflict-free:
 //   nib [lane k][row c][16 bytes]   (lane (g, c) reads dword g: consecutive)
 //   q8  [lane k][token t][32 bytes] (lane (g, c) reads 8 bytes at 8 g)
 // The copies are inline-asm global_load_lds, so their vmcnt waits are
@@ -1156,68 +993,32 @@ static bool launch_b16s(const PfArgs& a, hipStream_t s) {
     return true;
 }
 
+
 // Kernel choice.  More than 16 activation rows: the 64 x 64 staged tile
-// (prefill_q4k_tiled_kernel; GLLM_Q4K_TILED=0 selects the older 64 rows x 32
-// tokens kernel, for measurement, same bits).  At most 16 rows (a decode
-// batch): 64 rows x 16 tokens; the per-block staging (q8 to f16, scale
-// decoding) is a fixed cost per workgroup, so 64 rows per workgroup beat
-// smaller tiles that would fill more CUs (measured at batch 8: 22.8 vs 28.4
-// us for 14336 x 4096), except where 64-row tiles leave a third of the CUs
-// idle: there prefill_q4k_b16_kernel (16-row tiles) runs unless
-// GLLM_Q4K_B16=0.
-static bool q4k_b16_on() {
-    static const bool on = [] {
-        const char* e = getenv("GLLM_Q4K_B16");
-        return !(e && e[0] == '0');
-    }();
-    return on;
-}
-
-// Lane-pair kernel at up to 8 tokens (GLLM_B16P=0 runs the per-lane ring
-// kernel instead, for measurement; same bits).  Batch 8, one sweep: 4096 x
-// 14336 26.2 / 25.5 / 26.9 us (per-lane ring / pairs, ring of 2 / pairs,
-// ring of 3), 4096 x 4096 11.8 / 11.3 / 12.0 us.
-static bool q4k_b16p_on() {
-    static const bool on = [] {
-        const char* e = getenv("GLLM_B16P");
-        return !(e && e[0] == '0');
-    }();
-    return on;
-}
-
-// GLLM_Q4K_B16S=0 keeps the register-ring 16-row kernel (measurement; same
-// bits).
-static bool q4k_b16s_on() {
-    static const bool on = [] {
-        const char* e = getenv("GLLM_Q4K_B16S");
-        return !(e && e[0] == '0');
-    }();
-    return on;
-}
-
+// (prefill_q4k_tiled_kernel).  At most 16 rows (a decode batch): 64 rows x
+// 16 tokens (prefill_q4k_mfma_kernel); the per-block staging (q8 to f16,
+// scale decoding) is a fixed cost per workgroup, so 64 rows per workgroup
+// beat smaller tiles that would fill more CUs (measured at batch 8: 22.8 vs
+// 28.4 us for 14336 x 4096), except where 64-row tiles leave a third of the
+// CUs idle: there 16-row tiles with block-parallel waves and operands in
+// per-wave LDS rings (prefill_q4k_b16p_kernel up to 8 tokens, four-wave
+// prefill_q4k_b16s_kernel at 9-16).  The tiled and ring kernels address a
+// weight with 32-bit offsets.
 int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
                     float* out, int out_stride, hipStream_t s) {
     if (rows <= 0 || blocks <= 0 || p <= 0) return GLLM_OK;
     PfArgs a{d_w, rb, rows, blocks, act, p, out, out_stride};
-    if (p > kTiledMinP && act.b16t && q4k_tiled_on() && (size_t)rows * rb < ((size_t)1 << 32)) {
+    const bool fits = (size_t)rows * rb < ((size_t)1 << 32);
+    if (p > kTiledMinP) {
+        if (!act.b16t || !fits)
+            return fail(GLLM_EINVAL, "prefill: %d rows of %zu B need f16 tiles and < 4 GiB", rows, rb);
         const TlMap mp = tl_map(rows, p);
         const int grid = 8 * mp.tg_size * mp.rg_size;
         hipLaunchKernelGGL(prefill_q4k_tiled_kernel, dim3(grid), dim3(512), 0, s, a, mp);
-    } else if (p > 16) {
-        launch_pf<4, 2>(a, s);
-    } else if (q4k_b16_on() && (rows + 63) / 64 < 2 * device_cus() / 3) {
-        // the 64-row tile leaves CUs idle: 16-row tiles, block-parallel
-        // waves, operands through per-wave LDS
-        // rings (eight waves at up to 8 tokens, four at 9-16, as the LDS
-        // allows); the register-ring kernel where the ring kernel cannot run
-        const bool fits = (size_t)rows * rb < ((size_t)1 << 32);
-        const bool done = fits && q4k_b16s_on() &&
-                          (p > 8 ? launch_b16s<4, 3, 16>(a, s)
-                           : q4k_b16p_on() ? launch_b16p<2>(a, s)
-                                           : launch_b16s<8, 2, 8>(a, s));
-        if (!done)
-            hipLaunchKernelGGL((prefill_q4k_b16_kernel<4, 1>), dim3((rows + 15) / 16), dim3(256), 0,
-                               s, a);
+    } else if ((rows + 63) / 64 < 2 * device_cus() / 3) {
+        if (!fits) return fail(GLLM_EINVAL, "prefill: weights of %zu B past 4 GiB", (size_t)rows * rb);
+        const bool done = p > 8 ? launch_b16s<4, 3, 16>(a, s) : launch_b16p<2>(a, s);
+        if (!done) return fail(GLLM_EDEVICE, "prefill: the LDS of the 16-row kernel was refused");
     } else {
         launch_pf<4, 1>(a, s);
     }

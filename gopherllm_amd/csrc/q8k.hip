@@ -74,9 +74,7 @@ __global__ __launch_bounds__(256) void q8k_prep_kernel(const float* __restrict__
     sx[e] = v;
     // amax over the block; v_max_f32 is IEEE maxNum, so a NaN element is
     // skipped exactly like the reference's `a > amax` scan.
-    float m = fabsf(v);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float m = wave_max(fabsf(v));
     if ((e & 63) == 0) wmax[e >> 6] = m;
     __syncthreads();
     const float amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
