@@ -11,6 +11,6 @@ from ._lib import (TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, TYPE_Q4_0, TYPE_Q4_1, TYPE_Q
 from .api import (KVCacheF16, Weight, act_bytes, available, q8k_prepare_dev, fill_normal_dev, matvec2_into,  # noqa: F401
                   matvec3_into, matvec_multi_dev, matvec_q4k_into, matvec_q6k_into,
                   matvec_q8_0_into, q8k_quantize_dev, quantize_rows_dev, row_bytes,
-                  swiglu_down_dev)
+                  stream_release, swiglu_down_dev)
 
 __all__ = [n for n in dir() if not n.startswith("_")]

@@ -40,6 +40,7 @@ SIGNATURES = {
     "gllm_hip_last_error": (C.c_char_p, []),
     "gllm_hip_set_device": (i32, [i32]),
     "gllm_hip_version": (C.c_char_p, []),
+    "gllm_hip_stream_release": (i32, [vp]),
     "gllm_hip_weight_new": (vp, [vp, sz, i32, i32, i32]),
     "gllm_hip_weight_from_device": (vp, [vp, sz, i32, i32, i32, vp]),
     "gllm_hip_weight_release": (None, [vp]),

@@ -83,6 +83,13 @@ def available() -> bool:
     return bool(load().gllm_hip_available())
 
 
+def stream_release(stream=None):
+    """The caller will enqueue no more work on `stream` (default: torch's
+    current stream): the calling thread's scratch for it is freed once it
+    drains, except buffers a captured graph may still use."""
+    call("gllm_hip_stream_release", _stream(stream))
+
+
 class Weight:
     """A quantized GGUF tensor resident in HBM (prepareMetalWeight, model.go:2454)."""
 

@@ -1022,8 +1022,8 @@ bool attend_exact_graphable(const gllm_hip_kv* kv, int n_heads, int n_kv, int hd
            span_cap <= kSmaxSpan1;
 }
 
-// scratch: p * n_heads * span_max floats of device memory, or null for the
-// calling thread's scratch.  d_end (with p == 1): the end position is read
+// scratch: p * n_heads * (span_max + 1) + 64 floats of device memory, or
+// null for the calling thread's scratch.  d_end (with p == 1): the end position is read
 // on the device and span_cap bounds the span, so the launches do not depend
 // on the position (a captured decode step replays for every position).
 int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
@@ -1091,7 +1091,8 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
         GLLM_HIP(hipGetLastError());
         return GLLM_OK;
     }
-    float* scr = (float*)thread_scratch(5, ((size_t)p * n_heads * (span_max + 1) + 64) * 4, s);
+    float* scr = scratch ? scratch
+                         : (float*)thread_scratch(5, ((size_t)p * n_heads * (span_max + 1) + 64) * 4, s);
     if (!scr) return scratch_error();
     float* scores = scr;
     float* inv = scr + (size_t)p * n_heads * span_max;

@@ -686,6 +686,26 @@ __global__ __launch_bounds__(FUSE || NL <= 8 ? 1024 : 512) void gemv_q4k_kernel(
         // the barrier, then one system-scope counter increment per
         // workgroup; the last workgroup reads the block with system-scope
         // loads.  No cache-wide writeback or invalidate is needed.
+        //
+        // Memory model.  In HIP terms the counter is a relaxed atomic, which
+        // orders nothing; the handoff rests on what gfx950 does with these
+        // instructions instead:
+        //  * a system-scope relaxed store is a global_store with sc0 sc1:
+        //    it writes through the XCD's L2 to memory (MALL / HBM), and its
+        //    vmcnt decrement means memory has acknowledged it;
+        //  * s_waitcnt vmcnt(0) in every thread, then s_barrier, so the
+        //    counter's atomic (issued after the barrier) leaves the CU only
+        //    once all 256 rows of this workgroup's stores are in memory;
+        //  * the system-scope atomic add executes at memory, so the workgroup
+        //    that reads total - 1 from it does so after every other
+        //    workgroup's rows were acknowledged there;
+        //  * that workgroup's system-scope loads (sc0 sc1) miss the
+        //    non-coherent L2 copies and read memory.
+        // A release / acquire pair at agent scope would give the same order
+        // through the HIP model, but on this part it writes back (release)
+        // and invalidates (acquire) the whole XCD L2: 36 us per launch
+        // against 18.4 us for this form.  The decode parity tests
+        // (tests/test_gpu_model.py, the SwiGLU epilogue cases) exercise it.
         const int blk = (((int)blockIdx.x - j.wg_begin[wi]) * j.rows_per_wg) / 256;
         wait_vmem_le<0>();  // this thread's output stores have completed
         __syncthreads();
@@ -2766,6 +2786,8 @@ std::string g_check_msg[64];
 
 }  // namespace
 
+int noalloc_prepare();
+
 int self_check() {
     int d = 0;
     if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) {
@@ -2782,6 +2804,9 @@ int self_check() {
         if (rc == GLLM_OK) rc = check_format(GLLM_TYPE_Q4_K, 1024, 3, plant);
         if (rc == GLLM_OK) rc = check_format(GLLM_TYPE_Q6_K, 512, 1, plant);
         if (rc == GLLM_OK) rc = check_format(GLLM_TYPE_Q8_0, 1024, 3, plant);
+        // the allocation-free entry point's device scratch, looked up now,
+        // outside any capture a caller may start later
+        if (rc == GLLM_OK) rc = noalloc_prepare();
         if (rc == GLLM_OK) {
             g_check_state[d] = 1;
         } else {

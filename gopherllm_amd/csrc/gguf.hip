@@ -674,9 +674,12 @@ gllm_hip_model* gllm_hip_model_from_gguf(const gllm_hip_gguf* g, int max_len) {
     // non-default value is refused rather than decoded into other tokens.
     auto present = [&](const char* k) { return find_meta(g, k) != nullptr; };
     const char* why = nullptr;
-    if (present("llama.rope.dimension_count") &&
-        (int)u32("llama.rope.dimension_count", 0) != c.head_dim)
-        why = "llama.rope.dimension_count != head_dim (partial rotary)";
+    // buildRopeInvFreq (model.go:1729-1732) rotates the whole head when the
+    // count is <= 0 or above head_dim; only 0 < count < head_dim (partial
+    // rotary) changes the graph
+    const int rope_dim = (int)u32("llama.rope.dimension_count", 0);
+    if (present("llama.rope.dimension_count") && rope_dim > 0 && rope_dim < c.head_dim)
+        why = "llama.rope.dimension_count below head_dim (partial rotary)";
     else if (present("llama.attention.value_length") &&
              (int)u32("llama.attention.value_length", 0) != c.head_dim)
         why = "llama.attention.value_length != head_dim";

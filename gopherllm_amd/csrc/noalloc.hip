@@ -41,8 +41,10 @@ constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 void* g_scratch_dev[kMaxDevices];  // device address of `scratch` on each GPU
 
-// Device address of this GPU's copy of `scratch`, looked up on the first
-// call on that device (with it current).  Null with the error set on failure.
+// Device address of this GPU's copy of `scratch`, looked up once per device
+// with it current: by the device's load-time check (noalloc_prepare), which
+// runs before its first weight exists, so never inside a caller's capture.
+// Null with the error set on failure.
 void* device_scratch() {
     int d = 0;
     if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= kMaxDevices) {
@@ -66,6 +68,12 @@ void* device_scratch() {
 }
 
 }  // namespace
+
+namespace gllm {
+// Resolves this device's address of `scratch` (and so loads this file's code
+// object) ahead of any call: the device's load-time check calls it.
+int noalloc_prepare() { return device_scratch() ? GLLM_OK : GLLM_EDEVICE; }
+}  // namespace gllm
 
 using namespace gllm;
 

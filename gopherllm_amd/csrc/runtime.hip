@@ -44,25 +44,30 @@ constexpr int kScratchSlots = 12;
 // Device scratch of one (host thread, stream) pair.  Work enqueued on one
 // stream runs in order, so slots keyed by the stream never serve two
 // concurrent kernels; two streams of one thread (a Go scheduler thread
-// running two Runners) get separate slots.
+// running two Runners) get separate slots.  in_graph: the slot's buffer was
+// handed out while the stream was capturing, so a graph may still use it.
 struct StreamScratch {
     void* p[kScratchSlots] = {};
     size_t n[kScratchSlots] = {};
+    bool in_graph[kScratchSlots] = {};
 };
 
-struct ThreadRes {
-    int device = -1;
+// Resources of one (host thread, device).  A buffer replaced by a larger one
+// is freed once its stream has drained, unless a captured graph may hold it
+// (then it goes to `retired` and stays allocated: the graph can be replayed
+// at any time).  Growth is geometric, so those total at most a few times the
+// largest.
+struct DeviceRes {
     hipStream_t stream = nullptr;
     std::unordered_map<hipStream_t, StreamScratch> scratch;
-    // Buffers replaced by a larger one.  Work already enqueued, or a graph a
-    // caller captured earlier, may still read them, so they are never freed
-    // (growth is geometric, so they total at most a few times the largest).
     std::vector<void*> retired;
     void* pinned[kScratchSlots] = {};
     size_t pinned_n[kScratchSlots] = {};
 };
 
-thread_local ThreadRes t_res;
+// Per device, so switching devices keeps (and later reuses) each device's
+// buffers instead of dropping them.
+thread_local std::unordered_map<int, DeviceRes> t_devs;
 thread_local int t_scratch_code = GLLM_ENOMEM;
 
 int current_device() {
@@ -73,19 +78,7 @@ int current_device() {
 
 // Buffers are kept for the thread's lifetime and never freed at exit: the
 // HIP runtime may already be torn down when thread_local destructors run.
-void reset_if_device_changed() {
-    int d = current_device();
-    if (t_res.device != d) {
-        t_res.scratch.clear();
-        t_res.retired.clear();
-        t_res.stream = nullptr;
-        for (int i = 0; i < kScratchSlots; i++) {
-            t_res.pinned[i] = nullptr;
-            t_res.pinned_n[i] = 0;
-        }
-        t_res.device = d;
-    }
-}
+DeviceRes& res() { return t_devs[current_device()]; }
 
 }  // namespace
 
@@ -104,27 +97,28 @@ int device_cus() {
 }
 
 hipStream_t thread_stream() {
-    reset_if_device_changed();
-    if (!t_res.stream) {
-        if (hipStreamCreateWithFlags(&t_res.stream, hipStreamNonBlocking) != hipSuccess) {
-            t_res.stream = nullptr;
+    DeviceRes& r = res();
+    if (!r.stream) {
+        if (hipStreamCreateWithFlags(&r.stream, hipStreamNonBlocking) != hipSuccess) {
+            r.stream = nullptr;
             set_error("hipStreamCreateWithFlags failed");
         }
     }
-    return t_res.stream;
+    return r.stream;
 }
 
 void* thread_scratch(int slot, size_t bytes, hipStream_t stream) {
-    reset_if_device_changed();
     if (slot < 0 || slot >= kScratchSlots) return nullptr;
-    StreamScratch& sc = t_res.scratch[stream];
+    DeviceRes& r = res();
+    StreamScratch& sc = r.scratch[stream];
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) (void)hipGetLastError();
+    const bool capturing = cs != hipStreamCaptureStatusNone;
     if (sc.n[slot] < bytes) {
         // Growing allocates; under stream capture that would either fail or
         // leave the captured graph holding a pointer this thread later
         // replaces.  The caller sizes the slot with one uncaptured call first.
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(stream, &cs) != hipSuccess) (void)hipGetLastError();
-        if (cs != hipStreamCaptureStatusNone) {
+        if (capturing) {
             t_scratch_code = GLLM_EUNSUP;
             set_error("scratch slot %d would grow to %zu bytes inside a stream capture; make the "
                       "same call once outside the capture first", slot, bytes);
@@ -138,33 +132,63 @@ void* thread_scratch(int slot, size_t bytes, hipStream_t stream) {
             set_error("hipMalloc(%zu) for scratch failed", n);
             return nullptr;
         }
-        if (sc.p[slot]) t_res.retired.push_back(sc.p[slot]);
+        if (sc.p[slot]) {
+            if (sc.in_graph[slot]) {
+                r.retired.push_back(sc.p[slot]);
+            } else if (hipStreamSynchronize(stream) == hipSuccess) {
+                // work already enqueued on this stream was its only user
+                (void)hipFree(sc.p[slot]);
+            } else {
+                (void)hipGetLastError();
+                r.retired.push_back(sc.p[slot]);
+            }
+        }
         sc.p[slot] = p;
         sc.n[slot] = n;
+        sc.in_graph[slot] = false;
     }
+    if (capturing) sc.in_graph[slot] = true;
     return sc.p[slot];
+}
+
+// The caller is done with `stream` (it will not enqueue on it again): its
+// scratch buffers are freed after the stream drains, except those a
+// captured graph may still use.
+int release_stream_scratch(hipStream_t stream) {
+    DeviceRes& r = res();
+    auto it = r.scratch.find(stream);
+    if (it == r.scratch.end()) return GLLM_OK;
+    const bool synced = hipStreamSynchronize(stream) == hipSuccess;
+    if (!synced) (void)hipGetLastError();
+    for (int i = 0; i < kScratchSlots; i++) {
+        if (!it->second.p[i]) continue;
+        if (it->second.in_graph[i] || !synced) r.retired.push_back(it->second.p[i]);
+        else (void)hipFree(it->second.p[i]);
+    }
+    r.scratch.erase(it);
+    return synced ? GLLM_OK : fail(GLLM_EDEVICE, "stream release: synchronisation failed");
 }
 
 int scratch_error() { return t_scratch_code; }
 
 void* thread_pinned(int slot, size_t bytes) {
-    reset_if_device_changed();
     if (slot < 0 || slot >= kScratchSlots) return nullptr;
-    if (t_res.pinned_n[slot] < bytes) {
-        if (t_res.pinned[slot]) (void)hipHostFree(t_res.pinned[slot]);
+    DeviceRes& r = res();
+    if (r.pinned_n[slot] < bytes) {
+        if (r.pinned[slot]) (void)hipHostFree(r.pinned[slot]);
         size_t n = bytes < 4096 ? 4096 : bytes + bytes / 4;
         void* p = nullptr;
         if (hipHostMalloc(&p, n, hipHostMallocDefault) != hipSuccess) {
             (void)hipGetLastError();
-            t_res.pinned[slot] = nullptr;
-            t_res.pinned_n[slot] = 0;
+            r.pinned[slot] = nullptr;
+            r.pinned_n[slot] = 0;
             set_error("hipHostMalloc(%zu) failed", n);
             return nullptr;
         }
-        t_res.pinned[slot] = p;
-        t_res.pinned_n[slot] = n;
+        r.pinned[slot] = p;
+        r.pinned_n[slot] = n;
     }
-    return t_res.pinned[slot];
+    return r.pinned[slot];
 }
 
 }  // namespace gllm
@@ -201,5 +225,7 @@ int gllm_hip_set_device(int device) {
 }
 
 const char* gllm_hip_version(void) { return "gopherllm-mi355x 0.1 (gfx950)"; }
+
+int gllm_hip_stream_release(void* stream) { return release_stream_scratch((hipStream_t)stream); }
 
 }  // extern "C"

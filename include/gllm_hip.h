@@ -84,6 +84,14 @@ const char* gllm_hip_last_error(void);
 int gllm_hip_set_device(int device);
 /* Library version string, for logs. */
 const char* gllm_hip_version(void);
+/* The caller will enqueue no more work on `stream` (a hipStream_t; null is
+ * the legacy default stream): the calling thread's scratch buffers for that
+ * stream on the current device are freed once the stream drains, except
+ * those handed out while the stream was being captured (a captured graph
+ * may still be replayed; they stay allocated).  No counterpart in the
+ * reference, whose CPU kernels have no streams; for callers that create and
+ * destroy many streams, so that their scratch does not accumulate. */
+int gllm_hip_stream_release(void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Weights (prepareMetalWeight, model.go:2454; gllm_metal_new_q4k,         */

@@ -284,15 +284,18 @@ def test_model_from_gguf_refuses_graph_changing_keys(tmp_path, key, value):
     f.close()
 
 
-def test_model_from_gguf_accepts_default_valued_keys(tmp_path):
+@pytest.mark.parametrize("rope_dim", [("u32", 64), ("u32", 0), ("u32", 128), ("i32", -1)])
+def test_model_from_gguf_accepts_default_valued_keys(tmp_path, rope_dim):
     """The same keys at their defaults (rope over the whole head, value
     length = head_dim, unit scales, no window) pass the check: the call then
-    fails only where this host has no device, not on the key check."""
+    fails only where this host has no device, not on the key check.  A rope
+    dimension count of 0, below 0 or above head_dim means the whole head
+    (buildRopeInvFreq, model.go:1729-1732), so it passes too."""
     from conftest import tiny_llama
     from gopherllm_amd import _lib, gguf
     m = tiny_llama(seed=2, n_layers=1, dim=256, hidden=512, n_heads=4, n_kv_heads=1, head_dim=64,
                    vocab=300)
-    extra = {"llama.rope.dimension_count": gguf.MetaValue("u32", 64),
+    extra = {"llama.rope.dimension_count": gguf.MetaValue(*rope_dim),
              "llama.attention.value_length": gguf.MetaValue("u32", 64),
              "llama.residual_scale": gguf.MetaValue("f32", 1.0),
              "llama.logit_scale": gguf.MetaValue("f32", 1.0),
@@ -304,5 +307,5 @@ def test_model_from_gguf_accepts_default_valued_keys(tmp_path):
     if h:
         L.gllm_hip_model_release(h)
     else:
-        assert "not supported" not in _lib.last_error()
+        assert "not supported" not in _lib.last_error(), _lib.last_error()
     f.close()

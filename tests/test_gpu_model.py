@@ -254,3 +254,71 @@ def test_swiglu_epilogue_decode_matches_oracle(hip):
         assert np.array_equal(bits(gpu.hidden()), bits(hid)), pos
         assert got == want, pos
         tok = want
+
+
+def test_prompt_longer_than_one_prefill_chunk(hip):
+    """A 700-token prompt runs as two prefill chunks (512 + 188 tokens; the
+    second attends over the first chunk's KV rows), then 8 greedy steps:
+    tokens, the prompt's last logits and every KV row equal the oracle's."""
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = tiny_llama(seed=13, n_layers=2, dim=256, hidden=512, n_heads=4, n_kv_heads=1, head_dim=64,
+                   vocab=1200)
+    prompt = np.random.default_rng(14).integers(0, 1200, 700)
+    max_len = 768
+    print("700-token prompt, two chunks", flush=True)
+    gpu = LlamaDecoder.from_host_model(m, max_len)
+    cpu = ref.Llama(m, max_len)
+    gt, gl = gpu.prefill(prompt, want_logits=True)
+    ct, cl = cpu.prefill(prompt)
+    assert gt == ct
+    assert np.array_equal(bits(gl), bits(cl))
+    g2 = LlamaDecoder.from_host_model(m, max_len)
+    c2 = ref.Llama(m, max_len)
+    want = c2.generate(prompt, 8)
+    got = g2.generate(prompt, 8)
+    assert np.array_equal(got, want), (got, want)
+    kv = g2.kv_cache()
+    used = len(prompt) + 7
+    for l in range(2):
+        k, v = kv.read(l, 0, used)
+        assert np.array_equal(k, c2.kcache(l, max_len)[:used]), l
+        assert np.array_equal(v, c2.vcache(l, max_len)[:used]), l
+
+
+def test_prefill_crossing_position_6144(hip):
+    """A 300-token prefill at positions 6000..6299 over a cache whose rows
+    0..5999 hold the same random f16 K/V on both sides: its later tokens span
+    more than 6144 positions, where prefill attention takes the generic
+    scores / softmax / values kernels (in the model's scores buffer).  The
+    logits, the token, the new KV rows and 4 decode steps after it equal the
+    oracle's."""
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = tiny_llama(seed=15, n_layers=1, dim=256, hidden=512, n_heads=4, n_kv_heads=1, head_dim=64,
+                   vocab=1200)
+    max_len, start, n = 6400, 6000, 300
+    kvd = 64
+    rng = np.random.default_rng(16)
+    k = rng.standard_normal((start, kvd), dtype=np.float32)
+    v = rng.standard_normal((start, kvd), dtype=np.float32)
+    gpu = LlamaDecoder.from_host_model(m, max_len)
+    cpu = ref.Llama(m, max_len)
+    print(f"fill KV rows 0..{start - 1}", flush=True)
+    kv = gpu.kv_cache()
+    for p in range(start):
+        kv.store_kv(0, p, k[p], v[p])
+    cpu.set_kv(0, 0, ref.f32_to_f16(k), ref.f32_to_f16(v))
+    prompt = rng.integers(0, 1200, n)
+    print(f"prefill {n} tokens at {start}", flush=True)
+    gt, gl = gpu.prefill(prompt, start_pos=start, want_logits=True)
+    ct, cl = cpu.prefill(prompt, start_pos=start)
+    assert gt == ct
+    assert np.array_equal(bits(gl), bits(cl))
+    gk, gv = kv.read(0, 0, start + n)
+    assert np.array_equal(gk, cpu.kcache(0, max_len)[:start + n])
+    assert np.array_equal(gv, cpu.vcache(0, max_len)[:start + n])
+    tok = gt
+    for pos in range(start + n, start + n + 4):
+        want, hid = cpu.decode(tok, pos)
+        got = gpu.decode(tok, pos)
+        assert got == want, pos
+        tok = want

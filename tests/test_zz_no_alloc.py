@@ -99,3 +99,53 @@ def test_noalloc_captured_on_a_fresh_stream(hip):
         # an eager call in between overwrites the shared scratch
         assert _call(L, "gllm_hip_matvec_dev_noalloc", w, other, 4, junk, rows) == 0
         torch.cuda.synchronize()
+
+
+_FIRST_CALL_CAPTURED = r"""
+import sys, ctypes as C
+import numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[1] + "/tests")
+import gopherllm_amd as g
+from conftest import normal, quant_matrix
+from oracle import oracle as ref
+L = g.load()
+assert g.available(), g._lib.last_error()
+rows, cols, p = 1024, 4096, 4
+data, _ = quant_matrix(ref.Q4_K, rows, cols, 940)
+w = g.Weight.from_host(data, g.TYPE_Q4_K, rows, cols)
+x = torch.from_numpy(normal(941, (p, cols))).cuda()
+out = torch.zeros((p, rows), device="cuda")
+s = torch.cuda.Stream()
+gr = torch.cuda.CUDAGraph()
+with torch.cuda.graph(gr, stream=s):  # the process's first noalloc call
+    rc = L.gllm_hip_matvec_dev_noalloc(w.handle, C.c_void_p(x.data_ptr()), p,
+                                       C.c_void_p(out.data_ptr()), rows, C.c_void_p(s.cuda_stream))
+assert rc == 0, g._lib.last_error()
+want = ref.matvec_batch(ref.Q4_K, data, normal(941, (p, cols)), rows, cols)
+for i in range(3):
+    out.zero_()
+    gr.replay()
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32)), i
+print("first noalloc call captured: ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_a_capture():
+    """In a fresh process, the very first allocation-free call is made inside
+    a stream capture: the device scratch address was looked up by the
+    device's load-time check (before the weight existed), so the capture
+    holds no lookup, and three replays equal the oracle."""
+    import os
+    import subprocess
+    import sys
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("child process: first noalloc call under capture", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED, root], capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "first noalloc call captured: ok" in r.stdout
