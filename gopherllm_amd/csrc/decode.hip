@@ -55,6 +55,11 @@ int kv_store_dev_impl(gllm_hip_kv* kv, int l, int pos, const float* d_k, const f
 int launch_argmax(const float* logits, int n, uint32_t* token, unsigned long long* keys,
                   hipStream_t s, const uint32_t* recent, int n_recent, float penalty);
 size_t argmax_keys(int n);
+bool argmax_fusable(const gllm_hip_weight* w);
+size_t argmax_epilogue_keys(const gllm_hip_weight* w);
+int gemv_argmax_f32(gllm_hip_weight* w, const float* x, float* logits, unsigned long long* keys,
+                    uint32_t* token, const uint32_t* recent, int n_recent, float penalty,
+                    hipStream_t s);
 }  // namespace gllm
 
 struct gllm_hip_model {
@@ -76,6 +81,8 @@ struct gllm_hip_model {
     uint32_t* d_tokens = nullptr;
     uint32_t* h_tokens = nullptr;  // pinned
     unsigned long long* argmax_keys = nullptr;  // argmax_keys(vocab) entries
+    // the head's argmax keys: vocab / 8 + 8 >= argmax_epilogue_keys(output)
+    unsigned long long* head_keys = nullptr;
     void* act = nullptr;           // Q8K activation buffers
     size_t act_n = 0;
     float* scores = nullptr;       // attention scores, max_p * n_heads * (max_len + 1) + 64
@@ -410,10 +417,19 @@ static int model_argmax(gllm_hip_model* m, uint32_t* d_token) {
 }
 
 // One greedy decode step on the token in d_tokens[0]: forward, the output
-// projection (full logits), then the (penalised) argmax into d_tokens[1].
+// projection (full logits), then the (penalised) argmax into d_tokens[1]:
+// in the projection's launch when its kernel allows (argmax_epilogue),
+// otherwise as two more launches.
 static int decode_step(gllm_hip_model* m, int pos, const int* d_pos) {
     // the token rides in the position buffer's header (word 1): one upload
     GLLM_TRY(forward(m, pos, 1, true, d_pos, (const uint32_t*)m->d_pos + 1));
+    if (m->head_keys && argmax_fusable(m->output) &&
+        argmax_epilogue_keys(m->output) <= (size_t)m->cfg.vocab / 8 + 8) {
+        const bool on = penalty_on(m);
+        return gemv_argmax_f32(m->output, m->xn, m->logits, m->head_keys, m->d_tokens + 1,
+                               on ? m->d_recent : nullptr, on ? m->window : 0, m->penalty,
+                               m->stream);
+    }
     gllm_hip_weight* ws[1] = {m->output};
     float* outs[1] = {m->logits};
     GLLM_TRY(matvec(m, 1, ws, m->xn, 1, outs));
@@ -500,6 +516,10 @@ gllm_hip_model* gllm_hip_model_new(const gllm_hip_model_config* cfg) {
         return bail("SwiGLU counters");
     if (hipMalloc(&m->argmax_keys, argmax_keys(cfg->vocab) * 8) != hipSuccess)
         return bail("argmax keys");
+    // one key per workgroup of the head's launch: ceil(vocab / (32 / G)) for
+    // G in {1, 2, 4}, at most vocab / 8 + 1
+    if (hipMalloc(&m->head_keys, ((size_t)cfg->vocab / 8 + 8) * 8) != hipSuccess)
+        return bail("head argmax keys");
     if (hipMalloc(&m->d_pos, pos_bytes(*cfg)) != hipSuccess) return bail("position");
     if (hipHostMalloc(&m->h_pos, pos_bytes(*cfg), hipHostMallocDefault) != hipSuccess)
         return bail("position");
@@ -517,6 +537,7 @@ void gllm_hip_model_release(gllm_hip_model* m) {
     if (m->h_tokens) (void)hipHostFree(m->h_tokens);
     if (m->act) (void)hipFree(m->act);
     if (m->argmax_keys) (void)hipFree(m->argmax_keys);
+    if (m->head_keys) (void)hipFree(m->head_keys);
     drop_decode_graph(m);
     if (m->scores) (void)hipFree(m->scores);
     if (m->d_pos) (void)hipFree(m->d_pos);

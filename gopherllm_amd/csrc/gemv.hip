@@ -31,6 +31,13 @@ bool float_dot_type(int t);
 int launch_float_dot(int n, gllm_hip_weight* const* ws, const float* d_x, float* const* outs,
                      hipStream_t s);
 
+struct ArgmaxOut {
+    unsigned long long* keys;  // null: no argmax epilogue
+    const uint32_t* recent;
+    int n_recent;
+    float penalty;
+};
+
 struct GemvJob {
     const uint8_t* w[3];
     float* out[3];
@@ -59,6 +66,9 @@ struct GemvJob {
     // workgroups quantises siluMulF32(out[0], out[1]) of the block into sq_act
     int* sq_cnt;
     ActQ8 sq_act;
+    // greedy argmax epilogue (batch-1 Q6_K, one weight): keys[gridDim.x]
+    // and the repeat-penalty window
+    ArgmaxOut am;
 };
 
 __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
@@ -1181,6 +1191,103 @@ __device__ __forceinline__ StagedAct stage_act(const GemvJob& j, uint8_t* lds, b
 // The repack stores lane k's four ql dwords together at 16k and its two qh
 // dwords at 128 + 8k, so a lane reads its share of a block in four loads.
 // ---------------------------------------------------------------------------
+// Greedy argmax over a logits vector: finite values only, strict >, lowest
+// index on ties, 0 when nothing is finite (argmaxQ6KRowsQ8,
+// kernels_amd64.go:294-331; finiteLogit sampling.go:385).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool finite_logit(float v) {
+    return (__float_as_uint(v) & 0x7f800000u) != 0x7f800000u;
+}
+
+// Packs (value, row) so that a larger key is a larger value, or the same
+// value at a lower row; 0 means "nothing finite seen".
+__device__ __forceinline__ unsigned long long argmax_key(float v, int r) {
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)r);
+}
+
+__device__ __forceinline__ unsigned long long wg_max_key(unsigned long long best) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const unsigned long long o = __shfl_xor(best, off);
+        best = o > best ? o : best;
+    }
+    __shared__ unsigned long long wbest[16];
+    const int nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+    __syncthreads();
+    unsigned long long b = 0;
+    for (int i = 0; i < nw; i++) b = wbest[i] > b ? wbest[i] : b;
+    return b;
+}
+
+// applyRepeatPenalty (sampling.go:136-153) on logit i, whose id appears
+// `count` times in the recent window: every occurrence applies the rule once
+// more, to the value the previous one left (non-finite -> -inf, positive /=
+// penalty, else *= penalty).  The rule reads only logit i, so applying it
+// count times equals the reference's in-order walk over the window.
+__device__ __forceinline__ float repeat_penalty(float v, int count, float penalty) {
+    for (int c = 0; c < count; c++) {
+        if (!finite_logit(v)) v = -INFINITY;
+        else if (v > 0.0f) v = v / penalty;
+        else v = v * penalty;
+    }
+    return v;
+}
+
+
+// Greedy argmax fused into the batch-1 epilogue of a row kernel (the decode
+// step's vocabulary head; ArgmaxMatvec model.go:754 -> argmaxQ6KRowsQ8,
+// kernels_amd64.go:294-331, keeps a running argmax while it dots the rows).
+// Every workgroup penalises its rows' logits and reduces them to one key,
+// stored at keys[blockIdx.x]; argmax_final_kernel reduces the keys.  Keys
+// order by value, then by lower row, so the result is the lowest-index
+// finite maximum whatever the reduction order (argmax_partial_kernel's keys).
+// Lanes own rows in groups of span = 8 * G lanes, ascending with the lane.
+// id0: recent[lane] (all ones past the window), loaded by the caller before
+// its weight stream so the window's latency hides behind it.  Each wave
+// counts its rows' window hits by ballot, takes the maximum of the keys'
+// upper words (the order-preserving image of the value, 0 for non-finite)
+// by DPP, then the lowest lane holding it by ballot; one barrier joins the
+// four wave keys.
+template <int G>
+__device__ inline void argmax_epilogue(const GemvJob& j, int r, float v, bool own, uint32_t id0) {
+    constexpr int span = 8 * G;
+    const ArgmaxOut& am = j.am;
+    const int lane = threadIdx.x & 63;
+    float x = v;
+    if (am.n_recent > 0 && am.penalty != 1.0f) {  // uniform
+        int hits = 0;
+        for (int c = 0; c < am.n_recent; c += 64) {
+            const uint32_t id = c == 0 ? id0
+                              : c + lane < am.n_recent ? am.recent[c + lane] : 0xffffffffu;
+#pragma unroll
+            for (int g = 0; g < 64 / span; g++) {
+                const int h = __popcll(__ballot(id == (uint32_t)__builtin_amdgcn_readlane(r, g * span)));
+                hits += lane / span == g ? h : 0;
+            }
+        }
+        x = repeat_penalty(v, hits, am.penalty);
+    }
+    const uint32_t u = own && finite_logit(x) ? (uint32_t)(argmax_key(x, r) >> 32) : 0u;
+    const uint32_t umax = wave_max_u32(u);
+    const unsigned long long hit = __ballot(own && u == umax);
+    const int rmin = __builtin_amdgcn_readlane(r, hit ? __builtin_ctzll(hit) : 0);
+    __shared__ unsigned long long wkey[4];
+    if (lane == 0)
+        wkey[threadIdx.x >> 6] =
+            umax ? ((unsigned long long)umax << 32) | (unsigned long long)(0xffffffffu - (uint32_t)rmin)
+                 : 0ull;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned long long a = wkey[0] > wkey[1] ? wkey[0] : wkey[1];
+        const unsigned long long b = wkey[2] > wkey[3] ? wkey[2] : wkey[3];
+        am.keys[blockIdx.x] = a > b ? a : b;
+    }
+}
+
+// ---------------------------------------------------------------------------
 //
 // G lanes share one AVX2 lane (G = 2, 4 for short matrices, so that a launch
 // still fills the chip): lane gi takes blocks gi, gi + G, ... and the
@@ -1318,6 +1425,10 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
     };
     Blk ring[D];
     XRegs<kFuseQB> xr;
+    uint32_t id0 = 0xffffffffu;  // the argmax epilogue's first 64 window ids
+    if constexpr (NT == 1) {
+        if (j.am.keys && (tid & 63) < j.am.n_recent) id0 = j.am.recent[tid & 63];
+    }
     if constexpr (FUSE) {
         xq_load<kFuseQB>(j.xf, B, xr);
         __builtin_amdgcn_sched_barrier(0);
@@ -1356,6 +1467,10 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
         const float v = tree8_strided<G>(accF[t] - accM[t]);  // VSUBPS + tree
         if (live && k == 0 && gi == G - 1 && t < j.ntok)
             j.out[wi][(size_t)(j.tok0 + t) * j.out_stride[wi] + r] = v;
+        if constexpr (NT == 1) {
+            if (j.am.keys)  // uniform
+                argmax_epilogue<G>(j, r, v, live && k == 0 && gi == G - 1, id0);
+        }
     }
 }
 
@@ -1535,57 +1650,11 @@ __global__ __launch_bounds__(256) void lane_ints_kernel(const uint8_t* __restric
     }
 }
 
-// ---------------------------------------------------------------------------
-// Greedy argmax over a logits vector: finite values only, strict >, lowest
-// index on ties, 0 when nothing is finite (argmaxQ6KRowsQ8,
-// kernels_amd64.go:294-331; finiteLogit sampling.go:385).
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ bool finite_logit(float v) {
-    return (__float_as_uint(v) & 0x7f800000u) != 0x7f800000u;
-}
-
-// Packs (value, row) so that a larger key is a larger value, or the same
-// value at a lower row; 0 means "nothing finite seen".
-__device__ __forceinline__ unsigned long long argmax_key(float v, int r) {
-    uint32_t u = __float_as_uint(v);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)r);
-}
-
 // Two stages: 256-thread workgroups each reduce kArgmaxChunk logits to one
 // key, then one workgroup reduces the keys.  Keys compare larger for a
 // larger finite value, or the same value at a lower row, so the result is
 // the lowest-index maximum regardless of the reduction order.
 constexpr int kArgmaxChunk = 1024;  // four logits per thread, all loads in flight together
-
-__device__ __forceinline__ unsigned long long wg_max_key(unsigned long long best) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const unsigned long long o = __shfl_xor(best, off);
-        best = o > best ? o : best;
-    }
-    __shared__ unsigned long long wbest[16];
-    const int nw = blockDim.x >> 6;
-    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
-    __syncthreads();
-    unsigned long long b = 0;
-    for (int i = 0; i < nw; i++) b = wbest[i] > b ? wbest[i] : b;
-    return b;
-}
-
-// applyRepeatPenalty (sampling.go:136-153) on logit i, whose id appears
-// `count` times in the recent window: every occurrence applies the rule once
-// more, to the value the previous one left (non-finite -> -inf, positive /=
-// penalty, else *= penalty).  The rule reads only logit i, so applying it
-// count times equals the reference's in-order walk over the window.
-__device__ __forceinline__ float repeat_penalty(float v, int count, float penalty) {
-    for (int c = 0; c < count; c++) {
-        if (!finite_logit(v)) v = -INFINITY;
-        else if (v > 0.0f) v = v / penalty;
-        else v = v * penalty;
-    }
-    return v;
-}
 
 // First stage; with n_recent > 0 and penalty != 1 the workgroup counts the
 // window's ids that fall in its chunk (ids >= n are ignored, as in the
@@ -1634,7 +1703,16 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
 __global__ __launch_bounds__(1024) void argmax_final_kernel(const unsigned long long* __restrict__ keys,
                                                             int nk, uint32_t* __restrict__ token) {
     unsigned long long best = 0;
-    for (int i = threadIdx.x; i < nk; i += 1024) best = keys[i] > best ? keys[i] : best;
+    for (int i0 = 0; i0 < nk; i0 += 8 * 1024) {
+        unsigned long long kv[8];  // all eight loads in flight together
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = i0 + threadIdx.x + k * 1024;
+            kv[k] = i < nk ? keys[i] : 0ull;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) best = kv[k] > best ? kv[k] : best;
+    }
     best = wg_max_key(best);
     if (threadIdx.x == 0) *token = best ? 0xffffffffu - (uint32_t)(best & 0xffffffffu) : 0u;
 }
@@ -2063,12 +2141,18 @@ struct NormIn {
 };
 
 int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* const* outs,
-             const int* strides, hipStream_t s, const float* xf, const NormIn* ni = nullptr) {
+             const int* strides, hipStream_t s, const float* xf, const NormIn* ni = nullptr,
+             const ArgmaxOut* am = nullptr) {
     if (n < 1 || n > 3) return fail(GLLM_EINVAL, "gemv: %d weights (1..3 supported)", n);
     if (xf && p != 1) return fail(GLLM_EINVAL, "gemv: fused quantisation is batch 1 only");
     GemvJob j{};
     j.n = n;
     j.xf = xf;
+    if (am) {
+        if (n != 1 || !xf || ws[0]->type != GLLM_TYPE_Q6_K)
+            return fail(GLLM_EINVAL, "gemv: the argmax epilogue needs one fused Q6_K launch");
+        j.am = *am;
+    }
     if (ni) {
         if (!xf || ws[0]->type != GLLM_TYPE_Q4_K)
             return fail(GLLM_EINVAL, "gemv: the RMSNorm prologue needs a fused Q4_K launch");
@@ -2160,6 +2244,43 @@ int gemv_f32(int n, gllm_hip_weight* const* ws, const float* d_xs, int p, float*
         }
         i = e;
     }
+    return GLLM_OK;
+}
+
+// True when W.x and its greedy argmax can run as one launch
+// (argmax_epilogue): a Q6_K weight whose batch-1 kernel quantises x itself.
+bool argmax_fusable(const gllm_hip_weight* w) {
+    gllm_hip_weight* ws[1] = {const_cast<gllm_hip_weight*>(w)};
+    return w->type == GLLM_TYPE_Q6_K && fused_quant(1, ws);
+}
+
+// Entries of the key buffer the argmax epilogue needs for w: one per
+// workgroup of its batch-1 launch (32 / G rows each).
+size_t argmax_epilogue_keys(const gllm_hip_weight* w) {
+    const int g = row_lanes_g(w->rows, w->blocks, 1, w->type);
+    return (size_t)(w->rows + kRowsPerWG / g - 1) / (kRowsPerWG / g);
+}
+
+// logits = W.x (batch 1) and, in the same launch, the workgroups' argmax
+// keys of the logits after the repeat penalty over recent[0 .. n_recent); then
+// argmax_final_kernel reduces the keys into *token.  keys: device memory of
+// argmax_epilogue_keys(w) entries.
+int gemv_argmax_f32(gllm_hip_weight* w, const float* x, float* logits, unsigned long long* keys,
+                    uint32_t* token, const uint32_t* recent, int n_recent, float penalty,
+                    hipStream_t s) {
+    if (!argmax_fusable(w)) return fail(GLLM_EUNSUP, "gemv: no argmax epilogue for this weight");
+    if (n_recent < 0 || (n_recent > 0 && !recent))
+        return fail(GLLM_EINVAL, "argmax: bad recent-token window (%d ids)", n_recent);
+    if (!(penalty > 0.0f) || penalty == INFINITY)
+        return fail(GLLM_EINVAL, "argmax: repeat penalty must be finite and positive");
+    const ArgmaxOut am{keys, recent, n_recent, penalty};
+    gllm_hip_weight* ws[1] = {w};
+    float* outs[1] = {logits};
+    ActQ8 none{};
+    GLLM_TRY(run_gemv(1, ws, none, 1, outs, nullptr, s, x, nullptr, &am));
+    const int nk = (int)argmax_epilogue_keys(w);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1024), 0, s, keys, nk, token);
+    GLLM_HIP(hipGetLastError());
     return GLLM_OK;
 }
 

@@ -213,8 +213,13 @@ __host__ __device__ __forceinline__ int q8perm_offset(int e) {
     return k * 32 + m * 4 + j;
 }
 
+// Exact int8 dot of four byte pairs plus c.  The clamp (saturation at the
+// int32 range) never acts on these sums (|dot| <= 4 * 128 * 128 and every
+// accumulation stays below 2^24); it selects the VOP3P v_dot4_i32_i8, which
+// takes c = 0 as an inline constant where the accumulating v_dot4c form
+// needs a v_mov of the zero first.
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
-    return __builtin_amdgcn_sdot4(a, b, c, false);
+    return __builtin_amdgcn_sdot4(a, b, c, true);
 }
 
 // DPP lane moves: a VALU operand modifier, no LDS round trip (a shuffle

@@ -69,15 +69,16 @@ def test_generate_with_repeat_penalty(hip):
     runtime.go:1035, 1089-1093) and every greedy choice applies
     applyRepeatPenalty (sampling.go:136-153).  Plain greedy on this model
     repeats one token; the penalties break that, and a window of 8 lets the
-    token return once it has slid out.  Decode steps after the first replay
-    the captured step graph, so the window reaches it through device memory."""
+    token return once it has slid out; a window of 90 holds more ids than
+    one wave's lanes.  Decode steps after the first replay the captured step
+    graph, so the window reaches it through device memory."""
     from gopherllm_amd.decoder import LlamaDecoder
     m = tiny_llama(seed=4, n_layers=3, dim=512, hidden=1536, n_heads=8, n_kv_heads=2, head_dim=64,
                    vocab=3000)
     prompt = np.random.default_rng(5).integers(0, 3000, 70)
     gpu = LlamaDecoder.from_host_model(m, 128)
     plain = ref.Llama(m, 128).generate(prompt, 24)
-    for pen, win in ((1.8, 64), (4.0, 8), (0.7, 16), (1.0, 64)):
+    for pen, win in ((1.8, 64), (4.0, 8), (0.7, 16), (1.0, 64), (1.3, 90)):
         print(f"repeat penalty {pen} window {win}", flush=True)
         cpu = ref.Llama(m, 128)
         cpu.set_repeat_penalty(pen, win)
