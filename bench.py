@@ -487,8 +487,11 @@ def suite(args):
                               "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
             del copies
 
-    for rows, cols in ((4096, 4096), (14336, 4096)) if "prefill" in only else ():
-        ws, wb = weights_for(g.TYPE_Q4_K, rows, cols, min_bytes=0)
+    pf_cases = [(g.TYPE_Q4_K, 4096, 4096), (g.TYPE_Q4_K, 14336, 4096), (g.TYPE_Q4_K, 4096, 14336),
+                (g.TYPE_Q6_K, 4096, 4096), (g.TYPE_Q6_K, 14336, 4096), (g.TYPE_Q6_K, 4096, 14336),
+                (g.TYPE_Q8_0, 14336, 4096)]
+    for qtype, rows, cols in pf_cases if "prefill" in only else ():
+        ws, wb = weights_for(qtype, rows, cols, min_bytes=0)
         P = 512
         x = torch.empty((P, cols), dtype=torch.float32, device="cuda")
         g.fill_normal_dev(x, 9, 1.0)
@@ -500,10 +503,15 @@ def suite(args):
 
         us = graph_time(body, 5) / 4
         ops = 2.0 * P * rows * cols
-        print(json.dumps({"suite": "configs[2] prefill", "type": "Q4_K", "rows": rows,
+        # the matrix-core kernels issue f16 MFMAs (Q6_K two per product: the
+        # code's 4-bit and 2-bit fields), hence both peaks
+        print(json.dumps({"suite": "configs[2] prefill", "type": qnames[qtype], "rows": rows,
                           "cols": cols, "tokens": P, "us": round(us, 1),
+                          "us_per_weight_mb": round(us / (wb / 1e6), 3),
                           "TOPS": round(ops / us / 1e6, 2),
-                          "frac_int8_mfma": round(ops / us / 1e6 / 5000.0, 4)}), flush=True)
+                          "frac_int8_mfma": round(ops / us / 1e6 / 5000.0, 4),
+                          "frac_f16_mfma": round(ops / us / 1e6 / 2500.0, 4),
+                          "timed": "Q8K quantisation of the 512 rows + the batched product"}), flush=True)
         del ws
 
     n_heads, n_kv, hd = 32, 8, 128

@@ -2140,6 +2140,12 @@ struct NormIn {
     ActQ8 sq_act;
 };
 
+// The batched Q6_K matrix-core kernel applies (launch_q6k_tiled).
+static bool q6k_tiled_fits(const ActQ8& act, int p, const gllm_hip_weight* w) {
+    return p > kTiledMinP && act.b16t && w->blocks % 8 == 0 &&
+           (size_t)w->rows * w->row_bytes < ((size_t)1 << 32);
+}
+
 int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* const* outs,
              const int* strides, hipStream_t s, const float* xf, const NormIn* ni = nullptr,
              const ArgmaxOut* am = nullptr) {
@@ -2186,6 +2192,12 @@ int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* 
         for (int i = 0; i < n; i++)
             GLLM_TRY(launch_q4k_mfma(ws[i]->d_data, ws[i]->row_bytes, ws[i]->rows, ws[i]->blocks,
                                      act, p, outs[i], j.out_stride[i], s));
+        return GLLM_OK;
+    }
+    if (w0->type == GLLM_TYPE_Q6_K && q6k_tiled_fits(act, p, w0)) {
+        for (int i = 0; i < n; i++)
+            GLLM_TRY(launch_q6k_tiled(ws[i]->d_data, ws[i]->row_bytes, ws[i]->rows, ws[i]->blocks,
+                                      act, p, outs[i], j.out_stride[i], s));
         return GLLM_OK;
     }
     for (int t0 = 0; t0 < p; t0 += kMaxTok) {

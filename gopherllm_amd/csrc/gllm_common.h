@@ -72,6 +72,10 @@ int launch_q8k_prep(const float* d_x, int cols, int p, const ActQ8& a, hipStream
 // out[t * out_stride + r] for p activation rows.
 int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
                     float* out, int out_stride, hipStream_t s);
+// Batched Q6_K x Q8_K on the matrix cores, same contract; needs the f16
+// tiles (p > kTiledMinP), blocks % 8 == 0 and rows * rb < 4 GiB.
+int launch_q6k_tiled(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
+                     float* out, int out_stride, hipStream_t s);
 // Same, for the activation siluMulF32(gate, up) computed on the fly.
 int launch_q8k_prep_silu(const float* d_gate, const float* d_up, int cols, int p, const ActQ8& a,
                          hipStream_t s);

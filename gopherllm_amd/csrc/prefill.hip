@@ -641,6 +641,265 @@ __global__ __launch_bounds__(512) void prefill_q4k_tiled_kernel(PfArgs a, TlMap 
     }
 }
 
+// --- Q6_K, more than 16 activation rows: 32 x 64 staged tiles --------------
+// q6kDotQ8KRow (kernels_amd64.s Q6KQ8QUAD, the batch-1 row kernel
+// gemv_q6k_kernel) per AVX2 lane k of a 256-element block b:
+//   I       = sum over the lane's 32 elements of sc(e) * code(e) * q8(e)
+//             (int32; code = ql | qh << 4 in 0..63, sc the element's int8 scale)
+//   o2      = fma(sc_{8+k}, 32 xs16_{8+k}, sc_k * 32 xs16_k)
+//   accM[k] = fma(d_b, o2, accM[k]);  accF[k] = fma(float(I), d_b * xscale_b, accF[k])
+// and tree8(accF - accM).  sc * code reaches 128 * 63, past the integers
+// f16 holds exactly, so the products split at the code's two fields:
+//   I = 16 * (sum sc * (code >> 4) * q8) + sum sc * (code & 15) * q8
+// with |sc * (code >> 4)| <= 384 and |sc * (code & 15)| <= 1920 exact in f16
+// and every partial sum of 32 products an integer below 2^24, so each of
+// the two v_mfma_f32_16x16x32_f16 results is its exact integer sum and
+// fma(hi, 16, lo) rounds 16 hi + lo once: float(I).  The chains then run in
+// VALU registers in the reference's order.
+// Workgroup: 32 rows x 64 tokens, eight waves; wave w owns rows 16 (w & 1)
+// .. + 15 and tokens 16 (w >> 1) .. + 15.  Per block, double-buffered in
+// LDS: both A operands of the 32 rows (dequantised once per workgroup from
+// the raw block bytes, copied global -> LDS two blocks ahead), the four
+// 16-token B tiles (the quantiser's f16 layout), the tokens' xs16 and
+// xscale and the rows' scales and d.  Weights need rows * rb < 4 GiB and
+// 16-byte aligned blocks (blocks % 8 == 0).
+constexpr int kQ6Rows = 32, kQ6Tok = 64;
+constexpr int kQ6RawPieces = 448;  // 7 waves x 64: 32 rows x 13 pieces of 16 bytes, then padding
+struct Q6Stage {
+    uint8_t alo[2 * 8 * 4 * 256];  // [row group][lane k][group g][row c][8 halves]: sc * (code & 15)
+    uint8_t ahi[2 * 8 * 4 * 256];  //                                                sc * (code >> 4)
+    uint8_t b16[4 * 8 * 4 * 256];  // [token tile][lane k][group g][token c][8 halves]
+    float x16[kQ6Tok][16];         // [token][16-group] xs16
+    float sc[16][kQ6Rows + 4];     // [scale index][row] int8 scale
+    float d[kQ6Rows], xs[kQ6Tok];
+};
+struct Q6Raw {
+    uint8_t q[kQ6RawPieces * 16];  // [row][208]: ql 128, qh 64, scales 16
+    uint32_t d[64];                // [row]: the dword holding d of blocks b & ~1, b | 1
+};
+
+// Block b's token operands into S: four 1 KB pieces of B per wave, the
+// tokens' xs16 (waves 0-3) and xscales (wave 4): five copies on waves 0-4,
+// four on 5-7.
+__device__ __forceinline__ void q6_copy_tokens(const PfArgs& a, int w, int lane, int tile0, int tok0,
+                                               int b, Q6Stage& S) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int ch = 4 * w + i, tt = ch >> 3, piece = ch & 7;
+        const int gt = min(tile0 + tt, a.act.tiles - 1);
+        const uint8_t* base = (const uint8_t*)a.act.b16t + ((size_t)b * a.act.tiles + gt) * 8192 + piece * 1024;
+        lds_copy16_s(base, 16 * lane, lds_addr(S.b16 + tt * 8192 + piece * 1024));
+    }
+    if (w < 4) {
+        const int t = min(tok0 + 16 * w + (lane >> 2), a.p - 1);
+        lds_copy16_s(a.act.xs16, (uint32_t)(((size_t)t * (a.blocks * 16) + (size_t)b * 16) * 4 + 16 * (lane & 3)),
+                     lds_addr(&S.x16[16 * w][0]));
+    } else if (w == 4) {
+        lds_copy4_s(a.act.xscale + b, (uint32_t)min(tok0 + lane, a.p - 1) * a.blocks * 4, lds_addr(&S.xs[0]));
+    }
+}
+
+// Block b of the 32 rows into R: waves 0-6 one 1 KB piece each (row-major
+// 208-byte blocks; pieces past the rows repeat a valid source into the
+// padding), wave 7 the rows' d dwords.  One copy per wave.
+__device__ __forceinline__ void q6_copy_raw(const PfArgs& a, int w, int lane, int row0, int b, Q6Raw& R) {
+    if (w < 7) {
+        const int pc = min(64 * w + lane, 32 * 13 - 1), r = pc / 13, off = (pc % 13) * 16;
+        const size_t row = (size_t)min(row0 + r, a.rows - 1);
+        lds_copy16_s(a.w, (uint32_t)(row * a.rb + (size_t)b * 208 + off), lds_addr(R.q + 1024 * w));
+    } else {
+        const size_t row = (size_t)min(row0 + (lane & 31), a.rows - 1);
+        lds_copy4_s(a.w, (uint32_t)(row * a.rb + (size_t)a.blocks * 208 + (size_t)(b & ~1) * 2),
+                    lds_addr(&R.d[0]));
+    }
+}
+
+// four bytes (values 0..255, exact) -> two half2 words
+__device__ __forceinline__ void u8x4_to_h(uint32_t v, uint32_t& lo, uint32_t& hi) {
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    const h2v bias = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const h2v a = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, v, 0x05010400u)) + bias;
+    const h2v c = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, v, 0x05030402u)) + bias;
+    lo = __builtin_bit_cast(uint32_t, a);
+    hi = __builtin_bit_cast(uint32_t, c);
+}
+
+// Dequantisation of raw block R into S: thread t the A operands of (row
+// group r, lane k, group g, row c) = (r, t >> 6, (t >> 4) & 3, t & 15) for
+// r = 0, 1 (its 16-byte writes: consecutive per wave), the scales as floats
+// (thread t: scale index t >> 5 of row t & 31) and d (threads 0-31).
+__device__ __forceinline__ void q6_dequant(int tid, int b, const Q6Raw& R, Q6Stage& S) {
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    const int c = tid & 15, g = (tid >> 4) & 3, k = tid >> 6;
+    const int h = g >> 1, sh = 4 * (g & 1), hk = k >> 2;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const uint8_t* blk = R.q + (16 * r + c) * 208;
+        const uint2 ql = *(const uint2*)(blk + 16 * k + 8 * h);   // ql dwords 2h, 2h + 1 of lane k
+        const uint32_t qh = *(const uint32_t*)(blk + 128 + 8 * k + 4 * h);
+        // quads m = 2g, 2g + 1: scales 8h + 4 (g & 1) + hk and + 2
+        const int s0 = (int)(int8_t)blk[192 + 8 * h + sh + hk];
+        const int s1 = (int)(int8_t)blk[192 + 8 * h + sh + 2 + hk];
+        const h2v f0 = {(_Float16)(float)s0, (_Float16)(float)s0};
+        const h2v f1 = {(_Float16)(float)s1, (_Float16)(float)s1};
+        uint32_t l0, l1, l2, l3, h0, h1, h2, h3;
+        u8x4_to_h((ql.x >> sh) & 0x0f0f0f0fu, l0, l1);
+        u8x4_to_h((ql.y >> sh) & 0x0f0f0f0fu, l2, l3);
+        u8x4_to_h((qh >> sh) & 0x03030303u, h0, h1);
+        u8x4_to_h((qh >> (sh + 2)) & 0x03030303u, h2, h3);
+        // exact: products of small integers below 2048
+        const h2v a0 = __builtin_bit_cast(h2v, l0) * f0, a1 = __builtin_bit_cast(h2v, l1) * f0;
+        const h2v a2 = __builtin_bit_cast(h2v, l2) * f1, a3 = __builtin_bit_cast(h2v, l3) * f1;
+        const h2v b0 = __builtin_bit_cast(h2v, h0) * f0, b1 = __builtin_bit_cast(h2v, h1) * f0;
+        const h2v b2 = __builtin_bit_cast(h2v, h2) * f1, b3 = __builtin_bit_cast(h2v, h3) * f1;
+        const int off = ((r * 8 + k) * 4 + g) * 256 + c * 16;
+        h8v lo, hi;
+        lo[0] = a0[0]; lo[1] = a0[1]; lo[2] = a1[0]; lo[3] = a1[1];
+        lo[4] = a2[0]; lo[5] = a2[1]; lo[6] = a3[0]; lo[7] = a3[1];
+        hi[0] = b0[0]; hi[1] = b0[1]; hi[2] = b1[0]; hi[3] = b1[1];
+        hi[4] = b2[0]; hi[5] = b2[1]; hi[6] = b3[0]; hi[7] = b3[1];
+        *(h8v*)(S.alo + off) = lo;
+        *(h8v*)(S.ahi + off) = hi;
+    }
+    {
+        const int idx = tid >> 5, row = tid & 31;
+        S.sc[idx][row] = (float)(int8_t)R.q[row * 208 + 192 + idx];
+    }
+    if (tid < 32) S.d[tid] = f16_bits_to_f32((R.d[tid] >> (16 * (b & 1))) & 0xffffu);
+}
+
+// Workgroup -> tile map as tl_map, with 32-row tiles.
+static TlMap q6_map(int rows, int p) {
+    TlMap m;
+    m.row_tiles = (rows + kQ6Rows - 1) / kQ6Rows;
+    m.tok_tiles = (p + kQ6Tok - 1) / kQ6Tok;
+    m.h = 1;
+    while (m.h < 8 && (m.tok_tiles + m.h - 1) / m.h > 4) m.h *= 2;
+    m.v = 8 / m.h;
+    m.tg_size = (m.tok_tiles + m.h - 1) / m.h;
+    m.rg_size = (m.row_tiles + m.v - 1) / m.v;
+    return m;
+}
+
+__global__ __launch_bounds__(512) void prefill_q6k_tiled_kernel(PfArgs a, TlMap mp) {
+    __shared__ __align__(16) Q6Stage st[2];
+    __shared__ __align__(16) Q6Raw raw[2];
+    const int id = blockIdx.x, xcd = id & 7, local = id >> 3;
+    const int lt = local % mp.tg_size, lrow = local / mp.tg_size;
+    const int ttile = (xcd % mp.h) * mp.tg_size + lt, rtile = (xcd / mp.h) * mp.rg_size + lrow;
+    if (lrow >= mp.rg_size || ttile >= mp.tok_tiles || rtile >= mp.row_tiles) return;  // whole workgroup
+    const int row0 = rtile * kQ6Rows, tok0 = ttile * kQ6Tok, tile0 = tok0 / 16;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, c = lane & 15;
+    const int rg = w & 1, tt = w >> 1;
+    const int nb = a.blocks;
+
+    float accF[8][4], accM[8][4];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) accF[k][i] = accM[k][i] = 0.0f;
+
+    // prologue: raw blocks 0 and 1, token operands of block 0
+    q6_copy_raw(a, w, lane, row0, 0, raw[0]);
+    q6_copy_raw(a, w, lane, row0, min(1, nb - 1), raw[1]);
+    q6_copy_tokens(a, w, lane, tile0, tok0, 0, st[0]);
+    wait_vmem_le<0>();
+    lds_barrier();
+    q6_dequant(tid, 0, raw[0], st[0]);
+    wait_lgkm0();
+    lds_barrier();
+#pragma unroll 1
+    for (int b = 0; b < nb; b++) {
+        // unconditional copies (clamped to the last block, into buffers not
+        // read this iteration) keep the vmcnt counts constant: tokens of
+        // b + 1 (five copies on waves 0-4, four on 5-7), raw of b + 2 (one)
+        q6_copy_tokens(a, w, lane, tile0, tok0, min(b + 1, nb - 1), st[(b + 1) & 1]);
+        q6_copy_raw(a, w, lane, row0, min(b + 2, nb - 1), raw[b & 1]);
+        const Q6Stage& S = st[b & 1];
+        const int t = 16 * tt + c;  // this lane's token in the tile
+        const float xv = S.xs[t];
+        float dv[4], dxs[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            dv[i] = S.d[16 * rg + 4 * g + i];
+            dxs[i] = dv[i] * xv;  // VMULSS d * xscale
+        }
+        const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+        // lane k + 1's operands are read while lane k's products and chains
+        // run (one step ahead: more would not fit two waves per SIMD)
+        struct Ops {
+            h8v alo, ahi, bv;
+            float x0, x8;
+            f4v sk, sk8;
+        };
+        auto ops = [&](int k, Ops& o) __attribute__((always_inline)) {
+            o.alo = *(const h8v*)(S.alo + ((rg * 8 + k) * 4 + g) * 256 + c * 16);
+            o.ahi = *(const h8v*)(S.ahi + ((rg * 8 + k) * 4 + g) * 256 + c * 16);
+            o.bv = *(const h8v*)(S.b16 + ((tt * 8 + k) * 4 + g) * 256 + c * 16);
+            o.x0 = S.x16[t][k] * 32.0f;  // ScaleF32(xs, 32)
+            o.x8 = S.x16[t][8 + k] * 32.0f;
+            o.sk = *(const f4v*)&S.sc[k][16 * rg + 4 * g];
+            o.sk8 = *(const f4v*)&S.sc[8 + k][16 * rg + 4 * g];
+        };
+        Ops o[2];
+        ops(0, o[0]);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            if (k < 7) ops(k + 1, o[(k + 1) & 1]);
+            const Ops& cur = o[k & 1];
+            const f4v plo = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.alo, cur.bv, z, 0, 0, 0);
+            const f4v phi = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.ahi, cur.bv, z, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float iv = fmaf(phi[i], 16.0f, plo[i]);  // float(I)
+                float o2 = cur.sk[i] * cur.x0;                 // VMULPS
+                o2 = fmaf(cur.sk8[i], cur.x8, o2);             // VFMADD231PS
+                accM[k][i] = fmaf(dv[i], o2, accM[k][i]);
+                accF[k][i] = fmaf(iv, dxs[i], accF[k][i]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // raw block b + 1 (copied last iteration) has landed once at most
+        // this iteration's copies are outstanding
+        if (w < 5) wait_vmem_le<6>();
+        else wait_vmem_le<5>();
+        lds_barrier();  // raw b + 1 complete from every wave; stage (b + 1) & 1 free
+        q6_dequant(tid, min(b + 1, nb - 1), raw[(b + 1) & 1], st[(b + 1) & 1]);
+        wait_vmem_le<1>();  // token operands of b + 1
+        wait_lgkm0();
+        lds_barrier();
+    }
+    wait_vmem_le<0>();  // the clamped copies of the last iterations
+    const int tk = tok0 + 16 * tt + c;
+    if (tk < a.p) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int rr = row0 + 16 * rg + 4 * g + i;
+            if (rr >= a.rows) continue;
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = accF[k][i] - accM[k][i];
+            const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+            a.out[(size_t)tk * a.out_stride + rr] = (s0 + s1) + (s2 + s3);
+        }
+    }
+}
+
+int launch_q6k_tiled(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
+                     float* out, int out_stride, hipStream_t s) {
+    if (rows <= 0 || blocks <= 0 || p <= 0) return GLLM_OK;
+    if (!act.b16t || p <= kTiledMinP || blocks % 8 || (size_t)rows * rb >= ((size_t)1 << 32))
+        return fail(GLLM_EINVAL, "prefill: Q6_K tiles need > %d tokens, blocks %% 8 == 0, < 4 GiB",
+                    kTiledMinP);
+    PfArgs a{d_w, rb, rows, blocks, act, p, out, out_stride};
+    const TlMap mp = q6_map(rows, p);
+    hipLaunchKernelGGL(prefill_q6k_tiled_kernel, dim3(8 * mp.tg_size * mp.rg_size), dim3(512), 0, s, a,
+                       mp);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
 // --- at most 16 activation rows, operands through a per-wave LDS ring -----
 // One workgroup per 16 weight rows; wave w computes the MFMA products of
 // blocks b = w, w + NW, ... (16-row x 16-token tiles, one per AVX2 lane k),

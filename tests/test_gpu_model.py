@@ -200,12 +200,13 @@ def test_q4k_pair_with_a_q8_0_projection_matches_oracle(hip):
         tok = want
 
 
-@pytest.mark.parametrize("n_heads,n_kv", [(8, 2), (4, 4), (8, 1)])
+@pytest.mark.parametrize("n_heads,n_kv", [(8, 2), (4, 4), (8, 4), (8, 1)])
 def test_decode_attention_head_dim_128_matches_oracle(hip, n_heads, n_kv):
     """head_dim 128 generation steps (captured decode step: RoPE and the
-    K / V store folded into the scores launch, the value chains over V tiles
+    K / V store folded into the scores stage, scores and values in one
+    launch for up to 4 query heads per KV head, the value chains over V rows
     staged through LDS): hidden states, tokens and the cache rows equal the
-    oracle's, for spans that cross the 64-position tiles, with 1, 4 and 8
+    oracle's, for spans that cross the 64-position tiles, with 1, 2, 4 and 8
     query heads per KV head."""
     from gopherllm_amd.decoder import LlamaDecoder
     m = tiny_llama(seed=31, n_layers=2, dim=512, hidden=1024, n_heads=n_heads, n_kv_heads=n_kv,

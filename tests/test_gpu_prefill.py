@@ -20,10 +20,10 @@ def bits(a):
     return np.asarray(a, np.float32).view(np.uint32)
 
 
-def amd64(data, xs, rows, cols):
-    want = ref.matvec_batch_fast(ref.Q4_K, data, xs, rows, cols)
+def amd64(data, xs, rows, cols, qtype=ref.Q4_K):
+    want = ref.matvec_batch_fast(qtype, data, xs, rows, cols)
     if want is None:
-        want = ref.matvec_batch(ref.Q4_K, data, xs, rows, cols)
+        want = ref.matvec_batch(qtype, data, xs, rows, cols)
     return want.reshape(xs.shape[0], rows)
 
 
@@ -81,18 +81,25 @@ def test_prefill_extremes_closed_form(hip):
     assert_bits(got, amd64(data, xs, rows, cols), "extremes")
 
 
+def device_weight(hip, qtype, rows, cols, seed):
+    """Seeded N(0, 0.02) rows encoded on the device (the RTN encoders)."""
+    import torch
+    tmp = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    hip.fill_normal_dev(tmp, seed, 0.02)
+    raw = torch.empty(rows * hip.row_bytes(qtype, cols), dtype=torch.uint8, device="cuda")
+    hip.quantize_rows_dev(qtype, tmp, raw)
+    del tmp
+    return hip.Weight.from_device(raw, qtype, rows, cols), raw
+
+
 @pytest.mark.parametrize("rows", [4096, 14336])
 def test_prefill_configs2(hip, rows):
     """Q4_K rows x 4096 (seeded N(0, 0.02), device RTN encoder)
-    against 512 activation rows N(0, 1)."""
+    against 512 activation rows N(0, 1): every token against the amd64-order
+    oracle and against the GPU's own batch-1 path."""
     import torch
     cols, p = 4096, 512
-    tmp = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
-    hip.fill_normal_dev(tmp, 3000 + rows, 0.02)
-    raw = torch.empty(rows * hip.row_bytes(hip.TYPE_Q4_K, cols), dtype=torch.uint8, device="cuda")
-    hip.quantize_rows_dev(hip.TYPE_Q4_K, tmp, raw)
-    w = hip.Weight.from_device(raw, hip.TYPE_Q4_K, rows, cols)
-    del tmp
+    w, raw = device_weight(hip, hip.TYPE_Q4_K, rows, cols, 3000 + rows)
     x = torch.empty((p, cols), dtype=torch.float32, device="cuda")
     hip.fill_normal_dev(x, 77, 1.0)
     out = torch.empty((p, rows), dtype=torch.float32, device="cuda")
@@ -105,7 +112,59 @@ def test_prefill_configs2(hip, rows):
     got, per_token = out.cpu().numpy(), one.cpu().numpy()
     assert np.isfinite(got).all() and float(np.std(got)) > 0.1
     assert_bits(got, per_token, "batched vs per-token row kernel")
-    sel = [0, 1, 31, 32, 100, 255, 256, 511]
-    xh = x.cpu().numpy()[sel]
-    want = amd64(raw.cpu().numpy(), xh, rows, cols)
-    assert_bits(got[sel], want, "sampled tokens vs amd64 oracle")
+    want = amd64(raw.cpu().numpy(), x.cpu().numpy(), rows, cols)
+    assert_bits(got, want, "every token vs amd64 oracle")
+
+
+# Q6_K batches of more than 16 tokens take the matrix-core tiles when the
+# row has a multiple of 8 blocks (2048 columns and up); 1024 columns keep the
+# row kernels (same bits either way)
+@pytest.mark.parametrize("rows,cols,p", [(300, 2048, 17), (300, 2048, 33), (64, 2048, 100),
+                                         (1000, 4096, 64), (70, 14336, 40), (130, 1024, 40)])
+def test_prefill_q6k_bit_exact_small(hip, rows, cols, p):
+    data, _ = quant_matrix(ref.Q6_K, rows, cols, 600 + p + rows)
+    w = hip.Weight.from_host(data, ref.Q6_K, rows, cols)
+    xs = normal(601 + p, (p, cols))
+    print(f"prefill Q6_K {rows}x{cols} p={p}", flush=True)
+    got = w.matvec_batch(xs)
+    assert_bits(got, amd64(data, xs, rows, cols, ref.Q6_K), "vs amd64 oracle")
+
+
+def test_prefill_q6k_extremes(hip):
+    """Scales -128 and 127 with codes 63 (the largest |sc * code|, past f16's
+    exact integers: the split at the code's fields keeps it exact), zero and
+    large activations, against the oracle."""
+    rows, cols, p = 64, 2048, 24
+    rng = np.random.default_rng(91)
+    data, _ = quant_matrix(ref.Q6_K, rows, cols, 92)
+    blocks = data.reshape(rows * (cols // 256), 210)
+    blocks[0::2, 0:192] = 0xFF                  # every code 63
+    blocks[0::2, 192:208] = np.where(rng.random((len(blocks[0::2]), 16)) < 0.5, 0x80, 0x7F)
+    blocks[1::4, 192:208] = 0x80                # scale -128 with random codes
+    xs = normal(93, (p, cols))
+    xs[0] = 0.0
+    xs[1] *= 1e4
+    xs[2, :] = np.where(np.arange(cols) % 2 == 0, 1.0, -1.0)
+    w = hip.Weight.from_host(data, ref.Q6_K, rows, cols)
+    got = w.matvec_batch(xs)
+    assert_bits(got, amd64(data, xs, rows, cols, ref.Q6_K), "extremes vs amd64 oracle")
+
+
+@pytest.mark.parametrize("rows,cols", [(14336, 4096), (4096, 14336)])
+def test_prefill_q6k_configs2_shapes(hip, rows, cols):
+    """Q6_K at the configs[1] / configs[2] shapes (a Q4_K_M file's ffn_down
+    and attn_v are Q6_K), 512 tokens: every token against the amd64-order
+    oracle."""
+    import torch
+    p = 512
+    w, raw = device_weight(hip, hip.TYPE_Q6_K, rows, cols, 4000 + rows)
+    x = torch.empty((p, cols), dtype=torch.float32, device="cuda")
+    hip.fill_normal_dev(x, 78, 1.0)
+    out = torch.empty((p, rows), dtype=torch.float32, device="cuda")
+    print(f"prefill Q6_K {rows}x{cols} p={p}", flush=True)
+    w.matvec_dev(x, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all() and float(np.std(got)) > 0.1
+    want = amd64(raw.cpu().numpy(), x.cpu().numpy(), rows, cols, ref.Q6_K)
+    assert_bits(got, want, "every token vs amd64 oracle")
