@@ -489,7 +489,7 @@ def suite(args):
 
     pf_cases = [(g.TYPE_Q4_K, 4096, 4096), (g.TYPE_Q4_K, 14336, 4096), (g.TYPE_Q4_K, 4096, 14336),
                 (g.TYPE_Q6_K, 4096, 4096), (g.TYPE_Q6_K, 14336, 4096), (g.TYPE_Q6_K, 4096, 14336),
-                (g.TYPE_Q8_0, 14336, 4096)]
+                (g.TYPE_Q8_0, 14336, 4096), (g.TYPE_Q8_0, 4096, 14336)]
     for qtype, rows, cols in pf_cases if "prefill" in only else ():
         ws, wb = weights_for(qtype, rows, cols, min_bytes=0)
         P = 512

@@ -2194,6 +2194,13 @@ int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* 
                                      act, p, outs[i], j.out_stride[i], s));
         return GLLM_OK;
     }
+    if (w0->type == GLLM_TYPE_Q8_0 && p > kTiledMinP && (size_t)w0->rows * w0->row_bytes < ((size_t)1 << 32) &&
+        (size_t)p * w0->cols < ((size_t)1 << 32)) {
+        for (int i = 0; i < n; i++)
+            GLLM_TRY(launch_q8_0_tiled(ws[i]->d_data, ws[i]->row_bytes, ws[i]->rows, ws[i]->blocks,
+                                       act, p, outs[i], j.out_stride[i], s));
+        return GLLM_OK;
+    }
     if (w0->type == GLLM_TYPE_Q6_K && q6k_tiled_fits(act, p, w0)) {
         for (int i = 0; i < n; i++)
             GLLM_TRY(launch_q6k_tiled(ws[i]->d_data, ws[i]->row_bytes, ws[i]->rows, ws[i]->blocks,

@@ -76,6 +76,10 @@ int launch_q4k_mfma(const uint8_t* d_w, size_t rb, int rows, int blocks, const A
 // tiles (p > kTiledMinP), blocks % 8 == 0 and rows * rb < 4 GiB.
 int launch_q6k_tiled(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
                      float* out, int out_stride, hipStream_t s);
+// Batched Q8_0 x Q8_K (vector units, one weight pass per 64 tokens), same
+// contract; needs p > kTiledMinP and operands under 4 GiB.
+int launch_q8_0_tiled(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
+                      float* out, int out_stride, hipStream_t s);
 // Same, for the activation siluMulF32(gate, up) computed on the fly.
 int launch_q8k_prep_silu(const float* d_gate, const float* d_up, int cols, int p, const ActQ8& a,
                          hipStream_t s);

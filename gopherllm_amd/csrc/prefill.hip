@@ -900,6 +900,150 @@ int launch_q6k_tiled(const uint8_t* d_w, size_t rb, int rows, int blocks, const 
     return GLLM_OK;
 }
 
+// --- Q8_0, more than 16 activation rows: 64 x 64 staged tiles ---------------
+// q8_0DotQ8KRow (kernels_amd64.s Q80CHUNK) per AVX2 lane k of a 256-element
+// group: for its eight 32-value blocks q in order
+//   acc12 = fma(d_q, float(I_qk), acc12)   I_qk: the exact dot of the lane's
+//                                           4 weight and 4 activation bytes
+// then acc11[k] = fma(xscale, acc12, acc11[k]) and tree8(acc11).  The
+// per-block float chain sets the cost (25 VALU operations per row, token,
+// group and lane with v_dot4_i32_i8 for I), so this kernel stays on the
+// vector units and reads every weight byte once per 64 tokens.
+// Workgroup: 64 rows x 64 tokens, 512 threads; thread (rp, tq) = (t >> 4,
+// t & 15) owns rows 2 rp, 2 rp + 1 and tokens tq + 16 j (j < 4).  Per group,
+// double-buffered in LDS: the 64 rows' 272-byte groups as stored (8 f16 d,
+// then lane k's 8 dwords at 16 + 32 k) and the 64 tokens' q8perm bytes
+// (lane k's 32 at 32 k) in 272-byte rows, both copied global -> LDS one
+// group ahead, and the tokens' xscales.
+constexpr int kQ80Pieces = 64 * 17;  // 16-byte pieces of 64 rows (or tokens) x 272 bytes
+struct Q80Stage {
+    uint8_t w[kQ80Pieces * 16];  // [row][272]
+    uint8_t q[kQ80Pieces * 16];  // [token][272]: 256 q8perm bytes, 16 unused
+    float xs[64];
+};
+
+// Group b's operands into S: two 1 KB pieces of the rows and two of the
+// tokens per wave, the remaining 64 row pieces on wave 0, 64 token pieces on
+// wave 1, the xscales on wave 2: five copies on waves 0-2, four on 3-7.
+__device__ __forceinline__ void q80_copy(const PfArgs& a, int w, int lane, int row0, int tok0, int b,
+                                         Q80Stage& S) {
+    const int cols = a.blocks * 256;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        if (i == 2 && w != 0) break;  // wave-uniform
+        const int pc = (i < 2 ? 128 * w + 64 * i : 1024) + lane, r = pc / 17, off = (pc % 17) * 16;
+        const size_t row = (size_t)min(row0 + r, a.rows - 1);
+        lds_copy16_s(a.w, (uint32_t)(row * a.rb + (size_t)b * 272 + off), lds_addr(S.w + 16 * (pc - lane)));
+    }
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        if (i == 2 && w != 1) break;  // wave-uniform
+        const int pc = (i < 2 ? 128 * w + 64 * i : 1024) + lane, t = pc / 17, off = min((pc % 17) * 16, 240);
+        const size_t tok = (size_t)min(tok0 + t, a.p - 1);
+        lds_copy16_s(a.act.q8perm, (uint32_t)(tok * cols + (size_t)b * 256 + off), lds_addr(S.q + 16 * (pc - lane)));
+    }
+    if (w == 2)
+        lds_copy4_s(a.act.xscale + b, (uint32_t)min(tok0 + lane, a.p - 1) * a.blocks * 4, lds_addr(&S.xs[0]));
+}
+
+__global__ __launch_bounds__(512) void prefill_q8_0_tiled_kernel(PfArgs a, TlMap mp) {
+    __shared__ __align__(16) Q80Stage st[2];
+    const int id = blockIdx.x, xcd = id & 7, local = id >> 3;
+    const int lt = local % mp.tg_size, lrow = local / mp.tg_size;
+    const int ttile = (xcd % mp.h) * mp.tg_size + lt, rtile = (xcd / mp.h) * mp.rg_size + lrow;
+    if (lrow >= mp.rg_size || ttile >= mp.tok_tiles || rtile >= mp.row_tiles) return;  // whole workgroup
+    const int row0 = rtile * kTlRows, tok0 = ttile * kTlTok;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rp = tid >> 4, tq = tid & 15;
+    const int nb = a.blocks;
+
+    float acc11[2][4][8];
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int k = 0; k < 8; k++) acc11[r][j][k] = 0.0f;
+
+    q80_copy(a, w, lane, row0, tok0, 0, st[0]);
+    wait_vmem_le<0>();
+    lds_barrier();
+#pragma unroll 1
+    for (int b = 0; b < nb; b++) {
+        // unconditional copies (clamped to the last group, into the stage
+        // not read this iteration): five on waves 0-2, four on 3-7
+        q80_copy(a, w, lane, row0, tok0, min(b + 1, nb - 1), st[(b + 1) & 1]);
+        const Q80Stage& S = st[b & 1];
+        float d[2][8], xs[4];
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const uint4 dh = *(const uint4*)(S.w + (2 * rp + r) * 272);
+            const uint32_t dw[4] = {dh.x, dh.y, dh.z, dh.w};
+#pragma unroll
+            for (int q = 0; q < 8; q++) d[r][q] = f16_bits_to_f32((dw[q >> 1] >> (16 * (q & 1))) & 0xffffu);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) xs[j] = S.xs[tq + 16 * j];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            int wv[2][8], qv[4][8];
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                const int4 lo = *(const int4*)(S.w + (2 * rp + r) * 272 + 16 + 32 * k);
+                const int4 hi = *(const int4*)(S.w + (2 * rp + r) * 272 + 32 + 32 * k);
+                wv[r][0] = lo.x; wv[r][1] = lo.y; wv[r][2] = lo.z; wv[r][3] = lo.w;
+                wv[r][4] = hi.x; wv[r][5] = hi.y; wv[r][6] = hi.z; wv[r][7] = hi.w;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int4 lo = *(const int4*)(S.q + (tq + 16 * j) * 272 + 32 * k);
+                const int4 hi = *(const int4*)(S.q + (tq + 16 * j) * 272 + 32 * k + 16);
+                qv[j][0] = lo.x; qv[j][1] = lo.y; qv[j][2] = lo.z; qv[j][3] = lo.w;
+                qv[j][4] = hi.x; qv[j][5] = hi.y; qv[j][6] = hi.z; qv[j][7] = hi.w;
+            }
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float acc12 = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 8; q++)
+                        acc12 = fmaf((float)sdot4(wv[r][q], qv[j][q], 0), d[r][q], acc12);  // VFMADD231PS
+                    acc11[r][j][k] = fmaf(acc12, xs[j], acc11[r][j][k]);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        wait_vmem_le<0>();  // group b + 1's copies, issued before this group's products
+        lds_barrier();
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int rr = row0 + 2 * rp + r;
+        if (rr >= a.rows) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int t = tok0 + tq + 16 * j;
+            if (t >= a.p) continue;
+            const float* v = acc11[r][j];
+            const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+            a.out[(size_t)t * a.out_stride + rr] = (s0 + s1) + (s2 + s3);
+        }
+    }
+}
+
+int launch_q8_0_tiled(const uint8_t* d_w, size_t rb, int rows, int blocks, const ActQ8& act, int p,
+                      float* out, int out_stride, hipStream_t s) {
+    if (rows <= 0 || blocks <= 0 || p <= 0) return GLLM_OK;
+    if (p <= kTiledMinP || (size_t)rows * rb >= ((size_t)1 << 32) || (size_t)p * blocks * 256 >= ((size_t)1 << 32))
+        return fail(GLLM_EINVAL, "prefill: Q8_0 tiles need > %d tokens and < 4 GiB operands", kTiledMinP);
+    PfArgs a{d_w, rb, rows, blocks, act, p, out, out_stride};
+    const TlMap mp = tl_map(rows, p);
+    hipLaunchKernelGGL(prefill_q8_0_tiled_kernel, dim3(8 * mp.tg_size * mp.rg_size), dim3(512), 0, s,
+                       a, mp);
+    GLLM_HIP(hipGetLastError());
+    return GLLM_OK;
+}
+
 // --- at most 16 activation rows, operands through a per-wave LDS ring -----
 // One workgroup per 16 weight rows; wave w computes the MFMA products of
 // blocks b = w, w + NW, ... (16-row x 16-token tiles, one per AVX2 lane k),

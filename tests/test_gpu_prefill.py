@@ -1,4 +1,5 @@
-"""Batched prefill products on the matrix cores.
+"""Batched prefill products: Q4_K and Q6_K on the matrix cores,
+Q8_0 on 64 x 64 tiles of the vector units.
 
 matvecBatchQ8 (kernels_amd64.go:470-581) evaluates q4kDotQ8KRow once per
 (row, token), so the batched result must equal the per-token row kernel bit
@@ -167,4 +168,53 @@ def test_prefill_q6k_configs2_shapes(hip, rows, cols):
     got = out.cpu().numpy()
     assert np.isfinite(got).all() and float(np.std(got)) > 0.1
     want = amd64(raw.cpu().numpy(), x.cpu().numpy(), rows, cols, ref.Q6_K)
+    assert_bits(got, want, "every token vs amd64 oracle")
+
+
+@pytest.mark.parametrize("rows,cols,p", [(300, 1024, 17), (64, 256, 100), (1000, 4096, 64),
+                                         (70, 14336, 40), (130, 2048, 33)])
+def test_prefill_q8_0_bit_exact_small(hip, rows, cols, p):
+    """Q8_0 batches of more than 16 tokens (64 x 64 tiles on the vector
+    units): ragged row and token tiles against the amd64-order oracle."""
+    data, _ = quant_matrix(ref.Q8_0, rows, cols, 700 + p + rows)
+    w = hip.Weight.from_host(data, ref.Q8_0, rows, cols)
+    xs = normal(701 + p, (p, cols))
+    xs[0] = 0.0
+    xs[1] *= 1e4
+    print(f"prefill Q8_0 {rows}x{cols} p={p}", flush=True)
+    got = w.matvec_batch(xs)
+    assert_bits(got, amd64(data, xs, rows, cols, ref.Q8_0), "vs amd64 oracle")
+
+
+def test_prefill_q8_0_extremes(hip):
+    """Weights -128 and 127 against activations +-127: every 4-byte dot at
+    its extremes (the reference's VPMADDUBSW pairs stay inside int16)."""
+    rows, cols, p = 64, 1024, 20
+    data, _ = quant_matrix(ref.Q8_0, rows, cols, 94)
+    blocks = data.reshape(rows * (cols // 32), 34)
+    blocks[0::2, 2:] = 0x80                     # -128
+    blocks[1::2, 2:] = 0x7F                     # 127
+    xs = np.where(np.arange(cols) % 3 == 0, 1.0, -1.0).astype(np.float32) * np.ones((p, 1), np.float32)
+    xs[1::2] *= -1.0
+    w = hip.Weight.from_host(data, ref.Q8_0, rows, cols)
+    got = w.matvec_batch(xs)
+    assert_bits(got, amd64(data, xs, rows, cols, ref.Q8_0), "extremes vs amd64 oracle")
+
+
+@pytest.mark.parametrize("rows,cols", [(14336, 4096), (4096, 14336)])
+def test_prefill_q8_0_configs2_shapes(hip, rows, cols):
+    """Q8_0 at the configs[1] / configs[2] shapes, 512 tokens: every token
+    against the amd64-order oracle."""
+    import torch
+    p = 512
+    w, raw = device_weight(hip, hip.TYPE_Q8_0, rows, cols, 5000 + rows)
+    x = torch.empty((p, cols), dtype=torch.float32, device="cuda")
+    hip.fill_normal_dev(x, 79, 1.0)
+    out = torch.empty((p, rows), dtype=torch.float32, device="cuda")
+    print(f"prefill Q8_0 {rows}x{cols} p={p}", flush=True)
+    w.matvec_dev(x, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all() and float(np.std(got)) > 0.1
+    want = amd64(raw.cpu().numpy(), x.cpu().numpy(), rows, cols, ref.Q8_0)
     assert_bits(got, want, "every token vs amd64 oracle")
