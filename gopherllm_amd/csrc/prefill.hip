@@ -641,7 +641,7 @@ __global__ __launch_bounds__(512) void prefill_q4k_tiled_kernel(PfArgs a, TlMap 
     }
 }
 
-// --- Q6_K, more than 16 activation rows: 32 x 64 staged tiles --------------
+// --- Q6_K, more than 16 activation rows: 64 x 64 staged tiles --------------
 // q6kDotQ8KRow (kernels_amd64.s Q6KQ8QUAD, the batch-1 row kernel
 // gemv_q6k_kernel) per AVX2 lane k of a 256-element block b:
 //   I       = sum over the lane's 32 elements of sc(e) * code(e) * q8(e)
@@ -656,33 +656,47 @@ __global__ __launch_bounds__(512) void prefill_q4k_tiled_kernel(PfArgs a, TlMap 
 // the two v_mfma_f32_16x16x32_f16 results is its exact integer sum and
 // fma(hi, 16, lo) rounds 16 hi + lo once: float(I).  The chains then run in
 // VALU registers in the reference's order.
-// Workgroup: 32 rows x 64 tokens, eight waves; wave w owns rows 16 (w & 1)
-// .. + 15 and tokens 16 (w >> 1) .. + 15.  Per block, double-buffered in
-// LDS: both A operands of the 32 rows (dequantised once per workgroup from
-// the raw block bytes, copied global -> LDS two blocks ahead), the four
-// 16-token B tiles (the quantiser's f16 layout), the tokens' xs16 and
-// xscale and the rows' scales and d.  Weights need rows * rb < 4 GiB and
+// Workgroup: 64 rows x 64 tokens, eight waves; wave w owns rows 16 (w & 3)
+// .. + 15 and the token tiles 2 (w >> 2), 2 (w >> 2) + 1.  Per block,
+// double-buffered in LDS and copied global -> LDS one block ahead: the 64
+// rows' block bytes as stored (ql, qh, scales; the A operands are built
+// from them by the wave that uses them, lane (g, c) the 8 codes of row c,
+// lane k, kappa 8 g .. + 7), the four 16-token B tiles (the quantiser's f16
+// layout) and the tokens' xs16 and xscale; the rows' scales and d as floats
+// are prepared once per block.  Weights need rows * rb < 4 GiB and
 // 16-byte aligned blocks (blocks % 8 == 0).
-constexpr int kQ6Rows = 32, kQ6Tok = 64;
-constexpr int kQ6RawPieces = 448;  // 7 waves x 64: 32 rows x 13 pieces of 16 bytes, then padding
+constexpr int kQ6Rows = 64, kQ6Tok = 64;
+constexpr int kQ6RawPieces = 64 * 13;  // 64 rows x 13 pieces of 16 bytes (208-byte blocks)
 struct Q6Stage {
-    uint8_t alo[2 * 8 * 4 * 256];  // [row group][lane k][group g][row c][8 halves]: sc * (code & 15)
-    uint8_t ahi[2 * 8 * 4 * 256];  //                                                sc * (code >> 4)
+    uint8_t q[kQ6RawPieces * 16];  // [row][208]: ql 128, qh 64, scales 16
+    uint32_t dw[64];               // [row]: the dword holding d of blocks b & ~1, b | 1
     uint8_t b16[4 * 8 * 4 * 256];  // [token tile][lane k][group g][token c][8 halves]
     float x16[kQ6Tok][16];         // [token][16-group] xs16
-    float sc[16][kQ6Rows + 4];     // [scale index][row] int8 scale
-    float d[kQ6Rows], xs[kQ6Tok];
-};
-struct Q6Raw {
-    uint8_t q[kQ6RawPieces * 16];  // [row][208]: ql 128, qh 64, scales 16
-    uint32_t d[64];                // [row]: the dword holding d of blocks b & ~1, b | 1
+    float xs[kQ6Tok];
+    float sc[16][kQ6Rows];         // [scale index][row] int8 scale
+    float d[kQ6Rows];
 };
 
-// Block b's token operands into S: four 1 KB pieces of B per wave, the
-// tokens' xs16 (waves 0-3) and xscales (wave 4): five copies on waves 0-4,
-// four on 5-7.
-__device__ __forceinline__ void q6_copy_tokens(const PfArgs& a, int w, int lane, int tile0, int tok0,
-                                               int b, Q6Stage& S) {
+// Block b's operands into S: the 832 raw pieces (two 1 KB copies on waves
+// 0-5, one on wave 6), the rows' d dwords (wave 7), four 1 KB pieces of B
+// per wave, the tokens' xs16 (waves 0-3) and xscales (wave 4).
+__device__ __forceinline__ void q6_copy(const PfArgs& a, int w, int lane, int row0, int tile0, int tok0,
+                                        int b, Q6Stage& S) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        // pieces 128 w + 64 i + lane of 832: waves 0-5 two each, wave 6 one
+        const int pc = 128 * w + 64 * i + lane;
+        if (pc < kQ6RawPieces) {  // wave-uniform: 832 = 6.5 x 128
+            const int r = pc / 13, off = (pc % 13) * 16;
+            const size_t row = (size_t)min(row0 + r, a.rows - 1);
+            lds_copy16_s(a.w, (uint32_t)(row * a.rb + (size_t)b * 208 + off), lds_addr(S.q + 16 * (pc - lane)));
+        }
+    }
+    if (w == 7) {
+        const size_t row = (size_t)min(row0 + lane, a.rows - 1);
+        lds_copy4_s(a.w, (uint32_t)(row * a.rb + (size_t)a.blocks * 208 + (size_t)(b & ~1) * 2),
+                    lds_addr(&S.dw[0]));
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int ch = 4 * w + i, tt = ch >> 3, piece = ch & 7;
@@ -699,19 +713,13 @@ __device__ __forceinline__ void q6_copy_tokens(const PfArgs& a, int w, int lane,
     }
 }
 
-// Block b of the 32 rows into R: waves 0-6 one 1 KB piece each (row-major
-// 208-byte blocks; pieces past the rows repeat a valid source into the
-// padding), wave 7 the rows' d dwords.  One copy per wave.
-__device__ __forceinline__ void q6_copy_raw(const PfArgs& a, int w, int lane, int row0, int b, Q6Raw& R) {
-    if (w < 7) {
-        const int pc = min(64 * w + lane, 32 * 13 - 1), r = pc / 13, off = (pc % 13) * 16;
-        const size_t row = (size_t)min(row0 + r, a.rows - 1);
-        lds_copy16_s(a.w, (uint32_t)(row * a.rb + (size_t)b * 208 + off), lds_addr(R.q + 1024 * w));
-    } else {
-        const size_t row = (size_t)min(row0 + (lane & 31), a.rows - 1);
-        lds_copy4_s(a.w, (uint32_t)(row * a.rb + (size_t)a.blocks * 208 + (size_t)(b & ~1) * 2),
-                    lds_addr(&R.d[0]));
-    }
+// The rows' scales and d of block b as floats: thread t scale index t >> 5
+// of rows t & 31 and 32 + (t & 31); threads 0-63 d of row t.
+__device__ __forceinline__ void q6_prep(int tid, int b, Q6Stage& S) {
+    const int idx = tid >> 5, r = tid & 31;
+    S.sc[idx][r] = (float)(int8_t)S.q[r * 208 + 192 + idx];
+    S.sc[idx][32 + r] = (float)(int8_t)S.q[(32 + r) * 208 + 192 + idx];
+    if (tid < 64) S.d[tid] = f16_bits_to_f32((S.dw[tid] >> (16 * (b & 1))) & 0xffffu);
 }
 
 // four bytes (values 0..255, exact) -> two half2 words
@@ -724,66 +732,46 @@ __device__ __forceinline__ void u8x4_to_h(uint32_t v, uint32_t& lo, uint32_t& hi
     hi = __builtin_bit_cast(uint32_t, c);
 }
 
-// Dequantisation of raw block R into S: thread t the A operands of (row
-// group r, lane k, group g, row c) = (r, t >> 6, (t >> 4) & 3, t & 15) for
-// r = 0, 1 (its 16-byte writes: consecutive per wave), the scales as floats
-// (thread t: scale index t >> 5 of row t & 31) and d (threads 0-31).
-__device__ __forceinline__ void q6_dequant(int tid, int b, const Q6Raw& R, Q6Stage& S) {
-    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
-    const int c = tid & 15, g = (tid >> 4) & 3, k = tid >> 6;
-    const int h = g >> 1, sh = 4 * (g & 1), hk = k >> 2;
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-        const uint8_t* blk = R.q + (16 * r + c) * 208;
-        const uint2 ql = *(const uint2*)(blk + 16 * k + 8 * h);   // ql dwords 2h, 2h + 1 of lane k
-        const uint32_t qh = *(const uint32_t*)(blk + 128 + 8 * k + 4 * h);
-        // quads m = 2g, 2g + 1: scales 8h + 4 (g & 1) + hk and + 2
-        const int s0 = (int)(int8_t)blk[192 + 8 * h + sh + hk];
-        const int s1 = (int)(int8_t)blk[192 + 8 * h + sh + 2 + hk];
-        const h2v f0 = {(_Float16)(float)s0, (_Float16)(float)s0};
-        const h2v f1 = {(_Float16)(float)s1, (_Float16)(float)s1};
-        uint32_t l0, l1, l2, l3, h0, h1, h2, h3;
-        u8x4_to_h((ql.x >> sh) & 0x0f0f0f0fu, l0, l1);
-        u8x4_to_h((ql.y >> sh) & 0x0f0f0f0fu, l2, l3);
-        u8x4_to_h((qh >> sh) & 0x03030303u, h0, h1);
-        u8x4_to_h((qh >> (sh + 2)) & 0x03030303u, h2, h3);
-        // exact: products of small integers below 2048
-        const h2v a0 = __builtin_bit_cast(h2v, l0) * f0, a1 = __builtin_bit_cast(h2v, l1) * f0;
-        const h2v a2 = __builtin_bit_cast(h2v, l2) * f1, a3 = __builtin_bit_cast(h2v, l3) * f1;
-        const h2v b0 = __builtin_bit_cast(h2v, h0) * f0, b1 = __builtin_bit_cast(h2v, h1) * f0;
-        const h2v b2 = __builtin_bit_cast(h2v, h2) * f1, b3 = __builtin_bit_cast(h2v, h3) * f1;
-        const int off = ((r * 8 + k) * 4 + g) * 256 + c * 16;
-        h8v lo, hi;
-        lo[0] = a0[0]; lo[1] = a0[1]; lo[2] = a1[0]; lo[3] = a1[1];
-        lo[4] = a2[0]; lo[5] = a2[1]; lo[6] = a3[0]; lo[7] = a3[1];
-        hi[0] = b0[0]; hi[1] = b0[1]; hi[2] = b1[0]; hi[3] = b1[1];
-        hi[4] = b2[0]; hi[5] = b2[1]; hi[6] = b3[0]; hi[7] = b3[1];
-        *(h8v*)(S.alo + off) = lo;
-        *(h8v*)(S.ahi + off) = hi;
-    }
-    {
-        const int idx = tid >> 5, row = tid & 31;
-        S.sc[idx][row] = (float)(int8_t)R.q[row * 208 + 192 + idx];
-    }
-    if (tid < 32) S.d[tid] = f16_bits_to_f32((R.d[tid] >> (16 * (b & 1))) & 0xffffu);
+// A operands (low and high code fields) of lane (g, c) for lane k from its
+// row's raw bytes: quads m = 2g, 2g + 1 of lane k (ql dwords 2h, 2h + 1 and
+// qh dword h of the lane, h = g >> 1, nibble / bit-pair shift 4 (g & 1))
+// with scales 8h + 4 (g & 1) + (k >> 2) and + 2.
+struct Q6Raw8 {
+    uint2 ql;
+    uint32_t qh, sc;
+};
+__device__ __forceinline__ void q6_raw(const uint8_t* row, int k, int g, Q6Raw8& o) {
+    const int h = g >> 1;
+    o.ql = *(const uint2*)(row + 16 * k + 8 * h);
+    o.qh = *(const uint32_t*)(row + 128 + 8 * k + 4 * h);
+    o.sc = *(const uint32_t*)(row + 192 + 8 * h + 4 * (g & 1));
 }
-
-// Workgroup -> tile map as tl_map, with 32-row tiles.
-static TlMap q6_map(int rows, int p) {
-    TlMap m;
-    m.row_tiles = (rows + kQ6Rows - 1) / kQ6Rows;
-    m.tok_tiles = (p + kQ6Tok - 1) / kQ6Tok;
-    m.h = 1;
-    while (m.h < 8 && (m.tok_tiles + m.h - 1) / m.h > 4) m.h *= 2;
-    m.v = 8 / m.h;
-    m.tg_size = (m.tok_tiles + m.h - 1) / m.h;
-    m.rg_size = (m.row_tiles + m.v - 1) / m.v;
-    return m;
+__device__ __forceinline__ void q6_operands(const Q6Raw8& o, int k, int g, h8v& lo, h8v& hi) {
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    const int sh = 4 * (g & 1), hk = k >> 2;
+    // scale bytes hk and hk + 2 of o.sc, as exact f16 (byte ^ 0x80 = s + 128)
+    const uint32_t sv = o.sc ^ 0x80808080u;
+    const h2v m1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const h2v f0 = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, sv, hk ? 0x04010401u : 0x04000400u)) + m1152;
+    const h2v f1 = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, sv, hk ? 0x04030403u : 0x04020402u)) + m1152;
+    uint32_t l0, l1, l2, l3, h0, h1, h2, h3;
+    u8x4_to_h((o.ql.x >> sh) & 0x0f0f0f0fu, l0, l1);
+    u8x4_to_h((o.ql.y >> sh) & 0x0f0f0f0fu, l2, l3);
+    u8x4_to_h((o.qh >> sh) & 0x03030303u, h0, h1);
+    u8x4_to_h((o.qh >> (sh + 2)) & 0x03030303u, h2, h3);
+    // exact: products of small integers below 2048
+    const h2v a0 = __builtin_bit_cast(h2v, l0) * f0, a1 = __builtin_bit_cast(h2v, l1) * f0;
+    const h2v a2 = __builtin_bit_cast(h2v, l2) * f1, a3 = __builtin_bit_cast(h2v, l3) * f1;
+    const h2v b0 = __builtin_bit_cast(h2v, h0) * f0, b1 = __builtin_bit_cast(h2v, h1) * f0;
+    const h2v b2 = __builtin_bit_cast(h2v, h2) * f1, b3 = __builtin_bit_cast(h2v, h3) * f1;
+    lo[0] = a0[0]; lo[1] = a0[1]; lo[2] = a1[0]; lo[3] = a1[1];
+    lo[4] = a2[0]; lo[5] = a2[1]; lo[6] = a3[0]; lo[7] = a3[1];
+    hi[0] = b0[0]; hi[1] = b0[1]; hi[2] = b1[0]; hi[3] = b1[1];
+    hi[4] = b2[0]; hi[5] = b2[1]; hi[6] = b3[0]; hi[7] = b3[1];
 }
 
 __global__ __launch_bounds__(512) void prefill_q6k_tiled_kernel(PfArgs a, TlMap mp) {
     __shared__ __align__(16) Q6Stage st[2];
-    __shared__ __align__(16) Q6Raw raw[2];
     const int id = blockIdx.x, xcd = id & 7, local = id >> 3;
     const int lt = local % mp.tg_size, lrow = local / mp.tg_size;
     const int ttile = (xcd % mp.h) * mp.tg_size + lt, rtile = (xcd / mp.h) * mp.rg_size + lrow;
@@ -791,97 +779,111 @@ __global__ __launch_bounds__(512) void prefill_q6k_tiled_kernel(PfArgs a, TlMap 
     const int row0 = rtile * kQ6Rows, tok0 = ttile * kQ6Tok, tile0 = tok0 / 16;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c = lane & 15;
-    const int rg = w & 1, tt = w >> 1;
+    const int rg = w & 3, tg = w >> 2;
     const int nb = a.blocks;
 
-    float accF[8][4], accM[8][4];
+    float accF[2][8][4], accM[2][8][4];
 #pragma unroll
-    for (int k = 0; k < 8; k++)
+    for (int n = 0; n < 2; n++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) accF[k][i] = accM[k][i] = 0.0f;
+        for (int k = 0; k < 8; k++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) accF[n][k][i] = accM[n][k][i] = 0.0f;
 
-    // prologue: raw blocks 0 and 1, token operands of block 0
-    q6_copy_raw(a, w, lane, row0, 0, raw[0]);
-    q6_copy_raw(a, w, lane, row0, min(1, nb - 1), raw[1]);
-    q6_copy_tokens(a, w, lane, tile0, tok0, 0, st[0]);
+    q6_copy(a, w, lane, row0, tile0, tok0, 0, st[0]);
     wait_vmem_le<0>();
     lds_barrier();
-    q6_dequant(tid, 0, raw[0], st[0]);
+    q6_prep(tid, 0, st[0]);
     wait_lgkm0();
     lds_barrier();
 #pragma unroll 1
     for (int b = 0; b < nb; b++) {
-        // unconditional copies (clamped to the last block, into buffers not
-        // read this iteration) keep the vmcnt counts constant: tokens of
-        // b + 1 (five copies on waves 0-4, four on 5-7), raw of b + 2 (one)
-        q6_copy_tokens(a, w, lane, tile0, tok0, min(b + 1, nb - 1), st[(b + 1) & 1]);
-        q6_copy_raw(a, w, lane, row0, min(b + 2, nb - 1), raw[b & 1]);
+        // unconditional copies of block b + 1 (clamped to the last block)
+        // into the stage not read this iteration
+        q6_copy(a, w, lane, row0, tile0, tok0, min(b + 1, nb - 1), st[(b + 1) & 1]);
         const Q6Stage& S = st[b & 1];
-        const int t = 16 * tt + c;  // this lane's token in the tile
-        const float xv = S.xs[t];
-        float dv[4], dxs[4];
+        // per-lane LDS offsets, rebuilt every block behind an empty asm so
+        // the compiler keeps one register per operand stream instead of
+        // hoisting an address per (lane k, tile) out of the loop
+        const int h = g >> 1;
+        uint32_t o_ql = (16 * rg + c) * 208 + 8 * h, o_qh = (16 * rg + c) * 208 + 128 + 4 * h;
+        uint32_t o_sc = (16 * rg + c) * 208 + 192 + 8 * h + 4 * (g & 1);
+        uint32_t o_b = (2 * tg * 8 * 4 + g) * 256 + c * 16, o_x = (32 * tg + c) * 64;
+        uint32_t o_k = (16 * rg + 4 * g) * 4;
+        asm volatile("" : "+v"(o_ql), "+v"(o_qh), "+v"(o_sc), "+v"(o_b), "+v"(o_x), "+v"(o_k));
+        const uint8_t* q = S.q;
+        const uint8_t* bt = S.b16;
+        const uint8_t* xt = (const uint8_t*)&S.x16[0][0];
+        const uint8_t* sct = (const uint8_t*)&S.sc[0][0];
+        float dv[4], dxs[2][4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            dv[i] = S.d[16 * rg + 4 * g + i];
-            dxs[i] = dv[i] * xv;  // VMULSS d * xscale
+        for (int i = 0; i < 4; i++) dv[i] = S.d[16 * rg + 4 * g + i];
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            const float xv = S.xs[32 * tg + 16 * n + c];
+#pragma unroll
+            for (int i = 0; i < 4; i++) dxs[n][i] = dv[i] * xv;  // VMULSS d * xscale
         }
         const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
-        // lane k + 1's operands are read while lane k's products and chains
-        // run (one step ahead: more would not fit two waves per SIMD)
-        struct Ops {
-            h8v alo, ahi, bv;
-            float x0, x8;
-            f4v sk, sk8;
-        };
-        auto ops = [&](int k, Ops& o) __attribute__((always_inline)) {
-            o.alo = *(const h8v*)(S.alo + ((rg * 8 + k) * 4 + g) * 256 + c * 16);
-            o.ahi = *(const h8v*)(S.ahi + ((rg * 8 + k) * 4 + g) * 256 + c * 16);
-            o.bv = *(const h8v*)(S.b16 + ((tt * 8 + k) * 4 + g) * 256 + c * 16);
-            o.x0 = S.x16[t][k] * 32.0f;  // ScaleF32(xs, 32)
-            o.x8 = S.x16[t][8 + k] * 32.0f;
-            o.sk = *(const f4v*)&S.sc[k][16 * rg + 4 * g];
-            o.sk8 = *(const f4v*)&S.sc[8 + k][16 * rg + 4 * g];
-        };
-        Ops o[2];
-        ops(0, o[0]);
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            if (k < 7) ops(k + 1, o[(k + 1) & 1]);
-            const Ops& cur = o[k & 1];
-            const f4v plo = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.alo, cur.bv, z, 0, 0, 0);
-            const f4v phi = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.ahi, cur.bv, z, 0, 0, 0);
+            Q6Raw8 raw;
+            raw.ql = *(const uint2*)(q + o_ql + 16 * k);
+            raw.qh = *(const uint32_t*)(q + o_qh + 8 * k);
+            raw.sc = *(const uint32_t*)(q + o_sc);
+            h8v bv[2];
+            float x0[2], x8[2];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float iv = fmaf(phi[i], 16.0f, plo[i]);  // float(I)
-                float o2 = cur.sk[i] * cur.x0;                 // VMULPS
-                o2 = fmaf(cur.sk8[i], cur.x8, o2);             // VFMADD231PS
-                accM[k][i] = fmaf(dv[i], o2, accM[k][i]);
-                accF[k][i] = fmaf(iv, dxs[i], accF[k][i]);
+            for (int n = 0; n < 2; n++) {
+                bv[n] = *(const h8v*)(bt + o_b + n * 8192 + k * 1024);
+                x0[n] = *(const float*)(xt + o_x + n * 1024 + 4 * k) * 32.0f;  // ScaleF32(xs, 32)
+                x8[n] = *(const float*)(xt + o_x + n * 1024 + 4 * (8 + k)) * 32.0f;
             }
+            const f4v sk = *(const f4v*)(sct + o_k + k * 256);
+            const f4v sk8 = *(const f4v*)(sct + o_k + (8 + k) * 256);
+            h8v alo, ahi;
+            q6_operands(raw, k, g, alo, ahi);
+#pragma unroll
+            for (int n = 0; n < 2; n++) {
+                const f4v plo = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bv[n], z, 0, 0, 0);
+                const f4v phi = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bv[n], z, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float iv = fmaf(phi[i], 16.0f, plo[i]);  // float(I)
+                    float o2 = sk[i] * x0[n];                      // VMULPS
+                    o2 = fmaf(sk8[i], x8[n], o2);                  // VFMADD231PS
+                    accM[n][k][i] = fmaf(dv[i], o2, accM[n][k][i]);
+                    accF[n][k][i] = fmaf(iv, dxs[n][i], accF[n][k][i]);
+                }
+            }
+            // lane k's accumulators final here: without the pin the compiler
+            // interleaves the eight lanes' chains past the register file
+#pragma unroll
+            for (int n = 0; n < 2; n++)
+                asm volatile("" : "+v"(accF[n][k][0]), "+v"(accF[n][k][1]), "+v"(accF[n][k][2]),
+                             "+v"(accF[n][k][3]), "+v"(accM[n][k][0]), "+v"(accM[n][k][1]),
+                             "+v"(accM[n][k][2]), "+v"(accM[n][k][3]));
             __builtin_amdgcn_sched_barrier(0);
         }
-        // raw block b + 1 (copied last iteration) has landed once at most
-        // this iteration's copies are outstanding
-        if (w < 5) wait_vmem_le<6>();
-        else wait_vmem_le<5>();
-        lds_barrier();  // raw b + 1 complete from every wave; stage (b + 1) & 1 free
-        q6_dequant(tid, min(b + 1, nb - 1), raw[(b + 1) & 1], st[(b + 1) & 1]);
-        wait_vmem_le<1>();  // token operands of b + 1
+        wait_vmem_le<0>();  // block b + 1's copies, issued before this block's products
+        lds_barrier();
+        q6_prep(tid, min(b + 1, nb - 1), st[(b + 1) & 1]);
         wait_lgkm0();
         lds_barrier();
     }
-    wait_vmem_le<0>();  // the clamped copies of the last iterations
-    const int tk = tok0 + 16 * tt + c;
-    if (tk < a.p) {
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+        const int t = tok0 + 32 * tg + 16 * n + c;
+        if (t >= a.p) continue;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int rr = row0 + 16 * rg + 4 * g + i;
             if (rr >= a.rows) continue;
             float v[8];
 #pragma unroll
-            for (int k = 0; k < 8; k++) v[k] = accF[k][i] - accM[k][i];
+            for (int k = 0; k < 8; k++) v[k] = accF[n][k][i] - accM[n][k][i];
             const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
-            a.out[(size_t)tk * a.out_stride + rr] = (s0 + s1) + (s2 + s3);
+            a.out[(size_t)t * a.out_stride + rr] = (s0 + s1) + (s2 + s3);
         }
     }
 }
@@ -893,7 +895,7 @@ int launch_q6k_tiled(const uint8_t* d_w, size_t rb, int rows, int blocks, const 
         return fail(GLLM_EINVAL, "prefill: Q6_K tiles need > %d tokens, blocks %% 8 == 0, < 4 GiB",
                     kTiledMinP);
     PfArgs a{d_w, rb, rows, blocks, act, p, out, out_stride};
-    const TlMap mp = q6_map(rows, p);
+    const TlMap mp = tl_map(rows, p);
     hipLaunchKernelGGL(prefill_q6k_tiled_kernel, dim3(8 * mp.tg_size * mp.rg_size), dim3(512), 0, s, a,
                        mp);
     GLLM_HIP(hipGetLastError());
