@@ -294,7 +294,30 @@ def decode_bench(args):
         out["cpu_baseline"] = decode_cpu_baseline(d, prompt, toks, P, N, args.cpu_seconds)
     else:
         d.release()
+    out["q4km"] = q4km_prefill(P, prompt)
     return out
+
+
+def q4km_prefill(P, prompt):
+    """Prefill of the same 512 ids on a Q4_K_M-style 8B-shape decoder (Q6_K
+    attn_v / ffn_down on every other layer: synth.q4km_type), the second of
+    two runs, plus one greedy step as a smoke check of the mixed graph."""
+    import torch
+
+    from gopherllm_amd import synth
+
+    cfg = dict(synth.LLAMA3_8B)
+    d = synth.build_decoder(cfg, max_len=P + 8, seed=1, type_of=synth.q4km_type)
+    d.prefill(prompt)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tok = d.prefill(prompt)
+    t1 = time.perf_counter()
+    tok = d.decode(tok, P)
+    d.release()
+    return {"workload": "Llama-3-8B-shape synthetic decoder, Q4_K layers with Q6_K attn_v and "
+                        "ffn_down on even layers, Q6_K head; prompt 512 ids (the decode record's)",
+            "prefill_tok_s": round(P / (t1 - t0), 2)}
 
 
 def decode_cpu_baseline(d, prompt, toks, P, N, seconds):

@@ -57,13 +57,23 @@ class _Scratch:
         return Weight.from_device(dst, qtype, rows, cols)
 
 
-def build_decoder(cfg: dict, max_len: int, seed: int = 1) -> LlamaDecoder:
-    """A resident decoder with synthetic weights of shape `cfg`."""
+def q4km_type(cfg: dict, layer: int, name: str) -> int:
+    """Q4_K_M-style mix (llama.cpp's Q4_K_M keeps attn_v and ffn_down at a
+    higher precision on part of the layers): Q6_K for those two tensors on
+    every other layer, the configuration's layer type elsewhere."""
+    return _lib.TYPE_Q6_K if name in ("wv", "w2") and layer % 2 == 0 else cfg["layer_type"]
+
+
+def build_decoder(cfg: dict, max_len: int, seed: int = 1, type_of=None) -> LlamaDecoder:
+    """A resident decoder with synthetic weights of shape `cfg`; type_of(cfg,
+    layer, name) picks a layer tensor's type (default: cfg["layer_type"])."""
     import torch
 
     shapes = layer_shapes(cfg)
+    tof = type_of or (lambda c, l, name: c["layer_type"])
+    types = {tof(cfg, l, name) for l in range(cfg["n_layers"]) for name in shapes}
     big = max([r * c for r, c in shapes.values()] + [cfg["vocab"] * cfg["dim"]])
-    big_bytes = max([r * row_bytes(cfg["layer_type"], c) for r, c in shapes.values()] +
+    big_bytes = max([r * row_bytes(t, c) for r, c in shapes.values() for t in types] +
                     [cfg["vocab"] * row_bytes(t, cfg["dim"]) for t in (cfg["emb_type"], cfg["out_type"])])
     sc = _Scratch(torch, big, big_bytes)
     d = LlamaDecoder(cfg, max_len)
@@ -76,7 +86,7 @@ def build_decoder(cfg: dict, max_len: int, seed: int = 1) -> LlamaDecoder:
     for l in range(cfg["n_layers"]):
         for name, slot in LAYER_SLOTS.items():
             r, c = shapes[name]
-            d.set_weight(l, slot, sc.weight(cfg["layer_type"], r, c, tensor_seed(seed, l, name)))
+            d.set_weight(l, slot, sc.weight(tof(cfg, l, name), r, c, tensor_seed(seed, l, name)))
         d.set_norm(l, _lib.T_ATTN_NORM, ones)
         d.set_norm(l, _lib.T_FFN_NORM, ones)
     torch.cuda.synchronize()

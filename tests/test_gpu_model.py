@@ -324,3 +324,36 @@ def test_prefill_crossing_position_6144(hip):
         got = gpu.decode(tok, pos)
         assert got == want, pos
         tok = want
+
+
+def test_prefill_mixed_types_take_the_batched_tiles(hip):
+    """Q4_K_M-style mix at widths whose rows hold a multiple of 8 blocks
+    (dim 2048, hidden 4096): the prefill's Q6_K attn_v / ffn_down run the
+    matrix-core tiles and a Q8_0 ffn_down the vector-unit tiles (prompt of
+    90 tokens: ragged 64-token tiles), then greedy steps; logits, hidden
+    states and tokens equal the oracle's."""
+    from gopherllm_amd.decoder import LlamaDecoder
+
+    def types(l, name):
+        if name == "w2" and l == 1:
+            return ref.Q8_0
+        return q4km_types(l, name)
+
+    m = tiny_llama(seed=51, n_layers=2, dim=2048, hidden=4096, n_heads=16, n_kv_heads=4,
+                   head_dim=128, vocab=600, type_of=types)
+    prompt = np.random.default_rng(52).integers(0, 600, 90)
+    max_len = 104
+    gpu = LlamaDecoder.from_host_model(m, max_len)
+    cpu = ref.Llama(m, max_len)
+    print("mixed-type model, tiled prefill", flush=True)
+    gt, gl = gpu.prefill(prompt, want_logits=True)
+    ct, cl = cpu.prefill(prompt)
+    assert np.array_equal(bits(gl), bits(cl))
+    assert gt == ct
+    tok = ct
+    for pos in range(len(prompt), len(prompt) + 4):
+        want, hid = cpu.decode(tok, pos)
+        got = gpu.decode(tok, pos)
+        assert np.array_equal(bits(gpu.hidden()), bits(hid)), pos
+        assert got == want, pos
+        tok = want
