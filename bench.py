@@ -802,7 +802,19 @@ def summarize_decode_trace(path):
     import csv
 
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
-    ends = [i for i, r in enumerate(rows) if "argmax_final" in r["Kernel_Name"]][-41:]
+    # decode steps end with the vocabulary head and argmax_final_kernel; take
+    # the longest run of them less than 10 ms apart (the configs[4] decode,
+    # not the Q4_K_M record's lone step), its last 40 steps
+    ends = [i for i, r in enumerate(rows) if "argmax_final" in r["Kernel_Name"] and i > 0 and
+            "gemv_q6k" in rows[i - 1]["Kernel_Name"]]
+    runs, cur = [], []
+    for i in ends:
+        if cur and int(rows[i]["Start_Timestamp"]) - int(rows[cur[-1]]["Start_Timestamp"]) > 10_000_000:
+            runs.append(cur)
+            cur = []
+        cur.append(i)
+    runs.append(cur)
+    ends = max(runs, key=len)[-41:]
     seg = rows[ends[0] + 1: ends[-1] + 1]
     steps = len(ends) - 1
     agg = collections.defaultdict(lambda: [0, 0.0])

@@ -438,7 +438,8 @@ __host__ __device__ constexpr int vdec_pad(int span_max) {
 }
 static size_t vdec_lds_bytes(int kvmul, int span_max) {
     const size_t pad = (size_t)vdec_pad(span_max);
-    return pad * (size_t)(2 * (64 / kvmul) + 4 * kvmul) + 64;
+    // then 1 / denom per head and the waves' maxima per head (5 kvmul floats)
+    return pad * (size_t)(2 * (64 / kvmul) + 4 * kvmul) + 128;
 }
 template <int KVMUL>
 __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
@@ -454,7 +455,7 @@ __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
     const int pad = vdec_pad(span_max);
     uint16_t* vt = (uint16_t*)lds;                  // [DW][pad] f16
     float* w = lds + (size_t)DW * pad / 2;          // [KVMUL][pad]
-    float* red = w + (size_t)KVMUL * pad;           // [KVMUL] 1 / denom
+    float* red = w + (size_t)KVMUL * pad;           // [KVMUL] 1 / denom, then [4][KVMUL] maxima
     // V slice, two positions per item: rows 2tp and 2tp + 1 of piece pc.
     // Loads go out in unrolled chunks of kVDecCh items per thread, every
     // address clamped to a cache row, so a chunk's loads are all in flight
@@ -518,25 +519,50 @@ __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
     const int span = min(d_end ? *d_end - start + 1 : span0, span_max);
     const int nitems = ((span + 1) >> 1) * NP;
     vstore(0, nitems);
-    sstore(0, span);
     for (int base = CH * kVDecThreads; base < nitems; base += CH * kVDecThreads) {
         vload(base, span - 1);
         vstore(base, nitems);
     }
-    for (int base = SC * kVDecThreads; base < span; base += SC * kVDecThreads) {
-        sload(base);
-        sstore(base, span);
-    }
-    __syncthreads();
-    if (wave < KVMUL) {
-        float* wr = w + (size_t)wave * pad;
-        float m = -__int_as_float(0x7f800000);
-        for (int t = lane; t < span; t += 64) m = fmaxf(m, wr[t]);
+    if (span <= SC * kVDecThreads) {  // uniform: the whole score rows are in registers
+        // each head's maximum (order-free: DPP within the waves, LDS across
+        // them), then fastExpF32(s - max) on the registers, stored as w
+        float* wm = red + KVMUL;  // [4 waves][KVMUL]
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        for (int t = lane; t < span; t += 64) wr[t] = fast_exp(wr[t] - m);
+        for (int hh = 0; hh < KVMUL; hh++) {
+            float m = -__int_as_float(0x7f800000);
+#pragma unroll
+            for (int k = 0; k < SC; k++)
+                if (tid + k * kVDecThreads < span) m = fmaxf(m, sv[hh][k]);
+            m = wave_max(m);
+            if (lane == 0) wm[wave * KVMUL + hh] = m;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int hh = 0; hh < KVMUL; hh++) {
+            const float m = fmaxf(fmaxf(wm[hh], wm[KVMUL + hh]), fmaxf(wm[2 * KVMUL + hh], wm[3 * KVMUL + hh]));
+#pragma unroll
+            for (int k = 0; k < SC; k++) {
+                const int t = tid + k * kVDecThreads;
+                if (t < span) w[(size_t)hh * pad + t] = fast_exp(sv[hh][k] - m);
+            }
+        }
+        __syncthreads();
+    } else {
+        sstore(0, span);
+        for (int base = SC * kVDecThreads; base < span; base += SC * kVDecThreads) {
+            sload(base);
+            sstore(base, span);
+        }
+        __syncthreads();
+        if (wave < KVMUL) {
+            float* wr = w + (size_t)wave * pad;
+            float m = -__int_as_float(0x7f800000);
+            for (int t = lane; t < span; t += 64) m = fmaxf(m, wr[t]);
+            m = wave_max(m);
+            for (int t = lane; t < span; t += 64) wr[t] = fast_exp(wr[t] - m);
+        }
+        __syncthreads();
     }
-    __syncthreads();
     const int hh = lane / DW, e = lane % DW;
     float acc = 0.0f;
     if (wave == 0) {
