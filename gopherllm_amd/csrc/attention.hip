@@ -407,6 +407,148 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 }
 
 
+// One decode token over a long span (past what attn_values_dec_kernel keeps
+// in LDS, up to kLongSpan): the arithmetic of attn_softmax_values_kernel<4>
+// (so the same bits), with V staged transposed.  Workgroup = (query head,
+// 32-element slice).  The score row sits in LDS as the softmax weights; V
+// streams in steps of two 64-position tiles: thread (position, 8-element
+// piece) holds 16 bytes of each tile, kLongP steps in flight, and writes
+// them element-major into the step's pair of LDS tiles (vt[e][t], rows
+// padded to 72 halves; two pairs alternate, one barrier per step).  Lanes
+// 0-31 of wave 0 run the 32 value chains reading eight positions of their
+// element per ds_read_b128 and the weights as broadcast quads (a tile's
+// operands read before its chain runs); lane 0 of wave 1 sums the
+// denominator in position order meanwhile.
+constexpr int kLongP = 8;        // steps (two tiles each) in flight per thread
+constexpr int kLongRow = 72;     // halves per element row of a staged tile (64 + 8 padding)
+constexpr int kLongSpan = 32768;
+static size_t long_lds_bytes(int span_max) {
+    return ((size_t)((span_max + 3) & ~3) + 8) * 4 + 4 * (size_t)32 * kLongRow * 2;
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_values_long_kernel(
+    const float* __restrict__ scores, const uint16_t* __restrict__ V, int kv_dim, int kvmul,
+    int start, int span0, int span_max, float* __restrict__ out, const int* __restrict__ d_end) {
+    constexpr int DW = 32, T = kVTile, P = kLongP;
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int h = blockIdx.x >> 2, slice = blockIdx.x & 3;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = h / kvmul;
+    const int wlen = (span_max + 3) & ~3;
+    float* w = lds;                          // [wlen]
+    float* red = w + wlen;                   // [8]
+    uint16_t* vt = (uint16_t*)(red + 8);     // [4 tiles][DW][kLongRow]
+    // thread (position lp of a tile, piece lc): 16 bytes of both tiles of a
+    // step, P steps ahead, rows clamped to span_max - 1 (inside the cache)
+    const uint16_t* Vg = V + (size_t)start * kv_dim + (size_t)g * kFusedHD + slice * DW;
+    const int lp = tid >> 2, lc = tid & 3;
+    uint4 pre[P][2];
+    auto fetch = [&](int st, uint4 (&r)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++)
+            r[hf] = *(const uint4*)(Vg + (size_t)min((2 * st + hf) * T + lp, span_max - 1) * kv_dim + 8 * lc);
+    };
+#pragma unroll
+    for (int q = 0; q < P; q++) fetch(q, pre[q]);
+    if (d_end) span0 = *d_end - start + 1;
+    const int span = min(span0, span_max);
+    const int nsteps = (span + 2 * T - 1) / (2 * T);
+    const float* srow = scores + (size_t)h * span_max;
+    float m = -__int_as_float(0x7f800000);
+    for (int t = tid; t < span; t += 256) {
+        const float v = srow[t];
+        w[t] = v;
+        m = fmaxf(m, v);
+    }
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int t = tid; t < span; t += 256) w[t] = fast_exp(w[t] - mx);
+    // (the first step's barrier orders the exp writes before their readers)
+    const bool chain = tid < DW;
+    const bool summer = tid == 64;
+    float acc = 0.0f, denom = 0.0f;
+    // the chains over one step's two tiles (positions base .. base + 127):
+    // both tiles' operands are read first (one LDS round trip), then the
+    // chain (or the denominator) runs over them in position order
+    auto run_step = [&](const uint16_t* pair, int base) __attribute__((always_inline)) {
+        const int n = max(0, min(2 * T, span - base));
+        if (chain) {
+            const uint16_t* vrow = pair + tid * kLongRow;
+            if (n == 2 * T) {
+                uint4 vv[2 * T / 8];
+                float4 wa[2 * T / 8], wb[2 * T / 8];
+#pragma unroll
+                for (int u = 0; u < 2 * T / 8; u++) {
+                    vv[u] = *(const uint4*)(vrow + (u >> 3) * DW * kLongRow + 8 * (u & 7));
+                    wa[u] = *(const float4*)&w[base + 8 * u];
+                    wb[u] = *(const float4*)&w[base + 8 * u + 4];
+                }
+#pragma unroll
+                for (int u = 0; u < 2 * T / 8; u++) {
+                    const uint4 v = vv[u];
+                    const float4 a = wa[u];
+                    const float4 b = wb[u];
+                    acc = fmaf(a.x, f16_bits_to_f32(v.x & 0xffffu), acc);
+                    acc = fmaf(a.y, f16_bits_to_f32(v.x >> 16), acc);
+                    acc = fmaf(a.z, f16_bits_to_f32(v.y & 0xffffu), acc);
+                    acc = fmaf(a.w, f16_bits_to_f32(v.y >> 16), acc);
+                    acc = fmaf(b.x, f16_bits_to_f32(v.z & 0xffffu), acc);
+                    acc = fmaf(b.y, f16_bits_to_f32(v.z >> 16), acc);
+                    acc = fmaf(b.z, f16_bits_to_f32(v.w & 0xffffu), acc);
+                    acc = fmaf(b.w, f16_bits_to_f32(v.w >> 16), acc);
+                }
+            } else {
+                for (int p = 0; p < n; p++)
+                    acc = fmaf(w[base + p], f16_bits_to_f32(vrow[(p / T) * DW * kLongRow + p % T]), acc);
+            }
+        } else if (summer) {
+            if (n == 2 * T) {
+                float4 q[2 * T / 4];
+#pragma unroll
+                for (int u = 0; u < 2 * T / 4; u++) q[u] = *(const float4*)&w[base + 4 * u];
+#pragma unroll
+                for (int u = 0; u < 2 * T / 4; u++) {
+                    denom = denom + q[u].x;
+                    denom = denom + q[u].y;
+                    denom = denom + q[u].z;
+                    denom = denom + q[u].w;
+                }
+            } else {
+                for (int p = 0; p < n; p++) denom = denom + w[base + p];
+            }
+        }
+    };
+    // one step: stage both tiles from registers, refill those registers P
+    // steps ahead, barrier, then run the two tiles' chains
+    auto step = [&](int st, uint4 (&r)[2]) __attribute__((always_inline)) {
+        uint16_t* pair = vt + (size_t)(st & 1) * 2 * DW * kLongRow;
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+            const uint32_t pv[4] = {r[hf].x, r[hf].y, r[hf].z, r[hf].w};
+            uint16_t* buf = pair + hf * DW * kLongRow;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                buf[(8 * lc + j) * kLongRow + lp] = (uint16_t)(pv[j >> 1] >> (16 * (j & 1)));
+        }
+        fetch(st + P, r);
+        wait_lgkm0();
+        lds_barrier();
+        run_step(pair, 2 * st * T);
+    };
+    // whole groups of P steps, unconditionally (a branch around a step would
+    // make the compiler's vmcnt waits drain the prefetch): steps past the
+    // span stage clamped rows nobody reads and run no chain steps
+    for (int s0 = 0; s0 < nsteps; s0 += P) {
+#pragma unroll
+        for (int q = 0; q < P; q++) step(s0 + q, pre[q]);
+    }
+    if (summer) red[4] = denom > 0.0f ? 1.0f / denom : 1.0f;
+    __syncthreads();
+    if (chain) out[(size_t)h * kFusedHD + slice * DW + tid] = acc * red[4];
+}
+
 template <int DS>
 static size_t smax_lds_bytes(int span_max) {
     return ((size_t)((span_max + 3) & ~3) + 8) * 4 + 2 * (size_t)kVTile * (kFusedHD / DS) * 2;
@@ -1093,6 +1235,22 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
             else
                 hipLaunchKernelGGL(attn_values_dec_kernel<1>, grid, dim3(kVDecThreads), lds, s, sc,
                                    kv->v[l], kv->kv_dim_v, start, span0, span_max, d_out, d_end);
+        } else if (p == 1 && span_max <= kLongSpan) {
+            static const bool lds_ok = [] {
+                // dynamic LDS beyond 64 KB for long rows
+                return hipFuncSetAttribute((const void*)attn_values_long_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)long_lds_bytes(kLongSpan)) == hipSuccess;
+            }();
+            if (!lds_ok) {
+                (void)hipGetLastError();
+                if (long_lds_bytes(span_max) > 65536)
+                    return fail(GLLM_EDEVICE, "attend: %zu bytes of LDS not available",
+                                long_lds_bytes(span_max));
+            }
+            hipLaunchKernelGGL(attn_values_long_kernel, dim3(n_heads * 4), dim3(256),
+                               long_lds_bytes(span_max), s, sc, kv->v[l], kv->kv_dim_v, kvmul,
+                               start, span0, span_max, d_out, d_end);
         } else if (p == 1) {
             static const bool lds_ok = [] {
                 // dynamic LDS beyond 64 KB for long rows

@@ -78,7 +78,7 @@ def rope_rows(x, first_pos, n_heads, theta=500000.0):
     return out
 
 
-@pytest.mark.parametrize("ctx", [4096, 32768])
+@pytest.mark.parametrize("ctx", [4001, 4096, 32768])
 def test_decode_attention_configs3(hip, ctx):
     """32 q heads, 8 kv heads, head_dim 128, F16 KV at 4096 and
     32768, RoPE theta 500000 on Q (at the decode position ctx - 1) and on
