@@ -781,8 +781,10 @@ __global__ __launch_bounds__(256) void gemv_q4k_any_kernel(GemvJob j) {
 // whole weight slice in flight from the start.
 //
 // FUSE = 1: the workgroup quantises x itself (xq_load issued before the
-// weight loads, as in gemv_q4k_kernel); FUSE = 0: pre-quantised activations
-// copied to LDS with direct global->LDS loads.
+// weight loads, as in gemv_q4k_kernel); FUSE = 2 (3 with a residual): the
+// RMSNorm runs in front of the quantiser (norm_regs, as in gemv_q4k_kernel);
+// FUSE = 0: pre-quantised activations copied to LDS with direct global->LDS
+// loads.
 // ---------------------------------------------------------------------------
 // Rows per workgroup of a launch shape: NTH / (8 NS) row groups, RP rows
 // per lane.
@@ -827,20 +829,26 @@ __global__ __launch_bounds__(NTH) void gemv_q4k_bp_kernel(GemvJob j) {
     constexpr int RW = R * RP;
     constexpr int NW = NTH / 64;
     constexpr int QB = FUSE ? (B + NW - 1) / NW : 1;
+    constexpr bool NORM = FUSE >= 2;
     constexpr int cols = B * 256;
     constexpr int XS = q4k_bp_xstride(B);
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x;
     const int k = tid & 7, u = tid >> 3, s = u % NS, g = u / NS;
-    int wi = 0;
-    while (wi + 1 < j.n && (int)blockIdx.x >= j.wg_begin[wi + 1]) wi++;
-    const int r0 = ((int)blockIdx.x - j.wg_begin[wi]) * RW;
-    const int nrows = j.rows[wi];
+    // the launch's weights' rows laid end to end (a workgroup may straddle
+    // two of them): Q, K and V of 4096 + 1024 + 1024 rows fill 256
+    // workgroups of 24 rows where per-weight workgroups would need 257
+    const int r0 = (int)blockIdx.x * RW;
+    const int n1 = j.rows[0], n2 = j.n > 1 ? n1 + j.rows[1] : n1;
+    const int nrows = j.n > 2 ? n2 + j.rows[2] : n2;
     const uint8_t* rowp[RP];
 #pragma unroll
     for (int p = 0; p < RP; p++) {
-        const int r = r0 + g + R * p;
-        rowp[p] = j.w[wi] + (size_t)(r < nrows ? r : nrows - 1) * j.rb;  // dead rows read a valid row
+        int r = r0 + g + R * p;
+        r = r < nrows ? r : nrows - 1;  // dead rows read a valid row
+        rowp[p] = r < n1 ? j.w[0] + (size_t)r * j.rb
+                : r < n2 ? j.w[1] + (size_t)(r - n1) * j.rb
+                         : j.w[2] + (size_t)(r - n2) * j.rb;
     }
     int8_t* q8b = (int8_t*)smem;
     float* xs32b = (float*)(smem + cols);
@@ -852,8 +860,11 @@ __global__ __launch_bounds__(NTH) void gemv_q4k_bp_kernel(GemvJob j) {
         H[p] = *(const uint4*)(rowp[p] + q4k_hdr_off(NS * (k < NB ? k : NB - 1) + s));
     __builtin_amdgcn_sched_barrier(0);
     XRegs<QB> xr;
+    XRegs<NORM ? QB : 1> wr, resr;
     if constexpr (FUSE) {
         xq_load<QB, true>(j.xf, B, xr);
+        if constexpr (NORM) xq_load<QB, true>(j.nw, B, wr);
+        if constexpr (FUSE == 3) xq_load<QB, true>(j.res, B, resr);
     } else {
         stage_act_asm<1>(j, smem);
     }
@@ -867,7 +878,7 @@ __global__ __launch_bounds__(NTH) void gemv_q4k_bp_kernel(GemvJob j) {
             Q[i][p] = *(const uint4*)(rowp[p] + nib0 + (size_t)i * NS * 128);
             __builtin_amdgcn_sched_barrier(0);
         }
-    wait_vmem_le<P * RP>();  // this wave's headers and x (or staged activations)
+    wait_vmem_le<P * RP>();  // this wave's headers and x, norm weights, residual (or staged activations)
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = P; i < NB; i++)
@@ -882,6 +893,9 @@ __global__ __launch_bounds__(NTH) void gemv_q4k_bp_kernel(GemvJob j) {
     for (int i = 0; i < NB; i++)
 #pragma unroll
         for (int p = 0; p < RP; p++) hd[i][p] = Q4KHdr(hdr_of<1>(H[p], i), ms);
+    if constexpr (NORM)  // x' staged over the exchange, which is written after the barrier below
+        norm_regs<QB, FUSE == 3>(xr, wr, resr, B, j.eps, blockIdx.x == 0 ? j.xout : nullptr,
+                                 (float*)X);
     if constexpr (FUSE) xq_store<QB, false>(xr, B, q8b, xs32b, nullptr, xscb);
     wait_lgkm0();
     lds_barrier();
@@ -915,7 +929,11 @@ __global__ __launch_bounds__(NTH) void gemv_q4k_bp_kernel(GemvJob j) {
                 accM = fmaf(v.z, v.w, accM);  // VMULPS + VFMADD231PS
             }
             const float v = tree8(accF - accM);  // VSUBPS + tree
-            if (k == 0 && r0 + cr < nrows) j.out[wi][r0 + cr] = v;
+            const int r = r0 + cr;
+            if (k == 0 && r < nrows) {
+                float* o = r < n1 ? j.out[0] + r : r < n2 ? j.out[1] + (r - n1) : j.out[2] + (r - n2);
+                *o = v;
+            }
         }
     }
 }
@@ -1984,6 +2002,7 @@ struct Q4KBpShape {
 static Q4KBpShape q4k_bp_pick(int total_rows, int B) {
     const bool rows4k = total_rows >= 3584 && total_rows <= 4608;
     if (B == 16 && rows4k) return {8, 1024, 1, 1};
+    if (B == 16 && total_rows == 6144) return {4, 768, 1, 1};  // Q/K/V at 8B: 256 x 24 rows
     if (B == 56 && rows4k) return {14, 896, 1, 2};
     return {0, 0, 0, 0};
 }
@@ -1992,17 +2011,19 @@ template <int B, int NS, int NTH, int RP, int P>
 static int launch_q4k_bp_inst(GemvJob& j, const int* rows, hipStream_t s) {
     constexpr int RW = q4k_bp_rows(NS, NTH, RP);
     j.rows_per_wg = RW;
-    int wg = 0;
-    for (int i = 0; i < j.n; i++) {
-        j.wg_begin[i] = wg;
-        wg += (rows[i] + RW - 1) / RW;
-    }
-    j.wg_begin[j.n] = wg;
-    constexpr size_t lds = q4k_bp_lds(B, NS, NTH, RP);
+    int total = 0;
+    for (int i = 0; i < j.n; i++) total += rows[i];
+    const int wg = (total + RW - 1) / RW;  // rows of all weights end to end
+    constexpr size_t cols = (size_t)B * 256;
+    constexpr size_t lds_x = q4k_bp_lds(B, NS, NTH, RP);
+    constexpr size_t lds_n = q4k_norm_off(cols) + cols * 4 + kNormLds;  // x' over the exchange
+    constexpr size_t lds = lds_x > lds_n ? lds_x : lds_n;
     static_assert(lds <= kStagedActMax, "block-parallel LDS");
     void (*kern)(GemvJob) = gemv_q4k_bp_kernel<B, NS, NTH, RP, 0, P>;
     if constexpr (B * 256 <= kFuseCols) {
-        if (j.xf) kern = gemv_q4k_bp_kernel<B, NS, NTH, RP, 1, P>;
+        if (j.xf && j.nw) kern = j.res ? gemv_q4k_bp_kernel<B, NS, NTH, RP, 3, P>
+                                       : gemv_q4k_bp_kernel<B, NS, NTH, RP, 2, P>;
+        else if (j.xf) kern = gemv_q4k_bp_kernel<B, NS, NTH, RP, 1, P>;
     }
     if (lds > 64 * 1024 && !lds_opt_in((const void*)kern))
         return fail(GLLM_EDEVICE, "gemv: %zu B of LDS refused", lds);
@@ -2017,12 +2038,13 @@ static int launch_q4k_bp(GemvJob& j, const int* rows, hipStream_t s, bool* done)
     int total = 0;
     for (int i = 0; i < j.n; i++) total += rows[i];
     const Q4KBpShape sh = q4k_bp_pick(total, j.blocks);
-    *done = sh.ns != 0 && (!j.xf || j.cols <= kFuseCols) && !j.nw;
+    *done = sh.ns != 0 && (!j.xf || j.cols <= kFuseCols) && (!j.nw || j.xf) && !j.sq_cnt;
     if (!*done) return GLLM_OK;
 #define GLLM_BP_INST(b_, ns_, nth_, rp_, p_)                                               \
     if (j.blocks == b_ && sh.ns == ns_ && sh.nth == nth_ && sh.rp == rp_ && sh.p == p_) \
         return launch_q4k_bp_inst<b_, ns_, nth_, rp_, p_>(j, rows, s);
     GLLM_BP_INST(16, 8, 1024, 1, 1)
+    GLLM_BP_INST(16, 4, 768, 1, 1)
     GLLM_BP_INST(56, 14, 896, 1, 2)
 #undef GLLM_BP_INST
     return fail(GLLM_EINVAL, "gemv: no block-parallel instance (%d, %d, %d, %d, %d)", j.blocks, sh.ns,
