@@ -22,18 +22,66 @@ namespace gllm {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// fastExpF32 (fastmath.go:47-77), operation for operation.
+// fastExpF32 (fastmath.go:47-77), operation for operation, without
+// branches: the two range checks select the result, so a thread's several
+// exps interleave instead of running one exec-masked block after another.
+// Inside the range |t| < 128, so the clamp only keeps the int conversion
+// defined for inputs the selects discard (a NaN still gives NaN).  The
+// empty asm keeps the compiler from turning the first select back into a
+// branch around the polynomial.
 __device__ __forceinline__ float fast_exp(float x) {
-    if (x > 88.02969f) return __int_as_float(0x7f800000);
-    if (x < -87.33654f) return 0.0f;
     const float t = x * 1.44269502f;  // float32(1.4426950408889634)
-    int k;
-    if (t >= 0.0f) k = (int)(t + 0.5f);
-    else k = (int)(t - 0.5f);
+    const float tc = fminf(fmaxf(t, -256.0f), 256.0f);
+    const int k = (int)(tc + (tc >= 0.0f ? 0.5f : -0.5f));
     const float r = (float)((double)x - (double)k * 0.6931471805599453);
     const float p = 1.0f + r * (1.0f + r * (0.5f + r * ((float)(1.0 / 6) +
                     r * ((float)(1.0 / 24) + r * ((float)(1.0 / 120) + r * (float)(1.0 / 720))))));
-    return p * __int_as_float((127 + k) << 23);
+    float v = p * __uint_as_float((uint32_t)(127 + k) << 23);
+    asm volatile("" : "+v"(v));  // computed unconditionally: the selects stay selects
+    return x > 88.02969f ? __int_as_float(0x7f800000) : x < -87.33654f ? 0.0f : v;
+}
+
+// fast_exp of N independent values, step by step across all of them so
+// their dependent chains interleave (one wave per SIMD hides no latency
+// otherwise); each value sees exactly fast_exp's operations.
+template <int N>
+__device__ __forceinline__ void fast_exp_n(const float (&x)[N], float (&y)[N]) {
+    int k[N];
+    float r[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const float t = x[i] * 1.44269502f;
+        const float tc = fminf(fmaxf(t, -256.0f), 256.0f);
+        k[i] = (int)(tc + (tc >= 0.0f ? 0.5f : -0.5f));
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) r[i] = (float)((double)x[i] - (double)k[i] * 0.6931471805599453);
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const float p = 1.0f + r[i] * (1.0f + r[i] * (0.5f + r[i] * ((float)(1.0 / 6) +
+                        r[i] * ((float)(1.0 / 24) + r[i] * ((float)(1.0 / 120) + r[i] * (float)(1.0 / 720))))));
+        y[i] = p * __uint_as_float((uint32_t)(127 + k[i]) << 23);
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" : "+v"(y[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++)
+        y[i] = x[i] > 88.02969f ? __int_as_float(0x7f800000) : x[i] < -87.33654f ? 0.0f : y[i];
+}
+
+// row[t] = fast_exp(row[t] - mx) for t = first, first + stride, ... < span,
+// N positions at a time so that their chains interleave.
+template <int N>
+__device__ __forceinline__ void exp_row(float* row, int first, int stride, int span, float mx) {
+    for (int t0 = first; t0 < span; t0 += N * stride) {
+        float xv[N], ev[N];
+#pragma unroll
+        for (int i = 0; i < N; i++) xv[i] = row[min(t0 + i * stride, span - 1)] - mx;
+        fast_exp_n(xv, ev);
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if (t0 + i * stride < span) row[t0 + i * stride] = ev[i];
+    }
 }
 
 }  // namespace gllm
@@ -105,7 +153,7 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(float* __restrict__ s
     if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
     __syncthreads();
     const float mx = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
-    for (int i = threadIdx.x; i < span; i += 256) s[i] = fast_exp(s[i] - mx);
+    exp_row<8>(s, threadIdx.x, 256, span, mx);
     __syncthreads();
     if (threadIdx.x == 0) {
         float denom = 0.0f;
@@ -149,18 +197,19 @@ __global__ __launch_bounds__(128) void attn_values_kernel(const float* __restric
 
 // Exact path for head_dim 128 in two launches that keep the three-kernel
 // arithmetic (and so its results) while spreading the work over many CUs:
-//   attn_scores128_kernel  one workgroup per (kv head, 64-position chunk,
-//       query token); thread (head, position) runs the eight lanes of
-//       dotF32F16AVX2 (sequential fma chains over elements 8i + j) and the
-//       8->4->2->1 tree, then * scale.  Scores go to a global scratch row
-//       per (token, head).
+//   attn_scores128_kernel  one workgroup per (kv head, 32-position chunk,
+//       query token); the eight lanes of dotF32F16AVX2 (sequential fma
+//       chains over elements 8i + j) of a (head, position) run in two
+//       threads, lanes 0-3 and 4-7, which then join for the 8->4->2->1
+//       tree, then * scale.  Scores go to a global scratch row per
+//       (token, head).
 //   attn_softmax_values_kernel  one workgroup per (query head, token): the
 //       row is read into LDS, max, fastExpF32(s - max), the denominator
 //       summed in position order by one thread, then one thread per element
 //       runs out = fma(w_t, v_t, out) in position order over V tiles staged
 //       through LDS (prefetched from kernel entry), and * 1/denom.
 constexpr int kFusedHD = 128;
-constexpr int kScoreChunk = 64;   // positions per scores workgroup
+constexpr int kScoreChunk = 32;   // positions per scores workgroup
 constexpr int kVTile = 64;        // positions per staged V tile (16 KB)
 constexpr int kVPrefetch = 4;     // tiles in flight per thread (registers)
 constexpr int kSmaxSpan = 6144;   // longest span the softmax/values kernel keeps in LDS, several tokens
@@ -188,52 +237,57 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
     const float* __restrict__ q, const uint16_t* K, int kv_dim, int n_kv, int kvmul,
     int start, int span0, int span_max, float scale, float* __restrict__ scores,
     const int* __restrict__ d_end, AttnRope rope) {
-    __shared__ float qs[4 * kFusedHD];
+    constexpr int pairs = kFusedHD / 2;
+    __shared__ __align__(16) float qs[4 * kFusedHD];
     __shared__ __align__(16) uint16_t kcur[kFusedHD];
     // the chunk's K rows, [16-byte piece][row]: copied once per workgroup
-    // (four 1 KB copies per wave), read by every head's thread of a row
+    // (two 1 KB copies per wave), read by every head's threads of a row
     __shared__ __align__(16) uint8_t kst[kFusedHD / 8][kScoreChunk][16];
     const int g = blockIdx.x, chunk = blockIdx.y, tok = blockIdx.z;
-    const int tid = threadIdx.x;
-    if (d_end) span0 = *d_end - start + 1;  // position read on the device (graph replay)
-    const int span = span0 + tok;
-    if (chunk * kScoreChunk >= span) return;  // uniform
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n_heads = n_kv * kvmul;
     const float* qg = q + ((size_t)tok * n_heads + (size_t)g * kvmul) * kFusedHD;
+    // Everything that does not need the position goes out before it is read:
+    // the K copies (wave wv, copy u: lane l copies row l % 32 of piece
+    // 4 wv + 2 u + l / 32, rows clamped to span_max - 1, inside the cache;
+    // rows past the span are copied and never read), then this thread's q
+    // pair and, when the caller uploads them, the current RoPE rows.
+    {
+        const int row = min(chunk * kScoreChunk + (lane & 31), span_max - 1);
+        const uint16_t* krow = K + (size_t)(start + row) * kv_dim + (size_t)g * kFusedHD + 8 * (lane >> 5);
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+            lds_copy16(krow + 8 * (4 * wv + 2 * u), lds_addr(&kst[4 * wv + 2 * u][0][0]));
+    }
+    // (unconditional loads, clamped or from a dummy row: a load under a
+    // branch is waited for at the branch's end, behind the copies)
+    const bool qthr = tid < kvmul * pairs;  // kvmul <= 4: one q pair per thread
+    const int pr = tid % pairs;
+    const float2 qv = *(const float2*)(qg + 2 * (qthr ? tid : 0));
+    const float* rc = rope.cur ? rope.cur : qg;
+    float sn = rc[pr], cs = rc[pairs + pr];
+    if (d_end) span0 = *d_end - start + 1;  // position read on the device (graph replay)
+    const int span = span0 + tok;
+    if (chunk * kScoreChunk >= span) {  // uniform
+        wait_vmem_le<0>();  // the copies land before the workgroup's LDS is released
+        return;
+    }
     const int tcur = span - 1;  // the new position (rope mode: one token)
     const bool has_cur = rope.sin_tab && tcur / kScoreChunk == chunk;
-    // this thread's K row first, so its latency overlaps the query staging
-    // (clamped to span_max - 1, inside the cache; rows past the span are
-    // loaded and dropped; the new position's row comes from kcur below)
-    const int h = tid / kScoreChunk, t = chunk * kScoreChunk + tid % kScoreChunk;
-    uint4 kr[kFusedHD / 8];
-    {
-        // wave wv copies pieces 4 wv .. 4 wv + 3 of the chunk's 64 rows; lane
-        // l the row chunk * 64 + l (clamped to span_max - 1, inside the cache)
-        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
-        const uint16_t* krow = K + (size_t)(start + min(chunk * kScoreChunk + l, span_max - 1)) * kv_dim +
-                               (size_t)g * kFusedHD;
-#pragma unroll
-        for (int pc = 0; pc < 4; pc++)
-            lds_copy16(krow + 8 * (4 * wv + pc), lds_addr(&kst[4 * wv + pc][0][0]));
-    }
     if (rope.sin_tab) {
-        // the current position's rows: from rope.cur when the caller uploads
-        // them with the position (no wait on the position before the load)
-        const int pos = start + tcur, pairs = kFusedHD / 2;
-        const float* srow = rope.cur ? rope.cur : rope.sin_tab + (size_t)pos * pairs;
-        const float* crow = rope.cur ? rope.cur + pairs : rope.cos_tab + (size_t)pos * pairs;
-        for (int i = tid; i < kvmul * pairs; i += 256) {
-            const int pr = i % pairs;
-            const float sn = srow[pr];
-            const float cs = crow[pr];
-            const float v0 = qg[2 * i], v1 = qg[2 * i + 1];
-            qs[2 * i] = v0 * cs - v1 * sn;
-            qs[2 * i + 1] = v0 * sn + v1 * cs;
+        // applyPreparedRope on q; the workgroup holding the new position
+        // also rotates its k row (kept in kcur) and stores it and the v row
+        const int pos = start + tcur;
+        if (!rope.cur) {
+            sn = rope.sin_tab[(size_t)pos * pairs + pr];
+            cs = rope.cos_tab[(size_t)pos * pairs + pr];
+        }
+        if (qthr) {
+            qs[2 * tid] = qv.x * cs - qv.y * sn;
+            qs[2 * tid + 1] = qv.x * sn + qv.y * cs;
         }
         if (has_cur && tid < pairs) {
-            const float sn = srow[tid];
-            const float cs = crow[tid];
             const float* e = rope.k + (size_t)g * kFusedHD + 2 * tid;
             const float v0 = e[0], v1 = e[1];
             const uint16_t r0 = f32_to_f16_bits(v0 * cs - v1 * sn);
@@ -255,32 +309,39 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
     }
     wait_vmem_le<0>();  // this wave's K copies have landed
     __syncthreads();
-    if (h >= kvmul || t >= span) return;
-    if (has_cur && t == tcur) {
+    // wave h = query head h of the group; lanes l and l + 32 share position
+    // l and run the chains j = 0..3 and 4..7 (elements 8c + j, c in order)
+    const int h = wv, half = lane >> 5, t = chunk * kScoreChunk + (lane & 31);
+    if (h >= kvmul) return;  // uniform
+    // the new position's row comes from kcur: one stride per lane
+    const bool cur = has_cur && t == tcur;
+    const uint8_t* kb = cur ? (const uint8_t*)kcur + 8 * half : &kst[0][lane & 31][8 * half];
+    const int kstride = cur ? 16 : kScoreChunk * 16;
+    uint2 kr[kFusedHD / 8];
 #pragma unroll
-        for (int c = 0; c < kFusedHD / 8; c++) kr[c] = *(const uint4*)&kcur[8 * c];
-    } else {
+    for (int c = 0; c < kFusedHD / 8; c++) kr[c] = *(const uint2*)(kb + c * kstride);
+    const float* qh = qs + h * kFusedHD + 4 * half;
+    float acc[4];
 #pragma unroll
-        for (int c = 0; c < kFusedHD / 8; c++) kr[c] = *(const uint4*)&kst[c][tid & 63][0];
-    }
-    const float* qh = qs + h * kFusedHD;
-    float acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) acc[j] = 0.0f;
+    for (int j = 0; j < 4; j++) acc[j] = 0.0f;
 #pragma unroll
     for (int c = 0; c < kFusedHD / 8; c++) {
-        const uint32_t kw[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
         const float4 qa = *(const float4*)(qh + 8 * c);
-        const float4 qb = *(const float4*)(qh + 8 * c + 4);
-        const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            acc[j] = fmaf(f16_bits_to_f32((kw[j >> 1] >> (16 * (j & 1))) & 0xffffu), qv[j], acc[j]);
+        acc[0] = fmaf(f16_bits_to_f32(kr[c].x & 0xffffu), qa.x, acc[0]);
+        acc[1] = fmaf(f16_bits_to_f32(kr[c].x >> 16), qa.y, acc[1]);
+        acc[2] = fmaf(f16_bits_to_f32(kr[c].y & 0xffffu), qa.z, acc[2]);
+        acc[3] = fmaf(f16_bits_to_f32(kr[c].y >> 16), qa.w, acc[3]);
     }
-    const float a0 = acc[0] + acc[4], a1 = acc[1] + acc[5];
-    const float a2 = acc[2] + acc[6], a3 = acc[3] + acc[7];
-    scores[((size_t)tok * n_heads + (size_t)g * kvmul + h) * span_max + t] =
-        ((a0 + a1) + (a2 + a3)) * scale;
+    // chains 4..7 from the partner lane: (y0 + y4, ...), then the tree
+    float o[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) o[j] = __shfl_xor(acc[j], 32);
+    if (half == 0 && t < span) {
+        const float a0 = acc[0] + o[0], a1 = acc[1] + o[1];
+        const float a2 = acc[2] + o[2], a3 = acc[3] + o[3];
+        scores[((size_t)tok * n_heads + (size_t)g * kvmul + h) * span_max + t] =
+            ((a0 + a1) + (a2 + a3)) * scale;
+    }
 }
 
 // DS workgroups share one (query head, token): workgroup slice c runs the
@@ -339,7 +400,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
     const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int t = tid; t < span; t += 256) w[t] = fast_exp(w[t] - mx);
+    exp_row<8>(w, tid, 256, span, mx);
     // (the first tile barrier orders the exp writes before their readers)
     // values: threads 0..DW-1 own one element each; the first thread of the
     // next wave (a wave that otherwise only stages V) sums the denominator
@@ -464,7 +525,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     if (lane == 0) red[wave] = m;
     __syncthreads();
     const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int t = tid; t < span; t += 256) w[t] = fast_exp(w[t] - mx);
+    exp_row<8>(w, tid, 256, span, mx);
     // (the first step's barrier orders the exp writes before their readers)
     const bool chain = tid < DW;
     const bool summer = tid == 64;
@@ -679,15 +740,24 @@ __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
             if (lane == 0) wm[wave * KVMUL + hh] = m;
         }
         __syncthreads();
+        // every exp is computed, interleaved, before the guarded stores (the
+        // compiler would otherwise sink each one into its store's branch and
+        // run them one after another)
+        float xv[KVMUL * SC], ev[KVMUL * SC];
 #pragma unroll
         for (int hh = 0; hh < KVMUL; hh++) {
             const float m = fmaxf(fmaxf(wm[hh], wm[KVMUL + hh]), fmaxf(wm[2 * KVMUL + hh], wm[3 * KVMUL + hh]));
 #pragma unroll
+            for (int k = 0; k < SC; k++) xv[hh * SC + k] = sv[hh][k] - m;
+        }
+        fast_exp_n(xv, ev);
+#pragma unroll
+        for (int hh = 0; hh < KVMUL; hh++)
+#pragma unroll
             for (int k = 0; k < SC; k++) {
                 const int t = tid + k * kVDecThreads;
-                if (t < span) w[(size_t)hh * pad + t] = fast_exp(sv[hh][k] - m);
+                if (t < span) w[(size_t)hh * pad + t] = ev[hh * SC + k];
             }
-        }
         __syncthreads();
     } else {
         sstore(0, span);
@@ -701,7 +771,7 @@ __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
             float m = -__int_as_float(0x7f800000);
             for (int t = lane; t < span; t += 64) m = fmaxf(m, wr[t]);
             m = wave_max(m);
-            for (int t = lane; t < span; t += 64) wr[t] = fast_exp(wr[t] - m);
+            exp_row<8>(wr, lane, 64, span, m);
         }
         __syncthreads();
     }
