@@ -617,7 +617,7 @@ static size_t smax_lds_bytes(int span_max) {
 
 // Softmax + values for one decode token, head_dim 128, KVMUL query heads per
 // kv head (the arithmetic of attn_softmax_values_kernel, so the same bits).
-// Workgroup = (kv head g, slice c of DW = 64 / KVMUL elements), 256 threads:
+// Workgroup = (kv head g, slice c of DW = 64 / KVMUL elements), kVDecThreads threads:
 //   * every thread stages part of the slice's V rows into LDS transposed,
 //     vt[e][t] (element-major, two positions per 32-bit store), and part of
 //     the KVMUL score rows into w[hh][t];
@@ -630,9 +630,9 @@ static size_t smax_lds_bytes(int span_max) {
 // One workgroup holds the whole span: vt and w take (2 * DW + 4 * KVMUL)
 // bytes per position (vdec_lds_bytes).  The kv head's V rows are read by
 // 2 * KVMUL workgroups, each its own slice, once.
-constexpr int kVDecThreads = 256;
+constexpr int kVDecThreads = 512;  // two waves per SIMD: the exps of one fill the other's stalls
 constexpr int kVDecCh = 3;  // V items (two 16-byte loads each) per thread per chunk
-constexpr int kVDecSc = 3;  // score positions per thread and head per chunk
+constexpr int kVDecSc = 2;  // score positions per thread and head per chunk
 __host__ __device__ constexpr int vdec_pad(int span_max) {
     // rows of vt / w: at least span_max + 64 positions (the value chains read
     // up to 56 past the span), 8 mod 128 so the 16 lanes' ds_read_b128 of
@@ -641,8 +641,8 @@ __host__ __device__ constexpr int vdec_pad(int span_max) {
 }
 static size_t vdec_lds_bytes(int kvmul, int span_max) {
     const size_t pad = (size_t)vdec_pad(span_max);
-    // then 1 / denom per head and the waves' maxima per head (5 kvmul floats)
-    return pad * (size_t)(2 * (64 / kvmul) + 4 * kvmul) + 128;
+    // then 1 / denom per head and the waves' maxima per head ((1 + 8) kvmul floats)
+    return pad * (size_t)(2 * (64 / kvmul) + 4 * kvmul) + 160;
 }
 template <int KVMUL>
 __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
@@ -652,13 +652,14 @@ __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
     constexpr int DW = 64 / KVMUL;    // elements per workgroup
     constexpr int NP = DW / 8;        // 16-byte pieces per V row slice
     constexpr int NS = kFusedHD / DW;  // slices per kv head
+    constexpr int NW = kVDecThreads / 64;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int g = blockIdx.x / NS, c = blockIdx.x % NS;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pad = vdec_pad(span_max);
     uint16_t* vt = (uint16_t*)lds;                  // [DW][pad] f16
     float* w = lds + (size_t)DW * pad / 2;          // [KVMUL][pad]
-    float* red = w + (size_t)KVMUL * pad;           // [KVMUL] 1 / denom, then [4][KVMUL] maxima
+    float* red = w + (size_t)KVMUL * pad;           // [KVMUL] 1 / denom, then [NW][KVMUL] maxima
     // V slice, two positions per item: rows 2tp and 2tp + 1 of piece pc.
     // Loads go out in unrolled chunks of kVDecCh items per thread, every
     // address clamped to a cache row, so a chunk's loads are all in flight
@@ -729,7 +730,7 @@ __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
     if (span <= SC * kVDecThreads) {  // uniform: the whole score rows are in registers
         // each head's maximum (order-free: DPP within the waves, LDS across
         // them), then fastExpF32(s - max) on the registers, stored as w
-        float* wm = red + KVMUL;  // [4 waves][KVMUL]
+        float* wm = red + KVMUL;  // [NW waves][KVMUL]
 #pragma unroll
         for (int hh = 0; hh < KVMUL; hh++) {
             float m = -__int_as_float(0x7f800000);
@@ -740,24 +741,31 @@ __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
             if (lane == 0) wm[wave * KVMUL + hh] = m;
         }
         __syncthreads();
-        // every exp is computed, interleaved, before the guarded stores (the
-        // compiler would otherwise sink each one into its store's branch and
-        // run them one after another)
-        float xv[KVMUL * SC], ev[KVMUL * SC];
+        // the exps of each position set k that holds a position of the span
+        // for this wave, computed (interleaved over the heads) before the
+        // guarded stores: the compiler would otherwise sink each one into its
+        // store's branch and run them one after another
+        float mx[KVMUL];
 #pragma unroll
         for (int hh = 0; hh < KVMUL; hh++) {
-            const float m = fmaxf(fmaxf(wm[hh], wm[KVMUL + hh]), fmaxf(wm[2 * KVMUL + hh], wm[3 * KVMUL + hh]));
+            float m = wm[hh];
 #pragma unroll
-            for (int k = 0; k < SC; k++) xv[hh * SC + k] = sv[hh][k] - m;
+            for (int v = 1; v < NW; v++) m = fmaxf(m, wm[v * KVMUL + hh]);
+            mx[hh] = m;
         }
-        fast_exp_n(xv, ev);
 #pragma unroll
-        for (int hh = 0; hh < KVMUL; hh++)
+        for (int k = 0; k < SC; k++) {
+            if (64 * wave + k * kVDecThreads >= span) break;  // uniform
+            float xv[KVMUL], ev[KVMUL];
 #pragma unroll
-            for (int k = 0; k < SC; k++) {
-                const int t = tid + k * kVDecThreads;
-                if (t < span) w[(size_t)hh * pad + t] = ev[hh * SC + k];
+            for (int hh = 0; hh < KVMUL; hh++) xv[hh] = sv[hh][k] - mx[hh];
+            fast_exp_n(xv, ev);
+            const int t = tid + k * kVDecThreads;
+            if (t < span) {
+#pragma unroll
+                for (int hh = 0; hh < KVMUL; hh++) w[(size_t)hh * pad + t] = ev[hh];
             }
+        }
         __syncthreads();
     } else {
         sstore(0, span);
