@@ -38,6 +38,7 @@ HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
 ROWS, COLS = 14336, 4096
 PMC_FILE = os.path.join(ROOT, "profiles", "gemv_q4k_14336x4096_pmc.json")
+CEILING_FILE = os.path.join(ROOT, "profiles", "read_ceiling_14336x4096.json")
 
 
 def alg_bytes(rows, cols, p=1):
@@ -168,6 +169,9 @@ def run(args):
     nbytes = alg_bytes(rows, cols)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     achieved = nbytes / (kernel_us * 1e-6) / 1e9
+    ceiling_us = None
+    if os.path.exists(CEILING_FILE):
+        ceiling_us = json.load(open(CEILING_FILE))["best"]["us"]
     traffic, trace_us = None, None
     if os.path.exists(PMC_FILE):
         pmc = json.load(open(PMC_FILE))
@@ -211,6 +215,10 @@ def run(args):
             # shape (profiles/gemv_q4k_14336x4096.md), beside the live step figure
             "trace_kernel_us": round(trace_us, 3) if trace_us else None,
             "trace_frac": round(nbytes / (trace_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if trace_us else None,
+            # the fastest launch that only reads the weight bytes, timed the
+            # same way (bench.py --read-ceiling, profiles/read_ceiling_14336x4096.md)
+            "read_ceiling_us": ceiling_us,
+            "frac_of_read_ceiling": round(ceiling_us / kernel_us, 4) if ceiling_us else None,
         },
     }
     if not args.no_cpu_baseline:
@@ -622,6 +630,72 @@ def launch_floor(args):
               flush=True)
 
 
+def read_ceiling(args):
+    """Ceiling of one streaming launch: the headline GEMV's 33,103,872 bytes
+    read once with 16-byte loads and nothing else (libgllm_probe.so, built
+    beside the product library).  Ten rotating copies (331 MB, past the
+    256 MB memory-side cache) make every launch read HBM; each point is
+    20 launches replayed from one HIP graph and timed with HIP events, as the
+    headline line times the GEMV, over grid sizes, workgroup sizes, loads in
+    flight per thread and two access patterns (grid-stride / one contiguous
+    chunk per workgroup).  Prints one line per point and a summary line with
+    the fastest."""
+    import ctypes as C
+
+    import torch
+
+    import gopherllm_amd as g
+    from gopherllm_amd import build as hipbuild
+
+    if not os.path.exists(hipbuild.PROBE_LIB):
+        raise SystemExit(f"{hipbuild.PROBE_LIB} is missing: run __graft_entry__.build() first")
+    lib = C.CDLL(hipbuild.PROBE_LIB)
+    fn = lib.gllm_probe_stream_read
+    fn.restype = C.c_int
+    fn.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    rows, cols = 14336, 4096
+    nbytes = rows * g.row_bytes(g.TYPE_Q4_K, cols)  # the GEMV's weight bytes
+    gemv_bytes = nbytes + 4 * cols + 4 * rows
+    copies = 10
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+    for i, b in enumerate(bufs):
+        b.view(torch.int32).random_(generator=torch.Generator(device="cuda").manual_seed(i))
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    reps = 20
+    best = None
+    for pattern in (0, 1):
+        for threads in (256, 512, 1024):
+            for wgs in (256, 512, 1024, 2048):
+                for depth in (2, 4, 8, 16):
+                    def body():
+                        s = torch.cuda.current_stream().cuda_stream
+                        for r in range(reps):
+                            rc = fn(bufs[r % copies].data_ptr(), nbytes, wgs, threads, depth, pattern,
+                                    sink.data_ptr(), s)
+                            if rc:
+                                raise RuntimeError(f"probe launch failed ({rc})")
+                    graph = timed_graph(torch, body)
+                    for _ in range(3):
+                        graph.replay()
+                    torch.cuda.synchronize()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for _ in range(5):
+                        graph.replay()
+                    e1.record()
+                    torch.cuda.synchronize()
+                    us = e0.elapsed_time(e1) / (5 * reps) * 1e3
+                    rec = {"read_ceiling": "point", "pattern": "grid-stride" if pattern == 0 else "chunk",
+                           "threads": threads, "workgroups": wgs, "loads_in_flight": depth,
+                           "us": round(us, 3), "GB_s": round(nbytes / us / 1e3, 1)}
+                    print(json.dumps(rec), flush=True)
+                    if best is None or us < best["us"]:
+                        best = rec
+    print(json.dumps({"read_ceiling": "best", "bytes": nbytes, **{k: v for k, v in best.items() if k != "read_ceiling"},
+                      "frac_of_8TBs": round(nbytes / best["us"] / 8e6, 4),
+                      "gemv_at_ceiling_us": round(gemv_bytes / (nbytes / best["us"]), 3)}), flush=True)
+
+
 def kernel_bench(args):
     """llm-kernel-bench.v1 (kernel_bench.go:26-203) for layer 0 of the
     synthetic Llama-3-8B-shape model of configs[4] (Q4_K layers and
@@ -914,6 +988,8 @@ def main():
     ap.add_argument("--ctx", type=int, default=0, help="suite attention: only this context")
     ap.add_argument("--profile-run", action="store_true",
                     help="eager launches for rocprofv3 counter collection")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="fastest single launch that only reads the headline GEMV's bytes (probe sweep)")
     ap.add_argument("--launch-floor", action="store_true",
                     help="per-node cost of short launches replayed from one HIP graph")
     ap.add_argument("--summarize-pmc", nargs="+", default=None,
@@ -937,6 +1013,9 @@ def main():
     args = ap.parse_args()
     if args.profile_run:
         profile_run()
+        return
+    if args.read_ceiling:
+        read_ceiling(args)
         return
     if args.launch_floor:
         launch_floor(args)

@@ -26,6 +26,9 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libgllm_hip.so")
+# measurement probes (bench.py --read-ceiling), a library of their own so the
+# product library's exports stay exactly include/gllm_hip.h
+PROBE_LIB = os.path.join(HERE, "libgllm_probe.so")
 ARCH = os.environ.get("GLLM_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
@@ -91,6 +94,17 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc link failed with exit code {res.returncode}")
     os.replace(tmp, LIB)
+    probe_srcs = sorted(glob.glob(os.path.join(CSRC, "probe", "*.hip")))
+    if probe_srcs:
+        tmp = PROBE_LIB + ".tmp"
+        cmd = [cc] + FLAGS + probe_srcs + ["-o", tmp]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            sys.stderr.write(res.stdout + res.stderr)
+            raise RuntimeError(f"hipcc failed for the probe library ({res.returncode})")
+        os.replace(tmp, PROBE_LIB)
     return LIB
 
 
