@@ -407,9 +407,11 @@ __device__ __forceinline__ void fused_act_store(const XRegs<kFuseQB>& xr, int B,
 // of the wave owning block b has x[256b + 32m + kk + 8e] in v[e]): x' is
 // staged in LDS (xs: cols floats, then 48 floats of scratch), threads 0..31
 // run the dotF32AVX2 accumulator chains (kernels_amd64.s:28-93: chain
-// 8r + k over elements 32c + 8r + k, c in order), 0..7 join them as
-// (y0 + y1) + (y2 + y3), thread 0 runs the 8 -> 1 tree and
-// float32(1 / sqrt(float64(ss / n + eps))); then v = (x' * w) * scale.
+// 8r + k over elements 32c + 8r + k, c in order), lanes 0..7 of wave 0
+// join them as (y0 + y1) + (y2 + y3) and lane 0 runs the 8 -> 1 tree and
+// float32(1 / sqrt(float64(ss / n + eps))), through cross-lane reads (one
+// workgroup barrier for the scale instead of three); then
+// v = (x' * w) * scale.
 // Barriers are LDS-only, so the caller's weight prefetch stays in flight.
 // xout (workgroup 0 only) receives x'.
 template <int QB, bool RES>
@@ -468,18 +470,14 @@ __device__ __forceinline__ void norm_regs(XRegs<QB>& xr, const XRegs<QB>& wr,
                 for (int u = 0; u < 16; u++) y = fmaf(xa[u], xa[u], y);
             }
         }
-        part[tid] = y;
-    }
-    wait_lgkm0();
-    lds_barrier();
-    if (tid < 8) part[32 + tid] = (part[tid] + part[8 + tid]) + (part[16 + tid] + part[24 + tid]);
-    wait_lgkm0();
-    lds_barrier();
-    if (tid == 0) {
-        const float a0 = part[32] + part[36], a1 = part[33] + part[37];
-        const float a2 = part[34] + part[38], a3 = part[35] + part[39];
-        const float ss = (a0 + a1) + (a2 + a3);
-        part[40] = (float)(1.0 / sqrt((double)(ss / (float)n + eps)));
+        // the joins inside wave 0 (lanes 0..31 hold the chains), the same
+        // additions in the same order: z_k = (y_k + y_8+k) + (y_16+k + y_24+k),
+        // a_i = z_i + z_i+4, ss = (a_0 + a_1) + (a_2 + a_3)
+        const float z = (y + __shfl_down(y, 8)) + (__shfl_down(y, 16) + __shfl_down(y, 24));
+        const float a = z + __shfl_down(z, 4);
+        const float hsum = a + __shfl_down(a, 1);
+        const float ss = hsum + __shfl_down(hsum, 2);
+        if (tid == 0) part[40] = (float)(1.0 / sqrt((double)(ss / (float)n + eps)));
     }
     wait_lgkm0();
     lds_barrier();
