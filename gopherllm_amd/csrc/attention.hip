@@ -475,19 +475,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 // streams in steps of two 64-position tiles: thread (position, 8-element
 // piece) holds 16 bytes of each tile, kLongP steps in flight, and writes
 // them element-major into the step's pair of LDS tiles (vt[e][t], rows
-// padded to 72 halves; two pairs alternate, one barrier per step).  Lanes
-// 0-31 of wave 0 run the 32 value chains reading eight positions of their
-// element per ds_read_b128 and the weights as broadcast quads (a tile's
-// operands read before its chain runs); lane 0 of wave 1 sums the
-// denominator in position order meanwhile.
-constexpr int kLongP = 8;        // steps (two tiles each) in flight per thread
+// padded to 72 halves; two pairs alternate, one barrier per step).  Waves
+// 1, 2, 3 and 5 do the staging; lanes 0-31 of wave 0 only run the 32 value
+// chains, reading eight positions of their element per ds_read_b128 and the
+// weights as broadcast quads, three groups of eight positions ahead of the
+// chain; lane 0 of wave 1 sums the denominator in position order meanwhile.
+// Wave 4, placed on wave 0's SIMD,
+// stays idle between the barriers: work there slows the chain (a staging
+// wave on that SIMD took ctx 32768 from 221 to 245 us).
+constexpr int kLongThreads = 384;  // wave 0: the value chains; waves 1-3, 5: staging
+constexpr int kLongP = 8;        // steps (two tiles each) in flight per staging thread
 constexpr int kLongRow = 72;     // halves per element row of a staged tile (64 + 8 padding)
 constexpr int kLongSpan = 32768;
 static size_t long_lds_bytes(int span_max) {
     return ((size_t)((span_max + 3) & ~3) + 8) * 4 + 4 * (size_t)32 * kLongRow * 2;
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_values_long_kernel(
+__global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_values_long_kernel(
     const float* __restrict__ scores, const uint16_t* __restrict__ V, int kv_dim, int kvmul,
     int start, int span0, int span_max, float* __restrict__ out, const int* __restrict__ d_end) {
     constexpr int DW = 32, T = kVTile, P = kLongP;
@@ -497,12 +501,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int g = h / kvmul;
     const int wlen = (span_max + 3) & ~3;
     float* w = lds;                          // [wlen]
-    float* red = w + wlen;                   // [8]
+    float* red = w + wlen;                   // [8]: the six waves' maxima, then 1 / denom
     uint16_t* vt = (uint16_t*)(red + 8);     // [4 tiles][DW][kLongRow]
-    // thread (position lp of a tile, piece lc): 16 bytes of both tiles of a
-    // step, P steps ahead, rows clamped to span_max - 1 (inside the cache)
+    // staging thread (position lp of a tile, piece lc), waves 1, 2, 3, 5:
+    // 16 bytes of both tiles of a step, P steps ahead, rows clamped to
+    // span_max - 1 (inside the cache); waves 0 and 4 issue wave 1's loads
+    // and never use them, so every thread's loads are unconditional
     const uint16_t* Vg = V + (size_t)start * kv_dim + (size_t)g * kFusedHD + slice * DW;
-    const int lp = tid >> 2, lc = tid & 3;
+    const int sid = wave == 0 ? tid : wave == 4 ? tid - 256 : wave < 4 ? tid - 64 : tid - 128;
+    const int lp = sid >> 2, lc = sid & 3;
+    const bool stager = wave != 0 && wave != 4;
     uint4 pre[P][2];
     auto fetch = [&](int st, uint4 (&r)[2]) __attribute__((always_inline)) {
 #pragma unroll
@@ -516,7 +524,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int nsteps = (span + 2 * T - 1) / (2 * T);
     const float* srow = scores + (size_t)h * span_max;
     float m = -__int_as_float(0x7f800000);
-    for (int t = tid; t < span; t += 256) {
+    for (int t = tid; t < span; t += kLongThreads) {
         const float v = srow[t];
         w[t] = v;
         m = fmaxf(m, v);
@@ -524,41 +532,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     m = wave_max(m);
     if (lane == 0) red[wave] = m;
     __syncthreads();
-    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    exp_row<8>(w, tid, 256, span, mx);
+    const float mx = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), fmaxf(red[4], red[5]));
+    exp_row<8>(w, tid, kLongThreads, span, mx);
     // (the first step's barrier orders the exp writes before their readers)
     const bool chain = tid < DW;
     const bool summer = tid == 64;
     float acc = 0.0f, denom = 0.0f;
-    // the chains over one step's two tiles (positions base .. base + 127):
-    // both tiles' operands are read first (one LDS round trip), then the
-    // chain (or the denominator) runs over them in position order
+    // the chains over one step's two tiles (positions base .. base + 127),
+    // groups of eight positions read three groups ahead of the chain (a
+    // group's reads take about a third of its chain's time), then the chain
+    // (or the denominator) in position order
     auto run_step = [&](const uint16_t* pair, int base) __attribute__((always_inline)) {
         const int n = max(0, min(2 * T, span - base));
         if (chain) {
             const uint16_t* vrow = pair + tid * kLongRow;
             if (n == 2 * T) {
-                uint4 vv[2 * T / 8];
-                float4 wa[2 * T / 8], wb[2 * T / 8];
+                constexpr int NG = 2 * T / 8;  // groups of eight positions
+                struct Grp {
+                    uint4 v;
+                    float4 a, b;
+                };
+                auto ld = [&](Grp& r, int u) __attribute__((always_inline)) {
+                    r.v = *(const uint4*)(vrow + (u >> 3) * DW * kLongRow + 8 * (u & 7));
+                    r.a = *(const float4*)&w[base + 8 * u];
+                    r.b = *(const float4*)&w[base + 8 * u + 4];
+                };
+                auto run = [&](const Grp& r) __attribute__((always_inline)) {
+                    acc = fmaf(r.a.x, f16_bits_to_f32(r.v.x & 0xffffu), acc);
+                    acc = fmaf(r.a.y, f16_bits_to_f32(r.v.x >> 16), acc);
+                    acc = fmaf(r.a.z, f16_bits_to_f32(r.v.y & 0xffffu), acc);
+                    acc = fmaf(r.a.w, f16_bits_to_f32(r.v.y >> 16), acc);
+                    acc = fmaf(r.b.x, f16_bits_to_f32(r.v.z & 0xffffu), acc);
+                    acc = fmaf(r.b.y, f16_bits_to_f32(r.v.z >> 16), acc);
+                    acc = fmaf(r.b.z, f16_bits_to_f32(r.v.w & 0xffffu), acc);
+                    acc = fmaf(r.b.w, f16_bits_to_f32(r.v.w >> 16), acc);
+                };
+                Grp ring[4];
+                ld(ring[0], 0);
+                ld(ring[1], 1);
+                ld(ring[2], 2);
 #pragma unroll
-                for (int u = 0; u < 2 * T / 8; u++) {
-                    vv[u] = *(const uint4*)(vrow + (u >> 3) * DW * kLongRow + 8 * (u & 7));
-                    wa[u] = *(const float4*)&w[base + 8 * u];
-                    wb[u] = *(const float4*)&w[base + 8 * u + 4];
-                }
-#pragma unroll
-                for (int u = 0; u < 2 * T / 8; u++) {
-                    const uint4 v = vv[u];
-                    const float4 a = wa[u];
-                    const float4 b = wb[u];
-                    acc = fmaf(a.x, f16_bits_to_f32(v.x & 0xffffu), acc);
-                    acc = fmaf(a.y, f16_bits_to_f32(v.x >> 16), acc);
-                    acc = fmaf(a.z, f16_bits_to_f32(v.y & 0xffffu), acc);
-                    acc = fmaf(a.w, f16_bits_to_f32(v.y >> 16), acc);
-                    acc = fmaf(b.x, f16_bits_to_f32(v.z & 0xffffu), acc);
-                    acc = fmaf(b.y, f16_bits_to_f32(v.z >> 16), acc);
-                    acc = fmaf(b.z, f16_bits_to_f32(v.w & 0xffffu), acc);
-                    acc = fmaf(b.w, f16_bits_to_f32(v.w >> 16), acc);
+                for (int u = 0; u < NG; u++) {
+                    if (u + 3 < NG) ld(ring[(u + 3) & 3], u + 3);
+                    __builtin_amdgcn_sched_barrier(0);
+                    run(ring[u & 3]);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
                 for (int p = 0; p < n; p++)
@@ -585,13 +603,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // steps ahead, barrier, then run the two tiles' chains
     auto step = [&](int st, uint4 (&r)[2]) __attribute__((always_inline)) {
         uint16_t* pair = vt + (size_t)(st & 1) * 2 * DW * kLongRow;
+        if (stager) {  // uniform
 #pragma unroll
-        for (int hf = 0; hf < 2; hf++) {
-            const uint32_t pv[4] = {r[hf].x, r[hf].y, r[hf].z, r[hf].w};
-            uint16_t* buf = pair + hf * DW * kLongRow;
+            for (int hf = 0; hf < 2; hf++) {
+                const uint32_t pv[4] = {r[hf].x, r[hf].y, r[hf].z, r[hf].w};
+                uint16_t* buf = pair + hf * DW * kLongRow;
 #pragma unroll
-            for (int j = 0; j < 8; j++)
-                buf[(8 * lc + j) * kLongRow + lp] = (uint16_t)(pv[j >> 1] >> (16 * (j & 1)));
+                for (int j = 0; j < 8; j++)
+                    buf[(8 * lc + j) * kLongRow + lp] = (uint16_t)(pv[j >> 1] >> (16 * (j & 1)));
+            }
         }
         fetch(st + P, r);
         wait_lgkm0();
@@ -605,9 +625,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int q = 0; q < P; q++) step(s0 + q, pre[q]);
     }
-    if (summer) red[4] = denom > 0.0f ? 1.0f / denom : 1.0f;
+    if (summer) red[6] = denom > 0.0f ? 1.0f / denom : 1.0f;
     __syncthreads();
-    if (chain) out[(size_t)h * kFusedHD + slice * DW + tid] = acc * red[4];
+    if (chain) out[(size_t)h * kFusedHD + slice * DW + tid] = acc * red[6];
 }
 
 template <int DS>
@@ -1326,7 +1346,7 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
                     return fail(GLLM_EDEVICE, "attend: %zu bytes of LDS not available",
                                 long_lds_bytes(span_max));
             }
-            hipLaunchKernelGGL(attn_values_long_kernel, dim3(n_heads * 4), dim3(256),
+            hipLaunchKernelGGL(attn_values_long_kernel, dim3(n_heads * 4), dim3(kLongThreads),
                                long_lds_bytes(span_max), s, sc, kv->v[l], kv->kv_dim_v, kvmul,
                                start, span0, span_max, d_out, d_end);
         } else if (p == 1) {
