@@ -472,80 +472,103 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 // in LDS, up to kLongSpan): the arithmetic of attn_softmax_values_kernel<4>
 // (so the same bits), with V staged transposed.  Workgroup = (query head,
 // 32-element slice).  The score row sits in LDS as the softmax weights; V
-// streams in steps of two 64-position tiles: thread (position, 8-element
-// piece) holds 16 bytes of each tile, kLongP steps in flight, and writes
-// them element-major into the step's pair of LDS tiles (vt[e][t], rows
-// padded to 72 halves; two pairs alternate, one barrier per step).  Waves
-// 1, 2, 3 and 5 do the staging; lanes 0-31 of wave 0 only run the 32 value
-// chains, reading eight positions of their element per ds_read_b128 and the
-// weights as broadcast quads, three groups of eight positions ahead of the
-// chain; lane 0 of wave 1 sums the denominator in position order meanwhile.
-// Wave 4, placed on wave 0's SIMD,
-// stays idle between the barriers: work there slows the chain (a staging
-// wave on that SIMD took ctx 32768 from 221 to 245 us).
-constexpr int kLongThreads = 384;  // wave 0: the value chains; waves 1-3, 5: staging
-constexpr int kLongP = 8;        // steps (two tiles each) in flight per staging thread
+// streams in steps of two 64-position tiles, kLongP steps in flight.  A
+// staging lane (waves 1, 2, 3, 5) loads one element pair of eight positions
+// (eight dwords), splits them into the two elements' eight-position runs
+// (v_perm) and writes each run with one ds_write_b128, element-major
+// (vt[e][t], rows padded to 72 halves; two pairs of tiles alternate, one
+// barrier per step).  Wave 0 only runs the chains, eight positions of its
+// element per ds_read_b128 and the weights as broadcast quads, three groups
+// of eight positions ahead: lanes 0-31 the 32 value chains, lane 32 the
+// denominator, as fma(w, 1.0, denom) over a row of ones that every tile
+// carries (w * 1 is exact, so each step rounds as denom + w does).  Wave 4,
+// placed on wave 0's SIMD, stays idle between the barriers: work there slows
+// the chain.
+constexpr int kLongThreads = 384;  // wave 0: the chains; waves 1-3, 5: staging
+constexpr int kLongP = 8;        // steps (two tiles each) in flight per staging lane
 constexpr int kLongRow = 72;     // halves per element row of a staged tile (64 + 8 padding)
+constexpr int kLongRows = 33;    // rows per staged tile: 32 elements and the row of ones
 constexpr int kLongSpan = 32768;
 static size_t long_lds_bytes(int span_max) {
-    return ((size_t)((span_max + 3) & ~3) + 8) * 4 + 4 * (size_t)32 * kLongRow * 2;
+    return ((size_t)((span_max + 3) & ~3) + 8) * 4 + 4 * (size_t)kLongRows * kLongRow * 2;
 }
 
 __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_values_long_kernel(
     const float* __restrict__ scores, const uint16_t* __restrict__ V, int kv_dim, int kvmul,
     int start, int span0, int span_max, float* __restrict__ out, const int* __restrict__ d_end) {
-    constexpr int DW = 32, T = kVTile, P = kLongP;
+    constexpr int DW = 32, T = kVTile, P = kLongP, TR = kLongRows * kLongRow;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int h = blockIdx.x >> 2, slice = blockIdx.x & 3;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = h / kvmul;
     const int wlen = (span_max + 3) & ~3;
     float* w = lds;                          // [wlen]
-    float* red = w + wlen;                   // [8]: the six waves' maxima, then 1 / denom
-    uint16_t* vt = (uint16_t*)(red + 8);     // [4 tiles][DW][kLongRow]
-    // staging thread (position lp of a tile, piece lc), waves 1, 2, 3, 5:
-    // 16 bytes of both tiles of a step, P steps ahead, rows clamped to
-    // span_max - 1 (inside the cache); waves 0 and 4 issue wave 1's loads
-    // and never use them, so every thread's loads are unconditional
-    const uint16_t* Vg = V + (size_t)start * kv_dim + (size_t)g * kFusedHD + slice * DW;
-    const int sid = wave == 0 ? tid : wave == 4 ? tid - 256 : wave < 4 ? tid - 64 : tid - 128;
-    const int lp = sid >> 2, lc = sid & 3;
+    float* red = w + wlen;                   // [8]: the six waves' maxima
+    uint16_t* vt = (uint16_t*)(red + 8);     // [4 tiles][kLongRows][kLongRow]
+    // staging lane: stager si covers positions 32 si .. 32 si + 31 of a step,
+    // lane (position group pg, element pair c) eight of them, rows clamped to
+    // span_max - 1 (inside the cache)
     const bool stager = wave != 0 && wave != 4;
-    uint4 pre[P][2];
-    auto fetch = [&](int st, uint4 (&r)[2]) __attribute__((always_inline)) {
+    const int si = wave < 4 ? wave - 1 : 3;
+    const int c = lane & 15, pg = lane >> 4;
+    const uint16_t* Vg = V + (size_t)start * kv_dim + (size_t)g * kFusedHD + slice * DW + 2 * c;
+    const int sp0 = 32 * si + 8 * pg;  // first position of the lane's run within a step
+    uint32_t pre[P][8];
+    auto fetch = [&](int st, uint32_t (&r)[8]) __attribute__((always_inline)) {
+        const int p0 = 2 * st * T + sp0;
 #pragma unroll
-        for (int hf = 0; hf < 2; hf++)
-            r[hf] = *(const uint4*)(Vg + (size_t)min((2 * st + hf) * T + lp, span_max - 1) * kv_dim + 8 * lc);
+        for (int j = 0; j < 8; j++)
+            r[j] = *(const uint32_t*)(Vg + (size_t)min(p0 + j, span_max - 1) * kv_dim);
     };
+    if (stager) {
 #pragma unroll
-    for (int q = 0; q < P; q++) fetch(q, pre[q]);
+        for (int q = 0; q < P; q++) fetch(q, pre[q]);
+    }
     if (d_end) span0 = *d_end - start + 1;
     const int span = min(span0, span_max);
     const int nsteps = (span + 2 * T - 1) / (2 * T);
     const float* srow = scores + (size_t)h * span_max;
+    // the score row into LDS, sixteen loads in flight per thread (positions
+    // clamped to span - 1: the duplicates leave the maximum unchanged)
     float m = -__int_as_float(0x7f800000);
-    for (int t = tid; t < span; t += kLongThreads) {
-        const float v = srow[t];
-        w[t] = v;
-        m = fmaxf(m, v);
+    for (int t0 = tid; t0 < span; t0 += 16 * kLongThreads) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = srow[min(t0 + u * kLongThreads, span - 1)];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            if (t0 + u * kLongThreads < span) w[t0 + u * kLongThreads] = v[u];
+            m = fmaxf(m, v[u]);
+        }
     }
     m = wave_max(m);
     if (lane == 0) red[wave] = m;
+    if (wave == 4) {  // the row of ones in each of the four tiles
+#pragma unroll
+        for (int k = 0; k < 4; k++) vt[k * TR + DW * kLongRow + lane] = (uint16_t)0x3C00;
+    }
     __syncthreads();
     const float mx = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), fmaxf(red[4], red[5]));
     exp_row<8>(w, tid, kLongThreads, span, mx);
     // (the first step's barrier orders the exp writes before their readers)
-    const bool chain = tid < DW;
-    const bool summer = tid == 64;
-    float acc = 0.0f, denom = 0.0f;
-    // the chains over one step's two tiles (positions base .. base + 127),
-    // groups of eight positions read three groups ahead of the chain (a
-    // group's reads take about a third of its chain's time), then the chain
-    // (or the denominator) in position order
-    auto run_step = [&](const uint16_t* pair, int base) __attribute__((always_inline)) {
-        const int n = max(0, min(2 * T, span - base));
-        if (chain) {
-            const uint16_t* vrow = pair + tid * kLongRow;
+    if (wave == 0) {
+        const bool chain = tid <= DW;
+        const uint16_t* vrow0 = vt + tid * kLongRow;
+        float acc = 0.0f;
+        // the chains over one step's two tiles (positions base .. base + 127),
+        // groups of eight positions read three groups ahead of the chain (a
+        // group's reads take about a third of its chain's time), then the
+        // chain in position order; as many barriers as the staging waves
+        // take (nsteps rounded up to whole groups of P), the steps past the
+        // span run nothing
+        const int nbar = (nsteps + P - 1) / P * P;
+        for (int st = 0; st < nbar; st++) {
+            lds_barrier();
+            if (!chain) continue;
+            const uint16_t* vrow = vrow0 + (size_t)(st & 1) * 2 * TR;
+            const int base = 2 * st * T;
+            const int n = min(2 * T, span - base);
             if (n == 2 * T) {
                 constexpr int NG = 2 * T / 8;  // groups of eight positions
                 struct Grp {
@@ -553,7 +576,7 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(1,
                     float4 a, b;
                 };
                 auto ld = [&](Grp& r, int u) __attribute__((always_inline)) {
-                    r.v = *(const uint4*)(vrow + (u >> 3) * DW * kLongRow + 8 * (u & 7));
+                    r.v = *(const uint4*)(vrow + (u >> 3) * TR + 8 * (u & 7));
                     r.a = *(const float4*)&w[base + 8 * u];
                     r.b = *(const float4*)&w[base + 8 * u + 4];
                 };
@@ -580,54 +603,46 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(1,
                 }
             } else {
                 for (int p = 0; p < n; p++)
-                    acc = fmaf(w[base + p], f16_bits_to_f32(vrow[(p / T) * DW * kLongRow + p % T]), acc);
-            }
-        } else if (summer) {
-            if (n == 2 * T) {
-                float4 q[2 * T / 4];
-#pragma unroll
-                for (int u = 0; u < 2 * T / 4; u++) q[u] = *(const float4*)&w[base + 4 * u];
-#pragma unroll
-                for (int u = 0; u < 2 * T / 4; u++) {
-                    denom = denom + q[u].x;
-                    denom = denom + q[u].y;
-                    denom = denom + q[u].z;
-                    denom = denom + q[u].w;
-                }
-            } else {
-                for (int p = 0; p < n; p++) denom = denom + w[base + p];
+                    acc = fmaf(w[base + p], f16_bits_to_f32(vrow[(p / T) * TR + p % T]), acc);
             }
         }
-    };
-    // one step: stage both tiles from registers, refill those registers P
-    // steps ahead, barrier, then run the two tiles' chains
-    auto step = [&](int st, uint4 (&r)[2]) __attribute__((always_inline)) {
-        uint16_t* pair = vt + (size_t)(st & 1) * 2 * DW * kLongRow;
-        if (stager) {  // uniform
+        const float denom = __shfl(acc, DW);
+        const float inv = denom > 0.0f ? 1.0f / denom : 1.0f;
+        if (tid < DW) out[(size_t)h * kFusedHD + slice * DW + tid] = acc * inv;
+    } else if (stager) {
+        // one step: split the eight dwords into the two elements' runs, write
+        // them, refill the registers P steps ahead, barrier; whole groups of
+        // P steps (a branch around a step would make the compiler's vmcnt
+        // waits drain the prefetch): steps past the span stage clamped rows
+        // that no chain reads
+        uint16_t* dst0 = vt + ((sp0 >> 6) * kLongRows + 2 * c) * kLongRow + (sp0 & 63);
+        auto step = [&](int st, uint32_t (&r)[8]) __attribute__((always_inline)) {
+            uint16_t* dst = dst0 + (size_t)(st & 1) * 2 * TR;
+            uint4 lo, hi;
+            lo.x = __builtin_amdgcn_perm(r[1], r[0], 0x05040100u);
+            lo.y = __builtin_amdgcn_perm(r[3], r[2], 0x05040100u);
+            lo.z = __builtin_amdgcn_perm(r[5], r[4], 0x05040100u);
+            lo.w = __builtin_amdgcn_perm(r[7], r[6], 0x05040100u);
+            hi.x = __builtin_amdgcn_perm(r[1], r[0], 0x07060302u);
+            hi.y = __builtin_amdgcn_perm(r[3], r[2], 0x07060302u);
+            hi.z = __builtin_amdgcn_perm(r[5], r[4], 0x07060302u);
+            hi.w = __builtin_amdgcn_perm(r[7], r[6], 0x07060302u);
+            *(uint4*)dst = lo;
+            *(uint4*)(dst + kLongRow) = hi;
+            fetch(st + P, r);
+            wait_lgkm0();
+            lds_barrier();
+        };
+        for (int s0 = 0; s0 < nsteps; s0 += P) {
 #pragma unroll
-            for (int hf = 0; hf < 2; hf++) {
-                const uint32_t pv[4] = {r[hf].x, r[hf].y, r[hf].z, r[hf].w};
-                uint16_t* buf = pair + hf * DW * kLongRow;
-#pragma unroll
-                for (int j = 0; j < 8; j++)
-                    buf[(8 * lc + j) * kLongRow + lp] = (uint16_t)(pv[j >> 1] >> (16 * (j & 1)));
-            }
+            for (int q = 0; q < P; q++) step(s0 + q, pre[q]);
         }
-        fetch(st + P, r);
-        wait_lgkm0();
-        lds_barrier();
-        run_step(pair, 2 * st * T);
-    };
-    // whole groups of P steps, unconditionally (a branch around a step would
-    // make the compiler's vmcnt waits drain the prefetch): steps past the
-    // span stage clamped rows nobody reads and run no chain steps
-    for (int s0 = 0; s0 < nsteps; s0 += P) {
+    } else {
+        for (int s0 = 0; s0 < nsteps; s0 += P) {
 #pragma unroll
-        for (int q = 0; q < P; q++) step(s0 + q, pre[q]);
+            for (int q = 0; q < P; q++) lds_barrier();
+        }
     }
-    if (summer) red[6] = denom > 0.0f ? 1.0f / denom : 1.0f;
-    __syncthreads();
-    if (chain) out[(size_t)h * kFusedHD + slice * DW + tid] = acc * red[6];
 }
 
 template <int DS>
