@@ -650,6 +650,133 @@ static size_t smax_lds_bytes(int span_max) {
     return ((size_t)((span_max + 3) & ~3) + 8) * 4 + 2 * (size_t)kVTile * (kFusedHD / DS) * 2;
 }
 
+// The value chain of one element over a staged span: out = fma(w_t, v_t,
+// out) in position order from 0, eight positions per ds_read_b128 of the
+// element's vt row and two of the weight row, in a ring of four groups read
+// three ahead (reads past the span stay inside the rows: they hold at least
+// span + 56 positions).
+__device__ __forceinline__ float dec_value_chain(const uint16_t* vrow, const float* wrow, int span) {
+    float acc = 0.0f;
+    struct Grp {
+        uint4 v;
+        float4 a, b;
+    };
+    auto ld = [&](Grp& r, int t) __attribute__((always_inline)) {
+        r.v = *(const uint4*)(vrow + t);
+        r.a = *(const float4*)(wrow + t);
+        r.b = *(const float4*)(wrow + t + 4);
+    };
+    auto run = [&](const Grp& r) __attribute__((always_inline)) {
+        acc = fmaf(r.a.x, f16_bits_to_f32(r.v.x & 0xffffu), acc);
+        acc = fmaf(r.a.y, f16_bits_to_f32(r.v.x >> 16), acc);
+        acc = fmaf(r.a.z, f16_bits_to_f32(r.v.y & 0xffffu), acc);
+        acc = fmaf(r.a.w, f16_bits_to_f32(r.v.y >> 16), acc);
+        acc = fmaf(r.b.x, f16_bits_to_f32(r.v.z & 0xffffu), acc);
+        acc = fmaf(r.b.y, f16_bits_to_f32(r.v.z >> 16), acc);
+        acc = fmaf(r.b.z, f16_bits_to_f32(r.v.w & 0xffffu), acc);
+        acc = fmaf(r.b.w, f16_bits_to_f32(r.v.w >> 16), acc);
+    };
+    Grp r0, r1, r2, r3;
+    int t0 = 0;
+    ld(r0, 0);
+    ld(r1, 8);
+    ld(r2, 16);
+    for (; t0 + 32 <= span; t0 += 32) {
+        ld(r3, t0 + 24);
+        __builtin_amdgcn_sched_barrier(0);
+        run(r0);
+        __builtin_amdgcn_sched_barrier(0);
+        ld(r0, t0 + 32);
+        __builtin_amdgcn_sched_barrier(0);
+        run(r1);
+        __builtin_amdgcn_sched_barrier(0);
+        ld(r1, t0 + 40);
+        __builtin_amdgcn_sched_barrier(0);
+        run(r2);
+        __builtin_amdgcn_sched_barrier(0);
+        ld(r2, t0 + 48);
+        __builtin_amdgcn_sched_barrier(0);
+        run(r3);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // r0, r1, r2 hold groups t0, t0 + 8, t0 + 16
+    if (t0 + 8 <= span) {
+        run(r0);
+        t0 += 8;
+        if (t0 + 8 <= span) {
+            run(r1);
+            t0 += 8;
+            if (t0 + 8 <= span) {
+                run(r2);
+                t0 += 8;
+            }
+        }
+    }
+    for (int t = t0; t < span; t++) acc = fmaf(wrow[t], f16_bits_to_f32(vrow[t]), acc);
+    return acc;
+}
+
+// The softmax denominator of one weight row: denom + w_t in position order
+// from 0, with the value chain's ring (two quads per group, three groups
+// ahead), so that it keeps pace with the chains.
+__device__ __forceinline__ float dec_denominator(const float* wrow, int span) {
+    float den = 0.0f;
+    struct Grp {
+        float4 a, b;
+    };
+    auto ld = [&](Grp& r, int t) __attribute__((always_inline)) {
+        r.a = *(const float4*)(wrow + t);
+        r.b = *(const float4*)(wrow + t + 4);
+    };
+    auto run = [&](const Grp& r) __attribute__((always_inline)) {
+        den = den + r.a.x;
+        den = den + r.a.y;
+        den = den + r.a.z;
+        den = den + r.a.w;
+        den = den + r.b.x;
+        den = den + r.b.y;
+        den = den + r.b.z;
+        den = den + r.b.w;
+    };
+    Grp r0, r1, r2, r3;
+    int t0 = 0;
+    ld(r0, 0);
+    ld(r1, 8);
+    ld(r2, 16);
+    for (; t0 + 32 <= span; t0 += 32) {
+        ld(r3, t0 + 24);
+        __builtin_amdgcn_sched_barrier(0);
+        run(r0);
+        __builtin_amdgcn_sched_barrier(0);
+        ld(r0, t0 + 32);
+        __builtin_amdgcn_sched_barrier(0);
+        run(r1);
+        __builtin_amdgcn_sched_barrier(0);
+        ld(r1, t0 + 40);
+        __builtin_amdgcn_sched_barrier(0);
+        run(r2);
+        __builtin_amdgcn_sched_barrier(0);
+        ld(r2, t0 + 48);
+        __builtin_amdgcn_sched_barrier(0);
+        run(r3);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (t0 + 8 <= span) {
+        run(r0);
+        t0 += 8;
+        if (t0 + 8 <= span) {
+            run(r1);
+            t0 += 8;
+            if (t0 + 8 <= span) {
+                run(r2);
+                t0 += 8;
+            }
+        }
+    }
+    for (int t = t0; t < span; t++) den = den + wrow[t];
+    return den;
+}
+
 // Softmax + values for one decode token, head_dim 128, KVMUL query heads per
 // kv head (the arithmetic of attn_softmax_values_kernel, so the same bits).
 // Workgroup = (kv head g, slice c of DW = 64 / KVMUL elements), kVDecThreads threads:
@@ -659,9 +786,9 @@ static size_t smax_lds_bytes(int span_max) {
 //   * wave hh (< KVMUL) takes row hh's max (order-free) and replaces the row
 //     by fastExpF32(s - max);
 //   * wave 0 runs the KVMUL * DW value chains, lane (hh, e):
-//     out = fma(w_t, v_t, out) in position order, eight positions per
-//     ds_read_b128 of vt and two of w; lanes 64 + hh (wave 1) sum row hh's
-//     denominator in position order meanwhile; then out *= 1 / denom.
+//     out = fma(w_t, v_t, out) in position order (dec_value_chain); wave 1's
+//     lanes (hh, e) sum row hh's denominator in position order meanwhile
+//     (dec_denominator); then out *= 1 / denom.
 // One workgroup holds the whole span: vt and w take (2 * DW + 4 * KVMUL)
 // bytes per position (vdec_lds_bytes).  The kv head's V rows are read by
 // 2 * KVMUL workgroups, each its own slice, once.
@@ -689,7 +816,11 @@ __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
     constexpr int NS = kFusedHD / DW;  // slices per kv head
     constexpr int NW = kVDecThreads / 64;
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    const int g = blockIdx.x / NS, c = blockIdx.x % NS;
+    // kv head g = workgroup % n_kv: workgroups go to the eight XCDs in turn,
+    // so with n_kv = 8 all slices of a head share one XCD's L2, which reads
+    // the head's V lines from memory once for all of them
+    const int n_kv = gridDim.x / NS;
+    const int g = blockIdx.x % n_kv, c = blockIdx.x / n_kv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pad = vdec_pad(span_max);
     uint16_t* vt = (uint16_t*)lds;                  // [DW][pad] f16
@@ -821,79 +952,10 @@ __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
     const int hh = lane / DW, e = lane % DW;
     float acc = 0.0f;
     if (wave == 0) {
-        const uint16_t* vrow = vt + (size_t)e * pad;
-        const float* wrow = w + (size_t)hh * pad;
-        // groups of eight positions in a ring of four, three groups ahead
-        // (reads past the span stay inside the row: pad >= span_max + 64)
-        struct Grp {
-            uint4 v;
-            float4 a, b;
-        };
-        auto ld = [&](Grp& r, int t) __attribute__((always_inline)) {
-            r.v = *(const uint4*)(vrow + t);
-            r.a = *(const float4*)(wrow + t);
-            r.b = *(const float4*)(wrow + t + 4);
-        };
-        auto run = [&](const Grp& r) __attribute__((always_inline)) {
-            acc = fmaf(r.a.x, f16_bits_to_f32(r.v.x & 0xffffu), acc);
-            acc = fmaf(r.a.y, f16_bits_to_f32(r.v.x >> 16), acc);
-            acc = fmaf(r.a.z, f16_bits_to_f32(r.v.y & 0xffffu), acc);
-            acc = fmaf(r.a.w, f16_bits_to_f32(r.v.y >> 16), acc);
-            acc = fmaf(r.b.x, f16_bits_to_f32(r.v.z & 0xffffu), acc);
-            acc = fmaf(r.b.y, f16_bits_to_f32(r.v.z >> 16), acc);
-            acc = fmaf(r.b.z, f16_bits_to_f32(r.v.w & 0xffffu), acc);
-            acc = fmaf(r.b.w, f16_bits_to_f32(r.v.w >> 16), acc);
-        };
-        Grp r0, r1, r2, r3;
-        int t0 = 0;
-        ld(r0, 0);
-        ld(r1, 8);
-        ld(r2, 16);
-        for (; t0 + 32 <= span; t0 += 32) {
-            ld(r3, t0 + 24);
-            __builtin_amdgcn_sched_barrier(0);
-            run(r0);
-            __builtin_amdgcn_sched_barrier(0);
-            ld(r0, t0 + 32);
-            __builtin_amdgcn_sched_barrier(0);
-            run(r1);
-            __builtin_amdgcn_sched_barrier(0);
-            ld(r1, t0 + 40);
-            __builtin_amdgcn_sched_barrier(0);
-            run(r2);
-            __builtin_amdgcn_sched_barrier(0);
-            ld(r2, t0 + 48);
-            __builtin_amdgcn_sched_barrier(0);
-            run(r3);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        // r0, r1, r2 hold groups t0, t0 + 8, t0 + 16
-        if (t0 + 8 <= span) {
-            run(r0);
-            t0 += 8;
-            if (t0 + 8 <= span) {
-                run(r1);
-                t0 += 8;
-                if (t0 + 8 <= span) {
-                    run(r2);
-                    t0 += 8;
-                }
-            }
-        }
-        for (int t = t0; t < span; t++) acc = fmaf(wrow[t], f16_bits_to_f32(vrow[t]), acc);
-    } else if (wave == 1 && lane < KVMUL) {
-        const float* wr = w + (size_t)lane * pad;
-        float denom = 0.0f;
-        int t = 0;
-        for (; t + 4 <= span; t += 4) {
-            const float4 q = *(const float4*)(wr + t);
-            denom = denom + q.x;
-            denom = denom + q.y;
-            denom = denom + q.z;
-            denom = denom + q.w;
-        }
-        for (; t < span; t++) denom = denom + wr[t];
-        red[lane] = denom > 0.0f ? 1.0f / denom : 1.0f;
+        acc = dec_value_chain(vt + (size_t)e * pad, w + (size_t)hh * pad, span);
+    } else if (wave == 1) {  // lanes (hh, e): row hh's denominator, every e the same
+        const float den = dec_denominator(w + (size_t)hh * pad, span);
+        if (e == 0) red[hh] = den > 0.0f ? 1.0f / den : 1.0f;
     }
     __syncthreads();
     if (wave == 0) out[(size_t)(g * KVMUL + hh) * kFusedHD + c * DW + e] = acc * red[hh];

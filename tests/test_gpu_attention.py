@@ -107,6 +107,26 @@ def test_decode_attention_configs3(hip, ctx):
     assert np.allclose(out.cpu().numpy(), want, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("ctx,start", [(1, 0), (7, 0), (300, 123), (640, 0), (2049, 0),
+                                       (3272, 0), (3273, 0)])
+def test_decode_attention_whole_span_in_lds(hip, ctx, start):
+    """One decode token whose span fits one workgroup's LDS image (the
+    one-token values kernel up to 3272 positions, the long-span kernel from
+    3273): bit-exact against the oracle for spans that end inside and on the
+    32-position value groups and score chunks, and for a window that starts
+    past position 0."""
+    import torch
+    kv, k16, v16 = fill_cache(hip, 1, ctx, 50 + ctx)
+    q = normal(51 + ctx, N_HEADS * HD)
+    dq = torch.from_numpy(q).cuda()
+    out = torch.empty(N_HEADS * HD, dtype=torch.float32, device="cuda")
+    print(f"attention whole span ctx {ctx} start {start}", flush=True)
+    kv.attend_dev(0, dq, N_HEADS, N_KV, HD, start, ctx - 1, float(SCALE), out, mode=hip.ATTN_EXACT)
+    torch.cuda.synchronize()
+    want = _all_heads_oracle(q, k16, v16, start, ctx - 1)
+    assert np.array_equal(bits(out.cpu().numpy()), bits(want))
+
+
 def test_splitk_short_spans(hip):
     import torch
     kv, k16, v16 = fill_cache(hip, 1, 200, 40)
