@@ -234,8 +234,8 @@ struct AttnRope {
 };
 
 __global__ __launch_bounds__(256) void attn_scores128_kernel(
-    const float* __restrict__ q, const uint16_t* K, int kv_dim, int n_kv, int kvmul,
-    int start, int span0, int span_max, float scale, float* __restrict__ scores,
+    const float* __restrict__ q, const uint16_t* K, const uint16_t* V, int kv_dim, int n_kv,
+    int kvmul, int start, int span0, int span_max, float scale, float* __restrict__ scores,
     const int* __restrict__ d_end, AttnRope rope) {
     constexpr int pairs = kFusedHD / 2;
     __shared__ __align__(16) float qs[4 * kFusedHD];
@@ -259,6 +259,16 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
 #pragma unroll
         for (int u = 0; u < 2; u++)
             lds_copy16(krow + 8 * (4 * wv + 2 * u), lds_addr(&kst[4 * wv + 2 * u][0][0]));
+    }
+    // one dword of each 128-byte line of the chunk's V rows of this kv head
+    // (lane l: row l / 2, line l % 2; the four waves touch the same lines):
+    // workgroup (g, chunk) runs on XCD g % 8, as do the values launch's
+    // workgroups of kv head g, which then find these lines in that XCD's L2
+    uint32_t vtouch;
+    {
+        const int row = min(chunk * kScoreChunk + (lane >> 1), span_max - 1);
+        vtouch = *(const uint32_t*)(V + (size_t)(start + row) * kv_dim + (size_t)g * kFusedHD +
+                                    64 * (lane & 1));
     }
     // (unconditional loads, clamped or from a dummy row: a load under a
     // branch is waited for at the branch's end, behind the copies)
@@ -307,8 +317,9 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
     } else {
         for (int i = tid; i < kvmul * kFusedHD; i += 256) qs[i] = qg[i];
     }
-    wait_vmem_le<0>();  // this wave's K copies have landed
+    wait_vmem_le<0>();  // this wave's K copies (and the V touch) have landed
     __syncthreads();
+    if (span < 0) scores[vtouch & 0xffu] = 0.0f;  // keeps the V touch (span > 0 here)
     // wave h = query head h of the group; lanes l and l + 32 share position
     // l and run the chains j = 0..3 and 4..7 (elements 8c + j, c in order)
     const int h = wv, half = lane >> 5, t = chunk * kScoreChunk + (lane & 31);
@@ -1393,8 +1404,8 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
         if (!sc) return scratch_error();
         const int nchunk = (span_max + kScoreChunk - 1) / kScoreChunk;
         hipLaunchKernelGGL(attn_scores128_kernel, dim3(n_kv, nchunk, p), dim3(256), 0, s, d_q,
-                           kv->k[l], kv->kv_dim_k, n_kv, kvmul, start, span0, span_max, scale, sc,
-                           d_end, rope);
+                           kv->k[l], kv->v[l], kv->kv_dim_k, n_kv, kvmul, start, span0, span_max,
+                           scale, sc, d_end, rope);
         GLLM_HIP(hipGetLastError());
         // one token: four workgroups per head (a quarter of each V row apiece);
         // prefill tokens already give n_heads * p workgroups
