@@ -35,9 +35,7 @@ int gemv_norm_swiglu_f32(gllm_hip_weight* const* gu, gllm_hip_weight* down, cons
                          const float* res, const float* nw, float eps, float* xout, float* gate,
                          float* up, float* out, void* act_buf, int* cnt, hipStream_t s);
 int gemv_norm_f32(int n, gllm_hip_weight* const* ws, const float* x, const float* res,
-                  const float* nw, float eps, float* xout, float* const* outs, hipStream_t s,
-                  const uint16_t* touch_k, const int* touch_pos, int touch_kv_dim,
-                  int touch_heads, int touch_hd);
+                  const float* nw, float eps, float* xout, float* const* outs, hipStream_t s);
 bool row_kernel_type(int t);
 bool rows_type(int t);
 int launch_weight_rows(const gllm_hip_weight* w, const uint32_t* d_ids, int n, float* d_out,
@@ -312,14 +310,11 @@ static int forward(gllm_hip_model* m, int pos0, int p, bool decode, const int* d
     // addInPlace(x, res) + rmsNormInto(x, norm) + the fused projections:
     // inside the projections' launch when their row kernels take the norm
     // prologue, else the add_rmsnorm kernel first
-    // touch_k: the Q/K/V launch of a captured step touches the layer's K rows
-    // 0 .. pos - 1 (by kv head, on the XCD where the scores launch reads them)
     auto norm_project = [&](int n, gllm_hip_weight* const* ws, const float* res,
-                            const float* norm, float* const* outs,
-                            const uint16_t* touch_k = nullptr) -> int {
+                            const float* norm, float* const* outs) -> int {
         if (fuse && norm_fusable(n, ws)) {
             GLLM_TRY(gemv_norm_f32(n, ws, X[xi], res, norm, c.rms_eps, res ? X[xi ^ 1] : nullptr,
-                                   outs, s, touch_k, d_pos, kvd, c.n_kv_heads, hd));
+                                   outs, s));
             if (res) xi ^= 1;
             return GLLM_OK;
         }
@@ -334,8 +329,7 @@ static int forward(gllm_hip_model* m, int pos0, int p, bool decode, const int* d
         {
             gllm_hip_weight* ws[3] = {W[GLLM_T_WQ], W[GLLM_T_WK], W[GLLM_T_WV]};
             float* outs[3] = {m->q, m->k, m->v};
-            GLLM_TRY(norm_project(3, ws, pending, m->d_norms + (size_t)(2 * l) * c.dim, outs,
-                                  gllm_hip_kv_k_dev(m->kv, l)));
+            GLLM_TRY(norm_project(3, ws, pending, m->d_norms + (size_t)(2 * l) * c.dim, outs));
         }
         if (d_pos) {
             // captured decode step: RoPE and the K/V store run inside the

@@ -38,20 +38,6 @@ struct ArgmaxOut {
     float penalty;
 };
 
-// Cache-line touches for the next launch (the decode step's Q/K/V launch
-// touches the layer's K rows that the attention scores launch reads next):
-// workgroup b touches lines of kv head b % heads, rows 0 .. *pos - 1, one
-// dword per 128-byte line (lpr = ceil(hd / 64) lines per head row of hd
-// halves).  k null: none.
-struct LineTouch {
-    const uint16_t* k;
-    const int* pos;
-    int kv_dim;
-    int heads;
-    int hd;
-    int lpr;
-};
-
 struct GemvJob {
     const uint8_t* w[3];
     float* out[3];
@@ -83,8 +69,6 @@ struct GemvJob {
     // greedy argmax epilogue (batch-1 Q6_K, one weight): keys[gridDim.x]
     // and the repeat-penalty window
     ArgmaxOut am;
-    // cache-line touches (RMSNorm-prologue launches of gemv_q4k_bp_kernel)
-    LineTouch pf;
 };
 
 __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
@@ -852,13 +836,6 @@ __global__ __launch_bounds__(NTH) void gemv_q4k_bp_kernel(GemvJob j) {
     // the launch's weights' rows laid end to end (a workgroup may straddle
     // two of them): Q, K and V of 4096 + 1024 + 1024 rows fill 256
     // workgroups of 24 rows where per-weight workgroups would need 257
-    // the touch position first: the oldest load, so waiting for it later
-    // waits for nothing else (a weight row stands in when there is none)
-    int tpos = 0;
-    if constexpr (NORM) {
-        tpos = *(j.pf.pos ? j.pf.pos : (const int*)j.w[0]);
-        __builtin_amdgcn_sched_barrier(0);
-    }
     const int r0 = (int)blockIdx.x * RW;
     const int n1 = j.rows[0], n2 = j.n > 1 ? n1 + j.rows[1] : n1;
     const int nrows = j.n > 2 ? n2 + j.rows[2] : n2;
@@ -908,21 +885,6 @@ __global__ __launch_bounds__(NTH) void gemv_q4k_bp_kernel(GemvJob j) {
             Q[i][p] = *(const uint4*)(rowp[p] + nib0 + (size_t)i * NS * 128);
             __builtin_amdgcn_sched_barrier(0);
         }
-    // the line touches, after every weight load (no wait here depends on
-    // them; unconditional, clamped to the last line, or a weight line when
-    // there are none)
-    uint32_t touch = 0;
-    if constexpr (NORM) {
-        const int pos = j.pf.k ? tpos : 0;
-        const int nh = j.pf.heads > 0 ? j.pf.heads : 1, lpr = j.pf.lpr > 0 ? j.pf.lpr : 1;
-        const int hk = (int)blockIdx.x % nh, nwh = max(1, (int)gridDim.x / nh);
-        const int line = min((int)blockIdx.x / nh + nwh * tid, max(lpr * pos, 1) - 1);
-        const uint16_t* tp = j.pf.k ? j.pf.k + (size_t)(line / lpr) * j.pf.kv_dim +
-                                          (size_t)hk * j.pf.hd + 64 * (line % lpr)
-                                    : (const uint16_t*)rowp[0];
-        touch = *(const uint32_t*)tp;
-        __builtin_amdgcn_sched_barrier(0);
-    }
     const MinSel ms(k);
     Q4KHdr hd[NB][RP];
 #pragma unroll
@@ -972,8 +934,6 @@ __global__ __launch_bounds__(NTH) void gemv_q4k_bp_kernel(GemvJob j) {
             }
         }
     }
-    if constexpr (NORM)
-        if (nrows < 0) j.out[0][touch & 0xffu] = 0.0f;  // keeps the touch (nrows > 0)
 }
 
 // ---------------------------------------------------------------------------
@@ -2198,7 +2158,6 @@ struct NormIn {
     float eps;
     int* sq_cnt;
     ActQ8 sq_act;
-    LineTouch pf;
 };
 
 // The batched Q6_K matrix-core kernel applies (launch_q6k_tiled).
@@ -2229,7 +2188,6 @@ int run_gemv(int n, gllm_hip_weight* const* ws, const ActQ8& act, int p, float* 
         j.eps = ni->eps;
         j.sq_cnt = ni->sq_cnt;
         j.sq_act = ni->sq_act;
-        j.pf = ni->pf;
         if (j.sq_cnt && (n != 2 || !j.res))
             return fail(GLLM_EINVAL, "gemv: the SwiGLU epilogue needs the gate/up pair and a residual");
     }
@@ -2378,13 +2336,9 @@ bool norm_fusable(int n, gllm_hip_weight* const* ws) {
 // projections (model.go:2686-2790); res may be null; xout (optional)
 // receives fma(res, 1, x), the updated residual stream.
 int gemv_norm_f32(int n, gllm_hip_weight* const* ws, const float* x, const float* res,
-                  const float* nw, float eps, float* xout, float* const* outs, hipStream_t s,
-                  const uint16_t* touch_k, const int* touch_pos, int touch_kv_dim,
-                  int touch_heads, int touch_hd) {
+                  const float* nw, float eps, float* xout, float* const* outs, hipStream_t s) {
     if (!norm_fusable(n, ws)) return fail(GLLM_EUNSUP, "gemv: no RMSNorm prologue for this group");
-    const LineTouch pf{touch_pos && touch_hd > 0 ? touch_k : nullptr, touch_pos, touch_kv_dim,
-                       touch_heads > 0 ? touch_heads : 1, touch_hd, (touch_hd + 63) / 64};
-    const NormIn ni{nw, res, xout, eps, nullptr, ActQ8{}, pf};
+    const NormIn ni{nw, res, xout, eps, nullptr, ActQ8{}};
     ActQ8 none{};
     return run_gemv(n, ws, none, 1, outs, nullptr, s, x, &ni);
 }
@@ -2413,7 +2367,7 @@ int gemv_norm_swiglu_f32(gllm_hip_weight* const* gu, gllm_hip_weight* down, cons
     if (!swiglu_epi_ok(gu, down)) return fail(GLLM_EUNSUP, "gemv: no SwiGLU epilogue for this FFN");
     ActQ8 act;
     act_carve(act_buf, down->cols, 1, &act);
-    const NormIn ni{nw, res, xout, eps, cnt, act, LineTouch{}};
+    const NormIn ni{nw, res, xout, eps, cnt, act};
     float* outs[2] = {gate, up};
     ActQ8 none{};
     GLLM_TRY(run_gemv(2, gu, none, 1, outs, nullptr, s, x, &ni));
