@@ -75,13 +75,19 @@ __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w
 __device__ __forceinline__ int ubyte(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xffu); }
 
 // Blocks per lane in flight in the Q6_K / Q8_0 row kernels.  Batch 1 keeps
-// four (its activation operands ride in the same registers); larger batches
-// read the activations per token and keep two, which holds the VGPR count at
-// the occupancy the memory stream needs.
+// four for Q6_K (its activation operands ride in the same registers) and
+// three for Q8_0; larger batches read the activations per token and keep
+// two, which holds the VGPR count at the occupancy the memory stream needs.
+// A batch-1 Q6_K launch of many workgroups or long rows takes three
+// (gemv_q6k_kernel DQ = 3: 157 instead of 201 VGPRs, three waves per SIMD
+// instead of two).  Measured in A/B runs on one box: the 128256 x 4096 head
+// of the decode step 602.6 -> 605.0 tok/s, 4096 x 14336 22.6 -> 21.9 us;
+// 14336 x 4096 (448 workgroups) 14.3 against 14.8 us keeps four.  Q8_0 at
+// three: 4096 x 14336 17.6 -> 17.1 us, 14336 x 4096 unchanged.
 template <int NT>
 constexpr int kQ6Depth = NT == 1 ? 4 : 2;
 template <int NT>
-constexpr int kQ8Depth = NT == 1 ? 4 : 2;
+constexpr int kQ8Depth = NT == 1 ? 3 : 2;
 
 __device__ __forceinline__ int locate(const GemvJob& j, int wg, int* wi) {
     int i = 0;
@@ -1314,10 +1320,10 @@ __device__ inline void argmax_epilogue(const GemvJob& j, int r, float v, bool ow
 // activation into LDS itself (x loads first, weight prefetch second), so the
 // matvec is one launch; lanes past the last row then compute a clamped row
 // and store nothing, since the whole workgroup takes part in the barrier.
-template <int NT, int G, bool FUSE = false>
+template <int NT, int G, bool FUSE = false, int DQ = 0>
 __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJob j) {
     static_assert(!FUSE || NT == 1, "fused quantisation is batch 1 only");
-    constexpr int D = kQ6Depth<NT>;
+    constexpr int D = DQ ? DQ : kQ6Depth<NT>;
     __shared__ __attribute__((aligned(16))) uint8_t fa_raw[FUSE ? sizeof(FusedAct) : 16];
     FusedAct& fa = *(FusedAct*)fa_raw;
     extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
@@ -1969,11 +1975,15 @@ static bool lds_opt_in(const void* kern) {
 }
 
 // The Q6_K, Q8_0 and other-format row kernel for this type, batch tile NT
-// and G; FUSE selects the variant that quantises x itself.
+// and G; FUSE selects the variant that quantises x itself; shallow: the
+// batch-1 Q6_K ring of three blocks (kQ6Depth).
 template <int NT, bool FUSE>
-static void (*row_kernel(int type, int g))(GemvJob) {
+static void (*row_kernel(int type, int g, bool shallow))(GemvJob) {
     switch (type) {
     case GLLM_TYPE_Q6_K:
+        if (NT == 1 && shallow)
+            return pick_g<NT>(g, gemv_q6k_kernel<NT, 1, FUSE, 3>, gemv_q6k_kernel<NT, 2, FUSE, 3>,
+                              gemv_q6k_kernel<NT, 4, FUSE, 3>);
         return pick_g<NT>(g, gemv_q6k_kernel<NT, 1, FUSE>, gemv_q6k_kernel<NT, 2, FUSE>,
                           gemv_q6k_kernel<NT, 4, FUSE>);
     case GLLM_TYPE_Q8_0:
@@ -2121,9 +2131,11 @@ int launch_gemv_nt(GemvJob& j, int type, int grid, const int* rows, hipStream_t 
         wg += (rows[i] + j.rows_per_wg - 1) / j.rows_per_wg;
     }
     j.wg_begin[j.n] = wg;
-    void (*kern)(GemvJob) = row_kernel<NT, false>(type, g);
+    // many workgroups (two or more per CU) or long rows: occupancy over depth
+    const bool shallow = wg >= 2 * device_cus() || j.blocks >= 32;
+    void (*kern)(GemvJob) = row_kernel<NT, false>(type, g, shallow);
     if constexpr (NT == 1) {
-        if (j.xf) kern = row_kernel<1, true>(type, g);
+        if (j.xf) kern = row_kernel<1, true>(type, g, shallow);
     }
     size_t lds = 0;
     j.sa = 0;
