@@ -788,6 +788,24 @@ __device__ __forceinline__ float dec_denominator(const float* wrow, int span) {
     return den;
 }
 
+// wave_max of N values, each DPP step taken for all of them before the next
+// (N independent chains interleave); the same comparisons as wave_max.
+template <int N>
+__device__ __forceinline__ void wave_max_n(float (&a)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; i++) a[i] = fmaxf(a[i], dpp_f<kQuadXor1>(a[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++) a[i] = fmaxf(a[i], dpp_f<kQuadXor2>(a[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++) a[i] = fmaxf(a[i], dpp_f<kRowHalfMirror>(a[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++) a[i] = fmaxf(a[i], dpp_f<kRowMirror>(a[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++)
+        a[i] = fmaxf(fmaxf(readlane_f(a[i], 0), readlane_f(a[i], 16)),
+                     fmaxf(readlane_f(a[i], 32), readlane_f(a[i], 48)));
+}
+
 // Softmax + values for one decode token, head_dim 128, KVMUL query heads per
 // kv head (the arithmetic of attn_softmax_values_kernel, so the same bits).
 // Workgroup = (kv head g, slice c of DW = 64 / KVMUL elements), kVDecThreads threads:
@@ -908,20 +926,28 @@ __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
         // each head's maximum (order-free: DPP within the waves, LDS across
         // them), then fastExpF32(s - max) on the registers, stored as w
         float* wm = red + KVMUL;  // [NW waves][KVMUL]
+        {
+            // the heads' cross-lane maxima step by step together (their DPP
+            // chains interleave)
+            float m[KVMUL];
 #pragma unroll
-        for (int hh = 0; hh < KVMUL; hh++) {
-            float m = -__int_as_float(0x7f800000);
+            for (int hh = 0; hh < KVMUL; hh++) {
+                m[hh] = -__int_as_float(0x7f800000);
 #pragma unroll
-            for (int k = 0; k < SC; k++)
-                if (tid + k * kVDecThreads < span) m = fmaxf(m, sv[hh][k]);
-            m = wave_max(m);
-            if (lane == 0) wm[wave * KVMUL + hh] = m;
+                for (int k = 0; k < SC; k++)
+                    if (tid + k * kVDecThreads < span) m[hh] = fmaxf(m[hh], sv[hh][k]);
+            }
+            wave_max_n(m);
+            if (lane == 0) {
+#pragma unroll
+                for (int hh = 0; hh < KVMUL; hh++) wm[wave * KVMUL + hh] = m[hh];
+            }
         }
         __syncthreads();
-        // the exps of each position set k that holds a position of the span
-        // for this wave, computed (interleaved over the heads) before the
-        // guarded stores: the compiler would otherwise sink each one into its
-        // store's branch and run them one after another
+        // the exps of every position set and head in one interleaved pass,
+        // computed before the guarded stores: the compiler would otherwise
+        // sink each one into its store's branch and run them one after
+        // another (sets past the span compute values nobody stores)
         float mx[KVMUL];
 #pragma unroll
         for (int hh = 0; hh < KVMUL; hh++) {
@@ -930,17 +956,18 @@ __global__ __launch_bounds__(kVDecThreads) void attn_values_dec_kernel(
             for (int v = 1; v < NW; v++) m = fmaxf(m, wm[v * KVMUL + hh]);
             mx[hh] = m;
         }
+        float xv[SC * KVMUL], ev[SC * KVMUL];
+#pragma unroll
+        for (int k = 0; k < SC; k++)
+#pragma unroll
+            for (int hh = 0; hh < KVMUL; hh++) xv[k * KVMUL + hh] = sv[hh][k] - mx[hh];
+        fast_exp_n(xv, ev);
 #pragma unroll
         for (int k = 0; k < SC; k++) {
-            if (64 * wave + k * kVDecThreads >= span) break;  // uniform
-            float xv[KVMUL], ev[KVMUL];
-#pragma unroll
-            for (int hh = 0; hh < KVMUL; hh++) xv[hh] = sv[hh][k] - mx[hh];
-            fast_exp_n(xv, ev);
             const int t = tid + k * kVDecThreads;
             if (t < span) {
 #pragma unroll
-                for (int hh = 0; hh < KVMUL; hh++) w[(size_t)hh * pad + t] = ev[hh];
+                for (int hh = 0; hh < KVMUL; hh++) w[(size_t)hh * pad + t] = ev[k * KVMUL + hh];
             }
         }
         __syncthreads();
