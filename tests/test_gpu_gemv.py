@@ -175,6 +175,21 @@ def test_argmax_matches_oracle(hip, qtype):
     assert zero.argmax_matvec(normal(5, cols)) == 0
 
 
+def test_q6k_fused_many_workgroups_matches_oracle(hip):
+    """Batch-1 Q6_K that quantises x itself over 625 workgroups (20000 rows
+    of 4096 columns: the three-block ring the vocabulary head takes at two
+    or more workgroups per CU): every output and the argmax against the
+    amd64-order oracle."""
+    rows, cols = 20000, 4096
+    data, _ = quant_matrix(ref.Q6_K, rows, cols, 420)
+    w = hip.Weight.from_host(data, ref.Q6_K, rows, cols)
+    x = normal(421, cols)
+    print(f"Q6_K fused {rows}x{cols}", flush=True)
+    got = w.matvec_into(x)
+    assert np.array_equal(bits(got), bits(ref.matvec(ref.Q6_K, data, x, rows, cols)))
+    assert w.argmax_matvec(x) == ref.argmax_matvec(ref.Q6_K, data, x, rows, cols)
+
+
 @pytest.mark.parametrize("qtype", [ref.Q6_K, ref.Q4_K, ref.Q8_0])
 def test_argmax_penalized_matches_oracle(hip, qtype):
     """applyRepeatPenalty + argmaxFiniteToken (sampling.go:136-153, 399-418)
