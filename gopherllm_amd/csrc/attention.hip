@@ -482,7 +482,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 // One decode token over a long span (past what attn_values_dec_kernel keeps
 // in LDS, up to kLongSpan): the arithmetic of attn_softmax_values_kernel<4>
 // (so the same bits), with V staged transposed.  Workgroup = (query head,
-// 32-element slice).  The score row sits in LDS as the softmax weights; V
+// 32-element slice).  The score row sits in LDS; its maximum is taken
+// before the first step, and each step's 128 weights are exponentiated in
+// place by the staging waves (lanes 0-31, one position each) just before
+// the step's barrier, so the chains start once the maximum is known.  V
 // streams in steps of two 64-position tiles, kLongP steps in flight.  A
 // staging lane (waves 1, 2, 3, 5) loads one element pair of eight positions
 // (eight dwords), splits them into the two elements' eight-position runs
@@ -509,10 +512,18 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(1,
     int start, int span0, int span_max, float* __restrict__ out, const int* __restrict__ d_end) {
     constexpr int DW = 32, T = kVTile, P = kLongP, TR = kLongRows * kLongRow;
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    const int h = blockIdx.x >> 2, slice = blockIdx.x & 3;
+    // Workgroup b runs on XCD b % 8.  The (kv head g, pair of quarters, q
+    // head of the group, quarter) items go out in runs of gridDim.x / 8 per
+    // XCD, so the 2 * kvmul workgroups that read one 128-byte V line share
+    // an L2, and kv head g lands on XCD g, where the scores launch touched
+    // its lines.
+    const int nb = gridDim.x, b = blockIdx.x;
+    const int item = nb % 8 == 0 ? (b % 8) * (nb / 8) + b / 8 : b;
+    const int gp = (item >> 1) / kvmul;
+    const int g = gp >> 1, slice = 2 * (gp & 1) + (item & 1);
+    const int h = g * kvmul + (item >> 1) % kvmul;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = h / kvmul;
     const int wlen = (span_max + 3) & ~3;
     float* w = lds;                          // [wlen]
     float* red = w + wlen;                   // [8]: the six waves' maxima
@@ -561,74 +572,96 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(1,
     }
     __syncthreads();
     const float mx = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), fmaxf(red[4], red[5]));
-    exp_row<8>(w, tid, kLongThreads, span, mx);
-    // (the first step's barrier orders the exp writes before their readers)
+    // (a step's barrier orders its exp writes before the chain's reads)
     if (wave == 0) {
-        const bool chain = tid <= DW;
-        const uint16_t* vrow0 = vt + tid * kLongRow;
+        // lanes 0-31 the value chains, lane 32 the denominator; lanes 33-63
+        // repeat lane 32's row so the wave runs one uniform path
+        const uint16_t* vrow0 = vt + min(tid, DW) * kLongRow;
         float acc = 0.0f;
-        // the chains over one step's two tiles (positions base .. base + 127),
-        // groups of eight positions read three groups ahead of the chain (a
-        // group's reads take about a third of its chain's time), then the
-        // chain in position order; as many barriers as the staging waves
-        // take (nsteps rounded up to whole groups of P), the steps past the
-        // span run nothing
+        // The chains in position order, groups of eight positions read three
+        // groups ahead in one ring over every whole step (two tiles,
+        // positions 128 st .. 128 st + 127): three groups before a step's
+        // end the wave waits for its reads, takes the next step's barrier
+        // (the staging waves may then refill this step's pair) and reads
+        // the next step's first groups under this step's last 24 FMAs.  As
+        // many barriers as the staging waves take (nsteps rounded up to
+        // whole groups of P); a partial last step runs position by position.
         const int nbar = (nsteps + P - 1) / P * P;
-        for (int st = 0; st < nbar; st++) {
-            lds_barrier();
-            if (!chain) continue;
+        const int nfull = span / (2 * T);
+        constexpr int NG = 2 * T / 8;  // groups of eight positions per step
+        struct Grp {
+            u32x4 v;
+            float4 a, b;
+        };
+        auto ld = [&](Grp& r, int st, int u) __attribute__((always_inline)) {
             const uint16_t* vrow = vrow0 + (size_t)(st & 1) * 2 * TR;
             const int base = 2 * st * T;
-            const int n = min(2 * T, span - base);
-            if (n == 2 * T) {
-                constexpr int NG = 2 * T / 8;  // groups of eight positions
-                struct Grp {
-                    uint4 v;
-                    float4 a, b;
-                };
-                auto ld = [&](Grp& r, int u) __attribute__((always_inline)) {
-                    r.v = *(const uint4*)(vrow + (u >> 3) * TR + 8 * (u & 7));
-                    r.a = *(const float4*)&w[base + 8 * u];
-                    r.b = *(const float4*)&w[base + 8 * u + 4];
-                };
-                auto run = [&](const Grp& r) __attribute__((always_inline)) {
-                    acc = fmaf(r.a.x, f16_bits_to_f32(r.v.x & 0xffffu), acc);
-                    acc = fmaf(r.a.y, f16_bits_to_f32(r.v.x >> 16), acc);
-                    acc = fmaf(r.a.z, f16_bits_to_f32(r.v.y & 0xffffu), acc);
-                    acc = fmaf(r.a.w, f16_bits_to_f32(r.v.y >> 16), acc);
-                    acc = fmaf(r.b.x, f16_bits_to_f32(r.v.z & 0xffffu), acc);
-                    acc = fmaf(r.b.y, f16_bits_to_f32(r.v.z >> 16), acc);
-                    acc = fmaf(r.b.z, f16_bits_to_f32(r.v.w & 0xffffu), acc);
-                    acc = fmaf(r.b.w, f16_bits_to_f32(r.v.w >> 16), acc);
-                };
-                Grp ring[4];
-                ld(ring[0], 0);
-                ld(ring[1], 1);
-                ld(ring[2], 2);
+            r.v = *(const u32x4*)(vrow + (u >> 3) * TR + 8 * (u & 7));
+            r.a = *(const float4*)&w[base + 8 * u];
+            r.b = *(const float4*)&w[base + 8 * u + 4];
+        };
+        auto run = [&](const Grp& r) __attribute__((always_inline)) {
+            acc = fmaf(r.a.x, f16_bits_to_f32(r.v.x & 0xffffu), acc);
+            acc = fmaf(r.a.y, f16_bits_to_f32(r.v.x >> 16), acc);
+            acc = fmaf(r.a.z, f16_bits_to_f32(r.v.y & 0xffffu), acc);
+            acc = fmaf(r.a.w, f16_bits_to_f32(r.v.y >> 16), acc);
+            acc = fmaf(r.b.x, f16_bits_to_f32(r.v.z & 0xffffu), acc);
+            acc = fmaf(r.b.y, f16_bits_to_f32(r.v.z >> 16), acc);
+            acc = fmaf(r.b.z, f16_bits_to_f32(r.v.w & 0xffffu), acc);
+            acc = fmaf(r.b.w, f16_bits_to_f32(r.v.w >> 16), acc);
+        };
+        Grp ring[4];
+        // one whole step; the last one takes no barrier inside and reads
+        // nothing ahead (no branch inside a step: the compiler would sink
+        // the chain below it and issue every read first)
+        auto whole = [&](int st, const bool last) __attribute__((always_inline)) {
 #pragma unroll
-                for (int u = 0; u < NG; u++) {
-                    if (u + 3 < NG) ld(ring[(u + 3) & 3], u + 3);
-                    __builtin_amdgcn_sched_barrier(0);
-                    run(ring[u & 3]);
-                    __builtin_amdgcn_sched_barrier(0);
+            for (int u = 0; u < NG; u++) {
+                if (u + 3 < NG) ld(ring[(u + 3) & 3], st, u + 3);
+                if (u == NG - 2 && !last) {
+                    wait_lgkm0();
+                    lds_barrier();  // barrier st + 1
+                    ld(ring[0], st + 1, 0);
+                    ld(ring[1], st + 1, 1);
                 }
-            } else {
-                for (int p = 0; p < n; p++)
-                    acc = fmaf(w[base + p], f16_bits_to_f32(vrow[(p / T) * TR + p % T]), acc);
+                if (u == NG - 1 && !last) ld(ring[2], st + 1, 2);
+                __builtin_amdgcn_sched_barrier(0);
+                run(ring[u & 3]);
+                __builtin_amdgcn_sched_barrier(0);
             }
+        };
+        if (nbar > 0) lds_barrier();  // barrier 0: step 0 staged
+        if (nfull > 0) {
+            ld(ring[0], 0, 0);
+            ld(ring[1], 0, 1);
+            ld(ring[2], 0, 2);
+            for (int st = 0; st < nfull - 1; st++) whole(st, false);
+            whole(nfull - 1, true);
+            if (nfull < nbar) lds_barrier();  // barrier nfull
         }
+        if (nfull < nsteps) {  // the partial last step (its barrier is taken)
+            const uint16_t* vrow = vrow0 + (size_t)(nfull & 1) * 2 * TR;
+            const int base = 2 * nfull * T;
+            for (int p = 0; p < span - base; p++)
+                acc = fmaf(w[base + p], f16_bits_to_f32(vrow[(p / T) * TR + p % T]), acc);
+        }
+        for (int b = min(nfull + 1, nbar); b < nbar; b++) lds_barrier();
         const float denom = __shfl(acc, DW);
         const float inv = denom > 0.0f ? 1.0f / denom : 1.0f;
         if (tid < DW) out[(size_t)h * kFusedHD + slice * DW + tid] = acc * inv;
     } else if (stager) {
         // one step: split the eight dwords into the two elements' runs, write
-        // them, refill the registers P steps ahead, barrier; whole groups of
+        // them, refill the registers P steps ahead, exponentiate the step's
+        // weights (lane l < 32 of stager si: position 32 si + l of the step,
+        // fast_exp as exp_row applies it), barrier; whole groups of
         // P steps (a branch around a step would make the compiler's vmcnt
         // waits drain the prefetch): steps past the span stage clamped rows
         // that no chain reads
         uint16_t* dst0 = vt + ((sp0 >> 6) * kLongRows + 2 * c) * kLongRow + (sp0 & 63);
         auto step = [&](int st, uint32_t (&r)[8]) __attribute__((always_inline)) {
             uint16_t* dst = dst0 + (size_t)(st & 1) * 2 * TR;
+            const int pw = 2 * st * T + 32 * si + (lane & 31);
+            const float sv = w[min(pw, span - 1)];
             uint4 lo, hi;
             lo.x = __builtin_amdgcn_perm(r[1], r[0], 0x05040100u);
             lo.y = __builtin_amdgcn_perm(r[3], r[2], 0x05040100u);
@@ -641,6 +674,8 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(1,
             *(uint4*)dst = lo;
             *(uint4*)(dst + kLongRow) = hi;
             fetch(st + P, r);
+            const float e = fast_exp(sv - mx);
+            if (lane < 32 && pw < span) w[pw] = e;
             wait_lgkm0();
             lds_barrier();
         };

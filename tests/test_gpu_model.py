@@ -30,6 +30,27 @@ def test_decode_steps_bit_exact(hip):
         tok = want
 
 
+def test_captured_decode_long_cache_bit_exact(hip):
+    """A cache longer than the one-token values kernel's LDS image (4000 >
+    3272 positions, head_dim 128): the captured decode step runs the
+    long-span values kernel with the span read on the device, from one
+    position through spans past one 128-position staging step; hidden
+    states and greedy tokens identical to the oracle's."""
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = tiny_llama(seed=21, n_layers=2, dim=512, hidden=1024, n_heads=4, n_kv_heads=1,
+                   head_dim=128, vocab=1000)
+    max_len = 4000
+    gpu = LlamaDecoder.from_host_model(m, max_len)
+    cpu = ref.Llama(m, max_len)
+    tok = 11
+    for pos in range(136):
+        want, hid = cpu.decode(tok, pos)
+        got = gpu.decode(tok, pos)
+        assert np.array_equal(bits(gpu.hidden()), bits(hid)), pos
+        assert got == want, pos
+        tok = want
+
+
 def test_prefill_then_decode_tokens_identical(hip):
     from gopherllm_amd.decoder import LlamaDecoder
     m = tiny_llama(seed=4, n_layers=3, dim=512, hidden=1536, n_heads=8, n_kv_heads=2, head_dim=64,
