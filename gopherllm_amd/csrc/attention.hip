@@ -236,7 +236,7 @@ struct AttnRope {
 __global__ __launch_bounds__(256) void attn_scores128_kernel(
     const float* __restrict__ q, const uint16_t* K, const uint16_t* V, int kv_dim, int n_kv,
     int kvmul, int start, int span0, int span_max, float scale, float* __restrict__ scores,
-    const int* __restrict__ d_end, AttnRope rope) {
+    const int* __restrict__ d_end, AttnRope rope, int touch) {
     constexpr int pairs = kFusedHD / 2;
     __shared__ __align__(16) float qs[4 * kFusedHD];
     __shared__ __align__(16) uint16_t kcur[kFusedHD];
@@ -263,12 +263,14 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
     // one dword of each 128-byte line of the chunk's V rows of this kv head
     // (lane l: row l / 2, line l % 2; the four waves touch the same lines):
     // workgroup (g, chunk) runs on XCD g % 8, as do the values launch's
-    // workgroups of kv head g, which then find these lines in that XCD's L2
+    // workgroups of kv head g, which then find these lines in that XCD's L2.
+    // touch == 0 (spans whose K and V pass through more than an L2): every
+    // lane reads the chunk's first line, which the K copies fetch anyway.
     uint32_t vtouch;
     {
-        const int row = min(chunk * kScoreChunk + (lane >> 1), span_max - 1);
-        vtouch = *(const uint32_t*)(V + (size_t)(start + row) * kv_dim + (size_t)g * kFusedHD +
-                                    64 * (lane & 1));
+        const int row = min(chunk * kScoreChunk + (touch ? lane >> 1 : 0), span_max - 1);
+        vtouch = *(const uint32_t*)((touch ? V : K) + (size_t)(start + row) * kv_dim +
+                                    (size_t)g * kFusedHD + (touch ? 64 * (lane & 1) : 0));
     }
     // (unconditional loads, clamped or from a dummy row: a load under a
     // branch is waited for at the branch's end, behind the copies)
@@ -503,6 +505,7 @@ constexpr int kLongP = 8;        // steps (two tiles each) in flight per staging
 constexpr int kLongRow = 72;     // halves per element row of a staged tile (64 + 8 padding)
 constexpr int kLongRows = 33;    // rows per staged tile: 32 elements and the row of ones
 constexpr int kLongSpan = 32768;
+constexpr int kTouchSpan = 8192;  // longest span whose V the scores launch touches
 static size_t long_lds_bytes(int span_max) {
     return ((size_t)((span_max + 3) & ~3) + 8) * 4 + 4 * (size_t)kLongRows * kLongRow * 2;
 }
@@ -1465,9 +1468,11 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
                             : (float*)thread_scratch(5, (size_t)p * n_heads * span_max * 4 + 256, s);
         if (!sc) return scratch_error();
         const int nchunk = (span_max + kScoreChunk - 1) / kScoreChunk;
+        // the V touch pays while one kv head's K and V rows fit an XCD's
+        // 4 MB L2 (256 bytes each per position)
         hipLaunchKernelGGL(attn_scores128_kernel, dim3(n_kv, nchunk, p), dim3(256), 0, s, d_q,
                            kv->k[l], kv->v[l], kv->kv_dim_k, n_kv, kvmul, start, span0, span_max,
-                           scale, sc, d_end, rope);
+                           scale, sc, d_end, rope, (int)(span_max <= kTouchSpan));
         GLLM_HIP(hipGetLastError());
         // one token: four workgroups per head (a quarter of each V row apiece);
         // prefill tokens already give n_heads * p workgroups
