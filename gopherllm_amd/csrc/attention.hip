@@ -233,6 +233,7 @@ struct AttnRope {
     const float* cur;      // optional: the current position's sin row then cos row
 };
 
+constexpr int kEagerRows = 2048;  // rows loaded before a device-side position is read
 __global__ __launch_bounds__(256) void attn_scores128_kernel(
     const float* __restrict__ q, const uint16_t* K, const uint16_t* V, int kv_dim, int n_kv,
     int kvmul, int start, int span0, int span_max, float scale, float* __restrict__ scores,
@@ -244,6 +245,18 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
     // (two 1 KB copies per wave), read by every head's threads of a row
     __shared__ __align__(16) uint8_t kst[kFusedHD / 8][kScoreChunk][16];
     const int g = blockIdx.x, chunk = blockIdx.y, tok = blockIdx.z;
+    // A captured step's launch covers the whole span cap: chunks past the
+    // first kEagerRows positions read the position first and leave before
+    // loading anything when they lie past the span.
+    // (near chunks wait for no argument load: the empty asm keeps the
+    // compiler from folding the pointer test into one flag ahead of the
+    // branch)
+    if (chunk * kScoreChunk >= kEagerRows) {  // uniform
+        const int* de = d_end;
+        asm volatile("" : "+s"(de));
+        if (de && chunk * kScoreChunk >= __builtin_amdgcn_readfirstlane(*de) - start + 1 + tok)
+            return;  // the whole workgroup
+    }
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n_heads = n_kv * kvmul;

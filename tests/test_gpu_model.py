@@ -51,6 +51,33 @@ def test_captured_decode_long_cache_bit_exact(hip):
         tok = want
 
 
+def test_captured_decode_past_eager_rows_bit_exact(hip):
+    """Captured decode steps at spans past 2048 positions in a 4000-position
+    cache: the scores chunks past the first 2048 rows read the position
+    before loading, those inside the span score their rows and those past it
+    leave at once; hidden states and greedy tokens identical to the oracle's
+    after a 2100-token prefill."""
+    from gopherllm_amd.decoder import LlamaDecoder
+    m = tiny_llama(seed=22, n_layers=2, dim=512, hidden=1024, n_heads=4, n_kv_heads=1,
+                   head_dim=128, vocab=1000)
+    max_len = 4000
+    gpu = LlamaDecoder.from_host_model(m, max_len)
+    cpu = ref.Llama(m, max_len)
+    prompt = np.random.default_rng(23).integers(0, 1000, 2100)
+    print("long-cache prefill 2100 tokens", flush=True)
+    gt = gpu.prefill(prompt)
+    ct, _ = cpu.prefill(prompt)
+    assert gt == ct
+    tok = ct
+    for pos in range(2100, 2104):
+        print(f"long-cache decode pos {pos}", flush=True)
+        want, hid = cpu.decode(tok, pos)
+        got = gpu.decode(tok, pos)
+        assert np.array_equal(bits(gpu.hidden()), bits(hid)), pos
+        assert got == want, pos
+        tok = want
+
+
 def test_prefill_then_decode_tokens_identical(hip):
     from gopherllm_amd.decoder import LlamaDecoder
     m = tiny_llama(seed=4, n_layers=3, dim=512, hidden=1536, n_heads=8, n_kv_heads=2, head_dim=64,
