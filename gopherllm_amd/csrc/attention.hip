@@ -234,10 +234,13 @@ struct AttnRope {
 };
 
 constexpr int kEagerRows = 2048;  // rows loaded before a device-side position is read
+// CM: also write each chunk's maximum per head to cmax (the long-span values
+// kernel's input; the other values kernels take the maximum themselves)
+template <bool CM>
 __global__ __launch_bounds__(256) void attn_scores128_kernel(
     const float* __restrict__ q, const uint16_t* K, const uint16_t* V, int kv_dim, int n_kv,
     int kvmul, int start, int span0, int span_max, float scale, float* __restrict__ scores,
-    const int* __restrict__ d_end, AttnRope rope, int touch) {
+    const int* __restrict__ d_end, AttnRope rope, int touch, float* __restrict__ cmax) {
     constexpr int pairs = kFusedHD / 2;
     __shared__ __align__(16) float qs[4 * kFusedHD];
     __shared__ __align__(16) uint16_t kcur[kFusedHD];
@@ -362,11 +365,18 @@ __global__ __launch_bounds__(256) void attn_scores128_kernel(
     float o[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) o[j] = __shfl_xor(acc[j], 32);
+    float sv = -__int_as_float(0x7f800000);
     if (half == 0 && t < span) {
         const float a0 = acc[0] + o[0], a1 = acc[1] + o[1];
         const float a2 = acc[2] + o[2], a3 = acc[3] + o[3];
-        scores[((size_t)tok * n_heads + (size_t)g * kvmul + h) * span_max + t] =
-            ((a0 + a1) + (a2 + a3)) * scale;
+        sv = ((a0 + a1) + (a2 + a3)) * scale;
+        scores[((size_t)tok * n_heads + (size_t)g * kvmul + h) * span_max + t] = sv;
+    }
+    // the chunk's maximum per head, for the long-span values kernel (fmaxf
+    // over the same values: the row's maximum is the chunks' maximum)
+    if (CM) {
+        const float mc = wave_max(sv);
+        if (lane == 0) cmax[((size_t)tok * n_heads + (size_t)g * kvmul + h) * gridDim.y + chunk] = mc;
     }
 }
 
@@ -524,8 +534,9 @@ static size_t long_lds_bytes(int span_max) {
 }
 
 __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_values_long_kernel(
-    const float* __restrict__ scores, const uint16_t* __restrict__ V, int kv_dim, int kvmul,
-    int start, int span0, int span_max, float* __restrict__ out, const int* __restrict__ d_end) {
+    const float* __restrict__ scores, const float* __restrict__ cmax, const uint16_t* __restrict__ V,
+    int kv_dim, int kvmul, int start, int span0, int span_max, float* __restrict__ out,
+    const int* __restrict__ d_end) {
     constexpr int DW = 32, T = kVTile, P = kLongP, TR = kLongRows * kLongRow;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     // Workgroup b runs on XCD b % 8.  The (kv head g, pair of quarters, q
@@ -563,28 +574,50 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(1,
 #pragma unroll
         for (int q = 0; q < P; q++) fetch(q, pre[q]);
     }
+    // wave 4 streams the raw score row into LDS one step ahead of the exps:
+    // lane l holds positions 2l and 2l + 1 of a step, P steps in flight
+    // (spre[k] holds the steps st == k mod P; rows clamped to span_max - 1)
+    const float* srow = scores + (size_t)h * span_max;
+    float spre[P][2];
+    auto sfetch = [&](int st, float (&r)[2]) __attribute__((always_inline)) {
+        const int p0 = 2 * st * T + 2 * lane;
+        r[0] = srow[min(p0, span_max - 1)];
+        r[1] = srow[min(p0 + 1, span_max - 1)];
+    };
+    if (wave == 4) {
+#pragma unroll
+        for (int q = 0; q < P; q++) sfetch(q, spre[q]);
+    }
     if (d_end) span0 = *d_end - start + 1;
     const int span = min(span0, span_max);
     const int nsteps = (span + 2 * T - 1) / (2 * T);
-    const float* srow = scores + (size_t)h * span_max;
-    // the score row into LDS, sixteen loads in flight per thread (positions
-    // clamped to span - 1: the duplicates leave the maximum unchanged)
+    auto sput = [&](int st, const float (&r)[2]) __attribute__((always_inline)) {
+        const int p0 = 2 * st * T + 2 * lane;
+        if (p0 < span) w[p0] = r[0];
+        if (p0 + 1 < span) w[p0 + 1] = r[1];
+    };
+    // the row's maximum from the scores launch's chunk maxima, read by waves
+    // 0 and 4 (no V prefetch queued ahead of their loads; chunks clamped to
+    // the span's last: the duplicates leave the maximum unchanged)
     float m = -__int_as_float(0x7f800000);
-    for (int t0 = tid; t0 < span; t0 += 16 * kLongThreads) {
-        float v[16];
+    if (wave == 0 || wave == 4) {
+        const int nck = (span + kScoreChunk - 1) / kScoreChunk;
+        const float* crow = cmax + (size_t)h * ((span_max + kScoreChunk - 1) / kScoreChunk);
+        for (int c0 = (wave == 0 ? 0 : 64) + lane; c0 < nck; c0 += 128 * 8) {
+            float v[8];
 #pragma unroll
-        for (int u = 0; u < 16; u++) v[u] = srow[min(t0 + u * kLongThreads, span - 1)];
+            for (int u = 0; u < 8; u++) v[u] = crow[min(c0 + u * 128, nck - 1)];
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-            if (t0 + u * kLongThreads < span) w[t0 + u * kLongThreads] = v[u];
-            m = fmaxf(m, v[u]);
+            for (int u = 0; u < 8; u++) m = fmaxf(m, v[u]);
         }
+        m = wave_max(m);
     }
-    m = wave_max(m);
     if (lane == 0) red[wave] = m;
-    if (wave == 4) {  // the row of ones in each of the four tiles
+    if (wave == 4) {  // the row of ones in each of the four tiles; step 0's scores
 #pragma unroll
         for (int k = 0; k < 4; k++) vt[k * TR + DW * kLongRow + lane] = (uint16_t)0x3C00;
+        sput(0, spre[0]);
+        sfetch(P, spre[0]);
     }
     __syncthreads();
     const float mx = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), fmaxf(red[4], red[5]));
@@ -596,7 +629,7 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(1,
         float acc = 0.0f;
         // The chains in position order, groups of eight positions read three
         // groups ahead in one ring over every whole step (two tiles,
-        // positions 128 st .. 128 st + 127): three groups before a step's
+        // positions 128 st .. 128 st + 127): two groups before a step's
         // end the wave waits for its reads, takes the next step's barrier
         // (the staging waves may then refill this step's pair) and reads
         // the next step's first groups under this step's last 24 FMAs.  As
@@ -700,9 +733,18 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(1,
             for (int q = 0; q < P; q++) step(s0 + q, pre[q]);
         }
     } else {
+        // wave 4: before barrier st, step st + 1's raw scores into LDS (the
+        // staging waves exponentiate them after barrier st), then the
+        // registers refilled P steps ahead; whole groups of P steps, as the
+        // staging waves run
         for (int s0 = 0; s0 < nsteps; s0 += P) {
 #pragma unroll
-            for (int q = 0; q < P; q++) lds_barrier();
+            for (int q = 0; q < P; q++) {
+                sput(s0 + q + 1, spre[(q + 1) % P]);
+                sfetch(s0 + q + 1 + P, spre[(q + 1) % P]);
+                wait_lgkm0();
+                lds_barrier();
+            }
         }
     }
 }
@@ -1454,8 +1496,8 @@ bool attend_exact_graphable(const gllm_hip_kv* kv, int n_heads, int n_kv, int hd
            span_cap <= kSmaxSpan1;
 }
 
-// scratch: p * n_heads * (span_max + 1) + 64 floats of device memory, or
-// null for the calling thread's scratch.  d_end (with p == 1): the end position is read
+// scratch: p * n_heads * (span_max + 1) + n_heads * ceil(span_max / 32) + 64
+// floats of device memory, or null for the calling thread's scratch.  d_end (with p == 1): the end position is read
 // on the device and span_cap bounds the span, so the launches do not depend
 // on the position (a captured decode step replays for every position).
 int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, int n_kv, int hd,
@@ -1477,15 +1519,24 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
     const AttnRope rope{rope_sin, rope_cos, d_knew, d_vnew, kv->k[l], kv->v[l], rope_cur};
     if (hd == kFusedHD && kvmul <= 4 && kv->kv_dim_k == kv->kv_dim_v &&
         span_max <= (p == 1 ? kSmaxSpan1 : kSmaxSpan)) {
-        float* sc = scratch ? scratch
-                            : (float*)thread_scratch(5, (size_t)p * n_heads * span_max * 4 + 256, s);
-        if (!sc) return scratch_error();
         const int nchunk = (span_max + kScoreChunk - 1) / kScoreChunk;
+        // the long-span values kernel takes the row's maximum from per-chunk
+        // maxima that the scores launch writes after the score rows
+        const bool long_path = p == 1 && !vdec_usable(kvmul, span_max) && span_max <= kLongSpan;
+        const size_t sc_floats = (size_t)p * n_heads * span_max + (long_path ? (size_t)n_heads * nchunk : 0);
+        float* sc = scratch ? scratch : (float*)thread_scratch(5, sc_floats * 4 + 256, s);
+        if (!sc) return scratch_error();
+        float* cmax = long_path ? sc + (size_t)n_heads * span_max : nullptr;
         // the V touch pays while one kv head's K and V rows fit an XCD's
         // 4 MB L2 (256 bytes each per position)
-        hipLaunchKernelGGL(attn_scores128_kernel, dim3(n_kv, nchunk, p), dim3(256), 0, s, d_q,
-                           kv->k[l], kv->v[l], kv->kv_dim_k, n_kv, kvmul, start, span0, span_max,
-                           scale, sc, d_end, rope, (int)(span_max <= kTouchSpan));
+        if (long_path)
+            hipLaunchKernelGGL(attn_scores128_kernel<true>, dim3(n_kv, nchunk, p), dim3(256), 0, s,
+                               d_q, kv->k[l], kv->v[l], kv->kv_dim_k, n_kv, kvmul, start, span0,
+                               span_max, scale, sc, d_end, rope, (int)(span_max <= kTouchSpan), cmax);
+        else
+            hipLaunchKernelGGL(attn_scores128_kernel<false>, dim3(n_kv, nchunk, p), dim3(256), 0, s,
+                               d_q, kv->k[l], kv->v[l], kv->kv_dim_k, n_kv, kvmul, start, span0,
+                               span_max, scale, sc, d_end, rope, (int)(span_max <= kTouchSpan), cmax);
         GLLM_HIP(hipGetLastError());
         // one token: four workgroups per head (a quarter of each V row apiece);
         // prefill tokens already give n_heads * p workgroups
@@ -1515,8 +1566,8 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
                                 long_lds_bytes(span_max));
             }
             hipLaunchKernelGGL(attn_values_long_kernel, dim3(n_heads * 4), dim3(kLongThreads),
-                               long_lds_bytes(span_max), s, sc, kv->v[l], kv->kv_dim_v, kvmul,
-                               start, span0, span_max, d_out, d_end);
+                               long_lds_bytes(span_max), s, sc, cmax, kv->v[l], kv->kv_dim_v,
+                               kvmul, start, span0, span_max, d_out, d_end);
         } else if (p == 1) {
             static const bool lds_ok = [] {
                 // dynamic LDS beyond 64 KB for long rows

@@ -85,7 +85,7 @@ struct gllm_hip_model {
     unsigned long long* head_keys = nullptr;
     void* act = nullptr;           // Q8K activation buffers
     size_t act_n = 0;
-    float* scores = nullptr;       // attention scores, max_p * n_heads * (max_len + 1) + 64
+    float* scores = nullptr;       // attention scores and the long-span kernel's chunk maxima
     int* d_pos = nullptr;          // decode position read by the captured decode step
     int* h_pos = nullptr;          // pinned staging for it
     hipGraphExec_t decode_graph = nullptr;  // one decode step, captured after a first eager step
@@ -266,7 +266,8 @@ static int ensure_buffers(gllm_hip_model* m, int p) {
     if (m->scores) (void)hipFree(m->scores);
     // every attention path of a chunk, the long-span one included, works in
     // this buffer (none grows the thread's scratch)
-    GLLM_HIP(hipMalloc(&m->scores, ((size_t)p * c.n_heads * (c.max_len + 1) + 64) * 4));
+    GLLM_HIP(hipMalloc(&m->scores, ((size_t)p * c.n_heads * (c.max_len + 1) +
+                                    (size_t)c.n_heads * ((c.max_len + 31) / 32) + 64) * 4));
     m->max_p = p;
     drop_decode_graph(m);  // it captured the old buffers
     return GLLM_OK;
