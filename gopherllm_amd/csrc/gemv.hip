@@ -990,7 +990,8 @@ __device__ __forceinline__ constexpr int ws_block(int pos) {
 // Loader LW copies the header slots n = LW, LW + NLD, ... (1 KB each), then
 // the blocks at copy positions LW, LW + NLD, ... (R / 8 copies each), and
 // sets a block's flag once its copies have completed, keeping up to D
-// blocks in flight before it waits.
+// blocks in flight before it waits.  Its one workgroup barrier comes after
+// its first D blocks' copies, before its first flag store.
 template <int B, int R, int NS, int NLD, int D, int LW, int I>
 __device__ __forceinline__ void ws_loader_blocks(const uint8_t* __restrict__ w, size_t rb, int r0,
                                                  int nrows, uint8_t* smem) {
@@ -1010,6 +1011,9 @@ __device__ __forceinline__ void ws_loader_blocks(const uint8_t* __restrict__ w, 
             }
         }
         if constexpr (I >= D) {
+            // the workgroup barrier that orders the flag clears before any
+            // flag store: a loader takes it here, after its first copies
+            if constexpr (I == D) lds_barrier();
             // block I - D is complete once at most the copies issued after it remain
             constexpr int after = (I < NBW ? I : NBW - 1) - (I - D);
             wait_vmem_le<after * PER>();
@@ -1069,8 +1073,9 @@ __global__ __launch_bounds__(R * 8 * NS + NLD * 64) void gemv_q4k_ws_kernel(
     // counters before anyone sets or reads them
     if (tid < B) __hip_atomic_store(flags + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (tid < 16) __hip_atomic_store(count + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    wait_lgkm0();
-    lds_barrier();
+    // the loaders' copies go out at once (the copies touch neither the flags
+    // nor the counters); each loader takes the barrier below inside its
+    // block loop, before its first flag store
     if (wave >= NCW) {
         if constexpr (NLD > 0) if (wave == NCW + 0) q4k_ws_loader<B, R, NS, NLD, D, 0>(w, rb, r0, nrows, smem);
         if constexpr (NLD > 1) if (wave == NCW + 1) q4k_ws_loader<B, R, NS, NLD, D, 1>(w, rb, r0, nrows, smem);
@@ -1078,6 +1083,8 @@ __global__ __launch_bounds__(R * 8 * NS + NLD * 64) void gemv_q4k_ws_kernel(
         if constexpr (NLD > 3) if (wave == NCW + 3) q4k_ws_loader<B, R, NS, NLD, D, 3>(w, rb, r0, nrows, smem);
         return;
     }
+    wait_lgkm0();
+    lds_barrier();
     int8_t* q8b = (int8_t*)smem;
     float* xs32b = (float*)(smem + cols);
     float* xscb = xs32b + cols / 32;
