@@ -521,8 +521,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 // of eight positions ahead: lanes 0-31 the 32 value chains, lane 32 the
 // denominator, as fma(w, 1.0, denom) over a row of ones that every tile
 // carries (w * 1 is exact, so each step rounds as denom + w does).  Wave 4,
-// placed on wave 0's SIMD, stays idle between the barriers: work there slows
-// the chain.
+// placed on wave 0's SIMD, only streams the raw score row (two loads and two
+// LDS writes a step): heavier work there slows the chain.
 constexpr int kLongThreads = 384;  // wave 0: the chains; waves 1-3, 5: staging
 constexpr int kLongP = 8;        // steps (two tiles each) in flight per staging lane
 constexpr int kLongRow = 72;     // halves per element row of a staged tile (64 + 8 padding)
