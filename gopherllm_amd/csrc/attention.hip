@@ -1528,15 +1528,17 @@ int attend_exact(const gllm_hip_kv* kv, int l, const float* d_q, int n_heads, in
         if (!sc) return scratch_error();
         float* cmax = long_path ? sc + (size_t)n_heads * span_max : nullptr;
         // the V touch pays while one kv head's K and V rows fit an XCD's
-        // 4 MB L2 (256 bytes each per position)
+        // 4 MB L2 (256 bytes each per position), and not ahead of the
+        // long-span kernel, whose deep V prefetch measured faster untouched
+        const int touch = span_max <= kTouchSpan && !long_path;
         if (long_path)
             hipLaunchKernelGGL(attn_scores128_kernel<true>, dim3(n_kv, nchunk, p), dim3(256), 0, s,
                                d_q, kv->k[l], kv->v[l], kv->kv_dim_k, n_kv, kvmul, start, span0,
-                               span_max, scale, sc, d_end, rope, (int)(span_max <= kTouchSpan), cmax);
+                               span_max, scale, sc, d_end, rope, touch, cmax);
         else
             hipLaunchKernelGGL(attn_scores128_kernel<false>, dim3(n_kv, nchunk, p), dim3(256), 0, s,
                                d_q, kv->k[l], kv->v[l], kv->kv_dim_k, n_kv, kvmul, start, span0,
-                               span_max, scale, sc, d_end, rope, (int)(span_max <= kTouchSpan), cmax);
+                               span_max, scale, sc, d_end, rope, touch, cmax);
         GLLM_HIP(hipGetLastError());
         // one token: four workgroups per head (a quarter of each V row apiece);
         // prefill tokens already give n_heads * p workgroups
